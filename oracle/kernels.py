@@ -1,0 +1,190 @@
+"""TEST INFRASTRUCTURE ONLY. The spec kernels restated as loops over tiles on CPU torch tensors.
+
+Each function follows one of the reference's examples loop for loop, with `@` accumulating bf16
+products in f32 (src/autokernel/mxu.py:21-43), and rounds where the spec rounds (`.astype(dtype)`).
+Sizes here must be ones a CPU finishes in seconds; the GPU tests compare against these on the same
+seeded inputs.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+import torch
+
+LANES = 128
+MASK_VALUE = -1e30
+
+
+def _f32(x: torch.Tensor) -> torch.Tensor:
+    return x.detach().to("cpu", torch.float32)
+
+
+def matmul(x: torch.Tensor, y: torch.Tensor, tm: int = 512, tn: int = 512, tk: int = 512) -> torch.Tensor:
+    """examples/matmul.py:22-35: out[i, j] tile = bf16(sum_k x[i, k] @ y[k, j]), f32 accumulation."""
+    M, K = x.shape
+    N = y.shape[1]
+    tm, tn, tk = min(tm, M), min(tn, N), min(tk, K)
+    xf, yf = _f32(x), _f32(y)
+    out = torch.zeros((M, N), dtype=x.dtype)
+    for i in range(0, M, tm):
+        for j in range(0, N, tn):
+            acc = torch.zeros((tm, tn), dtype=torch.float32)
+            for k in range(0, K, tk):
+                acc += xf[i:i + tm, k:k + tk] @ yf[k:k + tk, j:j + tn]
+            out[i:i + tm, j:j + tn] = acc.to(x.dtype)
+    return out
+
+
+def causal_matmul(x: torch.Tensor, y: torch.Tensor, tm: int = 512, tn: int = 512, tk: int = 512) -> torch.Tensor:
+    """examples/causal_matmul.py:23-40: tiles wholly above the diagonal (j > i + tm - 1) keep the zeros of
+    the allocation; computed tiles are zeroed above the diagonal by `where(cols <= rows, acc, 0)`."""
+    M, K = x.shape
+    N = y.shape[1]
+    tm, tn, tk = min(tm, M), min(tn, N), min(tk, K)
+    xf, yf = _f32(x), _f32(y)
+    out = torch.zeros((M, N), dtype=x.dtype)
+    for i in range(0, M, tm):
+        for j in range(0, N, tn):
+            if j > i + tm - 1:
+                continue
+            acc = torch.zeros((tm, tn), dtype=torch.float32)
+            for k in range(0, K, tk):
+                acc += xf[i:i + tm, k:k + tk] @ yf[k:k + tk, j:j + tn]
+            rows = i + torch.arange(tm).reshape(-1, 1)
+            cols = j + torch.arange(tn).reshape(1, -1)
+            out[i:i + tm, j:j + tn] = torch.where(cols <= rows, acc, torch.zeros(())).to(x.dtype)
+    return out
+
+
+def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bq: int = 512, bk: int = 512) -> torch.Tensor:
+    """examples/causal_attention.py:37-63: online softmax over key blocks not wholly in the future; scores
+    s = q @ k.T in f32, masked with -1e30 above the diagonal; p cast to bf16 before `p @ v` (f32 acc)."""
+    B, H, S, D = q.shape
+    bq, bk = min(bq, S), min(bk, S)
+    dtype = q.dtype
+    qf, kf, vf = _f32(q), _f32(k), _f32(v)
+    out = torch.zeros((B, H, S, D), dtype=dtype)
+    for b in range(B):
+        for h in range(H):
+            for i in range(0, S, bq):
+                row_max = torch.full((bq, 1), MASK_VALUE)
+                row_sum = torch.zeros((bq, 1))
+                acc = torch.zeros((bq, D))
+                for j in range(0, S, bk):
+                    if j > i + bq - 1:
+                        continue
+                    s = qf[b, h, i:i + bq] @ kf[b, h, j:j + bk].T
+                    rows = i + torch.arange(bq).reshape(-1, 1)
+                    cols = j + torch.arange(bk).reshape(1, -1)
+                    s = torch.where(cols <= rows, s, torch.tensor(MASK_VALUE))
+                    max_new = torch.maximum(row_max, s.max(dim=1, keepdim=True).values)
+                    p = torch.exp(s - max_new)
+                    alpha = torch.exp(row_max - max_new)
+                    row_sum = alpha * row_sum + p.sum(dim=1, keepdim=True)
+                    acc = alpha * acc + p.to(dtype).float() @ vf[b, h, j:j + bk]
+                    row_max = max_new
+                out[b, h, i:i + bq] = (acc / row_sum).to(dtype)
+    return out
+
+
+def attention_float64(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> np.ndarray:
+    """Causal softmax(q k^T) v in float64: what the reference's own tests compare attention against
+    (tests/test_examples.py:71-77 of the reference)."""
+    qd, kd, vd = (t.detach().cpu().double() for t in (q, k, v))
+    S = q.shape[2]
+    s = qd @ kd.transpose(-1, -2)
+    mask = torch.ones(S, S, dtype=torch.bool).tril()
+    s = s.masked_fill(~mask, float("-inf"))
+    return (torch.softmax(s, dim=-1) @ vd).numpy()
+
+
+def grouped_matmul(xs: torch.Tensor, w: torch.Tensor, group_expert: torch.Tensor, tn: int = 512,
+                   tk: int = 512) -> torch.Tensor:
+    """The grouped matmul of config 4 (examples/moe.py:167-187's runtime window `w[tile_expert[i // G]]`,
+    in the single-matrix form of tests/test_index_arrays.py:109-125): each group of G rows through its
+    expert's weights; groups with expert < 0 keep the zeros; the expert index is clamped into [0, E)."""
+    M, K = xs.shape
+    E, _, N = w.shape
+    G = M // group_expert.shape[0]
+    tn, tk = min(tn, N), min(tk, K)
+    xf, wf = _f32(xs), _f32(w)
+    ge = group_expert.cpu().numpy()
+    out = torch.zeros((M, N), dtype=xs.dtype)
+    for j in range(0, N, tn):
+        for i in range(0, M, G):
+            e = int(ge[i // G])
+            if e < 0:
+                continue
+            e = min(max(e, 0), E - 1)
+            acc = torch.zeros((G, tn))
+            for k in range(0, K, tk):
+                acc += xf[i:i + G, k:k + tk] @ wf[e, k:k + tk, j:j + tn]
+            out[i:i + G, j:j + tn] = acc.to(xs.dtype)
+    return out
+
+
+def paged_gqa_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, block_tables: torch.Tensor,
+                     lengths: torch.Tensor) -> torch.Tensor:
+    """examples/decode.py:199-223 (one new token, T = 1): each query head h attends its kv head
+    h // (H / Hkv) over positions < lengths[b], pages read through block_tables[b, p] (clamped); scores in
+    f32, p rounded to bf16 before `p @ v`; empty sequences give zeros."""
+    B, T, H, Dh = q.shape
+    P, W = k_pages.shape[1], k_pages.shape[2]
+    Hkv = W // Dh
+    group = H // Hkv
+    n_pages = k_pages.shape[0]
+    qf, kf, vf = _f32(q), _f32(k_pages), _f32(v_pages)
+    tables = block_tables.cpu().numpy()
+    lens = lengths.cpu().numpy()
+    out = torch.zeros((B, T, H, Dh), dtype=q.dtype)
+    for b in range(B):
+        L = int(lens[b])
+        pages = [min(max(int(tables[b, p]), 0), n_pages - 1) for p in range(tables.shape[1]) if p * P < L]
+        if not pages:
+            continue
+        kk = torch.cat([kf[p] for p in pages])[:, :].reshape(-1, Hkv, Dh)
+        vv = torch.cat([vf[p] for p in pages])[:, :].reshape(-1, Hkv, Dh)
+        for h in range(H):
+            g = h // group
+            row_max = torch.tensor(MASK_VALUE)
+            row_sum = torch.tensor(0.0)
+            acc = torch.zeros(Dh)
+            for n, page in enumerate(pages):
+                s = (kf[page].reshape(P, Hkv, Dh)[:, g] @ qf[b, 0, h])
+                pos = n * P + torch.arange(P)
+                s = torch.where(pos < L, s, torch.tensor(MASK_VALUE))
+                m_new = torch.maximum(row_max, s.max())
+                p = torch.exp(s - m_new)
+                alpha = torch.exp(row_max - m_new)
+                row_sum = alpha * row_sum + p.sum()
+                acc = alpha * acc + p.to(q.dtype).float() @ vf[page].reshape(P, Hkv, Dh)[:, g]
+                row_max = m_new
+            out[b, 0, h] = (acc / torch.clamp(row_sum, min=1e-30)).to(q.dtype)
+    return out
+
+
+def gqa_float64(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, block_tables: torch.Tensor,
+                lengths: torch.Tensor) -> np.ndarray:
+    """GQA decode attention in float64 over the pages (tests/test_decode.py:62-76 of the reference)."""
+    B, T, H, Dh = q.shape
+    P, W = k_pages.shape[1], k_pages.shape[2]
+    Hkv = W // Dh
+    out = np.zeros((B, T, H, Dh))
+    tables = block_tables.cpu().numpy()
+    lens = lengths.cpu().numpy()
+    kd, vd, qd = k_pages.double().cpu(), v_pages.double().cpu(), q.double().cpu()
+    for b in range(B):
+        L = int(lens[b])
+        if L == 0:
+            continue
+        npages = -(-L // P)
+        kk = torch.cat([kd[int(tables[b, p])] for p in range(npages)])[:L].reshape(L, Hkv, Dh)
+        vv = torch.cat([vd[int(tables[b, p])] for p in range(npages)])[:L].reshape(L, Hkv, Dh)
+        for h in range(H):
+            g = h // (H // Hkv)
+            s = kk[:, g] @ qd[b, 0, h]
+            out[b, 0, h] = (torch.softmax(s, 0) @ vv[:, g]).numpy()
+    return out

@@ -1,0 +1,52 @@
+"""Lower a planned loop nest to gfx950: HIP C++ source plus the host program that launches it.
+
+The reference's codegen emits one Pallas kernel per loop nest (src/autokernel/codegen.py:91-1755). Here a
+loop nest's traced tile code is matched against the kernel families the backend lowers, each a persistent
+HIP kernel generated from the plan and schedule:
+
+- `gemm`: `acc += a @ b` (or `@ b.T`) over a reduction loop, then a pointwise epilogue (dense, causal and
+  grouped matmuls);
+- `flash`: the online-softmax reduction of attention (causal flash attention, paged decode).
+
+A loop nest no family takes raises KernelError naming the kernel: the gfx950 backend doesn't lower it yet.
+"""
+
+from __future__ import annotations
+
+import re
+from typing import Any
+
+from ..errors import KernelError
+from ..pipeline import Pipeline
+from ..plan import Plan
+from ..schedule import Schedule
+from .program import Program
+
+__all__ = ["Program", "default_pipeline", "generate"]
+
+
+def _symbol(plan: Plan) -> str:
+    return "tj_" + re.sub(r"[^A-Za-z0-9_]", "_", plan.nest.name)
+
+
+def default_pipeline(plan: Plan, schedule: Schedule) -> Pipeline:
+    """Two LDS slots per streamed operand (a 256x256x64 bf16 matmul tile fills 128 KiB with two), two
+    output buffers: the starting point tuning moves from."""
+    return Pipeline(2, 2)
+
+
+def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool = False) -> Program:
+    """The program for this plan, schedule and pipeline."""
+    from . import flash, gemm
+
+    name = _symbol(plan)
+    found = gemm.match(plan)
+    if found is not None:
+        return gemm.lower(plan, schedule, pipeline, found, name)
+    found = flash.match(plan)
+    if found is not None:
+        return flash.lower(plan, schedule, pipeline, found, name)
+    raise KernelError(
+        f"{plan.nest.name}: the gfx950 backend has no lowering for this loop nest's tile code yet "
+        "(it lowers matmuls with pointwise epilogues and online-softmax attention)"
+    )

@@ -1,0 +1,146 @@
+"""Pieces every gfx950 lowering shares: addressing tiles of row-major arrays, decoding tiles and steps
+from the schedule, and the work lists that spread output tiles over the GPU's workgroups."""
+
+from __future__ import annotations
+
+import ast
+import heapq
+import math
+from dataclasses import dataclass
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from .. import gfx950
+from ..errors import KernelError
+from ..plan import Plan, Tile, Window
+from ..schedule import CODE_SHIFT, FILL_TABLE, STEP_CODE, TILE_TABLE, Schedule
+from .expr import int_expr
+
+__all__ = ["strides", "tile_base", "decode_tile", "decode_fill", "Index", "work_lists"]
+
+
+def strides(shape: Sequence[int]) -> List[int]:
+    out, n = [], 1
+    for d in reversed(shape):
+        out.append(n)
+        n *= d
+    return list(reversed(out))
+
+
+class Index:
+    """C expressions for index-array elements, `lengths[b]` -> `args.lengths[b]`, clamped into the array's
+    dims where `clamp` (a runtime window index, which JAX clamps into the dim it indexes)."""
+
+    def __init__(self, plan: Plan, names: Callable[[str], Optional[str]], args: str = "args") -> None:
+        self.plan, self.names, self.args = plan, names, args
+
+    def read(self, node: ast.Subscript) -> str:
+        ix = self.plan.index(node.value.id)  # type: ignore[attr-defined]
+        dims = node.slice.elts if isinstance(node.slice, ast.Tuple) else [node.slice]
+        flat = "0"
+        for d, (expr, stride) in enumerate(zip(dims, strides(ix.shape))):
+            flat = f"({flat} + {self.expr(expr)} * {stride})"
+        return f"{self.args}.{ix.name}[{flat}]"
+
+    def expr(self, node: ast.expr) -> str:
+        return int_expr(node, self.names, self.read)
+
+
+def tile_base(tile: Tile, shape: Sequence[int], index: Index, loop_value: Callable[[str], str]) -> Tuple[str, List[int]]:
+    """The flat offset (C) of a tile's first element given the loop values, and the strides of its sliced
+    dims. A runtime window index is clamped into its dim (as JAX clamps out-of-range indices)."""
+    terms = []
+    sliced = []
+    for w, dim, stride in zip(tile.windows, shape, strides(shape)):
+        if w.index is not None:
+            terms.append(f"(long long)ak_clamp({index.read(w.index)}, 0, {dim - 1}) * {stride}")
+        else:
+            off = str(w.offset) if w.offset else ""
+            if w.loop is not None:
+                off = f"({loop_value(w.loop)} + {w.offset})" if w.offset else loop_value(w.loop)
+            if off:
+                terms.append(f"(long long)({off}) * {stride}")
+        if w.size is not None:
+            sliced.append(stride)
+    return (" + ".join(terms) if terms else "0"), sliced
+
+
+def decode_tile(plan: Plan, sch: Schedule, t: str, prefix: str = "lv_") -> List[str]:
+    """C statements setting `<prefix><var>` to each parallel loop's value at tile `t` (the t-th that runs)."""
+    lines = []
+    outer, inner = sch.outer, sch.inner
+    if sch.tile_tables:
+        lines.append(f"const int rep_ = {t} / {sch.pattern_tiles}, tt_ = {t} % {sch.pattern_tiles};")
+        rest = "rep_"
+        for r in reversed(outer):
+            lines.append(f"const int {prefix}{r.var} = {r.start} + ({rest} % {r.count}) * {r.step};")
+            rest = f"({rest} / {r.count})"
+        for r in inner:
+            lines.append(f"const int {prefix}{r.var} = {r.start} + args.{TILE_TABLE % r.var}[tt_] * {r.step};")
+    else:
+        rest = t
+        for r in reversed(plan.parallel):
+            lines.append(f"const int {prefix}{r.var} = {r.start} + (({rest}) % {r.count}) * {r.step};")
+            rest = f"(({rest}) / {r.count})"
+    return lines
+
+
+def decode_fill(plan: Plan, sch: Schedule, f: str, prefix: str = "lv_") -> List[str]:
+    """C statements setting each parallel loop's value at the f-th tile a mask skips."""
+    lines = [f"const int frep_ = {f} / {sch.pattern_fills}, ff_ = {f} % {sch.pattern_fills};"]
+    rest = "frep_"
+    for r in reversed(sch.outer):
+        lines.append(f"const int {prefix}{r.var} = {r.start} + ({rest} % {r.count}) * {r.step};")
+        rest = f"({rest} / {r.count})"
+    for r in sch.inner:
+        lines.append(f"const int {prefix}{r.var} = {r.start} + args.{FILL_TABLE % r.var}[ff_] * {r.step};")
+    return lines
+
+
+def static_tile_steps(sch: Schedule) -> np.ndarray:
+    """For static step tables: each pattern tile's first step in the tables, and the end (one more entry)."""
+    tiles = sch.tables["step_tile"]
+    offsets = np.zeros(sch.pattern_tiles + 1, np.int32)
+    counts = np.bincount(tiles, minlength=sch.pattern_tiles)
+    offsets[1:] = np.cumsum(counts)
+    return offsets
+
+
+def work_lists(items: List[Tuple[int, int]], weights: List[float], groups: List[int], grid: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Spread work items over `grid` persistent workgroups: workgroup w runs on XCD w % 8, so items of one
+    locality group (`groups`, e.g. a band of output columns) go to the workgroups of one XCD, where they
+    share its L2; within an XCD, longest-first onto the least loaded workgroup. Returns (offsets[grid + 1],
+    items[n, 2]) with each workgroup's items contiguous, in the order it runs them."""
+    xcds = min(gfx950.XCDS, grid)
+    per_xcd: List[List[int]] = [[] for _ in range(xcds)]
+    ngroups = max(groups) + 1 if groups else 1
+    # Groups in order onto XCDs, balancing total weight.
+    load = [0.0] * xcds
+    group_items: Dict[int, List[int]] = {}
+    for k, g in enumerate(groups):
+        group_items.setdefault(g, []).append(k)
+    group_weight = {g: sum(weights[k] for k in ks) for g, ks in group_items.items()}
+    wgs_of = [list(range(x, grid, xcds)) for x in range(xcds)]
+    capacity = [len(w) for w in wgs_of]
+    for g in sorted(group_items):  # contiguous groups to the same XCD while it has room
+        x = min(range(xcds), key=lambda x: (load[x] / capacity[x], x))
+        per_xcd[x].extend(group_items[g])
+        load[x] += group_weight[g]
+    assigned: List[List[int]] = [[] for _ in range(grid)]
+    for x in range(xcds):
+        wgs = wgs_of[x]
+        heap = [(0.0, n, w) for n, w in enumerate(wgs)]
+        heapq.heapify(heap)
+        mine = sorted(per_xcd[x], key=lambda k: (-weights[k], k))
+        for k in mine:
+            l, n, w = heapq.heappop(heap)
+            assigned[w].append(k)
+            heapq.heappush(heap, (l + weights[k], n, w))
+    offsets = np.zeros(grid + 1, np.int32)
+    flat: List[Tuple[int, int]] = []
+    for w in range(grid):
+        for k in sorted(assigned[w]):
+            flat.append(items[k])
+        offsets[w + 1] = len(flat)
+    return offsets, np.array(flat, np.int32).reshape(-1, 2)

@@ -1,0 +1,61 @@
+"""Device-side helpers every generated gfx950 source starts with (written into the source: hiprtc gets no
+include paths, and the generated source is standalone, as the reference's generated modules are)."""
+
+PRELUDE = r"""
+// ---- tilejax_amd device prelude (gfx950) ----
+#ifndef __HIPCC_RTC__
+#include <hip/hip_runtime.h>  // hiprtc provides these itself; hipcc (offline inspection) needs them
+#endif
+typedef __bf16 ak_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float ak_f32x16 __attribute__((ext_vector_type(16)));
+typedef float ak_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int ak_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int ak_u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short ak_u16;
+
+#define AK_INLINE __device__ __forceinline__
+
+// Python's floor division and modulo on ints.
+AK_INLINE int ak_floordiv(int a, int b) { int q = a / b; return (q * b != a && ((a < 0) != (b < 0))) ? q - 1 : q; }
+AK_INLINE int ak_floormod(int a, int b) { int r = a % b; return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r; }
+AK_INLINE int ak_imin(int a, int b) { return a < b ? a : b; }
+AK_INLINE int ak_imax(int a, int b) { return a > b ? a : b; }
+AK_INLINE int ak_clamp(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// bf16 <-> f32. Rounding is to nearest, ties to even; NaN stays NaN.
+AK_INLINE unsigned ak_bf16_bits(float x) {
+  unsigned u = __builtin_bit_cast(unsigned, x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+AK_INLINE float ak_round_bf16(float x) { return __builtin_bit_cast(float, ak_bf16_bits(x) << 16); }
+AK_INLINE float ak_bf16_to_f32(unsigned short b) { return __builtin_bit_cast(float, (unsigned)b << 16); }
+AK_INLINE unsigned ak_pack_bf16x2(float lo, float hi) { return ak_bf16_bits(lo) | (ak_bf16_bits(hi) << 16); }
+AK_INLINE float ak_round_f16(float x) { return (float)(_Float16)x; }
+
+// Elementwise functions with the tile code's meaning.
+AK_INLINE float ak_exp(float x) { return __expf(x); }
+AK_INLINE float ak_exp2(float x) { return exp2f(x); }
+AK_INLINE float ak_rsqrt(float x) { return rsqrtf(x); }
+AK_INLINE float ak_rcp(float x) { return 1.0f / x; }
+AK_INLINE float ak_square(float x) { return x * x; }
+AK_INLINE float ak_sign(float x) { return (float)((x > 0.0f) - (x < 0.0f)); }
+AK_INLINE float ak_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// jnp.maximum/minimum propagate NaN.
+AK_INLINE float ak_maximum(float a, float b) { return (a != a || b != b) ? (a + b) : (a > b ? a : b); }
+AK_INLINE float ak_minimum(float a, float b) { return (a != a || b != b) ? (a + b) : (a < b ? a : b); }
+
+// 8x8 transpose of 16-bit elements held as 8 rows of 4 dwords: out[c] holds column c (8 elements).
+AK_INLINE void ak_transpose8x8_b16(const ak_u32x4 in[8], ak_u32x4 out[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      out[c][d] = __builtin_amdgcn_perm(in[2 * d + 1][c >> 1], in[2 * d][c >> 1], sel);
+    }
+  }
+}
+// ---- end of prelude ----
+"""

@@ -1,0 +1,69 @@
+"""Compile, ahead of time, the kernels the benchmark and GPU tests use, into the code-object cache.
+
+A kernel is compiled by hiprtc the first time it is lowered for a signature and schedule; the cache keeps
+the code object by a hash of its source, so compiling here (no GPU needed) saves the GPU run the
+compile. This is a build-speed measure only: nothing here is a tuning result.
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+from typing import Iterator, List, Tuple
+
+from . import jaxlite
+from .errors import KernelError
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _bf16(*shape: int) -> Tuple[Tuple[int, ...], jaxlite.DType]:
+    return (tuple(shape), jaxlite.bfloat16)
+
+
+def _i32(*shape: int) -> Tuple[Tuple[int, ...], jaxlite.DType]:
+    return (tuple(shape), jaxlite.int32)
+
+
+def standard() -> Iterator[Tuple[object, tuple]]:
+    """(kernel, lower() arguments) of the kernels the benchmark and the GPU tests build."""
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from examples import causal_matmul as cm
+    from examples import matmul as mm
+
+    T = mm.MatmulTiles
+    for n, tiles in ((8192, T(512, 512, 512)), (1024, T(512, 512, 512)), (8192, T(1024, 2048, 1024)),
+                     (512, T(256, 256, 128)), (1024, T(256, 256, 256))):
+        yield mm.matmul, (_bf16(n, n), _bf16(n, n), tiles)
+    for n, tiles in ((8192, T(512, 512, 512)), (1024, T(256, 256, 256)), (512, T(128, 128, 128))):
+        yield cm.causal_matmul, (_bf16(n, n), _bf16(n, n), tiles)
+    yield mm.matmul, (_bf16(512, 256), _bf16(256, 512), T(256, 256, 128))
+    try:
+        from examples import causal_attention as ca
+
+        A = ca.AttentionBlocks
+        for shape, blocks in (((4, 16, 2048, 128), A(512, 512)), ((1, 16, 4096, 128), A(512, 512)),
+                              ((2, 4, 512, 128), A(128, 128)), ((1, 2, 1024, 128), A(256, 256))):
+            yield ca.causal_attention, (_bf16(*shape), _bf16(*shape), _bf16(*shape), blocks)
+    except ImportError:
+        pass
+
+
+def compile_all(verbose: bool = True) -> List[str]:
+    """Lower and compile every standard kernel; the names of those the backend can't lower yet."""
+    skipped = []
+    for kernel, args in standard():
+        try:
+            lowered = kernel.lower(*args)
+        except KernelError as e:
+            skipped.append(f"{kernel.nest.name}: {str(e).splitlines()[0]}")
+            continue
+        from . import runtime
+
+        runtime.compile_source(lowered.source, f"{kernel.nest.name}.hip")
+        if verbose:
+            print(f"compiled {kernel.nest.name} {[a[0] for a in args[:-1]]} {args[-1]}", flush=True)
+    for s in skipped:
+        print("not lowered yet:", s, flush=True)
+    return skipped

@@ -1,0 +1,125 @@
+"""Where a kernel's time goes on the GPU: device time from HIP events, and the kernel's own trace regions.
+
+The reference reads libtpu trace regions `<k>/wait`, `<k>/out_wait`, `<k>/compute` from a profiler trace
+(src/autokernel/profiling.py:95-274). On gfx950 the same breakdown comes from the kernel itself: a kernel
+generated with `trace=True` stamps `s_memrealtime` (the 100 MHz constant clock) around its waits for
+input slices, its output stores and its compute, per workgroup, into a trace buffer; `measure` sums them.
+Device time per call is measured with HIP events on the stream the kernel runs on, after a warm-up call,
+as the median of `runs` calls (the reference's timing method: benchmarks/timing.py:12-22).
+
+`KernelProfile.bottleneck` classifies as the reference does: "dma" when exposed input waits plus output
+waits exceed 20 % of the device time, "overhead" when time outside every region exceeds 30 %, else
+"compute"; None when no regions were recorded.
+"""
+
+from __future__ import annotations
+
+import statistics
+from dataclasses import dataclass, field
+from typing import Any, Dict, Optional, Sequence
+
+from .errors import KernelError
+
+__all__ = ["DMA_BOUND_SHARE", "OVERHEAD_BOUND_SHARE", "KernelProfile", "measure", "profile", "summarize"]
+
+DMA_BOUND_SHARE = 0.2
+OVERHEAD_BOUND_SHARE = 0.3
+CLOCK_HZ = 100e6  # s_memrealtime
+
+
+@dataclass
+class KernelProfile:
+    """A kernel's time per call on the device (seconds), and, with trace regions, its breakdown."""
+
+    name: str
+    config: Any
+    calls: int
+    device_s: float
+    regions: bool = False
+    steps: float = 0.0
+    wait_s: float = 0.0
+    fill_s: float = 0.0
+    out_wait_s: float = 0.0
+    compute_s: float = 0.0
+    scopes: Dict[str, float] = field(default_factory=dict)
+    samples: Sequence[float] = ()
+
+    @property
+    def exposed_wait_s(self) -> float:
+        return max(0.0, self.wait_s - self.fill_s)
+
+    @property
+    def other_s(self) -> float:
+        return max(0.0, self.device_s - self.wait_s - self.out_wait_s - self.compute_s)
+
+    @property
+    def bottleneck(self) -> Optional[str]:
+        if not self.regions:
+            return None
+        if (self.exposed_wait_s + self.out_wait_s) > DMA_BOUND_SHARE * self.device_s:
+            return "dma"
+        if self.other_s > OVERHEAD_BOUND_SHARE * self.device_s:
+            return "overhead"
+        return "compute"
+
+    def __str__(self) -> str:
+        us = lambda s: f"{s * 1e6:10.1f} us"  # noqa: E731
+        lines = [f"{self.name} ({self.config}): {us(self.device_s).strip()} per call over {self.calls} calls"]
+        if self.regions:
+            per_step = self.device_s / self.steps if self.steps else 0.0
+            lines += [
+                f"  steps          {self.steps:10.0f}     ({per_step * 1e6:.2f} us each)",
+                f"  compute        {us(self.compute_s)}",
+                f"  input waits    {us(self.exposed_wait_s)}  (+{us(self.fill_s).strip()} filling the pipeline)",
+                f"  output waits   {us(self.out_wait_s)}",
+                f"  other          {us(self.other_s)}  (decoding steps, starting loads, draining)",
+                f"  bottleneck: {self.bottleneck}",
+            ]
+        return "\n".join(lines)
+
+
+def summarize(stamps: Any, name: str, config: Any, calls: int, device_s: float, workgroups: int) -> KernelProfile:
+    """A profile from a trace buffer of per-workgroup region totals (in clock ticks): rows of
+    [wait, fill, out_wait, compute, steps], summed over `calls` calls; time per call is the mean over
+    workgroups (they run side by side)."""
+    import numpy as np
+
+    t = np.asarray(stamps, dtype=np.float64).reshape(workgroups, -1)
+    per = t.sum(axis=0) / max(workgroups, 1) / max(calls, 1)
+    ticks = 1.0 / CLOCK_HZ
+    return KernelProfile(
+        name=name, config=config, calls=calls, device_s=device_s, regions=True,
+        wait_s=per[0] * ticks, fill_s=per[1] * ticks, out_wait_s=per[2] * ticks, compute_s=per[3] * ticks,
+        steps=float(t[:, 4].sum()) / max(calls, 1),
+    )
+
+
+def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile:
+    """Time a generated kernel: one warm-up call, then `runs` calls, each bracketed by HIP events on the
+    current stream; the median per call."""
+    import torch
+
+    from . import runtime
+
+    runtime.require_gpu()
+    stream = runtime.current_stream()
+    lowered.run(*inputs)
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(runs):
+        start, stop = runtime.Event(), runtime.Event()
+        start.record(stream)
+        lowered.run(*inputs)
+        stop.record(stream)
+        samples.append(start.elapsed_ms(stop) * 1e-3)
+    return KernelProfile(lowered.plan.nest.name, lowered.config, runs, statistics.median(samples), samples=samples)
+
+
+def profile(kernel: Any, args: Sequence[Any], runs: int = 5) -> KernelProfile:
+    """Where `kernel`'s time goes on the GPU for these inputs (and tunable, if given)."""
+    from .api import _tensor
+
+    arrays, _ = kernel._split(tuple(args))
+    config = kernel.lower(*args).config
+    lowered = kernel.lowered(kernel.signature(*arrays), config)
+    return measure(lowered, [_tensor(a) for a in arrays], runs)

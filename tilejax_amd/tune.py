@@ -1,0 +1,240 @@
+"""Tuning from first principles: test each candidate schedule against the reference, time it on the GPU,
+and let its profile pick the next schedules.
+
+The reference's tuner (src/autokernel/tune.py:57-368), on the MI355X: a schedule is a `Config` (the
+kernel's tunable and its `Pipeline`); `search` hill-climbs from the defaults, moving to the first proposal
+at least 1 % faster, for at most `BUDGET` candidates; a candidate that fails to build, compile or run, or
+whose result differs from the reference, is a `Trial` with an error (infinitely slow). `proposals` orders
+the next schedules by the bottleneck: exposed input waits -> one more LDS slot, then the neighbouring
+tunables moving fewer bytes; overhead -> neighbours with fewer, bigger steps; otherwise every neighbour,
+fewest steps first. Neighbours that build the same loops are skipped.
+
+Tuning needs a GPU; without one the defaults are used (and `kernel(...)` raises anyway: no CPU fallback).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from dataclasses import dataclass, field
+from typing import TYPE_CHECKING, Any, Callable, Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import profiling
+from .errors import KernelError
+from .pipeline import MAX_INPUT_BUFFERS, MAX_OUTPUT_BUFFERS, Pipeline
+from .plan import Kind, Operand, Plan
+from .profiling import KernelProfile
+from .schedule import Schedule
+from .tunable import choices, neighbours
+
+__all__ = ["BUDGET", "Config", "Trial", "Tuning", "proposals", "random_inputs", "search", "tune"]
+
+BUDGET = 12
+RUNS = 5
+EXPOSED_SHARE = 0.03
+MIN_GAIN = 0.01
+
+
+@dataclass(frozen=True)
+class Config:
+    """A schedule: the kernel's tunable (None if it has none) and its buffering."""
+
+    tunable: Any
+    pipeline: Pipeline
+    cursor: bool = False
+
+    def __str__(self) -> str:
+        if self.tunable is None:
+            return str(self.pipeline)
+        fields = ", ".join(f"{k}={getattr(self.tunable, k)!r}" for k in choices(self.tunable))
+        return f"{type(self.tunable).__name__}({fields}), {self.pipeline}"
+
+
+@dataclass
+class Trial:
+    config: Config
+    profile: Optional[KernelProfile] = None
+    error: Optional[str] = None
+
+    @property
+    def seconds(self) -> float:
+        return self.profile.device_s if self.profile else math.inf
+
+
+@dataclass
+class Tuning:
+    best: Trial
+    trials: List[Trial] = field(default_factory=list)
+
+    @property
+    def config(self) -> Config:
+        return self.best.config
+
+    def __str__(self) -> str:
+        lines = [f"chose {self.config}" + ("" if self.trials else " (the defaults: tuning needs a GPU)")]
+        for t in self.trials:
+            mark = "*" if t is self.best else " "
+            result = f"{t.seconds * 1e6:10.1f} us  {t.profile.bottleneck}" if t.profile else f"  {t.error}"
+            lines.append(f" {mark} {t.config!s:72} {result}")
+        return "\n".join(lines)
+
+
+def search(start: Config, measure: Callable[[Config], Trial], propose: Callable[[Trial], Sequence[Config]],
+           budget: int) -> Tuning:
+    """Climb from `start` (see the module docstring); KernelError if no candidate ran."""
+    best = measure(start)
+    trials = {start: best}
+    improved = True
+    while improved:
+        improved = False
+        for config in propose(best):
+            if config in trials:
+                continue
+            if len(trials) >= budget:
+                return Tuning(best, list(trials.values()))
+            trial = trials[config] = measure(config)
+            if trial.seconds < best.seconds * (1 - MIN_GAIN):
+                best, improved = trial, True
+                break
+    if best.profile is None:
+        errors = "; ".join(f"{t.config}: {t.error}" for t in trials.values())
+        raise KernelError(f"no schedule tried ran: {errors}")
+    return Tuning(best, list(trials.values()))
+
+
+@dataclass(frozen=True)
+class _Stats:
+    steps: int
+    bytes: int
+
+
+def _bytes(shape: Tuple[int, ...], dt: Any) -> int:
+    return math.prod(shape) * dt.itemsize
+
+
+def _stats(plan: Plan, schedule: Schedule) -> _Stats:
+    """Steps, and the bytes the tiles' copies move (a tile per copy: what the loop nest asks for)."""
+
+    def copies(op: Operand) -> int:
+        if op.kind is Kind.STREAM:
+            return schedule.steps if op.phase is None else schedule.phase_steps[op.phase]
+        return schedule.tiles if op.kind is Kind.TILE else 1
+
+    moved = sum(copies(op) * _bytes(op.tile.shape, op.tile.dtype) for op in plan.operands)
+    for out in plan.outputs:
+        moved += (schedule.tiles + schedule.fills) * _bytes(out.tile.shape, out.dtype)
+    return _Stats(schedule.steps, moved)
+
+
+def _loop_steps(plan: Plan) -> Tuple[Tuple[str, int, int], ...]:
+    return tuple((r.var, r.step, r.count) for r in plan.loops)
+
+
+def proposals(kernel: Any, signature: Any, trial: Trial) -> List[Config]:
+    """The schedules to try after `trial`, most promising first."""
+    config, prof = trial.config, trial.profile
+    if prof is None:
+        return _smaller(kernel, signature, config)
+    plan, schedule = kernel.build(signature, config.tunable)
+    here, pipe, loops = _stats(plan, schedule), config.pipeline, _loop_steps(plan)
+    exposed = EXPOSED_SHARE * prof.device_s
+    buffering = []
+    if prof.regions and prof.exposed_wait_s > exposed and pipe.input_buffers < MAX_INPUT_BUFFERS:
+        buffering.append(dataclasses.replace(pipe, input_buffers=pipe.input_buffers + 1))
+    if prof.regions and prof.out_wait_s > exposed and pipe.output_buffers < MAX_OUTPUT_BUFFERS:
+        buffering.append(dataclasses.replace(pipe, output_buffers=pipe.output_buffers + 1))
+    if not prof.regions and pipe.input_buffers < MAX_INPUT_BUFFERS:
+        buffering.append(dataclasses.replace(pipe, input_buffers=pipe.input_buffers + 1))
+    moves = [Config(config.tunable, p) for p in buffering]
+    near: List[Tuple[_Stats, Config]] = []
+    for tunable in neighbours(config.tunable) if config.tunable is not None else ():
+        try:
+            plan, schedule = kernel.build(signature, tunable)
+        except KernelError:
+            continue
+        if _loop_steps(plan) == loops:
+            continue
+        near.append((_stats(plan, schedule), Config(tunable, pipe)))
+    if prof.bottleneck == "dma":
+        near = sorted((n for n in near if (n[0].bytes, n[0].steps) < (here.bytes, here.steps)),
+                      key=lambda n: (n[0].bytes, n[0].steps))
+    elif prof.bottleneck == "overhead":
+        near = sorted((n for n in near if n[0].steps < here.steps), key=lambda n: n[0].steps)
+    else:
+        near = sorted(near, key=lambda n: n[0].steps)
+    return moves + [c for _, c in near]
+
+
+def _smaller(kernel: Any, signature: Any, config: Config) -> List[Config]:
+    """After `config` failed: two buffers, then the neighbouring tunables."""
+    least = Pipeline(2, 2)
+    found = [] if config.pipeline == least else [Config(config.tunable, least)]
+    for tunable in neighbours(config.tunable) if config.tunable is not None else ():
+        try:
+            kernel.build(signature, tunable)
+        except KernelError:
+            continue
+        found.append(Config(tunable, least))
+    return found
+
+
+def random_inputs(signature: Sequence[Tuple[Tuple[int, ...], Any]], bounds: Optional[Dict[int, int]] = None,
+                  seed: int = 0, device: Any = "cuda") -> List[torch.Tensor]:
+    """Inputs to tune on: normal floats, small ints; index arrays (`bounds`) from 0 to their bound."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    out = []
+    for i, (shape, dt) in enumerate(signature):
+        if bounds and i in bounds:
+            t = torch.randint(0, bounds[i] + 1, shape, generator=g, dtype=torch.int64).to(dt.torch)
+        elif dt.kind == "f":
+            t = torch.randn(shape, generator=g, dtype=torch.float32).to(dt.torch)
+        else:
+            t = torch.randint(-8, 8, shape, generator=g, dtype=torch.int64).to(dt.torch)
+        out.append(t.to(device))
+    return out
+
+
+def _index_bounds(kernel: Any, signature: Any, start: Config) -> Dict[int, int]:
+    plan, _ = kernel.build(signature, start.tunable)
+    furthest = max(r.start + r.count * r.step for r in plan.loops)
+    return {ix.param: furthest for ix in plan.indices}
+
+
+def _measure(kernel: Any, signature: Any, config: Config, inputs: Sequence[torch.Tensor], want: Any) -> Trial:
+    from .api import compare
+
+    try:
+        lowered = kernel.lowered(signature, config)
+        got = lowered.run(*inputs)
+        torch.cuda.synchronize()
+    except Exception as e:
+        return Trial(config, error=f"{type(e).__name__}: {str(e).splitlines()[0]}")
+    try:
+        gots = got if isinstance(got, tuple) else (got,)
+        wants = want if isinstance(want, tuple) else (want,)
+        for name, g, w in zip(kernel.nest.outputs, gots, wants):
+            compare(f"output {name!r}", g, w, inputs=tuple(dt for _, dt in signature))
+    except AssertionError as e:
+        return Trial(config, error=f"wrong result: {e}")
+    return Trial(config, profiling.measure(lowered, inputs, RUNS))
+
+
+def _can_time() -> bool:
+    return torch.cuda.is_available()
+
+
+def tune(kernel: Any, signature: Any, arrays: Optional[Sequence[Any]] = None, budget: int = BUDGET) -> Tuning:
+    """Tune `kernel` for inputs of this signature, on `arrays` if they are tensors on the GPU."""
+    start = kernel.default_config(signature)
+    if not _can_time():
+        return Tuning(Trial(start))
+    if arrays is not None and all(isinstance(a, torch.Tensor) and a.is_cuda for a in arrays):
+        inputs = list(arrays)
+    else:
+        inputs = random_inputs(signature, _index_bounds(kernel, signature, start))
+    args = [start.tunable] if start.tunable is not None else []
+    want = kernel.reference(*inputs, *args)
+    return search(start, lambda c: _measure(kernel, signature, c, inputs, want),
+                  lambda t: proposals(kernel, signature, t), budget)

@@ -12,6 +12,7 @@ typedef float ak_f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int ak_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int ak_u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short ak_u16;
+typedef short ak_i16x4 __attribute__((ext_vector_type(4)));
 
 #define AK_INLINE __device__ __forceinline__
 

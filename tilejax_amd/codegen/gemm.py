@@ -8,11 +8,17 @@ walking its own list of work items. An item is a hardware tile of BM x BN output
 (the loop nest's tile), or a fill: a hardware tile whose value the schedule or the epilogue fixes without
 computing (a tile the mask skips, or one the epilogue's `where` proves constant). For a compute item the
 workgroup walks the spec tile's steps (arithmetic, or decoded from the step tables), each split into
-BK-deep slices: operand slices go global -> registers -> LDS (a ring of `input_buffers` slots, swizzled
-16-byte chunks; the right operand of `a @ b` transposed in registers on the way, so both MFMA operands
-read K-contiguous), the next slices' loads in flight while the MFMAs of this one run
-(`v_mfma_f32_32x32x16_bf16`, f32 accumulators in registers), and the epilogue computed per element where
-the accumulator lives and stored as packed bf16.
+BK-deep slices that stream through `stages` LDS stages:
+
+- loads go straight from HBM to LDS (`buffer_load_dwordx4 ... lds`, 16 bytes a lane, one buffer resource
+  per operand tile), each lane fetching the global chunk that belongs at its XOR-swizzled LDS position;
+- the right operand of `a @ b` stays N-contiguous in LDS and is read transposed with
+  `ds_read_b64_tr_b16`, so both MFMA operands arrive K-contiguous with no register shuffles;
+- each stage is its own LDS array, which lets the compiler keep later stages' loads in flight while it
+  reads this one; the barrier for a slice sits one K16 step before it, so the next slice's first fragments
+  load under this slice's last MFMAs (`v_mfma_f32_32x32x16_bf16`, f32 accumulators in AGPRs), and
+  `sched_group_barrier` hints interleave each MFMA with an LDS read or a global load;
+- the epilogue is computed per element where the accumulator lives and stored as packed bf16.
 """
 
 from __future__ import annotations
@@ -147,6 +153,9 @@ def match(plan: Plan) -> Optional[GemmMatch]:
 
 @dataclass(frozen=True)
 class HwTile:
+    """A workgroup's share of a spec tile: BM x BN outputs, K walked in BK-deep slices through `stages` LDS
+    stages (one array per stage and operand)."""
+
     bm: int
     bn: int
     bk: int
@@ -158,23 +167,21 @@ class HwTile:
 
 
 def hardware_tile(m: GemmMatch, pipeline: Pipeline) -> HwTile:
-    """The workgroup's tile for a spec tile (tm, tn, tk) and the LDS ring depth the pipeline asks for."""
+    """The workgroup tile for a spec tile (tm, tn, tk): at most 256 x 256 outputs (four waves of 128 x 128 at
+    most), K slices of 64 (32 if tk is an odd multiple of 64, 16 for tk = 32) so every tile's slice count is even, and the
+    LDS stages the pipeline asks for where they divide a step's slices and fit in LDS."""
     bm, bn = min(m.tm, 256), min(m.tn, 256)
     if m.tm % bm or m.tn % bn or bm % 64 or bn % 64:
         raise KernelError(f"the gfx950 matmul lowering needs tiles that are multiples of 64 (got {m.tm} x {m.tn})")
-    stages = max(2, pipeline.input_buffers)
-    bk = 64
-    while m.tk % bk and bk > 16:
-        bk //= 2
-    if m.tk % bk:
-        raise KernelError(f"the gfx950 matmul lowering needs a reduction block that is a multiple of 16 (got {m.tk})")
-    while stages * (bm + bn) * bk * 2 > gfx950.LDS_BUDGET:
-        if bk > 32 and m.tk % (bk // 2) == 0:
-            bk //= 2
-        else:
-            stages -= 1
-    if stages < 2:
-        raise KernelError("the matmul's tiles don't fit in LDS double-buffered")
+    if m.tk % 64 and m.tk != 32:
+        raise KernelError(f"the gfx950 matmul lowering needs a reduction block of 32 or a multiple of 64 (got {m.tk})")
+    bk = 64 if m.tk % 128 == 0 else 32 if m.tk % 64 == 0 else 16
+    kslices = m.tk // bk
+    stages = 2
+    for s in range(max(2, pipeline.input_buffers), 1, -1):
+        if kslices % s == 0 and s * (bm + bn) * bk * 2 <= gfx950.LDS_BUDGET:
+            stages = s
+            break
     return HwTile(bm, bn, bk, stages)
 
 
@@ -333,48 +340,58 @@ class _Gemm:
 
     def _source(self, args: List[Arg]) -> str:
         plan, sch, m, hw = self.plan, self.sch, self.m, self.hw
-        bm, bn, bk, stages = hw.bm, hw.bn, hw.bk, hw.stages
+        bm, bn, bk, S = hw.bm, hw.bn, hw.bk, hw.stages
         wtm, wtn = bm // 2, bn // 2
         mi, ni = wtm // MFMA, wtn // MFMA
+        k16s = bk // 16
+        kslices = m.tk // bk
+        kvar = m.kvar
         index = Index(plan, lambda v: f"lv_{v}")
         a_shape = plan.inputs[m.a.param].shape
         b_shape = plan.inputs[m.b.param].shape
-        a_base, a_str = tile_base(m.a.tile, a_shape, index, lambda v: f"lv_{v}")
-        b_base, b_str = tile_base(m.b.tile, b_shape, index, lambda v: f"lv_{v}")
+        no_k = lambda v: "0" if v == kvar else f"lv_{v}"  # the reduction loop's offset goes per slice
+        a_base, a_str = tile_base(m.a.tile, a_shape, index, no_k)
+        b_base, b_str = tile_base(m.b.tile, b_shape, index, no_k)
         o_base, o_str = tile_base(m.out.tile, m.out.shape, index, lambda v: f"lv_{v}")
-        if a_str[1] != 1 or b_str[-1] != 1 or o_str[1] != 1:
+        if a_str[1] != 1 or b_str[1] != 1 or o_str[1] != 1:
             raise KernelError("the gfx950 matmul lowering reads and writes tiles whose last dim is the array's last")
+        for name, shape in ((m.a.tile.array, a_shape), (m.b.tile.array, b_shape)):
+            if 2 * int(np.prod(shape)) >= 2**31:
+                raise KernelError(f"`{name}` is 2 GiB or more: the gfx950 matmul lowering addresses operands with "
+                                  "32-bit buffer offsets")
         lda, ldb, ldo = a_str[0], b_str[0], o_str[0]
-        ca = bm * bk // 8 // THREADS  # 16-byte chunks of A per thread per slice
-        if ca < 1:
-            raise KernelError("matmul tile too small for a 256-thread workgroup")
-        kvar = m.kvar
-        phase = plan.phases[0].range if plan.phases else None
-        kslices = m.tk // bk
+        nt = m.b_nt
+        kca = bk // 8  # 16-byte chunks per K-contiguous row
+        nc = bn // 8  # 16-byte chunks per N-contiguous row (B of `a @ b`)
+        a_ld = bm * bk // 8 // THREADS
+        b_ld = bn * bk // 8 // THREADS
+        if a_ld < 1 or b_ld < 1 or (not nt and 64 % nc):
+            raise KernelError(f"matmul hardware tile {bm} x {bn} x {bk} is too small for a 256-thread workgroup")
 
-        # How a tile's steps are found.
+        def swa(row: str) -> str:  # K-contiguous rows: chunk XOR, conflict-free ds_read_b128 (64 banks)
+            return {8: f"((({row}) >> 1) & 7)", 4: f"((({row}) >> 2) & 3)", 2: f"((({row}) >> 3) & 1)"}[kca]
+
+        def swb(k: str) -> str:  # N-contiguous rows: chunk XOR, conflict-free ds_read_b64_tr_b16
+            return f"(((({k}) & 3) << 2) & {nc - 1})"
+
+        # How a tile's steps are found: `nsteps` and the reduction loop's value at step `st_`.
+        phase = plan.phases[0].range if plan.phases else None
         if phase is None:
             steps_setup = ["const int nsteps = 1;"]
-            step_k = "0"
+            kval = "0"
         elif not sch.step_tables:
             steps_setup = [f"const int nsteps = {phase.count};"]
-            step_k = f"({phase.start} + (s_) * {phase.step})"
-        elif not sch.runtime:
-            steps_setup = [
-                f"const int tt_s = t % {sch.pattern_tiles};",
-                "const int sbeg = args.tile_steps[tt_s], send = args.tile_steps[tt_s + 1];",
-                f"const int nsteps = ((args.{STEP_CODE}[sbeg] >> 2) & 1) ? 0 : send - sbeg;",
-            ]
-            step_k = (f"({phase.start} + ((args.{STEP_CODE}[sbeg + (s_)] >> {CODE_SHIFT}) / {sch.iterations} / "
-                      f"{sch.phase_radix}) * {phase.step})")
+            kval = f"({phase.start} + st_ * {phase.step})"
         else:
+            codes, offs = (f"args.{STEP_CODE}", "args.tile_steps") if not sch.runtime else ("args.rt_step_code",
+                                                                                            "args.rt_tile_steps")
             steps_setup = [
                 f"const int tt_s = t % {sch.pattern_tiles};",
-                "const int sbeg = args.rt_tile_steps[tt_s], send = args.rt_tile_steps[tt_s + 1];",
-                "const int nsteps = ((args.rt_step_code[sbeg] >> 2) & 1) ? 0 : send - sbeg;",
+                f"const int sbeg = {offs}[tt_s], send = {offs}[tt_s + 1];",
+                f"const int nsteps = (({codes}[sbeg] >> 2) & 1) ? 0 : send - sbeg;",
             ]
-            step_k = (f"({phase.start} + ((args.rt_step_code[sbeg + (s_)] >> {CODE_SHIFT}) / {sch.iterations} / "
-                      f"{sch.phase_radix}) * {phase.step})")
+            kval = (f"({phase.start} + (({codes}[sbeg + st_] >> {CODE_SHIFT}) / {sch.iterations} / "
+                    f"{sch.phase_radix}) * {phase.step})")
 
         # The epilogue, per accumulator element.
         def leaf(n: Node) -> Optional[str]:
@@ -403,42 +420,64 @@ class _Gemm:
             return None
 
         em = Emitter(leaf, m.out.tile.shape, prefix="e")
-        if isinstance(m.value, jaxlite.Sym):
-            result = em.emit(m.value.node)
-        else:
-            result = literal(m.value)
-        epi_lines = em.lines
+        result = em.emit(m.value.node) if isinstance(m.value, jaxlite.Sym) else literal(m.value)
+        epi = "\n              ".join(em.lines)
         out_bf16 = m.out.dtype.name == "bfloat16"
-
         struct = c_struct(f"{self.name}_args", args)
-        A = f"args.{m.a.tile.array}"
-        B = f"args.{m.b.tile.array}"
-        O = f"args.{m.out.name}_out"
+        A, B, O = f"args.{m.a.tile.array}", f"args.{m.b.tile.array}", f"args.{m.out.name}_out"
+        a_numel, b_numel = int(np.prod(a_shape)), int(np.prod(b_shape))
         fill_value = literal(m.out.fill if m.out.fill is not None else 0, m.out.dtype)
         const_value = literal(self.const_value if self.const_value is not None else 0.0, m.out.dtype)
-        tile_decode = "\n        ".join(decode_tile(plan, sch, "t"))
-        fill_decode = "\n        ".join(decode_fill(plan, sch, "t")) if sch.fills else ""
+        tile_decode = "\n    ".join(decode_tile(plan, sch, "t"))
         fill_block = ""
         if sch.fills:
-            fill_block = (f"if (kind == 1) {{\n      {{\n        {fill_decode}\n        const long long obase = {o_base};\n"
-                          f"        {_store_constant(bm, bn, out_bf16, O, 'obase', ldo, fill_value)}\n      }}\n      continue;\n    }}")
-        epi = "\n              ".join(epi_lines)
-        setup = "\n        ".join(steps_setup)
-        b_loader = self._b_loader(bn, bk, ldb, m.b_nt)
+            fill_decode = "\n      ".join(decode_fill(plan, sch, "t"))
+            fill_block = (f"if (kind == 1) {{\n      {fill_decode}\n      const long long obase = {o_base};\n      "
+                          f"{_store_constant(bm, bn, out_bf16, O, 'obase', ldo, fill_value)}\n      continue;\n    }}")
+        setup = "\n    ".join(steps_setup)
 
-        return f"""// Generated by tilejax_amd for `{plan.nest.name}`: a persistent gfx950 matmul kernel.
-// spec tile {m.tm} x {m.tn} x {m.tk}; hardware tile {bm} x {bn}, K slices of {bk}, {stages} LDS slots;
+        L: List[str] = []
+        w = L.append
+        w(f"""// Generated by tilejax_amd for `{plan.nest.name}`: a persistent gfx950 matmul kernel.
+// spec tile {m.tm} x {m.tn} x {m.tk}; workgroup tile {bm} x {bn}, K slices of {bk} through {S} LDS stages;
 // {sch.tiles} tiles of {sch.total_tiles} ({sch.fills} filled), {sch.steps} steps.
 {PRELUDE}
 {struct}
-
+#define AK_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define AK_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4))
+#define AK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+#define AK_LDS4(p) ((__attribute__((address_space(3))) ak_i16x4*)(p))""")
+        for s in range(S):  # one array per stage and operand: the compiler then keeps prefetches in flight
+            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sa{s}[{bm * bk}];")
+            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sb{s}[{bn * bk}];")
+        w(f"""
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
-  // LDS rings: A slices [BM][BK] and B slices transposed [BN][BK], 16-byte chunks XOR-swizzled by row.
-  __shared__ __attribute__((aligned(16))) ak_u16 lds_a[{stages}][{bm * bk}];
-  __shared__ __attribute__((aligned(16))) ak_u16 lds_b[{stages}][{bn * bk}];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS addresses stay in SGPRs
   const int wm = wave >> 1, wn = wave & 1;
-  const int q_begin = args.wg_items[blockIdx.x], q_end = args.wg_items[blockIdx.x + 1];
+  // Each wave's buffer_load ... lds fills 1 KiB of a stage, lane l's 16 bytes at 16 l: the lane loads the
+  // global chunk that belongs at that (swizzled) position.
+  const int a_row = wave * {64 // kca} + lane / {kca};
+  const unsigned a_voff = (unsigned)(a_row * {lda * 2} + (((lane % {kca}) ^ {swa('a_row')}) * 16));""")
+        if nt:
+            w(f"""  const unsigned b_voff = (unsigned)(a_row * {ldb * 2} + (((lane % {kca}) ^ {swa('a_row')}) * 16));""")
+        else:
+            w(f"""  const int b_k = wave * {64 // nc} + lane / {nc};
+  const unsigned b_voff = (unsigned)(b_k * {ldb * 2} + (((lane % {nc}) ^ {swb('b_k')}) * 16));""")
+        w(f"  int a_roff[{k16s}], b_roff[{k16s if nt else ni}];")
+        for k16 in range(k16s):
+            w(f"  {{ const int row = wm * {wtm} + (lane & 31); a_roff[{k16}] = row * {bk * 2} + "
+              f"((({2 * k16} + (lane >> 5)) ^ {swa('row')}) * 16); }}")
+            if nt:
+                w(f"  {{ const int row = wn * {wtn} + (lane & 31); b_roff[{k16}] = row * {bk * 2} + "
+                  f"((({2 * k16} + (lane >> 5)) ^ {swa('row')}) * 16); }}")
+        if not nt:
+            w("  { const int G = lane >> 4, s = lane & 15, k = 8 * (G >> 1) + (s >> 2);")
+            for j in range(ni):
+                w(f"    {{ const int n = wn * {wtn} + {j * 32} + 16 * (G & 1) + 4 * (s & 3);"
+                  f" b_roff[{j}] = k * {bn * 2} + (((n >> 3) ^ {swb('k')}) << 4) + (n & 7) * 2; }}")
+            w("  }")
+        w(f"""  const int q_begin = args.wg_items[blockIdx.x], q_end = args.wg_items[blockIdx.x + 1];
   for (int q = q_begin; q < q_end; ++q) {{
     const int t = args.items[2 * q], code = args.items[2 * q + 1];
     const int sub = code & 0xffff, kind = code >> 16;
@@ -451,7 +490,16 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
       continue;
     }}
     {setup}
-    const int total = nsteps * {kslices};
+    const int T = nsteps * {kslices};  // K slices (even)
+    const long long a_off = ({a_base}) + (long long)(sm * {bm}) * {lda};""")
+        if nt:
+            w(f"    const long long b_off = ({b_base}) + (long long)(sn * {bn}) * {ldb};")
+        else:
+            w(f"    const long long b_off = ({b_base}) + sn * {bn};")
+        w(f"""    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)({A} + a_off), (short)0,
+        (int)({a_numel}LL * 2 - a_off * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc((void*)({B} + b_off), (short)0,
+        (int)({b_numel}LL * 2 - b_off * 2), 0x00020000);
     ak_f32x16 acc[{mi}][{ni}];
 #pragma unroll
     for (int i_ = 0; i_ < {mi}; ++i_)
@@ -459,71 +507,95 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
       for (int j_ = 0; j_ < {ni}; ++j_)
 #pragma unroll
         for (int r_ = 0; r_ < 16; ++r_) acc[i_][j_][r_] = {literal(m.init)};
+    ak_bf16x8 fa[2][{mi}], fb[2][{ni}];
+    // Slice g's loads into stage s: the slice's step and K offset (slices past the tile's last reload it).
+    auto k_of = [&](int g) -> int {{
+      const int gg = g < T ? g : (T > 0 ? T - 1 : 0);
+      const int st_ = gg / {kslices};
+      return {kval} + (gg % {kslices}) * {bk};
+    }};""")
 
-    ak_u32x4 ra[{ca}];
-    {b_loader["decl"]}
-    // Fetch slice g (step g / {kslices}, K offset within it) into registers.
-    auto fetch = [&](int g) {{
-      const int s_ = g / {kslices}, kk = (g % {kslices}) * {bk};
-      {"const int lv_" + kvar + " = " + step_k + ";" if kvar else ""}
-      const __bf16* ap = {A} + ({a_base}) + (long long)(sm * {bm}) * {lda} + kk;
-      const __bf16* bp = {B} + ({b_base}) + {("(long long)(sn * " + str(bn) + ") * " + str(ldb) + " + kk") if m.b_nt else ("(long long)kk * " + str(ldb) + " + sn * " + str(bn))};
-#pragma unroll
-      for (int c = 0; c < {ca}; ++c) {{
-        const int chunk = tid + c * {THREADS};
-        const int row = chunk / {bk // 8}, kc = chunk % {bk // 8};
-        ra[c] = *(const ak_u32x4*)(ap + (long long)row * {lda} + kc * 8);
-      }}
-      {b_loader["fetch"]}
-    }};
-    auto stash = [&](int stage) {{
-#pragma unroll
-      for (int c = 0; c < {ca}; ++c) {{
-        const int chunk = tid + c * {THREADS};
-        const int row = chunk / {bk // 8}, kc = chunk % {bk // 8};
-        *(ak_u32x4*)(&lds_a[stage][row * {bk} + ((kc ^ (row & 7)) * 8)]) = ra[c];
-      }}
-      {b_loader["stash"]}
-    }};
-    if (total > 0) {{
-      fetch(0);
-      stash(0);
-      for (int p = 1; p < {stages - 1} && p < total; ++p) {{
-        fetch(p);
-        stash(p);
-      }}
-      if ({stages - 1} < total) fetch({stages - 1});
-      __syncthreads();
-      for (int g = 0; g < total; ++g) {{
-        const int stage = g % {stages};
-        const ak_u16* sa = lds_a[stage];
-        const ak_u16* sb = lds_b[stage];
-#pragma unroll
-        for (int k16 = 0; k16 < {bk // 16}; ++k16) {{
-          ak_bf16x8 af[{mi}], bf[{ni}];
-          const int chunk = k16 * 2 + (lane >> 5);
-#pragma unroll
-          for (int i_ = 0; i_ < {mi}; ++i_) {{
-            const int row = wm * {wtm} + i_ * 32 + (lane & 31);
-            af[i_] = *(const ak_bf16x8*)(&sa[row * {bk} + ((chunk ^ (row & 7)) * 8)]);
-          }}
-#pragma unroll
-          for (int j_ = 0; j_ < {ni}; ++j_) {{
-            const int row = wn * {wtn} + j_ * 32 + (lane & 31);
-            bf[j_] = *(const ak_bf16x8*)(&sb[row * {bk} + ((chunk ^ (row & 7)) * 8)]);
-          }}
-#pragma unroll
-          for (int i_ = 0; i_ < {mi}; ++i_)
-#pragma unroll
-            for (int j_ = 0; j_ < {ni}; ++j_)
-              acc[i_][j_] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j_], af[i_], acc[i_][j_], 0, 0, 0);
-        }}
-        if (g + {stages - 1} < total) stash((g + {stages - 1}) % {stages});
-        if (g + {stages} < total) fetch(g + {stages});
-        __syncthreads();
-      }}
-    }}
-    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
+        def issue(g: str, s: int, ind: str) -> List[str]:
+            out = [f"{ind}{{ const int k0 = k_of({g});"]
+            rows_a = THREADS // kca
+            for c in range(a_ld):
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, AK_LDS(&ak_sa{s}[({c * THREADS} + wave * 64) * 8]), "
+                           f"16, a_voff, (unsigned)({c * rows_a * lda * 2} + k0 * 2), 0, 0);")
+            for c in range(b_ld):
+                if nt:
+                    soff = f"(unsigned)({c * rows_a * ldb * 2} + k0 * 2)"
+                else:
+                    soff = f"(unsigned)((k0 + {c * (THREADS // nc)}) * {ldb * 2})"
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, AK_LDS(&ak_sb{s}[({c * THREADS} + wave * 64) * 8]), "
+                           f"16, b_voff, {soff}, 0, 0);")
+            out.append(f"{ind}}}")
+            return out
+
+        def reads(s: int, k16: int, b: int, ind: str) -> List[str]:
+            out = [f"{ind}fa[{b}][{i}] = *(const ak_bf16x8*)((const char*)ak_sa{s} + a_roff[{k16}] + {i * 32 * bk * 2});"
+                   for i in range(mi)]
+            for j in range(ni):
+                if nt:
+                    out.append(f"{ind}fb[{b}][{j}] = *(const ak_bf16x8*)((const char*)ak_sb{s} + b_roff[{k16}] + {j * 32 * bk * 2});")
+                else:
+                    o = k16 * 16 * bn * 2
+                    out.append(f"{ind}{{ ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4((const char*)ak_sb{s} + b_roff[{j}] + {o}));"
+                               f" ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4((const char*)ak_sb{s} + b_roff[{j}] + {o + 4 * bn * 2}));"
+                               f" fb[{b}][{j}] = __builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)); }}")
+            return out
+
+        def mfmas(b: int, ind: str) -> List[str]:
+            return [f"{ind}acc[{i}][{j}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[{b}][{j}], fa[{b}][{i}], acc[{i}][{j}], 0, 0, 0);"
+                    for i in range(mi) for j in range(ni)]
+
+        n_reads = mi + (ni if nt else 2 * ni)
+        per_slice = a_ld + b_ld
+
+        def hints(ind: str, issue_too: bool) -> List[str]:
+            # Interleave: each MFMA followed by one LDS read (and one global load where the slice issues).
+            out, r, v = [], n_reads, per_slice if issue_too else 0
+            for _ in range(mi * ni):
+                out.append(f"{ind}__builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
+                if r:
+                    out.append(f"{ind}__builtin_amdgcn_sched_group_barrier(0x100, 1, 0);")
+                    r -= 1
+                if v:
+                    out.append(f"{ind}__builtin_amdgcn_sched_group_barrier(0x020, 1, 0);")
+                    v -= 1
+            return out
+
+        ind = "    "
+        for s in range(S):
+            L.extend(issue(str(s), s, ind))
+        w(f"{ind}AK_WAIT_VM({per_slice * (S - 1)});")
+        w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+        L.extend(reads(0, 0, 0, ind))
+        w(f"{ind}for (int g = 0; g < T; g += {S}) {{")
+        ind2 = ind + "  "
+        for s in range(S):
+            for k16 in range(k16s):
+                cur = (s * k16s + k16) & 1
+                w(f"{ind2}{{")
+                if k16 < k16s - 1:
+                    L.extend(reads(s, k16 + 1, cur ^ 1, ind2 + "  "))
+                    L.extend(mfmas(cur, ind2 + "  "))
+                    L.extend(hints(ind2 + "  ", False))
+                else:
+                    # Last K16 of slice g + s: our reads of its stage are done, and (after the barrier) every
+                    # wave's; slice g + s + 1 has landed. Refill this stage with slice g + s + S and read the
+                    # next slice's first fragments while this slice's last MFMAs run.
+                    w(f"{ind2}  AK_WAIT_LGKM0();")
+                    w(f"{ind2}  AK_WAIT_VM({per_slice * (S - 2)});")
+                    w(f'{ind2}  asm volatile("s_barrier" ::: "memory");')
+                    L.extend(issue(f"g + {s + S}", s, ind2 + "  "))
+                    L.extend(reads((s + 1) % S, 0, cur ^ 1, ind2 + "  "))
+                    L.extend(mfmas(cur, ind2 + "  "))
+                    L.extend(hints(ind2 + "  ", True))
+                w(f"{ind2}}}")
+        w(f"{ind}}}")
+        w(f"{ind}AK_WAIT_VM(0);")
+        w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+        w(f"""    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
 #pragma unroll
     for (int i_ = 0; i_ < {mi}; ++i_) {{
       const int er = sm * {bm} + wm * {wtm} + i_ * 32 + (lane & 31);
@@ -546,56 +618,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
       }}
     }}
   }}
-}}
-"""
-
-    def _b_loader(self, bn: int, bk: int, ldb: int, nt: bool) -> Dict[str, str]:
-        if nt:  # b tile (tn, tk), K-contiguous: loaded like A
-            cb = bn * bk // 8 // THREADS
-            return {
-                "decl": f"ak_u32x4 rb[{cb}];",
-                "fetch": f"""#pragma unroll
-      for (int c = 0; c < {cb}; ++c) {{
-        const int chunk = tid + c * {THREADS};
-        const int row = chunk / {bk // 8}, kc = chunk % {bk // 8};
-        rb[c] = *(const ak_u32x4*)(bp + (long long)row * {ldb} + kc * 8);
-      }}""",
-                "stash": f"""#pragma unroll
-      for (int c = 0; c < {cb}; ++c) {{
-        const int chunk = tid + c * {THREADS};
-        const int row = chunk / {bk // 8}, kc = chunk % {bk // 8};
-        *(ak_u32x4*)(&lds_b[stage][row * {bk} + ((kc ^ (row & 7)) * 8)]) = rb[c];
-      }}""",
-            }
-        # b tile (tk, tn), N-contiguous: 8x8 blocks loaded row by row, transposed in registers.
-        blocks = (bk // 8) * (bn // 8)
-        per = (blocks + THREADS - 1) // THREADS
-        return {
-            "decl": f"ak_u32x4 rb[{per}][8];",
-            "fetch": f"""#pragma unroll
-      for (int c = 0; c < {per}; ++c) {{
-        const int blk = tid + c * {THREADS};
-        if (blk < {blocks}) {{
-          const int kb8 = blk / {bn // 8}, nb8 = blk % {bn // 8};
-#pragma unroll
-          for (int r = 0; r < 8; ++r) rb[c][r] = *(const ak_u32x4*)(bp + (long long)(kb8 * 8 + r) * {ldb} + nb8 * 8);
-        }}
-      }}""",
-            "stash": f"""#pragma unroll
-      for (int c = 0; c < {per}; ++c) {{
-        const int blk = tid + c * {THREADS};
-        if (blk < {blocks}) {{
-          const int kb8 = blk / {bn // 8}, nb8 = blk % {bn // 8};
-          ak_u32x4 col[8];
-          ak_transpose8x8_b16(rb[c], col);
-#pragma unroll
-          for (int cc = 0; cc < 8; ++cc) {{
-            const int row = nb8 * 8 + cc;
-            *(ak_u32x4*)(&lds_b[stage][row * {bk} + ((kb8 ^ (row & 7)) * 8)]) = col[cc];
-          }}
-        }}
-      }}""",
-        }
+}}""")
+        return "\n".join(L)
 
 
 def _cstore(dt: jaxlite.DType) -> str:

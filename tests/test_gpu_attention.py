@@ -1,0 +1,71 @@
+"""Parity of the generated gfx950 flash-attention kernels with the CPU oracle (oracle/kernels.py, the spec's
+loop nest with f32 accumulation) on the same seeded inputs, and at the BASELINE shape with a float32 torch
+reference on the GPU (the attention kernel is floating point).
+
+Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the output's largest magnitude (about
+2 bf16 ulp): the kernel and the oracle differ in f32 summation order and in where the online softmax
+rescales (the kernel steps through 64-key blocks, the spec through its own blocks).
+"""
+
+import pytest
+import torch
+
+from examples.causal_attention import AttentionBlocks, causal_attention
+from oracle import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(b, h, s, d, seed=0):
+    gens = [torch.Generator().manual_seed(seed + i) for i in range(3)]
+    q, k, v = (torch.randn(b, h, s, d, generator=g).to(torch.bfloat16) for g in gens)
+    return (q.float() * d**-0.5).to(torch.bfloat16), k, v
+
+
+def _close(got, want):
+    got, want = got.float().cpu(), want.float().cpu()
+    scale = want.abs().max().item()
+    bad = (got - want).abs() > 1e-2 * want.abs() + 1e-2 * scale
+    assert not bad.any(), f"{int(bad.sum())} of {want.numel()} differ; max |diff| {(got - want).abs().max().item()}"
+
+
+@pytest.mark.parametrize("shape,blocks", [
+    ((1, 2, 512, 128), AttentionBlocks(128, 128)),
+    ((2, 2, 512, 128), AttentionBlocks(256, 128)),
+    ((1, 2, 1024, 128), AttentionBlocks(256, 256)),
+    ((1, 1, 1024, 128), AttentionBlocks(512, 512)),
+])
+def test_causal_attention_matches_oracle(shape, blocks):
+    q, k, v = _inputs(*shape)
+    print(f"attention {shape} {blocks}", flush=True)
+    got = causal_attention(q.cuda(), k.cuda(), v.cuda(), blocks)
+    torch.cuda.synchronize()
+    _close(got, kernels.causal_attention(q, k, v, blocks.block_q, blocks.block_kv))
+
+
+def _reference_f32(q, k, v):
+    B, H, S, D = q.shape
+    qf, vf = q.float().reshape(B * H, S, D), v.float().reshape(B * H, S, D)
+    kt = k.float().reshape(B * H, S, D).transpose(-1, -2).contiguous()
+    mask = torch.ones(S, S, dtype=torch.bool, device=q.device).tril()
+    out = torch.empty(B * H, S, D, device=q.device)
+    for i in range(0, B * H, 8):
+        s = (qf[i:i + 8] @ kt[i:i + 8]).masked_fill(~mask, float("-inf"))
+        out[i:i + 8] = torch.softmax(s, -1) @ vf[i:i + 8]
+    return out.reshape(B, H, S, D)
+
+
+@pytest.mark.parametrize("shape", [(4, 16, 2048, 128), (1, 16, 4096, 128)])
+def test_causal_attention_baseline_shapes(shape):
+    q, k, v = (t.cuda() for t in _inputs(*shape, seed=7))
+    print(f"attention {shape} 512x512", flush=True)
+    got = causal_attention(q, k, v, AttentionBlocks(512, 512))
+    want = _reference_f32(q, k, v)
+    torch.cuda.synchronize()
+    _close(got, want)
+
+
+def test_verify_against_the_spec_reference():
+    q, k, v = _inputs(1, 2, 512, 128, seed=3)
+    err = causal_attention.verify(q.cuda(), k.cuda(), v.cuda(), AttentionBlocks(128, 128))
+    assert err < 0.1

@@ -1,5 +1,629 @@
-"""Lowering of online-softmax attention loop nests (placeholder until written)."""
-def match(plan):
+"""Lowering of online-softmax attention loop nests to one gfx950 flash-attention kernel.
+
+The family is the reference's causal attention spec (examples/causal_attention.py:37-63): per output tile
+of query rows, a reduction loop over key/value blocks whose body is
+
+    s  = score(q_tile @ k_block.T)                      # pointwise in s, positions, loop values
+    m' = maximum(m, max(s, axis=1))                     # m, l: row statistics (row-uniform)
+    p  = exp(s - m')
+    l' = exp(m - m') * l + sum(p, axis=1)
+    acc' = exp(m - m') * acc + p.astype(v.dtype) @ v_block
+    m  = m'
+
+and whose output is a pointwise function of acc and l. `match` recognises that structure in the traced
+tile code (whatever the spelling: widened statistics, `jnp.tile`, operand order) and extracts the two
+pointwise pieces, `score` and the epilogue, which are emitted per element.
+
+The kernel (one workgroup per block of BQ query rows, BQ = 32 x waves; blocks largest-first so the GPU
+balances them):
+
+- each wave owns 32 query rows and computes S^T = K Q^T with `v_mfma_f32_32x32x16_bf16`, so a lane holds
+  one query row's scores: the row max and sum are an in-lane reduction plus one exchange with lane ^ 32;
+- P^T (bf16) feeds O^T = V^T P^T straight from the S^T accumulators, V read transposed from LDS with
+  `ds_read_b64_tr_b16` in the order the accumulator layout gives the key positions;
+- K and V blocks of BKV rows stream HBM -> LDS (`buffer_load_dwordx4 ... lds`) through two stages, the next
+  block's loads in flight under this block's MFMAs;
+- the key blocks a work item visits are the spec's (its step tables), split into BKV-row blocks; per wave,
+  the host's interval analysis of `score` over each block's rectangle marks blocks where the mask keeps
+  every score (computed without it) and, after a block that gives every row a real score, blocks where it
+  keeps none (skipped: their probabilities are exactly zero).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+
+from .. import gfx950, jaxlite
+from ..errors import KernelError
+from ..jaxlite import Node
+from ..pipeline import Pipeline
+from ..plan import Kind, Operand, Output, Plan
+from ..schedule import CODE_SHIFT, STEP_CODE, Schedule
+from .common import Index, decode_tile, static_tile_steps, strides, tile_base
+from .device import PRELUDE
+from .expr import Emitter, Interval, intervals, literal, nodes_between
+from .program import Arg, Launch, Program, c_struct
+
+__all__ = ["FlashMatch", "match", "lower"]
+
+MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 once a row has a real score
+
+
+@dataclass
+class FlashMatch:
+    q: Operand  # TILE: (R, D) query rows
+    k: Operand  # STREAM: (bk, D)
+    v: Operand  # STREAM: (bk, Dv)
+    jvar: str  # the reduction loop over key blocks
+    scores: Node  # dot_nt(q, k): S
+    score: Node  # score(S): what the max and exp read
+    m_init: float
+    out: Output
+    value: Any  # the stored value (Node)
+    acc_leaf: Node  # acc in the end scope
+    sum_leaf: Node  # l in the end scope
+    rows: int
+    bk: int
+    d: int
+    dv: int
+
+
+def _is(n: Any, op: str) -> bool:
+    return isinstance(n, Node) and n.op == op
+
+
+def _strip(n: Any) -> Any:
+    """A value without the row broadcasts the spec spells (jnp.tile / broadcast_to / reshape to the same
+    elements): they don't change a row-uniform value."""
+    while isinstance(n, Node) and n.op in ("tile", "broadcast_to"):
+        n = n.args[0]
+    return n
+
+
+def _pair(n: Node, op: str) -> Optional[Tuple[Any, Any]]:
+    if _is(n, op):
+        return n.args[0], n.args[1]
     return None
-def lower(*a, **k):
-    raise NotImplementedError
+
+
+def _either(pair: Optional[Tuple[Any, Any]], test) -> Optional[Tuple[Any, Any]]:
+    """(x, other) where x passes `test`, trying both orders of a commutative pair."""
+    if pair is None:
+        return None
+    a, b = pair
+    if test(a):
+        return a, b
+    if test(b):
+        return b, a
+    return None
+
+
+def _full_value(v: Any) -> Optional[float]:
+    if isinstance(v, jaxlite.Sym) and _is(v.node, "full"):
+        return float(v.node.kwargs["value"])
+    if isinstance(v, (int, float)):
+        return float(v)
+    return None
+
+
+def match(plan: Plan) -> Optional[FlashMatch]:
+    """The attention this loop nest is, or None."""
+    if len(plan.outputs) != 1 or len(plan.phases) != 1 or len(plan.carried) != 3:
+        return None
+    body, seg0, last = plan.scopes["body0"], plan.scopes["seg0"], plan.scopes["last"]
+    phase = plan.phases[0].range
+    dots = [n for n in body.nodes if n.op in ("dot", "dot_nt")]
+    if len(dots) != 2:
+        return None
+    qk = next((n for n in dots if n.op == "dot_nt"), None)
+    pv = next((n for n in dots if n.op == "dot"), None)
+    if qk is None or pv is None or not (_is(qk.args[0], "load") and _is(qk.args[1], "load") and _is(pv.args[1], "load")):
+        return None
+    q, k, v = (plan.operand(n.kwargs["operand"]) for n in (qk.args[0], qk.args[1], pv.args[1]))
+    if q.kind is not Kind.TILE or k.kind is not Kind.STREAM or v.kind is not Kind.STREAM:
+        return None
+    if any(op.tile.dtype.name != "bfloat16" for op in (q, k, v)):
+        return None
+    # Which carried value is which, from how the body updates them.
+    new = {c: body.values.get(c) for c in plan.carried}
+    leaf = body.carried_in
+    acc = next((c for c, val in new.items() if isinstance(val, jaxlite.Sym) and _pair(val.node, "add")
+                and pv in val.node.args), None)
+    if acc is None:
+        return None
+    rest = [c for c in plan.carried if c != acc]
+    m_name = next((c for c in rest if isinstance(new[c], jaxlite.Sym) and _is(_strip(new[c].node), "maximum")), None)
+    if m_name is None:
+        return None
+    l_name = next(c for c in rest if c != m_name)
+    m_in, l_in, acc_in = leaf.get(m_name), leaf.get(l_name), leaf.get(acc)
+    if m_in is None or l_in is None or acc_in is None:
+        return None
+    # m' = maximum(m, max(score, axis=1))
+    m_new = _strip(new[m_name].node)
+    got = _either(_pair(m_new, "maximum"), lambda x: _strip(x) is m_in)
+    if got is None or not _is(got[1], "reduce_max") or got[1].kwargs.get("axis") not in (1, -1):
+        return None
+    score = got[1].args[0]
+    # p = exp(score - m'); alpha = exp(m - m')
+    exps = [n for n in body.nodes if n.op == "exp"]
+    p = next((n for n in exps if _is(n.args[0], "subtract") and n.args[0].args[0] is score
+              and _strip(n.args[0].args[1]) is m_new), None)
+    alpha = next((n for n in exps if _is(n.args[0], "subtract") and _strip(n.args[0].args[0]) is m_in
+                  and _strip(n.args[0].args[1]) is m_new), None)
+    if p is None or alpha is None:
+        return None
+    # l' = alpha * l + sum(p, axis=1)
+    l_new = new[l_name].node if isinstance(new[l_name], jaxlite.Sym) else None
+    got = _either(_pair(l_new, "add"), lambda x: _is(x, "reduce_sum") and x.args[0] is p)
+    if got is None or _either(_pair(got[1], "multiply"), lambda x: _strip(x) is alpha) is None:
+        return None
+    if _strip(_either(_pair(got[1], "multiply"), lambda x: _strip(x) is alpha)[1]) is not l_in:
+        return None
+    # acc' = alpha * acc + p.astype(v.dtype) @ v
+    scaled = _either(_pair(new[acc].node, "add"), lambda x: x is pv)[1]
+    got = _either(_pair(scaled, "multiply"), lambda x: _strip(x) is alpha)
+    if got is None or got[1] is not acc_in:
+        return None
+    p16 = pv.args[0]
+    if not (_is(p16, "astype") and p16.args[0] is p and p16.dtype.name == "bfloat16"):
+        return None
+    # The score is pointwise in S: everything between S and it is elementwise on positions and loop values.
+    stack, seen = [score], set()
+    while stack:
+        n = stack.pop()
+        if n.id in seen or n is qk:
+            continue
+        seen.add(n.id)
+        if n.op in ("dot", "dot_nt", "load", "carried", "reduce_max", "reduce_sum", "reshape", "concatenate"):
+            return None
+        stack.extend(n.inputs())
+    # Initial values: m a constant, l and acc zero.
+    m_init = _full_value(seg0.values.get(m_name))
+    if m_init is None or _full_value(seg0.values.get(l_name)) != 0.0 or _full_value(seg0.values.get(acc)) != 0.0:
+        return None
+    out = plan.outputs[0]
+    value = last.stores.get(out.name)
+    if not isinstance(value, jaxlite.Sym):
+        return None
+    acc_leaf, sum_leaf = last.carried_in.get(acc), last.carried_in.get(l_name)
+    if acc_leaf is None or sum_leaf is None:
+        return None
+    rows, d = q.tile.shape
+    bk, dk = k.tile.shape
+    bv, dv = v.tile.shape
+    if dk != d or bv != bk or tuple(out.tile.shape[-2:]) != (rows, dv) or qk.shape != (rows, bk):
+        return None
+    return FlashMatch(q, k, v, phase.var, qk, score, m_init, out, value, acc_leaf, sum_leaf, rows, bk, d, dv)
+
+
+# ---------------------------------------------------------------------------------------------- host side
+
+
+def _loop_window(op: Operand, var: str) -> Tuple[int, Any]:
+    """(dim, window) of the tile dim the loop `var` places."""
+    for dim, w in enumerate(op.tile.windows):
+        if w.loop == var:
+            return dim, w
+    raise KernelError(f"`{op.tile.text}` is not placed by loop `{var}`")
+
+
+class _Flash:
+    def __init__(self, plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str) -> None:
+        self.plan, self.sch, self.pipeline, self.m, self.name = plan, sch, pipeline, m, name
+        if m.d % 32 or m.dv % 32 or m.d > 128 or m.dv > 128:
+            raise KernelError(f"the gfx950 attention lowering takes head dims that are multiples of 32 up to 128 "
+                              f"(got {m.d} and {m.dv})")
+        self.nw = 8 if m.rows % 256 == 0 else 4 if m.rows % 128 == 0 else 0
+        if not self.nw:
+            raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of 128 rows (got {m.rows})")
+        self.bq = 32 * self.nw
+        self.bkv = 64
+        if m.bk % self.bkv:
+            raise KernelError(f"the gfx950 attention lowering needs key blocks of a multiple of 64 (got {m.bk})")
+        if plan.runtime or sch.runtime:
+            raise KernelError("attention with runtime masks is lowered by the decode path, not this one")
+        self.jr = plan.phases[0].range
+        self.kdim, self.kwin = _loop_window(m.k, m.jvar)
+        self.vdim, self.vwin = _loop_window(m.v, m.jvar)
+
+    # The blocks each work item visits, and the per-wave mask classes.
+    def _classify(self, values: Dict[str, int], r0: int, r1: int, c0: int, c1: int) -> str:
+        """'full' if score == S over rows [r0, r1] x cols [c0, c1] of the tile (spec-local positions) at these
+        loop values; 'none' if it is a constant below MASKED_BELOW there; else 'partial'."""
+        m = self.m
+        marker = Interval(data=True)
+
+        def leaf(n: Node) -> Optional[Interval]:
+            if n is m.scores:
+                return marker
+            if n.op == "iota":
+                dim = n.kwargs["dimension"]
+                if dim == len(n.shape) - 2:
+                    return Interval(r0, r1)
+                if dim == len(n.shape) - 1:
+                    return Interval(c0, c1)
+                return Interval()
+            if n.op == "loop":
+                val = values.get(n.kwargs["var"])
+                return Interval(val, val) if val is not None else Interval()
+            if n.op == "full":
+                return Interval(n.kwargs["value"], n.kwargs["value"], const=n.kwargs["value"])
+            if n.op in ("load", "carried", "index"):
+                return Interval(data=True)
+            return None
+
+        got = intervals(m.score, leaf)
+        if got is marker:
+            return "full"
+        if not got.data and got.const is not None and float(got.const) <= MASKED_BELOW:
+            return "none"
+        return "partial"
+
+    def _items(self):
+        plan, sch, m = self.plan, self.sch, self.m
+        jr, bkv, bq, nw = self.jr, self.bkv, self.bq, self.nw
+        subs = m.rows // bq
+        per_spec = m.bk // bkv
+        offsets = static_tile_steps(sch) if sch.step_tables else None
+        codes = sch.tables.get(STEP_CODE)
+        patterns: Dict[Tuple, Tuple[List[Tuple[int, int]], List[Tuple[int, int]]]] = {}
+        items, weights, blocks = [], [], []
+        for t in range(sch.tiles):
+            blocks_t = sch.blocks_at(t)
+            values = {r.var: r.value(b) for r, b in zip(plan.parallel, blocks_t)}
+            if offsets is not None:
+                pt = t % sch.pattern_tiles
+                steps = range(int(offsets[pt]), int(offsets[pt + 1]))
+                kbs = [((int(codes[s]) >> CODE_SHIFT) // sch.iterations // sch.phase_radix) for s in steps
+                       if not (int(codes[s]) & 4)]
+            else:
+                kbs = list(range(jr.count))
+            inner = tuple(values[r.var] for r in sch.inner) if sch.tile_tables or sch.step_tables else ()
+            key = (inner, tuple(kbs)) if (sch.tile_tables or sch.step_tables) else ("all",)
+            for sub in range(subs):
+                pkey = key + (sub,)
+                if pkey not in patterns:
+                    patterns[pkey] = self._pattern(values, kbs, sub)
+                blist, waves = patterns[pkey]
+                items.append((t, sub, len(blocks), len(blist), waves))
+                weights.append(sum(n for _, n in waves))
+                blocks.extend(blist)
+        return items, weights, blocks
+
+    def _pattern(self, values: Dict[str, int], kbs: Sequence[int], sub: int):
+        """For one work item: its hardware key blocks [(j value, offset in the spec block)], and per wave
+        (blocks computed without the mask, blocks to compute)."""
+        m, bkv, bq = self.m, self.bkv, self.bq
+        per_spec = m.bk // bkv
+        cand = [(self.jr.value(kb), o * bkv) for kb in kbs for o in range(per_spec)]
+        classes = []
+        for jv, off in cand:
+            vals = {**values, m.jvar: jv}
+            row = []
+            for wv in range(self.nw):
+                r0 = sub * bq + wv * 32
+                row.append(self._classify(vals, r0, r0 + 31, off, off + bkv - 1))
+            classes.append(row)
+        # Blocks after which each wave's rows all have a real score: a block whose first column keeps every
+        # one of the wave's scores.
+        keep_until = [len(cand)] * self.nw
+        for wv in range(self.nw):
+            established = False
+            last = 0
+            for b, (jv, off) in enumerate(cand):
+                if classes[b][wv] != "none" or not established:
+                    last = b + 1
+                if not established:
+                    r0 = sub * bq + wv * 32
+                    first = self._classify({**values, m.jvar: jv}, r0, r0 + 31, off, off)
+                    established = first == "full"
+            keep_until[wv] = last
+        n_blocks = max(keep_until) if keep_until else 0
+        blist = cand[:n_blocks]
+        waves = []
+        for wv in range(self.nw):
+            full = 0
+            while full < keep_until[wv] and classes[full][wv] == "full":
+                full += 1
+            waves.append((full, keep_until[wv]))
+        return blist, waves
+
+    # ------------------------------------------------------------------------------------------ program
+
+    def program(self) -> Program:
+        plan, sch, m = self.plan, self.sch, self.m
+        items, weights, blocks = self._items()
+        order = sorted(range(len(items)), key=lambda i: (-weights[i], i))
+        nw = self.nw
+        stride = 4 + 2 * nw
+        table = np.zeros((max(len(items), 1), stride), np.int32)
+        for row, i in enumerate(order):
+            t, sub, off, cnt, waves = items[i]
+            table[row, :4] = (t, sub, off, cnt)
+            for wv, (full, upto) in enumerate(waves):
+                table[row, 4 + 2 * wv] = full
+                table[row, 5 + 2 * wv] = upto
+        kvtab = np.array(blocks, np.int32).reshape(-1) if blocks else np.zeros(2, np.int32)
+        tables = {"fa_items": table.reshape(-1), "fa_blocks": kvtab}
+        for name, t in sch.tables.items():
+            if name.startswith("tile_") or name.startswith("fill_"):
+                tables[name] = t
+        self.tables = tables
+        args = self._args()
+        source = self._source(args, stride)
+        launch = Launch(self.name, args, (max(len(items), 1), 1, 1), (64 * nw, 1, 1), 0)
+        flop = 2.0 * sum(w for w in weights) * 32 * self.bkv * (m.d + m.dv)
+        return Program(
+            name=self.name, source=source, launches=[launch], outputs=[(m.out.shape, m.out.dtype)],
+            inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables,
+            lds_bytes=2 * self.bkv * (m.d + m.dv) * 2,
+            notes={"family": "flash", "block_q": self.bq, "block_kv": self.bkv, "waves": nw, "items": len(items),
+                   "executed_flop": flop},
+        )
+
+    def _args(self) -> List[Arg]:
+        plan, m = self.plan, self.m
+        args = []
+        for k, name in enumerate(plan.nest.params):
+            spec = plan.inputs[k]
+            if any(ix.name == name for ix in plan.indices):
+                args.append(Arg("input", k, "const int* __restrict__", name))
+            else:
+                args.append(Arg("input", k, "const ak_u16* __restrict__", name))
+        args.append(Arg("output", 0, "ak_u16* __restrict__", m.out.name + "_out"))
+        for name in self.tables:
+            args.append(Arg("table", name, "const int* __restrict__", name))
+        return args
+
+    def _source(self, args: List[Arg], stride: int) -> str:
+        plan, sch, m = self.plan, self.sch, self.m
+        nw, bq, bkv = self.nw, self.bq, self.bkv
+        D, DV = m.d, m.dv
+        T = 64 * nw
+        kt, ds, ks, dt_n = bkv // 32, D // 16, bkv // 16, DV // 32
+        chk, chv = D // 8, DV // 8
+        ldk_n = bkv * D // 8 // T
+        ldv_n = bkv * DV // 8 // T
+        if ldk_n < 1 or ldv_n < 1 or 64 % chk or 64 % chv:
+            raise KernelError("attention block too small for the workgroup")
+        index = Index(plan, lambda v: f"lv_{v}")
+        jvar = m.jvar
+        no_j = lambda v: "0" if v == jvar else f"lv_{v}"
+        q_shape = plan.inputs[m.q.param].shape
+        k_shape = plan.inputs[m.k.param].shape
+        v_shape = plan.inputs[m.v.param].shape
+        q_base, q_str = tile_base(m.q.tile, q_shape, index, lambda v: f"lv_{v}")
+        k_base, k_str = tile_base(m.k.tile, k_shape, index, no_j)
+        v_base, v_str = tile_base(m.v.tile, v_shape, index, no_j)
+        o_base, o_str = tile_base(m.out.tile, m.out.shape, index, lambda v: f"lv_{v}")
+        if q_str[-1] != 1 or k_str[-1] != 1 or v_str[-1] != 1 or o_str[-1] != 1:
+            raise KernelError("the gfx950 attention lowering reads rows whose last dim is contiguous")
+        ldq, ldk, ldv, ldo = q_str[0], k_str[0], v_str[0], o_str[0]
+        kstride_j = strides(k_shape)[self.kdim]
+        vstride_j = strides(v_shape)[self.vdim]
+        for arr, shape in ((m.k.tile.array, k_shape), (m.v.tile.array, v_shape)):
+            if 2 * math.prod(shape) >= 2**31:
+                raise KernelError(f"`{arr}` is 2 GiB or more: the attention lowering uses 32-bit buffer offsets")
+        k_numel, v_numel = math.prod(k_shape), math.prod(v_shape)
+
+        # score(S) per element: S is `sv`; rows/cols spec-local; the key loop's value is `lv_j`.
+        def sleaf(n: Node) -> Optional[str]:
+            if n is m.scores:
+                return "sv"
+            if n.op == "iota":
+                dim = n.kwargs["dimension"]
+                return "er" if dim == len(n.shape) - 2 else "ec" if dim == len(n.shape) - 1 else "0"
+            if n.op == "loop":
+                return f"lv_{n.kwargs['var']}"
+            if n.op == "full":
+                return literal(n.kwargs["value"], n.dtype)
+            if n.op == "index":
+                ix = plan.index(n.kwargs["array"])
+                flat = " + ".join(f"({sem.value(i)}) * {s}" for i, s in zip(n.args, strides(ix.shape))) or "0"
+                return f"args.{ix.name}[{flat}]"
+            return None
+
+        sem = Emitter(sleaf, (m.rows, m.bk), prefix="sc")
+        score_expr = sem.emit(m.score)
+        score_lines = " ".join(sem.lines)
+
+        # The stored value per element: acc (this element), l (the row's sum).
+        def eleaf(n: Node) -> Optional[str]:
+            if n is m.acc_leaf:
+                return "acc_v"
+            if _strip(n) is m.sum_leaf:
+                return "l_run"
+            if n.op == "iota":
+                dim = n.kwargs["dimension"]
+                return "er" if dim == len(n.shape) - 2 else "ed" if dim == len(n.shape) - 1 else "0"
+            if n.op == "loop":
+                return f"lv_{n.kwargs['var']}"
+            if n.op == "full":
+                return literal(n.kwargs["value"], n.dtype)
+            if n.op in ("carried", "load"):
+                raise KernelError("the attention epilogue reads only the accumulator and the row sum")
+            return None
+
+        eem = Emitter(eleaf, m.out.tile.shape, prefix="e")
+        out_expr = eem.emit(m.value.node)
+        epi_lines = "\n        ".join(eem.lines)
+        struct = c_struct(f"{self.name}_args", args)
+        tile_decode = "\n  ".join(decode_tile(plan, sch, "t"))
+        Q, K, V, O = (f"args.{m.q.tile.array}", f"args.{m.k.tile.array}", f"args.{m.v.tile.array}",
+                      f"args.{m.out.name}_out")
+        L: List[str] = []
+        w = L.append
+        w(f"""// Generated by tilejax_amd for `{plan.nest.name}`: a gfx950 flash-attention kernel.
+// spec tile {m.rows} x {m.bk} (head dims {D}, {DV}); workgroup {bq} query rows in {nw} waves, key blocks of {bkv}.
+{PRELUDE}
+{struct}
+#define AK_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define AK_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4))
+#define AK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+#define AK_LDS4(p) ((__attribute__((address_space(3))) ak_i16x4*)(p))""")
+        for s in range(2):
+            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
+            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
+        w(f"""
+extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_args args) {{
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int* item = args.fa_items + blockIdx.x * {stride};
+  const int t = item[0], sub = item[1], boff = item[2], nblk = item[3];
+  const int f_w = item[4 + 2 * wave], n_w = item[5 + 2 * wave];
+  {tile_decode}
+  const int er = sub * {bq} + wave * 32 + (lane & 31);   // this lane's query row in the spec tile
+  // Q^T fragments (srcB of S^T = K Q^T): row er, head dims 16 s + 8 (lane / 32) .. + 8
+  ak_bf16x8 qf[{ds}];
+  {{
+    const ak_u16* qp = {Q} + ({q_base}) + (long long)er * {ldq} + 8 * (lane >> 5);
+#pragma unroll
+    for (int s = 0; s < {ds}; ++s) qf[s] = *(const ak_bf16x8*)(qp + 16 * s);
+  }}
+  const long long k_off = {k_base};
+  const long long v_off = {v_base};
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)({K} + k_off), (short)0,
+      (int)({k_numel}LL * 2 - k_off * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)({V} + v_off), (short)0,
+      (int)({v_numel}LL * 2 - v_off * 2), 0x00020000);
+  // K rows XOR-swizzled for ds_read_b128 (chunk ^ row & 15), V rows for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2)
+  const int k_row = (wave * 64 + lane) / {chk}, v_row = (wave * 64 + lane) / {chv};
+  const unsigned k_voff = (unsigned)(k_row * {ldk * 2} + (((lane % {chk}) ^ (k_row & {min(15, chk - 1)})) * 16));
+  const unsigned v_voff = (unsigned)(v_row * {ldv * 2} + (((lane % {chv}) ^ (((v_row & 3) << 2) & {chv - 1})) * 16));
+  int k_roff[{ds}];
+#pragma unroll
+  for (int s = 0; s < {ds}; ++s) {{
+    const int row = lane & 31;
+    k_roff[s] = row * {D * 2} + (((2 * s + (lane >> 5)) ^ (row & {min(15, chk - 1)})) * 16);
+  }}
+  int v_roff[{dt_n}];
+  {{
+    const int G = lane >> 4, s = lane & 15, kv = 4 * (G >> 1) + (s >> 2);
+#pragma unroll
+    for (int dt = 0; dt < {dt_n}; ++dt) {{
+      const int d = 32 * dt + 16 * (G & 1) + 4 * (s & 3);
+      v_roff[dt] = kv * {DV * 2} + ((((d >> 3) ^ (((kv & 3) << 2) & {chv - 1}))) << 4) + (d & 7) * 2;
+    }}
+  }}
+  ak_f32x16 acc[{dt_n}];
+#pragma unroll
+  for (int i = 0; i < {dt_n}; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+  float m_run = {literal(m.m_init)}, l_run = 0.f;""")
+
+        def issue(b: str, s: int, ind: str) -> List[str]:
+            out = [f"{ind}{{ const int* bp = args.fa_blocks + 2 * (boff + ({b}));",
+                   f"{ind}  const int kpos = bp[0] + {self.kwin.offset} + bp[1], vpos = bp[0] + {self.vwin.offset} + bp[1];"]
+            rows_k, rows_v = T // chk, T // chv
+            for c in range(ldk_n):
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, AK_LDS(&ak_sk{s}[({c * T} + wave * 64) * 8]), 16, k_voff, "
+                           f"(unsigned)((kpos + {c * rows_k}) * {kstride_j * 2}), 0, 0);")
+            for c in range(ldv_n):
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, AK_LDS(&ak_sv{s}[({c * T} + wave * 64) * 8]), 16, v_voff, "
+                           f"(unsigned)((vpos + {c * rows_v}) * {vstride_j * 2}), 0, 0);")
+            out.append(f"{ind}}}")
+            return out
+
+        def compute(s: int, ind: str) -> List[str]:
+            o: List[str] = []
+            a = o.append
+            a(f"{ind}if (b_ < n_w) {{")
+            a(f"{ind}  const char* ks = (const char*)ak_sk{s}; const char* vs = (const char*)ak_sv{s};")
+            a(f"{ind}  const int lv_{jvar} = args.fa_blocks[2 * (boff + b_)], ec0 = args.fa_blocks[2 * (boff + b_) + 1] + (lane >> 5) * 4;")
+            a(f"{ind}  ak_f32x16 st[{kt}];")
+            for t in range(kt):
+                a(f"{ind}  #pragma unroll")
+                a(f"{ind}  for (int r = 0; r < 16; ++r) st[{t}][r] = 0.f;")
+            for t in range(kt):
+                for sl in range(ds):
+                    a(f"{ind}  st[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const ak_bf16x8*)(ks + k_roff[{sl}] + {t * 32 * D * 2}), qf[{sl}], st[{t}], 0, 0, 0);")
+            a(f"{ind}  float mx = -__builtin_inff();")
+            a(f"{ind}  if (b_ < f_w) {{")
+            for t in range(kt):
+                a(f"{ind}    #pragma unroll")
+                a(f"{ind}    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[{t}][r]);")
+            a(f"{ind}  }} else {{")
+            for t in range(kt):
+                a(f"{ind}    #pragma unroll")
+                a(f"{ind}    for (int r = 0; r < 16; ++r) {{")
+                a(f"{ind}      const int ec = ec0 + {32 * t} + (r >> 2) * 8 + (r & 3); (void)ec;")
+                a(f"{ind}      const float sv = st[{t}][r];")
+                a(f"{ind}      {score_lines}")
+                a(f"{ind}      st[{t}][r] = (float)({score_expr}); mx = fmaxf(mx, st[{t}][r]);")
+                a(f"{ind}    }}")
+            a(f"{ind}  }}")
+            a(f"{ind}  mx = fmaxf(mx, __shfl_xor(mx, 32));")
+            a(f"{ind}  const float m_new = ak_maximum(m_run, mx);")
+            a(f"{ind}  const float alpha = ak_exp(m_run - m_new);")
+            a(f"{ind}  float ps = 0.f;")
+            a(f"{ind}  ak_bf16x8 pf[{ks}];")
+            for t in range(kt):
+                for half in range(2):
+                    a(f"{ind}  {{ unsigned pk[4];")
+                    a(f"{ind}    #pragma unroll")
+                    a(f"{ind}    for (int r = 0; r < 8; r += 2) {{")
+                    a(f"{ind}      const float p0 = ak_exp(st[{t}][{8 * half} + r] - m_new), p1 = ak_exp(st[{t}][{8 * half} + r + 1] - m_new);")
+                    a(f"{ind}      ps += p0 + p1; pk[r >> 1] = ak_pack_bf16x2(p0, p1); }}")
+                    a(f"{ind}    pf[{2 * t + half}] = __builtin_bit_cast(ak_bf16x8, (ak_u32x4){{pk[0], pk[1], pk[2], pk[3]}}); }}")
+            a(f"{ind}  ps += __shfl_xor(ps, 32);")
+            a(f"{ind}  l_run = alpha * l_run + ps;")
+            a(f"{ind}  m_run = m_new;")
+            a(f"{ind}  #pragma unroll")
+            a(f"{ind}  for (int i = 0; i < {dt_n}; ++i) acc[i] *= alpha;")
+            for kk in range(ks):
+                for dt in range(dt_n):
+                    o1 = kk * 16 * DV * 2
+                    a(f"{ind}  {{ ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1}));"
+                      f" ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1 + 8 * DV * 2}));")
+                    a(f"{ind}    acc[{dt}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pf[{kk}], acc[{dt}], 0, 0, 0); }}")
+            a(f"{ind}}}")
+            return o
+
+        w("  if (nblk > 0) {")
+        L.extend(issue("0", 0, "    "))
+        w("  }")
+        w("  for (int b = 0; b < nblk; b += 2) {")
+        for s in range(2):
+            w(f"    {{ const int b_ = b + {s};")
+            w("      if (b_ < nblk) {")
+            w("        AK_WAIT_VM(0);")
+            w('        asm volatile("s_barrier" ::: "memory");')
+            w("        if (b_ + 1 < nblk) {")
+            L.extend(issue("b_ + 1", 1 - s, "          "))
+            w("        }")
+            L.extend(compute(s, "        "))
+            w("        AK_WAIT_LGKM0();")
+            w('        asm volatile("s_barrier" ::: "memory");')
+            w("      }")
+            w("    }")
+        w("  }")
+        w(f"""  // Output: lane = query row er, acc[dt][r] = head dim 32 dt + (r / 4) * 8 + (lane / 32) * 4 + r % 4.
+  ak_u16* op = (ak_u16*){O} + ({o_base}) + (long long)er * {ldo};
+#pragma unroll
+  for (int dt = 0; dt < {dt_n}; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {{
+      float res[4];
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {{
+        const int ed = 32 * dt + g4 * 8 + (lane >> 5) * 4 + e4; (void)ed;
+        const float acc_v = acc[dt][4 * g4 + e4];
+        {epi_lines}
+        res[e4] = (float)({out_expr});
+      }}
+      *(ak_u32x2*)(op + 32 * dt + g4 * 8 + (lane >> 5) * 4) = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
+    }}
+}}""")
+        return "\n".join(L)
+
+
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str) -> Program:
+    if m.out.dtype.name != "bfloat16":
+        raise KernelError("the gfx950 attention lowering stores bf16 outputs")
+    return _Flash(plan, sch, pipeline, m, name).program()

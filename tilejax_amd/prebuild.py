@@ -44,7 +44,9 @@ def standard() -> Iterator[Tuple[object, tuple]]:
 
         A = ca.AttentionBlocks
         for shape, blocks in (((4, 16, 2048, 128), A(512, 512)), ((1, 16, 4096, 128), A(512, 512)),
-                              ((2, 4, 512, 128), A(128, 128)), ((1, 2, 1024, 128), A(256, 256))):
+                              ((2, 4, 512, 128), A(128, 128)), ((1, 2, 1024, 128), A(256, 256)),
+                              ((1, 2, 512, 128), A(128, 128)), ((2, 2, 512, 128), A(256, 128)),
+                              ((1, 1, 1024, 128), A(512, 512))):
             yield ca.causal_attention, (_bf16(*shape), _bf16(*shape), _bf16(*shape), blocks)
     except ImportError:
         pass

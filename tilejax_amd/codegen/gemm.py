@@ -333,10 +333,17 @@ class _Gemm:
         args.append(Arg("output", 0, f"{_cstore(m.out.dtype)}* __restrict__", m.out.name + "_out"))
         for name in self.tables:
             args.append(Arg("table", name, "const int* __restrict__", name))
+        args.append(Arg("int", 2 * self._pitch(m.a), "int", "ak_pitch_a"))
+        args.append(Arg("int", 2 * self._pitch(m.b), "int", "ak_pitch_b"))
         if self.sch.runtime:
             args.append(Arg("workspace", "step_code", "const int* __restrict__", "rt_step_code"))
             args.append(Arg("workspace", "tile_steps", "const int* __restrict__", "rt_tile_steps"))
         return args
+
+    def _pitch(self, op: Operand) -> int:
+        """Elements between consecutive rows of an operand tile (its first sliced dim's stride)."""
+        shape = self.plan.inputs[op.param].shape
+        return [s for w, s in zip(op.tile.windows, strides(shape)) if w.size is not None][0]
 
     def _source(self, args: List[Arg]) -> str:
         plan, sch, m, hw = self.plan, self.sch, self.m, self.hw
@@ -458,12 +465,15 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
   // Each wave's buffer_load ... lds fills 1 KiB of a stage, lane l's 16 bytes at 16 l: the lane loads the
   // global chunk that belongs at that (swizzled) position.
   const int a_row = wave * {64 // kca} + lane / {kca};
-  const unsigned a_voff = (unsigned)(a_row * {lda * 2} + (((lane % {kca}) ^ {swa('a_row')}) * 16));""")
+  // Row pitches (bytes) come in as kernel arguments: as literals the compiler precomputes every load's
+  // offset into registers and spills them inside the K loop.
+  const unsigned pa = (unsigned)args.ak_pitch_a, pb = (unsigned)args.ak_pitch_b;
+  const unsigned a_voff = a_row * pa + (unsigned)((((lane % {kca}) ^ {swa('a_row')}) * 16));""")
         if nt:
-            w(f"""  const unsigned b_voff = (unsigned)(a_row * {ldb * 2} + (((lane % {kca}) ^ {swa('a_row')}) * 16));""")
+            w(f"""  const unsigned b_voff = a_row * pb + (unsigned)((((lane % {kca}) ^ {swa('a_row')}) * 16));""")
         else:
             w(f"""  const int b_k = wave * {64 // nc} + lane / {nc};
-  const unsigned b_voff = (unsigned)(b_k * {ldb * 2} + (((lane % {nc}) ^ {swb('b_k')}) * 16));""")
+  const unsigned b_voff = b_k * pb + (unsigned)((((lane % {nc}) ^ {swb('b_k')}) * 16));""")
         w(f"  int a_roff[{k16s}], b_roff[{k16s if nt else ni}];")
         for k16 in range(k16s):
             w(f"  {{ const int row = wm * {wtm} + (lane & 31); a_roff[{k16}] = row * {bk * 2} + "
@@ -490,7 +500,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
       continue;
     }}
     {setup}
-    const int T = nsteps * {kslices};  // K slices (even)
+    int T = nsteps * {kslices};  // K slices (even)
+    asm volatile("" : "+s"(T));  // an opaque trip count: a known one makes the compiler spill in the loop
     const long long a_off = ({a_base}) + (long long)(sm * {bm}) * {lda};""")
         if nt:
             w(f"    const long long b_off = ({b_base}) + (long long)(sn * {bn}) * {ldb};")
@@ -520,12 +531,12 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             rows_a = THREADS // kca
             for c in range(a_ld):
                 out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, AK_LDS(&ak_sa{s}[({c * THREADS} + wave * 64) * 8]), "
-                           f"16, a_voff, (unsigned)({c * rows_a * lda * 2} + k0 * 2), 0, 0);")
+                           f"16, a_voff, {c * rows_a}u * pa + (unsigned)k0 * 2u, 0, 0);")
             for c in range(b_ld):
                 if nt:
-                    soff = f"(unsigned)({c * rows_a * ldb * 2} + k0 * 2)"
+                    soff = f"{c * rows_a}u * pb + (unsigned)k0 * 2u"
                 else:
-                    soff = f"(unsigned)((k0 + {c * (THREADS // nc)}) * {ldb * 2})"
+                    soff = f"(unsigned)(k0 + {c * (THREADS // nc)}) * pb"
                 out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, AK_LDS(&ak_sb{s}[({c * THREADS} + wave * 64) * 8]), "
                            f"16, b_voff, {soff}, 0, 0);")
             out.append(f"{ind}}}")
@@ -596,14 +607,18 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
         w(f"{ind}AK_WAIT_VM(0);")
         w(f'{ind}asm volatile("s_barrier" ::: "memory");')
         w(f"""    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
+    // The lane index goes through an empty asm so the stores' addresses are computed here, not hoisted
+    // above the K loop where they would take registers the loop needs.
+    int lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
 #pragma unroll
     for (int i_ = 0; i_ < {mi}; ++i_) {{
-      const int er = sm * {bm} + wm * {wtm} + i_ * 32 + (lane & 31);
+      const int er = sm * {bm} + wm * {wtm} + i_ * 32 + (lane_e & 31);
 #pragma unroll
       for (int j_ = 0; j_ < {ni}; ++j_) {{
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {{
-          const int ec0 = sn * {bn} + wn * {wtn} + j_ * 32 + g4 * 8 + (lane >> 5) * 4;
+          const int ec0 = sn * {bn} + wn * {wtn} + j_ * 32 + g4 * 8 + (lane_e >> 5) * 4;
           float res[4];
 #pragma unroll
           for (int e4 = 0; e4 < 4; ++e4) {{

@@ -92,7 +92,7 @@ def main() -> int:
     ap.add_argument("--tiles", default="512,512,512", help="dense matmul spec tiles tm,tn,tk")
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of legs to run: dense,causal,attention")
+    ap.add_argument("--only", default="", help="comma list of legs to run: dense,causal,attention,moe,decode")
     ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -109,7 +109,7 @@ def main() -> int:
     from examples.causal_matmul import causal_matmul
     from examples.matmul import MatmulTiles, matmul
 
-    legs = set(args.only.split(",")) if args.only else {"dense", "causal", "attention"}
+    legs = set(args.only.split(",")) if args.only else {"dense", "causal", "attention", "moe", "decode"}
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
     x = torch.randn(N_DENSE, N_DENSE, generator=g).to(torch.bfloat16).to(dev)
@@ -158,6 +158,27 @@ def main() -> int:
         except Exception as e:  # not lowered yet: reported, not hidden
             _log(f"causal MHA: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
             out["attention"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
+
+    if "moe" in legs:
+        try:
+            from examples.moe import GroupTiles, grouped_matmul
+
+            g = torch.Generator().manual_seed(0)
+            counts = torch.multinomial(torch.full((8,), 1 / 8), 64, replacement=True, generator=g).bincount(minlength=8)
+            ge = torch.repeat_interleave(torch.arange(8), counts).to(torch.int32).to(dev)
+            xs = torch.randn(16384, 4096, generator=g).to(torch.bfloat16).to(dev)
+            w = (torch.randn(8, 4096, 14336, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+            gl = grouped_matmul.lower(xs, w, ge, GroupTiles(512, 512))
+            mms, _ = time_kernel(lambda: gl.run(xs, w, ge), args.steps, args.warmup)
+            mflop = 2.0 * 16384 * 4096 * 14336
+            mtf = mflop / (mms * 1e-3) / 1e12
+            _log(f"MoE grouped GEMM 16384x4096x14336 (8 experts): {mms * 1e3:.1f} us, {mtf:.1f} TFLOP/s")
+            out["moe"] = {"shape": [16384, 4096, 14336, 8], "tiles": [512, 512], "us": round(mms * 1e3, 2),
+                          "tflops": round(mtf, 2), "frac_peak": round(mtf / PEAK_TFLOPS, 4)}
+            del xs, w
+        except Exception as e:
+            _log(f"MoE: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
+            out["moe"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
 
     achieved = flop / (launch_ms * 1e-3) / 1e12
     traffic = float(args.traffic) if args.traffic else None

@@ -1,0 +1,40 @@
+"""Grouped matmul with runtime expert windows: each group of G rows of `xs` through its expert's weights.
+
+The spec of BASELINE config 4, in the form the reference's grouped kernels take
+(examples/moe.py:167-187 `expert_ffn`: the runtime mask `tile_expert[i // G] < 0` and the runtime window
+`w[tile_expert[i // G], ...]`; the single-matrix grouped form of tests/test_index_arrays.py:109-125):
+tokens arrive sorted by expert in groups of G rows, `group_expert[g]` names group g's expert (or -1 for an
+unused group, whose rows stay zero), and the window `w[group_expert[i // G], k : k + tk, j : j + tn]` is
+chosen on the device. Column blocks are the outer loop, so consecutive tiles walk the groups of one column
+band: a window shared by consecutive groups of one expert stays where it was fetched.
+"""
+
+import tilejax_amd as autokernel
+from tilejax_amd.jaxlite import jnp
+
+
+@autokernel.tunable
+class GroupTiles:
+    """Output columns per tile, and the reduction depth per step (the rows per tile are the group size)."""
+
+    tn: int = autokernel.choice(256, 512, 1024, 2048, default=512)
+    tk: int = autokernel.choice(256, 512, 1024, 2048, 4096, default=512)
+
+
+@autokernel.kernel
+def grouped_matmul(xs, w, group_expert, tiles=GroupTiles()):
+    M, K = xs.shape
+    E, _, N = w.shape
+    G = M // group_expert.shape[0]
+    tn, tk = min(tiles.tn, N), min(tiles.tk, K)
+    dtype = xs.dtype
+    out = jnp.zeros((M, N), dtype)
+    for j in range(0, N, tn):
+        for i in range(0, M, G):
+            acc = jnp.zeros((G, tn), jnp.float32)
+            for k in range(0, K, tk):
+                if group_expert[i // G] < 0:  # an unused group: decided on the device, before the kernel runs
+                    continue
+                acc += xs[i : i + G, k : k + tk] @ w[group_expert[i // G], k : k + tk, j : j + tn]
+            out = out.at[i : i + G, j : j + tn].set(acc.astype(dtype))
+    return out

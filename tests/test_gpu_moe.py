@@ -1,0 +1,80 @@
+"""Parity of the grouped matmul with runtime expert windows (BASELINE config 4's spec, examples/moe.py)
+with the CPU oracle, and of the device step-table builder with the reference's table semantics restated in
+oracle/schedule.py: bit-exact tables, counts and codes.
+
+Tolerance for the matmul: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want|.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from examples.moe import GroupTiles, grouped_matmul
+from oracle import kernels
+from oracle import schedule as oracle_schedule
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(M, K, N, E, experts, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    xs = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, K, N, generator=g) * 0.02).to(torch.bfloat16)
+    return xs, w, torch.tensor(experts, dtype=torch.int32)
+
+
+def _close(got, want):
+    got, want = got.float().cpu(), want.float().cpu()
+    scale = want.abs().max().item()
+    bad = (got - want).abs() > 1e-2 * want.abs() + 1e-2 * scale
+    assert not bad.any(), f"{int(bad.sum())} of {want.numel()} differ; max |diff| {(got - want).abs().max().item()}"
+
+
+@pytest.mark.parametrize("experts,tiles", [
+    ([0, 1, 2, 3], GroupTiles(512, 256)),
+    ([0, 0, 2, -1], GroupTiles(256, 512)),  # an unused group keeps its zeros
+    ([3, 9, -1, 1], GroupTiles(512, 512)),  # 9 is past the 4 experts: clamped to the last, as JAX clamps
+    ([-1, -1, -1, -1], GroupTiles(512, 256)),  # every group unused: every tile one empty step
+])
+def test_grouped_matmul_matches_oracle(experts, tiles):
+    xs, w, ge = _inputs(1024, 512, 1024, 4, experts)
+    print(f"grouped matmul experts={experts} {tiles}", flush=True)
+    got = grouped_matmul(xs.cuda(), w.cuda(), ge.cuda(), tiles)
+    torch.cuda.synchronize()
+    _close(got, kernels.grouped_matmul(xs, w, ge, tiles.tn, tiles.tk))
+    for g, e in enumerate(experts):
+        if e < 0:
+            assert not got[g * 256:(g + 1) * 256].float().any()
+
+
+def test_device_step_tables_are_bit_exact():
+    experts = [2, -1, 0, -1, 1, 1, -1, 3]
+    xs, w, ge = _inputs(2048, 1024, 512, 4, experts)
+    tiles = GroupTiles(512, 256)
+    lowered = grouped_matmul.lower(xs, w, ge, tiles)
+    got = lowered.program.step_tables(xs.cuda(), w.cuda(), ge.cuda())
+    tiles_i = [{"i": 256 * g} for g in range(8)]
+    step_tile, step_code, count = oracle_schedule.runtime_tables(
+        tiles_i, [("k", 0, 256, 4, lambda v: experts[v["i"] // 256] < 0)])
+    assert int(got["count"][0]) == count == 5 * 4 + 3
+    np.testing.assert_array_equal(got["step_tile"].cpu().numpy(), step_tile)
+    np.testing.assert_array_equal(got["step_code"].cpu().numpy(), step_code)
+    starts = got["tile_steps"].cpu().numpy()
+    assert starts[-1] == count and (np.diff(starts) >= 1).all()
+
+
+def test_baseline_config_against_torch():
+    """16384 tokens x 4096 -> 14336, 8 experts, groups of 256 with seeded multinomial
+    counts, sorted by expert; checked per group against a float32 product on the GPU."""
+    g = torch.Generator().manual_seed(0)
+    counts = torch.multinomial(torch.full((8,), 1 / 8), 64, replacement=True, generator=g).bincount(minlength=8)
+    ge = torch.repeat_interleave(torch.arange(8), counts).to(torch.int32)
+    xs = torch.randn(16384, 4096, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(8, 4096, 14336, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    print("grouped matmul 16384x4096x14336, 8 experts", flush=True)
+    got = grouped_matmul(xs, w, ge.cuda(), GroupTiles(512, 512))
+    for grp in range(0, 64, 9):
+        e = int(ge[grp])
+        rows = slice(grp * 256, (grp + 1) * 256)
+        want = xs[rows].float() @ w[e].float()
+        _close(got[rows], want)

@@ -33,7 +33,19 @@ class Index:
     dims where `clamp` (a runtime window index, which JAX clamps into the dim it indexes)."""
 
     def __init__(self, plan: Plan, names: Callable[[str], Optional[str]], args: str = "args") -> None:
-        self.plan, self.names, self.args = plan, names, args
+        loops = {r.var for r in plan.loops}
+
+        def resolve(v: str) -> Optional[str]:
+            if v in loops:
+                return names(v)
+            value = plan.env.get(v)  # a constant of the prologue or the module (G, a block size, ...)
+            if isinstance(value, bool):
+                return "true" if value else "false"
+            if isinstance(value, int):
+                return str(value)
+            return names(v)
+
+        self.plan, self.names, self.args = plan, resolve, args
 
     def read(self, node: ast.Subscript) -> str:
         ix = self.plan.index(node.value.id)  # type: ignore[attr-defined]

@@ -394,7 +394,7 @@ class _Gemm:
                                                                                             "args.rt_tile_steps")
             steps_setup = [
                 f"const int tt_s = t % {sch.pattern_tiles};",
-                f"const int sbeg = {offs}[tt_s], send = {offs}[tt_s + 1];",
+                f"const int sbeg = __builtin_amdgcn_readfirstlane({offs}[tt_s]), send = {offs}[tt_s + 1];",
                 f"const int nsteps = (({codes}[sbeg] >> 2) & 1) ? 0 : send - sbeg;",
             ]
             kval = (f"({phase.start} + (({codes}[sbeg + st_] >> {CODE_SHIFT}) / {sch.iterations} / "
@@ -500,7 +500,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
       continue;
     }}
     {setup}
-    int T = nsteps * {kslices};  // K slices (even)
+    int T = __builtin_amdgcn_readfirstlane(nsteps * {kslices});  // K slices (even; one value per wave)
     asm volatile("" : "+s"(T));  // an opaque trip count: a known one makes the compiler spill in the loop
     const long long a_off = ({a_base}) + (long long)(sm * {bm}) * {lda};""")
         if nt:

@@ -83,6 +83,19 @@ class Program:
 
     def __call__(self, *arrays: torch.Tensor, outputs: Optional[Sequence[torch.Tensor]] = None,
                  stream: Optional[int] = None) -> Any:
+        outputs, _ = self._run(arrays, outputs, stream, self.launches)
+        return outputs[0] if len(outputs) == 1 else tuple(outputs)
+
+    def step_tables(self, *arrays: torch.Tensor) -> Dict[str, torch.Tensor]:
+        """Run only the device step-table builder (runtime masks) and return its tables as int32 tensors:
+        step_tile, step_code, count (the reference's three) and tile_steps."""
+        builder = [launch for launch in self.launches if launch.symbol == self.notes.get("step_builder")]
+        if not builder:
+            raise KernelError(f"{self.name} has no runtime masks, so no device step tables")
+        _, workspace = self._run(arrays, None, None, builder)
+        return {name: t.view(torch.int32) for name, t in workspace.items()}
+
+    def _run(self, arrays, outputs, stream, launches):
         runtime.require_gpu()
         self.check_inputs(arrays)
         device = arrays[0].device
@@ -92,10 +105,10 @@ class Program:
         workspace = {name: torch.zeros(max(n, 4), dtype=torch.uint8, device=device) for name, n in self.workspace.items()}
         module = self.module(device.index or 0)
         stream = runtime.current_stream() if stream is None else stream
-        for launch in self.launches:
+        for launch in launches:
             args = pack(launch.args, arrays, outputs, tables, workspace)
             module.kernel(launch.symbol).launch(launch.grid, launch.block, launch.lds, args, stream)
-        return outputs[0] if len(outputs) == 1 else tuple(outputs)
+        return outputs, workspace
 
 
 def pack(args: Sequence[Arg], arrays: Sequence[torch.Tensor], outputs: Sequence[torch.Tensor],

@@ -39,6 +39,13 @@ def standard() -> Iterator[Tuple[object, tuple]]:
     for n, tiles in ((8192, T(512, 512, 512)), (1024, T(256, 256, 256)), (512, T(128, 128, 128))):
         yield cm.causal_matmul, (_bf16(n, n), _bf16(n, n), tiles)
     yield mm.matmul, (_bf16(512, 256), _bf16(256, 512), T(256, 256, 128))
+    from examples import moe
+
+    GT = moe.GroupTiles
+    for (m, k, n, e, g), tiles in (((1024, 512, 1024, 4, 4), GT(512, 256)), ((1024, 512, 1024, 4, 4), GT(256, 512)),
+                                   ((1024, 512, 1024, 4, 4), GT(512, 512)), ((2048, 1024, 512, 4, 8), GT(512, 256)),
+                                   ((16384, 4096, 14336, 8, 64), GT(512, 512))):
+        yield moe.grouped_matmul, (_bf16(m, k), _bf16(e, k, n), _i32(g), tiles)
     try:
         from examples import causal_attention as ca
 

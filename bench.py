@@ -180,6 +180,32 @@ def main() -> int:
             _log(f"MoE: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
             out["moe"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
 
+    if "decode" in legs:
+        try:
+            from examples.decode import paged_gqa_decode
+
+            B, H, Hkv, D, P, pages = 64, 32, 8, 128, 16, 512
+            g = torch.Generator().manual_seed(0)
+            lengths = torch.randint(128, 8193, (B,), generator=g, dtype=torch.int32)
+            q = (torch.randn(B, 1, H, D, generator=g) * D**-0.5).to(torch.bfloat16).to(dev)
+            table = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32).to(dev)
+            kp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
+            vp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
+            ln = lengths.to(dev)
+            dl = paged_gqa_decode.lower(q, kp, vp, table, ln)
+            dms, _ = time_kernel(lambda: dl.run(q, kp, vp, table, ln), args.steps, args.warmup)
+            # the valid K and V rows, plus queries, outputs, the page table and the lengths
+            dbytes = int(lengths.sum()) * Hkv * D * 2 * 2 + 2 * q.numel() * 2 + table.numel() * 4 + B * 4
+            gbs = dbytes / (dms * 1e-3) / 1e9
+            _log(f"paged GQA decode 64 seqs, 32/8 heads, 16-token pages: {dms * 1e3:.1f} us, {gbs:.0f} GB/s")
+            out["decode"] = {"sequences": B, "heads": [H, Hkv], "page": P, "sum_lengths": int(lengths.sum()),
+                             "us": round(dms * 1e3, 2), "bytes": dbytes, "gbs": round(gbs, 1),
+                             "frac_hbm_peak": round(gbs / 8000.0, 4)}
+            del kp, vp
+        except Exception as e:
+            _log(f"decode: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
+            out["decode"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
+
     achieved = flop / (launch_ms * 1e-3) / 1e12
     traffic = float(args.traffic) if args.traffic else None
     result = {

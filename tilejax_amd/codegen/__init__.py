@@ -6,7 +6,8 @@ HIP kernel generated from the plan and schedule:
 
 - `gemm`: `acc += a @ b` (or `@ b.T`) over a reduction loop, then a pointwise epilogue (dense, causal and
   grouped matmuls);
-- `flash`: the online-softmax reduction of attention (causal flash attention, paged decode).
+- `flash`: the online-softmax reduction of attention over static masks (causal flash attention);
+- `decode`: the same reduction under runtime masks and runtime page windows (paged decode attention).
 
 A loop nest no family takes raises KernelError naming the kernel: the gfx950 backend doesn't lower it yet.
 """
@@ -37,7 +38,7 @@ def default_pipeline(plan: Plan, schedule: Schedule) -> Pipeline:
 
 def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool = False) -> Program:
     """The program for this plan, schedule and pipeline."""
-    from . import flash, gemm
+    from . import decode, flash, gemm
 
     name = _symbol(plan)
     found = gemm.match(plan)
@@ -46,6 +47,9 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
     found = flash.match(plan)
     if found is not None:
         return flash.lower(plan, schedule, pipeline, found, name)
+    found = decode.match(plan)
+    if found is not None:
+        return decode.lower(plan, schedule, pipeline, found, name)
     raise KernelError(
         f"{plan.nest.name}: the gfx950 backend has no lowering for this loop nest's tile code yet "
         "(it lowers matmuls with pointwise epilogues and online-softmax attention)"

@@ -1,0 +1,481 @@
+"""Lowering of runtime-masked online-softmax loop nests (decode attention over a paged cache) to gfx950.
+
+The family is the reference's `paged_gqa_decode` (examples/decode.py:199-223): per output tile (one
+sequence) some setup code computes the query rows once (`block_diagonal(query_rows(q[b]))`), then a
+reduction loop over the cache's pages, under a runtime mask (`p * P >= lengths[b]`) and reading each page
+through a runtime window (`k_pages[block_tables[b, p], :, :]`), runs the online softmax that
+`flash.softmax_structure` recognises, and the output is some epilogue of the accumulator and the row sum
+(`finish(own_blocks(acc))`). It computes exactly that, as four launches on one stream:
+
+1. the device step-table builder (codegen/steps.py) evaluates the runtime mask: every sequence's pages in
+   order, compacted;
+2. a setup kernel materialises each tile's query rows (the setup code's value, per element) in a
+   workspace, so the attention kernel reads them as plain loads;
+3. the attention kernel splits the compacted step list evenly over one workgroup per CU (a sequence's
+   pages may span several workgroups, a workgroup several short sequences). Per step it streams the page's
+   K and V rows HBM -> LDS (`buffer_load_dwordx4 ... lds`, the next page in flight under this one's
+   compute); its four waves each take a quarter of the query rows' width, so S = Q K^T is four partial
+   products (`v_mfma_f32_16x16x32_bf16`) summed through LDS; every wave then runs the softmax on the full
+   scores and accumulates its quarter of `p @ V` (`v_mfma_f32_32x32x16_bf16`, V read transposed with
+   `ds_read_b64_tr_b16`). When a workgroup leaves a sequence it writes its partial (row max, row sum,
+   accumulator) to a workspace slot;
+4. a merge kernel per sequence rescales and sums its partials (the online softmax's own merge rule:
+   exact reassociation of the same sums) and evaluates the epilogue per output element.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional, Tuple
+
+import numpy as np
+
+from .. import gfx950, jaxlite
+from ..errors import KernelError
+from ..jaxlite import Node
+from ..pipeline import Pipeline
+from ..plan import Kind, Operand, Output, Plan
+from ..schedule import CODE_SHIFT, Schedule
+from .common import Index, strides, tile_base
+from .device import PRELUDE
+from .expr import ElementEmitter, literal
+from .flash import Softmax, _is, _strip, softmax_structure
+from .program import Arg, Launch, Program, c_struct
+from .steps import attach_step_builder
+
+__all__ = ["DecodeMatch", "match", "lower"]
+
+THREADS = 256
+WAVES = 4
+
+
+@dataclass
+class DecodeMatch:
+    sm: Softmax
+    k: Operand
+    v: Operand
+    q_node: Node  # the query rows' value: a setup-code value (carried) or a tile read
+    rows: int  # R: query rows
+    page: int  # P: key rows per step
+    width: int  # W: query/key width (= value width)
+    out: Output
+    value: Any
+    acc_leaf: Node
+    sum_leaf: Node
+
+
+def match(plan: Plan) -> Optional[DecodeMatch]:
+    """Decode attention (runtime-masked online softmax), or None."""
+    if not plan.runtime:
+        return None
+    sm = softmax_structure(plan)
+    if sm is None:
+        return None
+    k = plan.operand(sm.qk.args[1].kwargs["operand"])
+    v = plan.operand(sm.pv.args[1].kwargs["operand"])
+    if k.kind is not Kind.STREAM or v.kind is not Kind.STREAM or k.tile.dtype.name != "bfloat16" \
+            or v.tile.dtype.name != "bfloat16":
+        return None
+    qn = sm.qk.args[0]
+    seg0 = plan.scopes["seg0"]
+    if _is(qn, "carried") and qn.kwargs["name"] in sm.consts:
+        val = seg0.values.get(qn.kwargs["name"])
+        if not isinstance(val, jaxlite.Sym):
+            return None
+        q_node = val.node
+    elif _is(qn, "load"):
+        q_node = qn
+    else:
+        return None
+    if q_node.dtype.name != "bfloat16":
+        return None
+    rows, width = qn.shape
+    page, kw = k.tile.shape
+    vp, vw = v.tile.shape
+    if kw != width or vp != page or vw != width:
+        return None
+    last = plan.scopes["last"]
+    out = plan.outputs[0]
+    value = last.stores.get(out.name)
+    acc_leaf, sum_leaf = last.carried_in.get(sm.acc_name), last.carried_in.get(sm.l_name)
+    if not isinstance(value, jaxlite.Sym) or acc_leaf is None or sum_leaf is None:
+        return None
+    return DecodeMatch(sm, k, v, q_node, rows, page, width, out, value, acc_leaf, sum_leaf)
+
+
+class _Decode:
+    def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str) -> None:
+        self.plan, self.sch, self.m, self.name = plan, sch, m, name
+        if m.rows != 32 or m.page != 16 or m.width % (32 * WAVES):
+            raise KernelError(f"the gfx950 decode lowering takes 32 query rows, pages of 16 positions and widths "
+                              f"that are multiples of {32 * WAVES} (got {m.rows}, {m.page}, {m.width})")
+        if sch.repeats != 1:
+            raise KernelError("decode with parallel loops the runtime mask doesn't read is not lowered yet")
+        self.grid = gfx950.CUS
+        self.slots = self.grid + sch.pattern_tiles
+        self.phase = plan.phases[0].range
+        if (self.phase.count + 1) * m.rows * 4 > 96 * 1024:
+            raise KernelError("too many pages per sequence for the merge kernel's LDS")
+        self.index = Index(plan, lambda v: f"lv_{v}")
+        self.seg0 = plan.scopes["seg0"]
+
+    # -------------------------------------------------------------------------------- element emitters
+
+    def _emitter(self, extra) -> ElementEmitter:
+        """Per-element code of the tile code with the common leaves; `extra(node, idx)` adds the caller's."""
+        plan, m = self.plan, self.m
+        consts = set(m.sm.consts)
+        em: Optional[ElementEmitter] = None
+
+        def leaves(n: Node, idx: Tuple[str, ...]) -> Optional[str]:
+            got = extra(n, idx)
+            if got is not None:
+                return got
+            if n.op == "loop":
+                return f"lv_{n.kwargs['var']}"
+            if n.op == "index":
+                ix = plan.index(n.kwargs["array"])
+                flat = " + ".join(f"({em.at(i, ()) if isinstance(i, Node) else literal(i)}) * {s}"
+                                  for i, s in zip(n.args, strides(ix.shape))) or "0"
+                return f"args.{ix.name}[{flat}]"
+            if n.op == "carried" and n.kwargs["name"] in consts:
+                return em.at(self.seg0.values[n.kwargs["name"]].node, idx)
+            if n.op == "load":
+                op = plan.operand(n.kwargs["operand"])
+                if op.kind is Kind.STREAM:
+                    raise KernelError("setup and epilogue code may read only per-tile tiles")
+                shape = plan.inputs[op.param].shape
+                base, st = tile_base(op.tile, shape, self.index, lambda v: f"lv_{v}")
+                flat = " + ".join(f"(long long)({i}) * {s}" for i, s in zip(idx, st)) or "0"
+                return f"ak_bf16_to_f32(args.{op.tile.array}[({base}) + {flat}])"
+            return None
+
+        em = ElementEmitter(leaves)
+        return em
+
+    # ------------------------------------------------------------------------------------------ program
+
+    def program(self) -> Program:
+        plan, sch, m = self.plan, self.sch, self.m
+        R, W = m.rows, m.width
+        args: List[Arg] = []
+        for k, name in enumerate(plan.nest.params):
+            ctype = "const int* __restrict__" if any(ix.name == name for ix in plan.indices) else \
+                "const ak_u16* __restrict__"
+            args.append(Arg("input", k, ctype, name))
+        args.append(Arg("output", 0, "ak_u16* __restrict__", m.out.name + "_out"))
+        tables: Dict[str, np.ndarray] = {}
+        for r in sch.inner:
+            tables[f"tv_{r.var}"] = np.asarray(sch.tile_values[r.var], np.int32)
+            args.append(Arg("table", f"tv_{r.var}", "const int* __restrict__", f"tv_{r.var}"))
+        workspace = {"dc_q": 2 * sch.pattern_tiles * R * W, "dc_m": 4 * self.slots * R, "dc_l": 4 * self.slots * R,
+                     "dc_acc": 4 * self.slots * R * W}
+        for ws in ("step_tile", "step_code", "count", "tile_steps"):
+            args.append(Arg("workspace", ws, "int* __restrict__", f"rt_{ws}"))
+        args.append(Arg("workspace", "dc_q", "ak_u16* __restrict__", "dc_q"))
+        for ws in ("dc_m", "dc_l", "dc_acc"):
+            args.append(Arg("workspace", ws, "float* __restrict__", ws))
+        struct = c_struct(f"{self.name}_args", args)
+        source = "\n".join([f"// Generated by tilejax_amd for `{plan.nest.name}`: gfx950 split-KV decode attention.",
+                            PRELUDE, struct, self._setup_source(), self._attention_source(), self._merge_source()])
+        prog = Program(
+            name=self.name, source=source,
+            launches=[Launch(f"{self.name}_setup", args, (sch.pattern_tiles, 1, 1), (THREADS, 1, 1), 0),
+                      Launch(self.name, args, (self.grid, 1, 1), (THREADS, 1, 1), 0),
+                      Launch(f"{self.name}_merge", args, (sch.pattern_tiles, 1, 1), (THREADS, 1, 1), 0)],
+            outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
+            tables=tables, workspace=workspace, lds_bytes=2 * 2 * m.page * W * 2 + WAVES * m.page * R * 4,
+            notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page},
+        )
+        attach_step_builder(prog, plan, sch, self.name)
+        return prog
+
+    def _decode_tile(self, t: str) -> str:
+        return " ".join(f"const int lv_{r.var} = args.tv_{r.var}[{t}];" for r in self.sch.inner)
+
+    def _setup_source(self) -> str:
+        m = self.m
+        R, W = m.rows, m.width
+        em = self._emitter(lambda n, idx: None)
+        expr = em.at(m.q_node, ("qr", "qc"))
+        return f"""
+// The tile's query rows, materialised once per tile (the setup code's value, per element).
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const {self.name}_args args) {{
+  const int t = blockIdx.x;
+  {self._decode_tile("t")}
+  ak_u16* dst = args.dc_q + (long long)t * {R * W};
+  for (int e = threadIdx.x; e < {R * W}; e += {THREADS}) {{
+    const int qr = e / {W}, qc = e % {W};
+    dst[e] = (ak_u16)ak_bf16_bits((float)({expr}));
+  }}
+}}
+"""
+
+    def _attention_source(self) -> str:
+        plan, sch, m = self.plan, self.sch, self.m
+        R, P, W = m.rows, m.page, m.width
+        WQ = W // WAVES  # a wave's share of the width
+        slabs = WQ // 32  # K = 32 slabs of S^T = K Q^T per wave
+        dtiles = WQ // 32  # 32-wide tiles of acc^T per wave
+        loads = P * W // 8 // THREADS  # 16-byte loads per thread per operand per step
+        phase, index = self.phase, self.index
+        radix = sch.phase_radix * sch.iterations
+        jvar = phase.var
+        k_shape, v_shape = plan.inputs[m.k.param].shape, plan.inputs[m.v.param].shape
+        k_base, k_str = tile_base(m.k.tile, k_shape, index, lambda v: f"lv_{v}")
+        v_base, v_str = tile_base(m.v.tile, v_shape, index, lambda v: f"lv_{v}")
+        if k_str[-1] != 1 or v_str[-1] != 1:
+            raise KernelError("the decode lowering reads pages whose last dim is contiguous")
+        ldk, ldv = k_str[0], v_str[0]
+        for arr, shape in ((m.k.tile.array, k_shape), (m.v.tile.array, v_shape)):
+            if 2 * math.prod(shape) >= 2**31:
+                raise KernelError(f"`{arr}` is 2 GiB or more: the decode lowering uses 32-bit buffer offsets")
+
+        # score(S) per element: S is `sv`, rows `er`, positions `ep` (in the step's block).
+        def sleaf(n: Node, idx: Tuple[str, ...]) -> Optional[str]:
+            if n is m.sm.qk:
+                return "sv"
+            return None
+
+        score = self._emitter(sleaf).at(m.sm.score, ("er", "ep"))
+        chunks = W // 8
+        rows_per_load = THREADS // chunks
+        L: List[str] = []
+        w = L.append
+        for s in range(2):
+            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sk{s}[{P * W}];")
+            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sv{s}[{P * W}];")
+        w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{P}][{R}];")
+        w(f"""
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int count = args.rt_count[0];
+  const int per = (count + {self.grid - 1}) / {self.grid};
+  const int g0 = blockIdx.x * per, g1 = ak_imin(g0 + per, count);
+  if (g0 >= g1) return;
+  const int cb = wave * {WQ};  // this wave's columns of the width
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)args.{m.k.tile.array}, (short)0,
+      (int)({math.prod(k_shape)}LL * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)args.{m.v.tile.array}, (short)0,
+      (int)({math.prod(v_shape)}LL * 2), 0x00020000);
+  // Loads: LDS chunk position p = c * {THREADS} + tid: row p / {chunks}, chunk p % {chunks}; K rows swizzled
+  // for ds_read_b128 (chunk ^ row & 15), V rows for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2).
+  unsigned k_voff[{loads}], v_voff[{loads}];
+#pragma unroll
+  for (int c = 0; c < {loads}; ++c) {{
+    const int row = c * {rows_per_load} + tid / {chunks}, ch = tid % {chunks};
+    k_voff[c] = (unsigned)(row * {ldk * 2} + ((ch ^ (row & 15)) * 16));
+    v_voff[c] = (unsigned)(row * {ldv * 2} + ((ch ^ ((row & 3) << 2)) * 16));
+  }}
+  // K fragment (srcA of S^T, 16x16x32): position lane % 16, columns cb + 32 s + 8 (lane / 16)
+  int k_roff[{slabs}];
+#pragma unroll
+  for (int s = 0; s < {slabs}; ++s) {{
+    const int pos = lane & 15, ch = (cb + 32 * s + 8 * (lane >> 4)) >> 3;
+    k_roff[s] = pos * {W * 2} + ((ch ^ pos) << 4);
+  }}
+  // V^T fragment (srcA of acc^T, 32x32x16), tr16 reads: group G = lane / 16, s = lane % 16
+  int v_roff[{dtiles}];
+  {{
+    const int G = lane >> 4, s = lane & 15, pos = 8 * (G >> 1) + (s >> 2);
+#pragma unroll
+    for (int dt = 0; dt < {dtiles}; ++dt) {{
+      const int c = cb + 32 * dt + 16 * (G & 1) + 4 * (s & 3);
+      v_roff[dt] = pos * {W * 2} + ((((c >> 3) ^ ((pos & 3) << 2))) << 4) + (c & 7) * 2;
+    }}
+  }}
+  ak_bf16x8 qf[2][{slabs}];
+  ak_f32x16 acc[{dtiles}];
+  float m_run = {literal(m.sm.m_init)}, l_run = 0.f;
+  int cur_t = -1;
+  auto flush = [&](int t) {{
+    const int slot = t + blockIdx.x;
+    const int row = lane & 31;
+    if (wave == 0 && lane < 32) {{
+      args.dc_m[slot * {R} + row] = m_run;
+      args.dc_l[slot * {R} + row] = l_run;
+    }}
+    float* ap = args.dc_acc + (long long)slot * {R * W} + row * {W} + cb + (lane >> 5) * 4;
+#pragma unroll
+    for (int dt = 0; dt < {dtiles}; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *(ak_f32x4*)(ap + 32 * dt + 8 * g4) = ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};
+  }};
+  auto start_tile = [&](int t) {{
+    const ak_u16* qp = args.dc_q + (long long)t * {R * W} + cb + 8 * (lane >> 4);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int s = 0; s < {slabs}; ++s)
+        qf[tt][s] = *(const ak_bf16x8*)(qp + (long long)((lane & 15) + 16 * tt) * {W} + 32 * s);
+#pragma unroll
+    for (int i = 0; i < {dtiles}; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+    m_run = {literal(m.sm.m_init)};
+    l_run = 0.f;
+  }};""")
+
+        def issue(g: str, s: int, ind: str) -> List[str]:
+            return [
+                f"{ind}{{ const int t_ = args.rt_step_tile[{g}], code_ = args.rt_step_code[{g}];",
+                f"{ind}  if (!(code_ & 4)) {{",
+                f"{ind}    {self._decode_tile('t_')}",
+                f"{ind}    const int lv_{jvar} = {phase.start} + ((code_ >> {CODE_SHIFT}) / {radix}) * {phase.step};",
+                f"{ind}    const unsigned ko = (unsigned)(({k_base}) * 2), vo = (unsigned)(({v_base}) * 2);",
+                *(f"{ind}    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)"
+                  f"&dc_sk{s}[({c * THREADS} + wave * 64) * 8], 16, k_voff[{c}], ko, 0, 0);" for c in range(loads)),
+                *(f"{ind}    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)"
+                  f"&dc_sv{s}[({c * THREADS} + wave * 64) * 8], 16, v_voff[{c}], vo, 0, 0);" for c in range(loads)),
+                f"{ind}  }}",
+                f"{ind}}}",
+            ]
+
+        def step(g: str, s: int, ind: str) -> List[str]:
+            o: List[str] = []
+            a = o.append
+            a(f"{ind}{{ const int g_ = {g};")
+            a(f"{ind}  const int t = args.rt_step_tile[g_], code = args.rt_step_code[g_];")
+            a(f"{ind}  if (t != cur_t) {{ if (cur_t >= 0) flush(cur_t); start_tile(t); cur_t = t; }}")
+            a(f"{ind}  __builtin_amdgcn_s_waitcnt(0);")
+            a(f'{ind}  asm volatile("s_barrier" ::: "memory");')
+            a(f"{ind}  if (g_ + 1 < g1) {{")
+            o.extend(issue("g_ + 1", 1 - s, ind + "    "))
+            a(f"{ind}  }}")
+            a(f"{ind}  if (!(code & 4)) {{")
+            a(f"{ind}    {self._decode_tile('t')}")
+            a(f"{ind}    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step}; (void)lv_{jvar};")
+            a(f"{ind}    const char* ks = (const char*)dc_sk{s}; const char* vs = (const char*)dc_sv{s};")
+            # partial S^T over this wave's columns
+            a(f"{ind}    ak_f32x4 st[2] = {{ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}}};")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int s = 0; s < {slabs}; ++s) {{")
+            a(f"{ind}      const ak_bf16x8 kf = *(const ak_bf16x8*)(ks + k_roff[s]);")
+            a(f"{ind}      st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[0][s], st[0], 0, 0, 0);")
+            a(f"{ind}      st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[1][s], st[1], 0, 0, 0);")
+            a(f"{ind}    }}")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int r = 0; r < 4; ++r) {{")
+            a(f"{ind}      dc_sp[wave][4 * (lane >> 4) + r][lane & 15] = st[0][r];")
+            a(f"{ind}      dc_sp[wave][4 * (lane >> 4) + r][16 + (lane & 15)] = st[1][r];")
+            a(f"{ind}    }}")
+            a(f'{ind}    __syncthreads();')
+            # softmax: lane = query row er, positions 8 (lane / 32) + e
+            a(f"{ind}    const int er = lane & 31;")
+            a(f"{ind}    float sc[8];")
+            a(f"{ind}    float mx = -__builtin_inff();")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int e = 0; e < 8; ++e) {{")
+            a(f"{ind}      const int ep = 8 * (lane >> 5) + e;")
+            a(f"{ind}      const float sv = dc_sp[0][ep][er] + dc_sp[1][ep][er] + dc_sp[2][ep][er] + dc_sp[3][ep][er];")
+            a(f"{ind}      sc[e] = (float)({score});")
+            a(f"{ind}      mx = fmaxf(mx, sc[e]);")
+            a(f"{ind}    }}")
+            a(f"{ind}    mx = fmaxf(mx, __shfl_xor(mx, 32));")
+            a(f"{ind}    const float m_new = ak_maximum(m_run, mx);")
+            a(f"{ind}    const float alpha = ak_exp(m_run - m_new);")
+            a(f"{ind}    float ps = 0.f;")
+            a(f"{ind}    unsigned pk[4];")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int e = 0; e < 8; e += 2) {{")
+            a(f"{ind}      const float p0 = ak_exp(sc[e] - m_new), p1 = ak_exp(sc[e + 1] - m_new);")
+            a(f"{ind}      ps += p0 + p1; pk[e >> 1] = ak_pack_bf16x2(p0, p1);")
+            a(f"{ind}    }}")
+            a(f"{ind}    ps += __shfl_xor(ps, 32);")
+            a(f"{ind}    l_run = alpha * l_run + ps;")
+            a(f"{ind}    m_run = m_new;")
+            a(f"{ind}    const ak_bf16x8 pf = __builtin_bit_cast(ak_bf16x8, ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}});")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int dt = 0; dt < {dtiles}; ++dt) {{")
+            a(f"{ind}      acc[dt] *= alpha;")
+            a(f"{ind}      ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) ak_i16x4*)(vs + v_roff[dt]));")
+            a(f"{ind}      ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) ak_i16x4*)(vs + v_roff[dt] + {4 * W * 2}));")
+            a(f"{ind}      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pf, acc[dt], 0, 0, 0);")
+            a(f"{ind}    }}")
+            a(f"{ind}  }}")
+            a(f"{ind}}}")
+            return o
+
+        w("  {")
+        L.extend(issue("g0", 0, "    "))
+        w("  }")
+        w("  for (int g = g0; g < g1; g += 2) {")
+        L.extend(step("g", 0, "    "))
+        w("    if (g + 1 < g1) {")
+        L.extend(step("g + 1", 1, "      "))
+        w("    }")
+        w("  }")
+        w("  flush(cur_t);")
+        w("}")
+        return "\n".join(L)
+
+    def _merge_source(self) -> str:
+        plan, sch, m = self.plan, self.sch, self.m
+        R, W = m.rows, m.width
+        maxs = self.phase.count + 1  # partials per tile: at most its steps (+1 for the division's edges)
+        out_shape = m.out.tile.shape
+        index = self.index
+        o_base, o_str = tile_base(m.out.tile, m.out.shape, index, lambda v: f"lv_{v}")
+
+        def mleaf(n: Node, idx: Tuple[str, ...]) -> Optional[str]:
+            if n is m.acc_leaf:
+                return f"dc_acc_at(({idx[0]}), ({idx[1]}))"
+            if _strip(n) is m.sum_leaf or n is m.sum_leaf:
+                return f"dc_lsum[{idx[0]}]"
+            if n.op == "carried" and n.kwargs["name"] not in m.sm.consts:
+                raise KernelError("the decode epilogue reads only the accumulator and the row sum")
+            return None
+
+        expr = self._emitter(mleaf).at(m.value.node, tuple(f"o{k}" for k in range(len(out_shape))))
+        total = math.prod(out_shape)
+        unravel = []
+        rest = "e"
+        for k, st in enumerate(strides(out_shape)):
+            unravel.append(f"const int o{k} = ({rest}) / {st};")
+            rest = f"({rest}) % {st}"
+        flat_out = " + ".join(f"(long long)o{k} * {s}" for k, s in enumerate(o_str))
+        return f"""
+// Merge a tile's partials (row max m, row sum l, accumulator) and write its output, per element.
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const {self.name}_args args) {{
+  __shared__ float dc_w[{maxs}][{R}];
+  __shared__ float dc_lsum[{R}];
+  const int t = blockIdx.x;
+  {self._decode_tile("t")}
+  const int count = args.rt_count[0];
+  const int per = (count + {self.grid - 1}) / {self.grid};
+  const int ts = args.rt_tile_steps[t], te = args.rt_tile_steps[t + 1];
+  const int w0 = ts / per, w1 = (te - 1) / per;
+  const int n = w1 - w0 + 1;
+  for (int r = threadIdx.x; r < {R}; r += {THREADS}) {{
+    float mm = -__builtin_inff();
+    for (int k = 0; k < n; ++k) mm = fmaxf(mm, args.dc_m[(t + w0 + k) * {R} + r]);
+    float ls = 0.f;
+    for (int k = 0; k < n; ++k) {{
+      const float wk = ak_exp(args.dc_m[(t + w0 + k) * {R} + r] - mm);
+      dc_w[k][r] = wk;
+      ls += wk * args.dc_l[(t + w0 + k) * {R} + r];
+    }}
+    dc_lsum[r] = ls;
+  }}
+  __syncthreads();
+  auto dc_acc_at = [&](int r, int c) -> float {{
+    float v = 0.f;
+    for (int k = 0; k < n; ++k) v += dc_w[k][r] * args.dc_acc[(long long)(t + w0 + k) * {R * W} + r * {W} + c];
+    return v;
+  }};
+  ak_u16* op = args.{m.out.name}_out + ({o_base});
+  for (int e = threadIdx.x; e < {total}; e += {THREADS}) {{
+    {" ".join(unravel)}
+    op[{flat_out}] = (ak_u16)ak_bf16_bits((float)({expr}));
+  }}
+}}
+"""
+
+
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: str) -> Program:
+    if m.out.dtype.name != "bfloat16":
+        raise KernelError("the gfx950 decode lowering stores bf16 outputs")
+    return _Decode(plan, sch, m, name).program()

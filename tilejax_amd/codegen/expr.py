@@ -345,3 +345,152 @@ def intervals(root: Node, leaves: Callable[[Node], Optional[Interval]]) -> Inter
         return got
 
     return go(root)
+
+
+# --------------------------------------------------------------------------------------------- elements
+
+
+class ElementEmitter:
+    """One element of a traced tile value as a C expression, at C index expressions: the per-element view
+    of code that moves data around (reshape, concatenate, slices, jnp.tile, broadcasts) as well as computing
+    it pointwise. `leaves(node, idx)` gives the expression of a leaf the caller provides (an input tile, a
+    carried value, ...), or None.
+
+    Branches stay branches: `where` and `concatenate` become C conditionals, so only the chosen operand is
+    evaluated when the kernel runs."""
+
+    MAX_CHARS = 1 << 20
+
+    def __init__(self, leaves: Callable[[Node, Tuple[str, ...]], Optional[str]]) -> None:
+        self.leaves = leaves
+
+    def at(self, node: Any, idx: Sequence[str]) -> str:
+        text = self._at(node, tuple(idx))
+        if len(text) > self.MAX_CHARS:
+            raise KernelError("an element of this tile code is too large an expression to generate")
+        return text
+
+    def _val(self, arg: Any, idx: Tuple[str, ...], shape: Tuple[int, ...], dt: Optional[DType] = None) -> str:
+        if isinstance(arg, Node):
+            return self._at(arg, _broadcast_index(arg.shape, shape, idx))
+        if isinstance(arg, (bool, int, float)):
+            return literal(arg, dt)
+        raise KernelError(f"the gfx950 lowering can't compute {arg!r} per element")
+
+    def _at(self, n: Node, idx: Tuple[str, ...]) -> str:
+        leaf = self.leaves(n, idx)
+        if leaf is not None:
+            return leaf
+        op, a, dt, shape = n.op, n.args, n.dtype, tuple(n.shape)
+        ct = ctype(dt)
+        if op == "iota":
+            return f"({idx[n.kwargs['dimension']]})"
+        if op == "full":
+            return literal(n.kwargs["value"], dt)
+        if op in _BINARY:
+            x, y = self._val(a[0], idx, shape, dt), self._val(a[1], idx, shape, dt)
+            return _rounded(f"(({ct})({x}) {_BINARY[op]} ({ct})({y}))", dt) if dt.kind == "f" else \
+                f"(({ct})({x}) {_BINARY[op]} ({ct})({y}))"
+        if op in _COMPARE:
+            return f"(({self._val(a[0], idx, shape)}) {_COMPARE[op]} ({self._val(a[1], idx, shape)}))"
+        if op == "divide":
+            x, y = self._val(a[0], idx, shape, dt), self._val(a[1], idx, shape, dt)
+            return _rounded(f"(({ct})({x}) / ({ct})({y}))", dt)
+        if op in ("maximum", "minimum"):
+            x, y = self._val(a[0], idx, shape, dt), self._val(a[1], idx, shape, dt)
+            if dt.kind == "f":
+                return _rounded(f"ak_{op}(({ct})({x}), ({ct})({y}))", dt)
+            return f"((({x}) {'>' if op == 'maximum' else '<'} ({y})) ? ({x}) : ({y}))"
+        if op in ("logical_and", "logical_or"):
+            j = " && " if op == "logical_and" else " || "
+            return f"(({self._val(a[0], idx, shape)}){j}({self._val(a[1], idx, shape)}))"
+        if op in ("logical_not",) or (op == "invert" and dt.kind == "b"):
+            return f"(!({self._val(a[0], idx, shape)}))"
+        if op == "negative":
+            return f"(-({self._val(a[0], idx, shape, dt)}))"
+        if op == "where":
+            c = self._val(a[0], idx, shape)
+            return f"(({c}) ? ({ct})({self._val(a[1], idx, shape, dt)}) : ({ct})({self._val(a[2], idx, shape, dt)}))"
+        if op == "astype":
+            x = self._val(a[0], idx, shape)
+            if dt.kind == "f":
+                return _rounded(f"({ct})({x})", dt)
+            if dt.kind == "b":
+                return f"(({x}) != 0)"
+            return f"({ct})({x})"
+        if op in ("exp", "log", "sqrt", "rsqrt", "reciprocal", "square", "sigmoid", "abs"):
+            x = self._val(a[0], idx, shape, dt)
+            fn = {"exp": "ak_exp", "log": "__logf", "sqrt": "sqrtf", "rsqrt": "ak_rsqrt", "reciprocal": "ak_rcp",
+                  "square": "ak_square", "sigmoid": "ak_sigmoid", "abs": "fabsf"}[op]
+            return _rounded(f"{fn}((float)({x}))", dt)
+        if op == "broadcast_to":
+            return self._val(a[0], idx, shape)
+        if op == "tile":
+            src = a[0]
+            inner = tuple(idx[len(idx) - len(src.shape) + k] if len(src.shape) else "0" for k in range(len(src.shape)))
+            inner = tuple(f"(({i}) % {s})" if s != 1 else "0" for i, s in zip(inner, src.shape))
+            return self._at(src, inner)
+        if op == "reshape":
+            src = a[0]
+            flat = "0"
+            for i, s in zip(idx, shape):
+                flat = f"(({flat}) * {s} + ({i}))"
+            inner, rest = [], flat
+            st = strides_of(src.shape)
+            for s, d in zip(st, src.shape):
+                inner.append(f"((({rest}) / {s}) % {d})" if d != 1 else "0")
+            return self._at(src, tuple(inner))
+        if op == "concatenate":
+            pieces, axis = a[0], n.kwargs["axis"]
+            axis = axis % len(shape)
+            out, start = None, 0
+            branches = []
+            for p in pieces:
+                size = p.shape[axis]
+                sub = tuple(f"(({i}) - {start})" if k == axis and start else i for k, i in enumerate(idx))
+                branches.append((start, start + size, self._at(p, sub)))
+                start += size
+            expr = f"({ct})({branches[-1][2]})"
+            for lo, hi, text in reversed(branches[:-1]):
+                expr = f"((({idx[axis]}) < {hi}) ? ({ct})({text}) : {expr})"
+            return expr
+        if op == "getitem":
+            src, key = a[0], a[1]
+            key = key if isinstance(key, tuple) else (key,)
+            inner, k_out = [], 0
+            for k, d in enumerate(src.shape):
+                sel = key[k] if k < len(key) else slice(None)
+                if isinstance(sel, slice):
+                    start, _, step = sel.indices(d)
+                    i = idx[k_out]
+                    inner.append(f"({start} + ({i}) * {step})" if (start or step != 1) else i)
+                    k_out += 1
+                elif isinstance(sel, int):
+                    inner.append(str(sel % d))
+                else:
+                    raise KernelError("only static slices and integers index tile values per element")
+            return self._at(src, tuple(inner))
+        if op == "transpose":
+            perm = n.kwargs.get("axes") or tuple(reversed(range(len(shape))))
+            inner = [None] * len(perm)
+            for out_k, in_k in enumerate(perm):
+                inner[in_k] = idx[out_k]
+            return self._at(a[0], tuple(inner))
+        raise KernelError(f"the gfx950 lowering has no per-element form of `{op}` in tile setup or epilogue code")
+
+
+def strides_of(shape: Sequence[int]) -> List[int]:
+    out, n = [], 1
+    for d in reversed(tuple(shape)):
+        out.append(n)
+        n *= d
+    return list(reversed(out))
+
+
+def _broadcast_index(shape: Sequence[int], target: Sequence[int], idx: Tuple[str, ...]) -> Tuple[str, ...]:
+    """The index into an operand of `shape` broadcast (numpy rules) to `target` at index `idx`."""
+    shape, target = tuple(shape), tuple(target)
+    lead = len(target) - len(shape)
+    if lead < 0:
+        raise KernelError(f"can't broadcast {shape} to {target}")
+    return tuple("0" if s == 1 and t != 1 else idx[lead + k] for k, (s, t) in enumerate(zip(shape, target[lead:])))

@@ -77,10 +77,16 @@ def _is(n: Any, op: str) -> bool:
 
 
 def _strip(n: Any) -> Any:
-    """A value without the row broadcasts the spec spells (jnp.tile / broadcast_to / reshape to the same
-    elements): they don't change a row-uniform value."""
-    while isinstance(n, Node) and n.op in ("tile", "broadcast_to"):
-        n = n.args[0]
+    """A value without the row broadcasts the spec spells (jnp.tile / broadcast_to, or a slice of its
+    leading columns): they don't change a row-uniform value."""
+    while isinstance(n, Node):
+        if n.op in ("tile", "broadcast_to"):
+            n = n.args[0]
+        elif n.op == "getitem" and isinstance(n.args[1], tuple) and len(n.args[1]) == 2 and \
+                n.args[1][0] == slice(None) and isinstance(n.args[1][1], slice):
+            n = n.args[0]
+        else:
+            break
     return n
 
 
@@ -110,32 +116,44 @@ def _full_value(v: Any) -> Optional[float]:
     return None
 
 
-def match(plan: Plan) -> Optional[FlashMatch]:
-    """The attention this loop nest is, or None."""
-    if len(plan.outputs) != 1 or len(plan.phases) != 1 or len(plan.carried) != 3:
+@dataclass
+class Softmax:
+    """The online-softmax reduction of a loop nest's body, as `softmax_structure` finds it."""
+
+    qk: Node  # dot_nt(queries, keys)
+    pv: Node  # dot(p.astype, values)
+    score: Node
+    m_name: str
+    l_name: str
+    acc_name: str
+    m_init: float
+    consts: Tuple[str, ...]  # carried values the body never changes: per-tile values of the setup code
+
+
+def softmax_structure(plan: Plan) -> Optional[Softmax]:
+    """The online softmax of the body (the module docstring's form), or None. Besides the three statistics,
+    carried values may only be per-tile constants (assigned before the loop, read in it or after it)."""
+    if len(plan.outputs) != 1 or len(plan.phases) != 1:
         return None
-    body, seg0, last = plan.scopes["body0"], plan.scopes["seg0"], plan.scopes["last"]
-    phase = plan.phases[0].range
+    body, seg0 = plan.scopes["body0"], plan.scopes["seg0"]
     dots = [n for n in body.nodes if n.op in ("dot", "dot_nt")]
     if len(dots) != 2:
         return None
     qk = next((n for n in dots if n.op == "dot_nt"), None)
     pv = next((n for n in dots if n.op == "dot"), None)
-    if qk is None or pv is None or not (_is(qk.args[0], "load") and _is(qk.args[1], "load") and _is(pv.args[1], "load")):
+    if qk is None or pv is None or not (_is(qk.args[1], "load") and _is(pv.args[1], "load")):
         return None
-    q, k, v = (plan.operand(n.kwargs["operand"]) for n in (qk.args[0], qk.args[1], pv.args[1]))
-    if q.kind is not Kind.TILE or k.kind is not Kind.STREAM or v.kind is not Kind.STREAM:
-        return None
-    if any(op.tile.dtype.name != "bfloat16" for op in (q, k, v)):
-        return None
-    # Which carried value is which, from how the body updates them.
     new = {c: body.values.get(c) for c in plan.carried}
     leaf = body.carried_in
+    consts = tuple(c for c, val in new.items() if isinstance(val, jaxlite.Sym) and val.node is leaf.get(c))
+    consts += tuple(c for c in plan.carried if c not in new or new[c] is None)
     acc = next((c for c, val in new.items() if isinstance(val, jaxlite.Sym) and _pair(val.node, "add")
                 and pv in val.node.args), None)
     if acc is None:
         return None
-    rest = [c for c in plan.carried if c != acc]
+    rest = [c for c in plan.carried if c != acc and c not in consts]
+    if len(rest) != 2:
+        return None
     m_name = next((c for c in rest if isinstance(new[c], jaxlite.Sym) and _is(_strip(new[c].node), "maximum")), None)
     if m_name is None:
         return None
@@ -179,13 +197,35 @@ def match(plan: Plan) -> Optional[FlashMatch]:
         if n.id in seen or n is qk:
             continue
         seen.add(n.id)
-        if n.op in ("dot", "dot_nt", "load", "carried", "reduce_max", "reduce_sum", "reshape", "concatenate"):
+        if n.op in ("dot", "dot_nt", "load", "reduce_max", "reduce_sum", "reshape", "concatenate"):
+            return None
+        if n.op == "carried" and n.kwargs["name"] not in consts:
             return None
         stack.extend(n.inputs())
     # Initial values: m a constant, l and acc zero.
     m_init = _full_value(seg0.values.get(m_name))
     if m_init is None or _full_value(seg0.values.get(l_name)) != 0.0 or _full_value(seg0.values.get(acc)) != 0.0:
         return None
+    return Softmax(qk, pv, score, m_name, l_name, acc, m_init, consts)
+
+
+def match(plan: Plan) -> Optional[FlashMatch]:
+    """The attention this loop nest is (queries a TILE read, keys and values streamed, static masks), or
+    None."""
+    sm = softmax_structure(plan)
+    if sm is None or sm.consts or plan.runtime:
+        return None
+    qk, pv, score, m_init = sm.qk, sm.pv, sm.score, sm.m_init
+    if not _is(qk.args[0], "load"):
+        return None
+    q, k, v = (plan.operand(n.kwargs["operand"]) for n in (qk.args[0], qk.args[1], pv.args[1]))
+    if q.kind is not Kind.TILE or k.kind is not Kind.STREAM or v.kind is not Kind.STREAM:
+        return None
+    if any(op.tile.dtype.name != "bfloat16" for op in (q, k, v)):
+        return None
+    phase = plan.phases[0].range
+    last = plan.scopes["last"]
+    acc, l_name = sm.acc_name, sm.l_name
     out = plan.outputs[0]
     value = last.stores.get(out.name)
     if not isinstance(value, jaxlite.Sym):

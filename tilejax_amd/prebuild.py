@@ -46,6 +46,11 @@ def standard() -> Iterator[Tuple[object, tuple]]:
                                    ((1024, 512, 1024, 4, 4), GT(512, 512)), ((2048, 1024, 512, 4, 8), GT(512, 256)),
                                    ((16384, 4096, 14336, 8, 64), GT(512, 512))):
         yield moe.grouped_matmul, (_bf16(m, k), _bf16(e, k, n), _i32(g), tiles)
+    from examples import decode
+
+    for b, pages, n_pages in ((4, 64, 256), (64, 512, 32768)):
+        yield decode.paged_gqa_decode, (_bf16(b, 1, 32, 128), _bf16(n_pages, 16, 1024), _bf16(n_pages, 16, 1024),
+                                        _i32(b, pages), _i32(b))
     try:
         from examples import causal_attention as ca
 

@@ -84,6 +84,19 @@ def cpu_baseline(budget_s: float = 12.0):
                       f"512^3 tiles, median of {len(times)} calls ({t * 1e3:.1f} ms each)"}
 
 
+def _measured_traffic(tiles):
+    """HBM bytes per launch of the dense kernel at these tiles, from the committed rocprofv3 FETCH_SIZE and
+    WRITE_SIZE runs (profiles/traffic.json, scaled by a known-size copy), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = data.get("dense_8192_" + "x".join(str(t) for t in tiles))
+    return float(entry["bytes_per_launch"]) if entry else None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -93,7 +106,10 @@ def main() -> int:
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list of legs to run: dense,causal,attention,moe,decode")
-    ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3")
+    ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3; "
+                    "default: profiles/traffic.json")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first copy a 1 GiB tensor once: the known-size kernel rocprofv3 counters are scaled by")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): this build has no multi-GPU path",
@@ -108,6 +124,13 @@ def main() -> int:
 
     from examples.causal_matmul import causal_matmul
     from examples.matmul import MatmulTiles, matmul
+
+    if args.calibrate_copy:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     legs = set(args.only.split(",")) if args.only else {"dense", "causal", "attention", "moe", "decode"}
     dev = torch.device("cuda:0")
@@ -207,7 +230,7 @@ def main() -> int:
             out["decode"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
 
     achieved = flop / (launch_ms * 1e-3) / 1e12
-    traffic = float(args.traffic) if args.traffic else None
+    traffic = float(args.traffic) if args.traffic else _measured_traffic(out["dense"]["tiles"])
     result = {
         "metric": "bf16 TFLOP/s + % MFMA peak: 8192^3 matmul; causal MHA B4 H16 S2048 D128",
         "value": round(tflops, 2),

@@ -180,6 +180,23 @@ def _smaller(kernel: Any, signature: Any, config: Config) -> List[Config]:
     return found
 
 
+def _other_kernels(kernel: Any, signature: Any, start: Config) -> List[Config]:
+    """The bufferings of `start` whose generated kernels differ from its own."""
+    here = kernel.lowered(signature, start).source
+    found = []
+    for n in range(1, MAX_INPUT_BUFFERS + 1):
+        for m in range(1, MAX_OUTPUT_BUFFERS + 1):
+            config = Config(start.tunable, Pipeline(n, m))
+            if config == start:
+                continue
+            try:
+                if kernel.lowered(signature, config).source != here:
+                    found.append(config)
+            except KernelError:
+                continue
+    return found
+
+
 def random_inputs(signature: Sequence[Tuple[Tuple[int, ...], Any]], bounds: Optional[Dict[int, int]] = None,
                   seed: int = 0, device: Any = "cuda") -> List[torch.Tensor]:
     """Inputs to tune on: normal floats, small ints; index arrays (`bounds`) from 0 to their bound."""
@@ -230,6 +247,8 @@ def tune(kernel: Any, signature: Any, arrays: Optional[Sequence[Any]] = None, bu
     start = kernel.default_config(signature)
     if not _can_time():
         return Tuning(Trial(start))
+    if start.tunable is None and not _other_kernels(kernel, signature, start):
+        return Tuning(Trial(start))  # nothing to choose: every buffering builds the same kernel
     if arrays is not None and all(isinstance(a, torch.Tensor) and a.is_cuda for a in arrays):
         inputs = list(arrays)
     else:

@@ -119,6 +119,11 @@ class _Decode:
             raise KernelError("too many pages per sequence for the merge kernel's LDS")
         self.index = Index(plan, lambda v: f"lv_{v}")
         self.seg0 = plan.scopes["seg0"]
+        # The setup and merge kernels split each tile's elements over `chunks` workgroups (grid y), enough for
+        # about four workgroups per CU over all tiles, each thread keeping at least one element.
+        want = -(-4 * gfx950.CUS // sch.pattern_tiles)
+        self.setup_chunks = max(1, min(m.rows * m.width // THREADS, want))
+        self.merge_chunks = max(1, min(math.prod(m.out.tile.shape) // THREADS, want))
 
     # -------------------------------------------------------------------------------- element emitters
 
@@ -181,9 +186,9 @@ class _Decode:
                             PRELUDE, struct, self._setup_source(), self._attention_source(), self._merge_source()])
         prog = Program(
             name=self.name, source=source,
-            launches=[Launch(f"{self.name}_setup", args, (sch.pattern_tiles, 1, 1), (THREADS, 1, 1), 0),
+            launches=[Launch(f"{self.name}_setup", args, (sch.pattern_tiles, self.setup_chunks, 1), (THREADS, 1, 1), 0),
                       Launch(self.name, args, (self.grid, 1, 1), (THREADS, 1, 1), 0),
-                      Launch(f"{self.name}_merge", args, (sch.pattern_tiles, 1, 1), (THREADS, 1, 1), 0)],
+                      Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (THREADS, 1, 1), 0)],
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
             tables=tables, workspace=workspace, lds_bytes=2 * 2 * m.page * W * 2 + WAVES * m.page * R * 4,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page},
@@ -200,12 +205,13 @@ class _Decode:
         em = self._emitter(lambda n, idx: None)
         expr = em.at(m.q_node, ("qr", "qc"))
         return f"""
-// The tile's query rows, materialised once per tile (the setup code's value, per element).
+// The tile's query rows, materialised once per tile (the setup code's value, per element); workgroup (t, y)\n// writes chunk y of tile t's elements.
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const {self.name}_args args) {{
   const int t = blockIdx.x;
   {self._decode_tile("t")}
   ak_u16* dst = args.dc_q + (long long)t * {R * W};
-  for (int e = threadIdx.x; e < {R * W}; e += {THREADS}) {{
+  const int e1 = ak_imin((int)(blockIdx.y + 1) * {-(-R * W // self.setup_chunks)}, {R * W});
+  for (int e = blockIdx.y * {-(-R * W // self.setup_chunks)} + threadIdx.x; e < e1; e += {THREADS}) {{
     const int qr = e / {W}, qc = e % {W};
     dst[e] = (ak_u16)ak_bf16_bits((float)({expr}));
   }}
@@ -437,8 +443,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             unravel.append(f"const int o{k} = ({rest}) / {st};")
             rest = f"({rest}) % {st}"
         flat_out = " + ".join(f"(long long)o{k} * {s}" for k, s in enumerate(o_str))
+        chunk = -(-total // self.merge_chunks)
         return f"""
-// Merge a tile's partials (row max m, row sum l, accumulator) and write its output, per element.
+// Merge a tile's partials (row max m, row sum l, accumulator) and write its output, per element; workgroup\n// (t, y) writes chunk y of tile t's elements, each computing the tile's partial weights.
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const {self.name}_args args) {{
   __shared__ float dc_w[{maxs}][{R}];
   __shared__ float dc_lsum[{R}];
@@ -467,7 +474,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
     return v;
   }};
   ak_u16* op = args.{m.out.name}_out + ({o_base});
-  for (int e = threadIdx.x; e < {total}; e += {THREADS}) {{
+  const int e1 = ak_imin((int)(blockIdx.y + 1) * {chunk}, {total});
+  for (int e = blockIdx.y * {chunk} + threadIdx.x; e < e1; e += {THREADS}) {{
     {" ".join(unravel)}
     op[{flat_out}] = (ak_u16)ak_bf16_bits((float)({expr}));
   }}

@@ -7,10 +7,11 @@ none of whose blocks run keeps one empty step at block 0; each step gets its cod
 moved to the front in (t, kb) order and the rest follow in order (a stable partition); the count of kept
 steps is the third output.
 
-Here it is one workgroup of 1024 threads, generated from the mask expression: each thread evaluates the
-masks of a run of tiles, a block-wide scan turns kept/dropped counts into offsets, and every tile writes its
-entries. Besides the reference's three outputs it writes `tile_steps`, each pattern tile's first kept
-step (and the total at the end), which the matmul kernel uses to find a tile's steps without a search.
+Here it is one workgroup of 1024 threads, generated from the mask expression: each wave evaluates one tile's
+masks 64 blocks per ballot, a block-wide scan turns the tiles' kept counts into offsets, and each wave writes
+its tiles' entries at ballot-prefix positions. Besides the reference's three outputs it writes `tile_steps`,
+each pattern tile's first kept step (and the total at the end), which the kernels use to find a tile's steps
+without a search.
 """
 
 from __future__ import annotations
@@ -47,58 +48,87 @@ def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg]) -> str
     per = (pt + THREADS - 1) // THREADS
     return f"""
 {struct}
-// Step tables for `{plan.nest.name}`: {pt} pattern tiles x {count} blocks of `{phase.var}`.
+// Step tables for `{plan.nest.name}`: {pt} pattern tiles x {count} blocks of `{phase.var}`. One wave per tile at
+// a time: the mask of 64 blocks per ballot, kept/dropped counts by popcount, then a block-wide scan of the
+// tiles' counts, then each wave writes its tiles' entries at ballot-prefix positions.
 extern "C" __global__ void __launch_bounds__({THREADS}) {name}(const {name}_args args) {{
-  __shared__ int keep_n[{pt}], drop_n[{pt}], scan_k[{THREADS}], scan_d[{THREADS}];
-  const int tid = threadIdx.x;
-  const int t0 = tid * {per}, t1 = ak_imin(t0 + {per}, {pt});
-  int my_k = 0, my_d = 0;
-  for (int t = t0; t < t1; ++t) {{
-      {decode}
-      int kept = 0;
-      for (int kb = 0; kb < {count}; ++kb) {{
+  __shared__ int keep_n[{pt}], scan_k[{THREADS}];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int waves = {THREADS // 64};
+  for (int t = wave; t < {pt}; t += waves) {{
+    {decode}
+    int kept = 0;
+    for (int k0 = 0; k0 < {count}; k0 += 64) {{
+      const int kb = k0 + lane;
+      bool run = false;
+      if (kb < {count}) {{
         const int lv_{phase.var} = {phase.start} + kb * {phase.step};
-        kept += !({mask});
+        run = !({mask});
       }}
-      const int k = kept ? kept : 1;  // a tile with no block running takes one empty step
-      keep_n[t] = k;
-      drop_n[t] = {count} - k;
-      my_k += k;
-      my_d += {count} - k;
+      kept += __popcll(__ballot(run));
+    }}
+    if (lane == 0) keep_n[t] = kept ? kept : 1;  // a tile with no block running takes one empty step
   }}
-  scan_k[tid] = my_k;
-  scan_d[tid] = my_d;
   __syncthreads();
-  for (int s = 1; s < {THREADS}; s <<= 1) {{  // inclusive scan of the threads' totals
-    const int a = tid >= s ? scan_k[tid - s] : 0, b = tid >= s ? scan_d[tid - s] : 0;
+  // each thread sums a run of tiles; a block-wide inclusive scan of those sums
+  const int t0 = tid * {per}, t1 = ak_imin(t0 + {per}, {pt});
+  int my_k = 0;
+  for (int t = t0; t < t1; ++t) my_k += keep_n[t];
+  scan_k[tid] = my_k;
+  __syncthreads();
+  for (int s = 1; s < {THREADS}; s <<= 1) {{
+    const int a = tid >= s ? scan_k[tid - s] : 0;
     __syncthreads();
     scan_k[tid] += a;
-    scan_d[tid] += b;
     __syncthreads();
   }}
   const int total = scan_k[{THREADS - 1}];
-  int ok = scan_k[tid] - my_k, od = scan_d[tid] - my_d;
-  for (int t = t0; t < t1; ++t) {{
-      {decode}
-      args.rt_tile_steps[t] = ok;
-      int first = -1, last = -1;
-      for (int kb = 0; kb < {count}; ++kb) {{
+  // exclusive per-tile offsets of kept steps, in place over keep_n; tile t's dropped steps start t*count - that
+  {{
+    int ok = scan_k[tid] - my_k;
+    for (int t = t0; t < t1; ++t) {{ const int n = keep_n[t]; keep_n[t] = ok; ok += n; }}
+  }}
+  __syncthreads();
+  for (int t = wave; t < {pt}; t += waves) {{
+    {decode}
+    const int ok = keep_n[t], od = t * {count} - ok;
+    if (lane == 0) args.rt_tile_steps[t] = ok;
+    // first and last blocks that run
+    int first = -1, last = -1;
+    for (int k0 = 0; k0 < {count}; k0 += 64) {{
+      const int kb = k0 + lane;
+      bool run = false;
+      if (kb < {count}) {{
         const int lv_{phase.var} = {phase.start} + kb * {phase.step};
-        if (!({mask})) {{ if (first < 0) first = kb; last = kb; }}
+        run = !({mask});
       }}
-      const int empty = first < 0;
-      if (empty) {{ first = 0; last = 0; }}
-      int nk = 0, nd = 0;
-      for (int kb = 0; kb < {count}; ++kb) {{
+      const unsigned long long m = __ballot(run);
+      if (m) {{
+        if (first < 0) first = k0 + __ffsll((long long)m) - 1;
+        last = k0 + 63 - __clzll((long long)m);
+      }}
+    }}
+    const int empty = first < 0;
+    if (empty) {{ first = 0; last = 0; }}
+    int nk = 0, nd = 0;
+    for (int k0 = 0; k0 < {count}; k0 += 64) {{
+      const int kb = k0 + lane;
+      bool keep = false;
+      if (kb < {count}) {{
         const int lv_{phase.var} = {phase.start} + kb * {phase.step};
-        const int keep = empty ? (kb == 0) : !({mask});
+        keep = empty ? (kb == 0) : !({mask});
+      }}
+      const unsigned long long mk = __ballot(keep), md = __ballot(kb < {count} && !keep);
+      const unsigned long long below = (lane ? (~0ull >> (64 - lane)) : 0ull);
+      if (kb < {count}) {{
         const int code = ((kb * {radix}) << {CODE_SHIFT}) | ((empty && kb == 0) << 2) | ((kb == first) << 1) | (kb == last);
-        const int at = keep ? ok + nk++ : total + od + nd++;
+        const int at = keep ? ok + nk + __popcll(mk & below) : total + od + nd + __popcll(md & below);
         args.rt_step_tile[at] = t;
         args.rt_step_code[at] = code;
       }}
-      ok += keep_n[t];
-      od += drop_n[t];
+      nk += __popcll(mk);
+      nd += __popcll(md);
+    }}
   }}
   if (tid == 0) {{
     args.rt_count[0] = total;

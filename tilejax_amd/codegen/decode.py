@@ -12,13 +12,15 @@ through a runtime window (`k_pages[block_tables[b, p], :, :]`), runs the online 
 2. a setup kernel materialises each tile's query rows (the setup code's value, per element) in a
    workspace, so the attention kernel reads them as plain loads;
 3. the attention kernel splits the compacted step list evenly over one workgroup per CU (a sequence's
-   pages may span several workgroups, a workgroup several short sequences). Per step it streams the page's
-   K and V rows HBM -> LDS (`buffer_load_dwordx4 ... lds`, the next page in flight under this one's
-   compute); its four waves each take a quarter of the query rows' width, so S = Q K^T is four partial
-   products (`v_mfma_f32_16x16x32_bf16`) summed through LDS; every wave then runs the softmax on the full
-   scores and accumulates its quarter of `p @ V` (`v_mfma_f32_32x32x16_bf16`, V read transposed with
-   `ds_read_b64_tr_b16`). When a workgroup leaves a sequence it writes its partial (row max, row sum,
-   accumulator) to a workspace slot;
+   pages may span several workgroups, a workgroup several short sequences). It decodes its range's steps
+   (tile, code, page offsets) into LDS first, then streams pages with three in flight under each step's
+   compute: K fragments HBM -> registers (`buffer_load_dwordx4`, four register sets), V rows HBM -> LDS
+   (`buffer_load_dwordx4 ... lds`, four stages); only a tile change drains the queue. Its four waves each
+   take a quarter of the query rows' width, so S = Q K^T is four partial products
+   (`v_mfma_f32_16x16x32_bf16`) summed through LDS behind an LDS-only barrier; every wave then runs the
+   softmax on the full scores and accumulates its quarter of `p @ V` (`v_mfma_f32_32x32x16_bf16`, V read
+   transposed with `ds_read_b64_tr_b16`). When a workgroup leaves a sequence it writes its partial (row
+   max, row sum, accumulator) to a workspace slot;
 4. a merge kernel per sequence rescales and sums its partials (the online softmax's own merge rule:
    exact reassociation of the same sums) and evaluates the epilogue per output element.
 """
@@ -48,6 +50,7 @@ __all__ = ["DecodeMatch", "match", "lower"]
 
 THREADS = 256
 WAVES = 4
+DEPTH = 3  # K register sets and V LDS stages: pages fetched ahead of the step being computed
 
 
 @dataclass
@@ -114,6 +117,11 @@ class _Decode:
             raise KernelError("decode with parallel loops the runtime mask doesn't read is not lowered yet")
         self.grid = gfx950.CUS
         self.slots = self.grid + sch.pattern_tiles
+        self.max_per = -(-sch.pattern_steps // self.grid)  # most steps one workgroup takes
+        self.lds = DEPTH * m.page * m.width * 2 + WAVES * m.page * m.rows * 4 + 16 * self.max_per
+        if self.lds > gfx950.LDS_BYTES:
+            raise KernelError(f"decode over {sch.pattern_steps} pattern steps of {m.page} x {m.width} needs "
+                              f"{self.lds} bytes of LDS per workgroup (gfx950 has {gfx950.LDS_BYTES})")
         self.phase = plan.phases[0].range
         if (self.phase.count + 1) * m.rows * 4 > 96 * 1024:
             raise KernelError("too many pages per sequence for the merge kernel's LDS")
@@ -143,7 +151,7 @@ class _Decode:
                 ix = plan.index(n.kwargs["array"])
                 flat = " + ".join(f"({em.at(i, ()) if isinstance(i, Node) else literal(i)}) * {s}"
                                   for i, s in zip(n.args, strides(ix.shape))) or "0"
-                return f"args.{ix.name}[{flat}]"
+                return f"ak_ldc(args.{ix.name}, {flat})"
             if n.op == "carried" and n.kwargs["name"] in consts:
                 return em.at(self.seg0.values[n.kwargs["name"]].node, idx)
             if n.op == "load":
@@ -190,14 +198,14 @@ class _Decode:
                       Launch(self.name, args, (self.grid, 1, 1), (THREADS, 1, 1), 0),
                       Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (THREADS, 1, 1), 0)],
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
-            tables=tables, workspace=workspace, lds_bytes=2 * 2 * m.page * W * 2 + WAVES * m.page * R * 4,
+            tables=tables, workspace=workspace, lds_bytes=self.lds,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page},
         )
         attach_step_builder(prog, plan, sch, self.name)
         return prog
 
     def _decode_tile(self, t: str) -> str:
-        return " ".join(f"const int lv_{r.var} = args.tv_{r.var}[{t}];" for r in self.sch.inner)
+        return " ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, {t});" for r in self.sch.inner)
 
     def _setup_source(self) -> str:
         m = self.m
@@ -224,7 +232,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
         WQ = W // WAVES  # a wave's share of the width
         slabs = WQ // 32  # K = 32 slabs of S^T = K Q^T per wave
         dtiles = WQ // 32  # 32-wide tiles of acc^T per wave
-        loads = P * W // 8 // THREADS  # 16-byte loads per thread per operand per step
+        loads = P * W // 8 // THREADS  # 16-byte V loads per thread per step
+        D = DEPTH
         phase, index = self.phase, self.index
         radix = sch.phase_radix * sch.iterations
         jvar = phase.var
@@ -249,39 +258,46 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
         rows_per_load = THREADS // chunks
         L: List[str] = []
         w = L.append
-        for s in range(2):
-            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sk{s}[{P * W}];")
+        for s in range(D):  # one array per stage: the compiler then keeps the other stages' loads in flight
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sv{s}[{P * W}];")
         w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{P}][{R}];")
+        w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][4];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int count = args.rt_count[0];
   const int per = (count + {self.grid - 1}) / {self.grid};
-  const int g0 = blockIdx.x * per, g1 = ak_imin(g0 + per, count);
-  if (g0 >= g1) return;
+  const int g0 = blockIdx.x * per, n = ak_imin(g0 + per, count) - g0;
+  if (n <= 0) return;
+  // The range's steps, decoded once into LDS: tile, code, K and V page byte offsets. The loop then reads
+  // them from LDS, so no global load other than the pages themselves sits in the vector memory queue.
+  for (int j = tid; j < n; j += {THREADS}) {{
+    const int t = args.rt_step_tile[g0 + j], code = args.rt_step_code[g0 + j];
+    {self._decode_tile("t")}
+    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step};
+    dc_st[j][0] = t;
+    dc_st[j][1] = code;
+    dc_st[j][2] = (int)(({k_base}) * 2);
+    dc_st[j][3] = (int)(({v_base}) * 2);
+  }}
+  __syncthreads();
   const int cb = wave * {WQ};  // this wave's columns of the width
   const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)args.{m.k.tile.array}, (short)0,
       (int)({math.prod(k_shape)}LL * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)args.{m.v.tile.array}, (short)0,
       (int)({math.prod(v_shape)}LL * 2), 0x00020000);
-  // Loads: LDS chunk position p = c * {THREADS} + tid: row p / {chunks}, chunk p % {chunks}; K rows swizzled
-  // for ds_read_b128 (chunk ^ row & 15), V rows for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2).
-  unsigned k_voff[{loads}], v_voff[{loads}];
+  // V loads: LDS chunk position p = c * {THREADS} + tid: row p / {chunks}, chunk p % {chunks}, rows swizzled
+  // for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2).
+  unsigned v_voff[{loads}];
 #pragma unroll
   for (int c = 0; c < {loads}; ++c) {{
     const int row = c * {rows_per_load} + tid / {chunks}, ch = tid % {chunks};
-    k_voff[c] = (unsigned)(row * {ldk * 2} + ((ch ^ (row & 15)) * 16));
     v_voff[c] = (unsigned)(row * {ldv * 2} + ((ch ^ ((row & 3) << 2)) * 16));
   }}
-  // K fragment (srcA of S^T, 16x16x32): position lane % 16, columns cb + 32 s + 8 (lane / 16)
-  int k_roff[{slabs}];
-#pragma unroll
-  for (int s = 0; s < {slabs}; ++s) {{
-    const int pos = lane & 15, ch = (cb + 32 * s + 8 * (lane >> 4)) >> 3;
-    k_roff[s] = pos * {W * 2} + ((ch ^ pos) << 4);
-  }}
+  // K fragments (srcA of S^T, 16x16x32) straight from HBM into registers: position lane % 16, columns
+  // cb + 32 s + 8 (lane / 16)
+  const unsigned k_voff = (unsigned)((lane & 15) * {ldk * 2} + (cb + 8 * (lane >> 4)) * 2);
   // V^T fragment (srcA of acc^T, 32x32x16), tr16 reads: group G = lane / 16, s = lane % 16
   int v_roff[{dtiles}];
   {{
@@ -293,6 +309,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     }}
   }}
   ak_bf16x8 qf[2][{slabs}];
+  {" ".join(f"ak_bf16x8 kb{s}[{slabs}];" for s in range(D))}
   ak_f32x16 acc[{dtiles}];
   float m_run = {literal(m.sm.m_init)}, l_run = 0.f;
   int cur_t = -1;
@@ -324,51 +341,66 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     m_run = {literal(m.sm.m_init)};
     l_run = 0.f;
   }};""")
+        # Issue order, one group per arrow: ... -> V(j + D - 1) -> K(j + D) -> ... (step j issues the V page
+        # D - 1 steps ahead after its first barrier and the K fragments D steps ahead once its S product has
+        # read kb). Steps past the range issue the same loads out of the buffers' bounds (offset + 2^31: no
+        # memory access, zeros), so every step adds the same count and one wait count fits every step: K(j)
+        # and V(j) are done once the groups after V(j) (K(j+1) .. K(j+D-1)) alone are outstanding.
+        wait_n = (D - 1) * slabs + (D - 2) * loads
 
-        def issue(g: str, s: int, ind: str) -> List[str]:
+        def issue_k(x: str, ks: int, ind: str) -> List[str]:
             return [
-                f"{ind}{{ const int t_ = args.rt_step_tile[{g}], code_ = args.rt_step_code[{g}];",
-                f"{ind}  if (!(code_ & 4)) {{",
-                f"{ind}    {self._decode_tile('t_')}",
-                f"{ind}    const int lv_{jvar} = {phase.start} + ((code_ >> {CODE_SHIFT}) / {radix}) * {phase.step};",
-                f"{ind}    const unsigned ko = (unsigned)(({k_base}) * 2), vo = (unsigned)(({v_base}) * 2);",
-                *(f"{ind}    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)"
-                  f"&dc_sk{s}[({c * THREADS} + wave * 64) * 8], 16, k_voff[{c}], ko, 0, 0);" for c in range(loads)),
-                *(f"{ind}    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)"
-                  f"&dc_sv{s}[({c * THREADS} + wave * 64) * 8], 16, v_voff[{c}], vo, 0, 0);" for c in range(loads)),
-                f"{ind}  }}",
+                f"{ind}{{ const int x_ = {x}; const unsigned ob_ = x_ < n ? 0u : 0x80000000u;",
+                f"{ind}  const int ko_ = __builtin_amdgcn_readfirstlane(dc_st[ak_imin(x_, n - 1)][2]);",
+                *(f"{ind}  kb{ks}[{q}] = __builtin_bit_cast(ak_bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, k_voff + ob_ + {64 * q}, ko_, 0));"
+                  for q in range(slabs)),
                 f"{ind}}}",
             ]
 
-        def step(g: str, s: int, ind: str) -> List[str]:
+        def issue_v(x: str, vs: int, ind: str) -> List[str]:
+            return [
+                f"{ind}{{ const int x_ = {x}; const unsigned ob_ = x_ < n ? 0u : 0x80000000u;",
+                f"{ind}  const int vo_ = __builtin_amdgcn_readfirstlane(dc_st[ak_imin(x_, n - 1)][3]);",
+                *(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, AK_LDS(&dc_sv{vs}[({c * THREADS} + wave * 64) * 8]), 16, "
+                  f"v_voff[{c}] + ob_, vo_, 0, 0);" for c in range(loads)),
+                f"{ind}}}",
+            ]
+
+        def step(j: str, u: int, ind: str) -> List[str]:
+            """Step j (= u modulo D): its K fragments in kb{u}, its V page in dc_sv{u}."""
             o: List[str] = []
             a = o.append
-            a(f"{ind}{{ const int g_ = {g};")
-            a(f"{ind}  const int t = args.rt_step_tile[g_], code = args.rt_step_code[g_];")
-            a(f"{ind}  if (t != cur_t) {{ if (cur_t >= 0) flush(cur_t); start_tile(t); cur_t = t; }}")
-            a(f"{ind}  __builtin_amdgcn_s_waitcnt(0);")
+            a(f"{ind}{{ const int j_ = {j};")
+            a(f"{ind}  const int t = __builtin_amdgcn_readfirstlane(dc_st[j_][0]), code = __builtin_amdgcn_readfirstlane(dc_st[j_][1]);")
+            a(f"{ind}  if (t != cur_t) {{ if (cur_t >= 0) flush(cur_t); start_tile(t); cur_t = t; AK_WAIT_VM(0); }}")
+            a(f"{ind}  AK_WAIT_VM({wait_n});")
+            # every wave is past step j - 1, so its V stage is free; every thread's part of V(j) has landed
             a(f'{ind}  asm volatile("s_barrier" ::: "memory");')
-            a(f"{ind}  if (g_ + 1 < g1) {{")
-            o.extend(issue("g_ + 1", 1 - s, ind + "    "))
-            a(f"{ind}  }}")
-            a(f"{ind}  if (!(code & 4)) {{")
-            a(f"{ind}    {self._decode_tile('t')}")
-            a(f"{ind}    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step}; (void)lv_{jvar};")
-            a(f"{ind}    const char* ks = (const char*)dc_sk{s}; const char* vs = (const char*)dc_sv{s};")
+            o.extend(issue_v(f"j_ + {D - 1}", (u + D - 1) % D, ind + "  "))
+            a(f"{ind}  const bool run = !(code & 4);")
             # partial S^T over this wave's columns
+            a(f"{ind}  if (run) {{")
             a(f"{ind}    ak_f32x4 st[2] = {{ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}}};")
             a(f"{ind}    #pragma unroll")
-            a(f"{ind}    for (int s = 0; s < {slabs}; ++s) {{")
-            a(f"{ind}      const ak_bf16x8 kf = *(const ak_bf16x8*)(ks + k_roff[s]);")
-            a(f"{ind}      st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[0][s], st[0], 0, 0, 0);")
-            a(f"{ind}      st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[1][s], st[1], 0, 0, 0);")
+            a(f"{ind}    for (int q = 0; q < {slabs}; ++q) {{")
+            a(f"{ind}      st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb{u}[q], qf[0][q], st[0], 0, 0, 0);")
+            a(f"{ind}      st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb{u}[q], qf[1][q], st[1], 0, 0, 0);")
             a(f"{ind}    }}")
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int r = 0; r < 4; ++r) {{")
             a(f"{ind}      dc_sp[wave][4 * (lane >> 4) + r][lane & 15] = st[0][r];")
             a(f"{ind}      dc_sp[wave][4 * (lane >> 4) + r][16 + (lane & 15)] = st[1][r];")
             a(f"{ind}    }}")
-            a(f'{ind}    __syncthreads();')
+            a(f"{ind}  }}")
+            # kb{u} has been read: refill it D steps ahead
+            o.extend(issue_k(f"j_ + {D}", u, ind + "  "))
+            a(f"{ind}  if (run) {{")
+            a(f"{ind}    {self._decode_tile('t')}")
+            a(f"{ind}    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step}; (void)lv_{jvar};")
+            a(f"{ind}    const char* vs = (const char*)dc_sv{u};")
+            # an LDS-only barrier: the pages in flight stay in flight
+            a(f"{ind}    AK_WAIT_LGKM0();")
+            a(f'{ind}    asm volatile("s_barrier" ::: "memory");')
             # softmax: lane = query row er, positions 8 (lane / 32) + e
             a(f"{ind}    const int er = lane & 31;")
             a(f"{ind}    float sc[8];")
@@ -397,23 +429,34 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int dt = 0; dt < {dtiles}; ++dt) {{")
             a(f"{ind}      acc[dt] *= alpha;")
-            a(f"{ind}      ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) ak_i16x4*)(vs + v_roff[dt]));")
-            a(f"{ind}      ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) ak_i16x4*)(vs + v_roff[dt] + {4 * W * 2}));")
+            a(f"{ind}      ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt]));")
+            a(f"{ind}      ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt] + {4 * W * 2}));")
             a(f"{ind}      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pf, acc[dt], 0, 0, 0);")
             a(f"{ind}    }}")
             a(f"{ind}  }}")
             a(f"{ind}}}")
             return o
 
-        w("  {")
-        L.extend(issue("g0", 0, "    "))
+        # prologue: what steps -D .. -1 would have issued: K(0), then V(x) and K(x + 1) for x < D - 1
+        L.extend(issue_k("0", 0, "  "))
+        for x in range(D - 1):
+            L.extend(issue_v(str(x), x, "  "))
+            L.extend(issue_k(str(x + 1), x + 1, "  "))
+        # whole rounds of D steps with no condition between them (the compiler's wait counts stay exact),
+        # then the last steps; no wait drains the queue except at a tile change
+        w("  int j = 0;")
+        w(f"  for (; j + {D} <= n; j += {D}) {{")
+        for u in range(D):
+            L.extend(step(f"j + {u}", u, "    "))
         w("  }")
-        w("  for (int g = g0; g < g1; g += 2) {")
-        L.extend(step("g", 0, "    "))
-        w("    if (g + 1 < g1) {")
-        L.extend(step("g + 1", 1, "      "))
-        w("    }")
-        w("  }")
+        ind = "  "
+        for u in range(D - 1):
+            w(f"{ind}if (j + {u} < n) {{")
+            L.extend(step(f"j + {u}", u, ind + "  "))
+            ind += "  "
+        for u in range(D - 1):
+            ind = ind[:-2]
+            w(f"{ind}}}")
         w("  flush(cur_t);")
         w("}")
         return "\n".join(L)

@@ -16,10 +16,21 @@ typedef short ak_i16x4 __attribute__((ext_vector_type(4)));
 
 #define AK_INLINE __device__ __forceinline__
 
+// s_waitcnt with only vmcnt (<= n vector memory ops outstanding) or only lgkmcnt (0) waited for; gfx9's
+// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8.
+#define AK_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define AK_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4))
+#define AK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+#define AK_LDS4(p) ((__attribute__((address_space(3))) ak_i16x4*)(p))
+
 // Python's floor division and modulo on ints.
 AK_INLINE int ak_floordiv(int a, int b) { int q = a / b; return (q * b != a && ((a < 0) != (b < 0))) ? q - 1 : q; }
 AK_INLINE int ak_floormod(int a, int b) { int r = a % b; return (r != 0 && ((r < 0) != (b < 0))) ? r + b : r; }
 AK_INLINE int ak_imin(int a, int b) { return a < b ? a : b; }
+// A read of memory no kernel writes while this one runs (tables, index inputs) through the constant
+// address space: where the address is uniform the compiler makes it a scalar load, which leaves the vector
+// memory queue (and its in-order wait counts) to the data streams.
+template <typename T> AK_INLINE T ak_ldc(const T* p, long long i) { return ((const __attribute__((address_space(4))) T*)p)[i]; }
 AK_INLINE int ak_imax(int a, int b) { return a > b ? a : b; }
 AK_INLINE int ak_clamp(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 

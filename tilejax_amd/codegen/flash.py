@@ -501,11 +501,7 @@ class _Flash:
         w(f"""// Generated by tilejax_amd for `{plan.nest.name}`: a gfx950 flash-attention kernel.
 // spec tile {m.rows} x {m.bk} (head dims {D}, {DV}); workgroup {bq} query rows in {nw} waves, key blocks of {bkv}.
 {PRELUDE}
-{struct}
-#define AK_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
-#define AK_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4))
-#define AK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-#define AK_LDS4(p) ((__attribute__((address_space(3))) ak_i16x4*)(p))""")
+{struct}""")
         for s in range(2):
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")

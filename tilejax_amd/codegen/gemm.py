@@ -449,11 +449,7 @@ class _Gemm:
 // spec tile {m.tm} x {m.tn} x {m.tk}; workgroup tile {bm} x {bn}, K slices of {bk} through {S} LDS stages;
 // {sch.tiles} tiles of {sch.total_tiles} ({sch.fills} filled), {sch.steps} steps.
 {PRELUDE}
-{struct}
-#define AK_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
-#define AK_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4))
-#define AK_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-#define AK_LDS4(p) ((__attribute__((address_space(3))) ak_i16x4*)(p))""")
+{struct}""")
         for s in range(S):  # one array per stage and operand: the compiler then keeps prefetches in flight
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sa{s}[{bm * bk}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sb{s}[{bn * bk}];")

@@ -48,7 +48,7 @@ class Program:
     outputs: List[Tuple[Tuple[int, ...], jaxlite.DType]]
     inputs: List[Tuple[Tuple[int, ...], jaxlite.DType]]
     tables: Dict[str, np.ndarray] = field(default_factory=dict)
-    workspace: Dict[str, int] = field(default_factory=dict)  # name -> bytes (zeroed before the launches)
+    workspace: Dict[str, int] = field(default_factory=dict)  # name -> bytes (uninitialised: launches write before reading)
     lds_bytes: int = 0
     notes: Dict[str, Any] = field(default_factory=dict)  # what the lowering chose (hardware tiles, ...)
     _modules: Dict[int, runtime.Module] = field(default_factory=dict, repr=False)
@@ -102,7 +102,7 @@ class Program:
         if outputs is None:
             outputs = [torch.empty(shape, dtype=dt.torch, device=device) for shape, dt in self.outputs]
         tables = self.device_tables(device)
-        workspace = {name: torch.zeros(max(n, 4), dtype=torch.uint8, device=device) for name, n in self.workspace.items()}
+        workspace = {name: torch.empty(max(n, 4), dtype=torch.uint8, device=device) for name, n in self.workspace.items()}
         module = self.module(device.index or 0)
         stream = runtime.current_stream() if stream is None else stream
         for launch in launches:

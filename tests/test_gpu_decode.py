@@ -66,6 +66,25 @@ def test_decode_step_tables_are_bit_exact():
     np.testing.assert_array_equal(got["step_code"].cpu().numpy(), step_code)
 
 
+def test_decode_step_tables_ragged_words():
+    """100 pages per sequence: two mask words per tile, the second partial; an empty sequence, a full one,
+    and lengths either side of a word boundary (64 pages = 1024 positions)."""
+    lengths = (0, 5, 1600, 1023, 1025)
+    ins = _inputs(5, 32, 8, 128, 16, 100, lengths, seed=4)
+    print(f"decode step tables lengths={lengths}", flush=True)
+    lowered = paged_gqa_decode.lower(*ins)
+    got = lowered.program.step_tables(*(t.cuda() for t in ins))
+    step_tile, step_code, count = oracle_schedule.runtime_tables(
+        [{"b": b} for b in range(5)], [("p", 0, 1, 100, lambda v: v["p"] * 16 >= lengths[v["b"]])])
+    assert int(got["count"][0]) == count == 1 + 1 + 100 + 64 + 65
+    np.testing.assert_array_equal(got["step_tile"].cpu().numpy(), step_tile)
+    np.testing.assert_array_equal(got["step_code"].cpu().numpy(), step_code)
+    tile_steps = got["tile_steps"].cpu().numpy()
+    np.testing.assert_array_equal(tile_steps, np.cumsum([0, 1, 1, 100, 64, 65]))
+    out = paged_gqa_decode(*(t.cuda() for t in ins))
+    _close(out, kernels.paged_gqa_decode(*ins))
+
+
 def test_baseline_config_sampled():
     """64 sequences, 32 q heads / 8 kv heads, head dim 128, 16-token pages, a seeded
     random page table over 32768 pages, lengths uniform in [128, 8192]; sequences checked against a float32

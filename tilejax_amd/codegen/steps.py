@@ -7,9 +7,9 @@ none of whose blocks run keeps one empty step at block 0; each step gets its cod
 moved to the front in (t, kb) order and the rest follow in order (a stable partition); the count of kept
 steps is the third output.
 
-Here it is one workgroup of 1024 threads, generated from the mask expression: each wave evaluates one tile's
-masks 64 blocks per ballot, a block-wide scan turns the tiles' kept counts into offsets, and each wave writes
-its tiles' entries at ballot-prefix positions. Besides the reference's three outputs it writes `tile_steps`,
+Here it is one workgroup of 1024 threads, generated from the mask expression: the waves evaluate the masks
+64 blocks per ballot into words kept in LDS, a block-wide scan turns the tiles' kept counts into offsets, and
+each wave writes one word's entries at ballot-prefix positions. Besides the reference's three outputs it writes `tile_steps`,
 each pattern tile's first kept step (and the total at the end), which the kernels use to find a tile's steps
 without a search.
 """
@@ -28,7 +28,8 @@ from .expr import int_expr
 from .program import Arg, Launch, Program, c_struct
 
 THREADS = 1024
-MAX_TILES = 8192
+MAX_TILES = 4096
+MAX_WORDS = 4096  # 64-block mask words kept in LDS (32 KiB)
 
 
 def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg]) -> str:
@@ -43,31 +44,60 @@ def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg]) -> str
     index = Index(plan, lambda v: f"lv_{v}")
     mask = index.expr(phase.mask)
     radix = sch.phase_radix * sch.iterations
-    decode = "\n      ".join(f"const int lv_{r.var} = args.tv_{r.var}[t];" for r in sch.inner)
+    decode = " ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, t);" for r in sch.inner)
     struct = c_struct(f"{name}_args", args)
     per = (pt + THREADS - 1) // THREADS
+    nb = -(-count // 64)  # 64-block words per tile
+    words = pt * nb
+    if words > MAX_WORDS:
+        raise KernelError(f"runtime step tables for {pt} tiles x {count} blocks: the builder takes at most "
+                          f"{MAX_WORDS * 64} (tile, block) pairs")
+    waves = THREADS // 64
+    rounds = -(-pt // waves)
     return f"""
 {struct}
-// Step tables for `{plan.nest.name}`: {pt} pattern tiles x {count} blocks of `{phase.var}`. One wave per tile at
-// a time: the mask of 64 blocks per ballot, kept/dropped counts by popcount, then a block-wide scan of the
-// tiles' counts, then each wave writes its tiles' entries at ballot-prefix positions.
+// Step tables for `{plan.nest.name}`: {pt} pattern tiles x {count} blocks of `{phase.var}`, as {words} words of
+// 64 blocks. Pass 1: each wave evaluates one tile's words per round (a ballot each; the tile's loads are
+// made once), two rounds' loads in flight together. Then per-tile kept counts, a block-wide scan of them,
+// and pass 2: each wave writes one word's entries at ballot-prefix positions, from the words alone.
 extern "C" __global__ void __launch_bounds__({THREADS}) {name}(const {name}_args args) {{
-  __shared__ int keep_n[{pt}], scan_k[{THREADS}];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int waves = {THREADS // 64};
-  for (int t = wave; t < {pt}; t += waves) {{
-    {decode}
-    int kept = 0;
-    for (int k0 = 0; k0 < {count}; k0 += 64) {{
-      const int kb = k0 + lane;
-      bool run = false;
-      if (kb < {count}) {{
-        const int lv_{phase.var} = {phase.start} + kb * {phase.step};
-        run = !({mask});
+  __shared__ unsigned long long run_w[{words}];
+  __shared__ int before_w[{words}], keep_n[{pt}], first_t[{pt}], last_t[{pt}], scan_k[{THREADS}];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll 2
+  for (int i = 0; i < {rounds}; ++i) {{
+    const int t = wave + {waves} * i;
+    if (t < {pt}) {{
+      {decode}
+      for (int wi = 0; wi < {nb}; ++wi) {{
+        const int kb = wi * 64 + lane;
+        bool run = false;
+        if (kb < {count}) {{
+          const int lv_{phase.var} = {phase.start} + kb * {phase.step};
+          run = !({mask});
+        }}
+        const unsigned long long m = __ballot(run);
+        if (lane == 0) run_w[t * {nb} + wi] = m;
       }}
-      kept += __popcll(__ballot(run));
     }}
-    if (lane == 0) keep_n[t] = kept ? kept : 1;  // a tile with no block running takes one empty step
+  }}
+  __syncthreads();
+  // per tile: running blocks before each word, the first and last running block, the kept count
+  for (int t = tid; t < {pt}; t += {THREADS}) {{
+    int kept = 0, first = -1, last = -1;
+    for (int i = 0; i < {nb}; ++i) {{
+      const unsigned long long m = run_w[t * {nb} + i];
+      before_w[t * {nb} + i] = kept;
+      if (m) {{
+        if (first < 0) first = i * 64 + __ffsll((long long)m) - 1;
+        last = i * 64 + 63 - __clzll((long long)m);
+      }}
+      kept += __popcll(m);
+    }}
+    keep_n[t] = kept ? kept : 1;  // a tile with no block running takes one empty step
+    first_t[t] = first;
+    last_t[t] = last;
   }}
   __syncthreads();
   // each thread sums a run of tiles; a block-wide inclusive scan of those sums
@@ -89,45 +119,26 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {name}(const {name}_args
     for (int t = t0; t < t1; ++t) {{ const int n = keep_n[t]; keep_n[t] = ok; ok += n; }}
   }}
   __syncthreads();
-  for (int t = wave; t < {pt}; t += waves) {{
-    {decode}
-    const int ok = keep_n[t], od = t * {count} - ok;
-    if (lane == 0) args.rt_tile_steps[t] = ok;
-    // first and last blocks that run
-    int first = -1, last = -1;
-    for (int k0 = 0; k0 < {count}; k0 += 64) {{
-      const int kb = k0 + lane;
-      bool run = false;
-      if (kb < {count}) {{
-        const int lv_{phase.var} = {phase.start} + kb * {phase.step};
-        run = !({mask});
-      }}
-      const unsigned long long m = __ballot(run);
-      if (m) {{
-        if (first < 0) first = k0 + __ffsll((long long)m) - 1;
-        last = k0 + 63 - __clzll((long long)m);
-      }}
-    }}
+  const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+#pragma unroll 4
+  for (int i = 0; i < {-(-words // waves)}; ++i) {{
+    const int w = wave + {waves} * i;
+    if (w >= {words}) break;
+    const int t = w / {nb}, wi = w % {nb}, k0 = wi * 64, kb = k0 + lane;
+    int first = first_t[t], last = last_t[t], before = before_w[w];
     const int empty = first < 0;
-    if (empty) {{ first = 0; last = 0; }}
-    int nk = 0, nd = 0;
-    for (int k0 = 0; k0 < {count}; k0 += 64) {{
-      const int kb = k0 + lane;
-      bool keep = false;
-      if (kb < {count}) {{
-        const int lv_{phase.var} = {phase.start} + kb * {phase.step};
-        keep = empty ? (kb == 0) : !({mask});
-      }}
-      const unsigned long long mk = __ballot(keep), md = __ballot(kb < {count} && !keep);
-      const unsigned long long below = (lane ? (~0ull >> (64 - lane)) : 0ull);
-      if (kb < {count}) {{
-        const int code = ((kb * {radix}) << {CODE_SHIFT}) | ((empty && kb == 0) << 2) | ((kb == first) << 1) | (kb == last);
-        const int at = keep ? ok + nk + __popcll(mk & below) : total + od + nd + __popcll(md & below);
-        args.rt_step_tile[at] = t;
-        args.rt_step_code[at] = code;
-      }}
-      nk += __popcll(mk);
-      nd += __popcll(md);
+    unsigned long long mk = run_w[w];
+    if (empty) {{ first = 0; last = 0; mk = wi == 0 ? 1ull : 0ull; before = k0 > 0; }}
+    const unsigned long long valid = {count} - k0 >= 64 ? ~0ull : ((1ull << ({count} - k0)) - 1);
+    const unsigned long long md = valid & ~mk;
+    const int ok = keep_n[t] + before, od = t * {count} - keep_n[t] + (k0 - before);
+    if (wi == 0 && lane == 0) args.rt_tile_steps[t] = keep_n[t];
+    if (kb < {count}) {{
+      const bool keep = (mk >> lane) & 1;
+      const int code = ((kb * {radix}) << {CODE_SHIFT}) | ((empty && kb == 0) << 2) | ((kb == first) << 1) | (kb == last);
+      const int at = keep ? ok + __popcll(mk & below) : total + od + __popcll(md & below);
+      args.rt_step_tile[at] = t;
+      args.rt_step_code[at] = code;
     }}
   }}
   if (tid == 0) {{

@@ -48,7 +48,7 @@ def standard() -> Iterator[Tuple[object, tuple]]:
         yield moe.grouped_matmul, (_bf16(m, k), _bf16(e, k, n), _i32(g), tiles)
     from examples import decode
 
-    for b, pages, n_pages in ((4, 64, 256), (64, 512, 32768)):
+    for b, pages, n_pages in ((4, 64, 256), (5, 100, 500), (64, 512, 32768)):
         yield decode.paged_gqa_decode, (_bf16(b, 1, 32, 128), _bf16(n_pages, 16, 1024), _bf16(n_pages, 16, 1024),
                                         _i32(b, pages), _i32(b))
     try:

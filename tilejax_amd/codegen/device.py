@@ -34,16 +34,15 @@ template <typename T> AK_INLINE T ak_ldc(const T* p, long long i) { return ((con
 AK_INLINE int ak_imax(int a, int b) { return a > b ? a : b; }
 AK_INLINE int ak_clamp(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
-// bf16 <-> f32. Rounding is to nearest, ties to even; NaN stays NaN.
-AK_INLINE unsigned ak_bf16_bits(float x) {
-  unsigned u = __builtin_bit_cast(unsigned, x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+// bf16 <-> f32. Rounding is to nearest, ties to even (gfx950's v_cvt_pk_bf16_f32); NaN stays NaN.
+typedef __bf16 ak_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float ak_f32x2 __attribute__((ext_vector_type(2)));
+AK_INLINE unsigned ak_pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector((ak_f32x2){lo, hi}, ak_bf16x2));
 }
+AK_INLINE unsigned ak_bf16_bits(float x) { return ak_pack_bf16x2(x, 0.0f) & 0xffffu; }
 AK_INLINE float ak_round_bf16(float x) { return __builtin_bit_cast(float, ak_bf16_bits(x) << 16); }
 AK_INLINE float ak_bf16_to_f32(unsigned short b) { return __builtin_bit_cast(float, (unsigned)b << 16); }
-AK_INLINE unsigned ak_pack_bf16x2(float lo, float hi) { return ak_bf16_bits(lo) | (ak_bf16_bits(hi) << 16); }
 AK_INLINE float ak_round_f16(float x) { return (float)(_Float16)x; }
 
 // Elementwise functions with the tile code's meaning.

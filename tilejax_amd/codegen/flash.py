@@ -50,6 +50,8 @@ from .program import Arg, Launch, Program, c_struct
 
 __all__ = ["FlashMatch", "match", "lower"]
 
+LOG2E = 1.4426950408889634
+RESCALE_SLACK = 8.0  # natural-log units: p stays below e^8 between rescales
 MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 once a row has a real score
 
 
@@ -510,8 +512,8 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int* item = args.fa_items + blockIdx.x * {stride};
-  const int t = item[0], sub = item[1], boff = item[2], nblk = item[3];
-  const int f_w = item[4 + 2 * wave], n_w = item[5 + 2 * wave];
+  const int t = ak_ldc(item, 0), sub = ak_ldc(item, 1), boff = ak_ldc(item, 2), nblk = ak_ldc(item, 3);
+  const int f_w = ak_ldc(item, 4 + 2 * wave), n_w = ak_ldc(item, 5 + 2 * wave);
   {tile_decode}
   const int er = sub * {bq} + wave * 32 + (lane & 31);   // this lane's query row in the spec tile
   // Q^T fragments (srcB of S^T = K Q^T): row er, head dims 16 s + 8 (lane / 32) .. + 8
@@ -555,7 +557,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
 
         def issue(b: str, s: int, ind: str) -> List[str]:
             out = [f"{ind}{{ const int* bp = args.fa_blocks + 2 * (boff + ({b}));",
-                   f"{ind}  const int kpos = bp[0] + {self.kwin.offset} + bp[1], vpos = bp[0] + {self.vwin.offset} + bp[1];"]
+                   f"{ind}  const int kpos = ak_ldc(bp, 0) + {self.kwin.offset} + ak_ldc(bp, 1), vpos = ak_ldc(bp, 0) + {self.vwin.offset} + ak_ldc(bp, 1);"]
             rows_k, rows_v = T // chk, T // chv
             for c in range(ldk_n):
                 out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, AK_LDS(&ak_sk{s}[({c * T} + wave * 64) * 8]), 16, k_voff, "
@@ -571,7 +573,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             a = o.append
             a(f"{ind}if (b_ < n_w) {{")
             a(f"{ind}  const char* ks = (const char*)ak_sk{s}; const char* vs = (const char*)ak_sv{s};")
-            a(f"{ind}  const int lv_{jvar} = args.fa_blocks[2 * (boff + b_)], ec0 = args.fa_blocks[2 * (boff + b_) + 1] + (lane >> 5) * 4;")
+            a(f"{ind}  const int lv_{jvar} = ak_ldc(args.fa_blocks, 2 * (boff + b_)), ec0 = ak_ldc(args.fa_blocks, 2 * (boff + b_) + 1) + (lane >> 5) * 4;")
             a(f"{ind}  ak_f32x16 st[{kt}];")
             for t in range(kt):
                 a(f"{ind}  #pragma unroll")
@@ -596,7 +598,18 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             a(f"{ind}  }}")
             a(f"{ind}  mx = fmaxf(mx, __shfl_xor(mx, 32));")
             a(f"{ind}  const float m_new = ak_maximum(m_run, mx);")
-            a(f"{ind}  const float alpha = ak_exp(m_run - m_new);")
+            # Lazy rescaling: the running max moves (and acc, l are rescaled) only when some row's new max
+            # exceeds it by more than RESCALE_SLACK; otherwise p = exp(s - m_run) stays below e^slack and
+            # acc, l keep one common scale, so acc / l is unchanged.
+            a(f"{ind}  if (__ballot(!(m_new <= m_run + {RESCALE_SLACK}f))) {{")
+            a(f"{ind}    const float alpha = ak_exp(m_run - m_new);")
+            a(f"{ind}    l_run *= alpha;")
+            a(f"{ind}    m_run = m_new;")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int i = 0; i < {dt_n}; ++i) acc[i] *= alpha;")
+            a(f"{ind}  }}")
+            # p = exp(s - m) as one fma and v_exp_f32 (2^x)
+            a(f"{ind}  const float mb = -m_run * {LOG2E!r}f;")
             a(f"{ind}  float ps = 0.f;")
             a(f"{ind}  ak_bf16x8 pf[{ks}];")
             for t in range(kt):
@@ -604,14 +617,12 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                     a(f"{ind}  {{ unsigned pk[4];")
                     a(f"{ind}    #pragma unroll")
                     a(f"{ind}    for (int r = 0; r < 8; r += 2) {{")
-                    a(f"{ind}      const float p0 = ak_exp(st[{t}][{8 * half} + r] - m_new), p1 = ak_exp(st[{t}][{8 * half} + r + 1] - m_new);")
+                    a(f"{ind}      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[{t}][{8 * half} + r], {LOG2E!r}f, mb));")
+                    a(f"{ind}      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[{t}][{8 * half} + r + 1], {LOG2E!r}f, mb));")
                     a(f"{ind}      ps += p0 + p1; pk[r >> 1] = ak_pack_bf16x2(p0, p1); }}")
                     a(f"{ind}    pf[{2 * t + half}] = __builtin_bit_cast(ak_bf16x8, (ak_u32x4){{pk[0], pk[1], pk[2], pk[3]}}); }}")
             a(f"{ind}  ps += __shfl_xor(ps, 32);")
-            a(f"{ind}  l_run = alpha * l_run + ps;")
-            a(f"{ind}  m_run = m_new;")
-            a(f"{ind}  #pragma unroll")
-            a(f"{ind}  for (int i = 0; i < {dt_n}; ++i) acc[i] *= alpha;")
+            a(f"{ind}  l_run += ps;")
             for kk in range(ks):
                 for dt in range(dt_n):
                     o1 = kk * 16 * DV * 2

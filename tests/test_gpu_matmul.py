@@ -59,3 +59,46 @@ def test_matmul_verify_against_reference():
     x, y = _inputs(512, 256, 512, seed=5)
     err = matmul.verify(x.cuda(), y.cuda(), MatmulTiles(256, 256, 128))
     assert err < 1.0
+
+
+def test_causal_matmul_full_size_balanced_split():
+    """The 8192^3 causal matmul at 512^3 tiles: 528 computed 256x256 tiles on 256 workgroups, so 16 of them are
+    cut along K into 16 chunks whose partials a fixup kernel adds. Checked against the oracle everywhere."""
+    n, tiles = 8192, MatmulTiles(512, 512, 512)
+    x, y = _inputs(n, n, n, seed=7)
+    lowered = causal_matmul.lower(x, y, tiles)
+    assert lowered.program.notes["split"] == (16, 16, 8)
+    print(f"causal {n} {tiles} split {lowered.program.notes['split']}", flush=True)
+    got = lowered.run(x.cuda(), y.cuda())
+    torch.cuda.synchronize()
+    want = kernels.causal_matmul(x, y, tiles.tm, tiles.tn, tiles.tk)
+    _close(got, want)
+    assert not got.cpu().float().triu(1).any()
+
+
+def test_split_chunks_start_from_the_initial_value_once():
+    """A matmul nest whose accumulator starts at 1 and whose epilogue reads the tile's loop values: with 16
+    tiles on 256 workgroups each tile is cut into 4 chunks, and the fixup must add the start value once and
+    place every tile."""
+    from tests.helpers import make_kernel
+
+    k = make_kernel('''
+        def offset_matmul(x, y):
+            M, K = x.shape
+            N = y.shape[1]
+            out = jnp.zeros((M, N), jnp.float32)
+            for i in range(0, M, 256):
+                for j in range(0, N, 256):
+                    acc = jnp.full((256, 256), 1.0, jnp.float32)
+                    for kk in range(0, K, 512):
+                        acc += x[i : i + 256, kk : kk + 512] @ y[kk : kk + 512, j : j + 256]
+                    out = out.at[i : i + 256, j : j + 256].set(acc * 0.5 + (i + 2 * j))
+            return out
+    ''')
+    x, y = _inputs(1024, 2048, 1024, seed=11)
+    lowered = k.lower(x, y)
+    assert lowered.program.notes["split"] is not None
+    got = lowered.run(x.cuda(), y.cuda())
+    torch.cuda.synchronize()
+    want = k.reference(x, y)
+    assert torch.allclose(got.cpu(), want, rtol=1e-4, atol=1e-3), (got.cpu() - want).abs().max()

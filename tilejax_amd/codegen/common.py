@@ -119,40 +119,28 @@ def static_tile_steps(sch: Schedule) -> np.ndarray:
     return offsets
 
 
-def work_lists(items: List[Tuple[int, int]], weights: List[float], groups: List[int], grid: int) -> Tuple[np.ndarray, np.ndarray]:
-    """Spread work items over `grid` persistent workgroups: workgroup w runs on XCD w % 8, so items of one
-    locality group (`groups`, e.g. a band of output columns) go to the workgroups of one XCD, where they
-    share its L2; within an XCD, longest-first onto the least loaded workgroup. Returns (offsets[grid + 1],
-    items[n, 2]) with each workgroup's items contiguous, in the order it runs them."""
+def work_lists(items: List[Tuple[int, ...]], weights: List[float], groups: List[int], grid: int) -> Tuple[np.ndarray, np.ndarray]:
+    """Spread work items over `grid` persistent workgroups, longest first onto the least loaded workgroup.
+    Workgroup w runs on XCD w % 8 (each XCD has its own L2). Among equally loaded workgroups the next item
+    goes to the one that comes first in XCD-major order (XCD 0's workgroups, then XCD 1's, ...), and items
+    of equal weight are taken in locality order (`groups`, e.g. a band of output columns, then position).
+    So each round of equal items hands one XCD a run of neighbouring items, which share operand panels in
+    its L2, while the balance is that of plain longest-first (a triangle of causal tiles included).
+    Returns (offsets[grid + 1], items[n, width]) with each workgroup's items contiguous, in the order it
+    runs them (the order they were assigned, one round after another)."""
     xcds = min(gfx950.XCDS, grid)
-    per_xcd: List[List[int]] = [[] for _ in range(xcds)]
-    ngroups = max(groups) + 1 if groups else 1
-    # Groups in order onto XCDs, balancing total weight.
-    load = [0.0] * xcds
-    group_items: Dict[int, List[int]] = {}
-    for k, g in enumerate(groups):
-        group_items.setdefault(g, []).append(k)
-    group_weight = {g: sum(weights[k] for k in ks) for g, ks in group_items.items()}
-    wgs_of = [list(range(x, grid, xcds)) for x in range(xcds)]
-    capacity = [len(w) for w in wgs_of]
-    for g in sorted(group_items):  # contiguous groups to the same XCD while it has room
-        x = min(range(xcds), key=lambda x: (load[x] / capacity[x], x))
-        per_xcd[x].extend(group_items[g])
-        load[x] += group_weight[g]
+    slot = [(w % xcds) * ((grid + xcds - 1) // xcds) + w // xcds for w in range(grid)]
+    heap = [(0.0, slot[w], w) for w in range(grid)]
+    heapq.heapify(heap)
     assigned: List[List[int]] = [[] for _ in range(grid)]
-    for x in range(xcds):
-        wgs = wgs_of[x]
-        heap = [(0.0, n, w) for n, w in enumerate(wgs)]
-        heapq.heapify(heap)
-        mine = sorted(per_xcd[x], key=lambda k: (-weights[k], k))
-        for k in mine:
-            l, n, w = heapq.heappop(heap)
-            assigned[w].append(k)
-            heapq.heappush(heap, (l + weights[k], n, w))
+    for k in sorted(range(len(items)), key=lambda k: (-weights[k], groups[k], k)):
+        load, sl, w = heapq.heappop(heap)
+        assigned[w].append(k)
+        heapq.heappush(heap, (load + weights[k], sl, w))
+    width = len(items[0]) if items else 2
     offsets = np.zeros(grid + 1, np.int32)
-    flat: List[Tuple[int, int]] = []
+    flat: List[Tuple[int, ...]] = []
     for w in range(grid):
-        for k in sorted(assigned[w]):
-            flat.append(items[k])
+        flat.extend(items[k] for k in assigned[w])
         offsets[w + 1] = len(flat)
-    return offsets, np.array(flat, np.int32).reshape(-1, 2)
+    return offsets, np.array(flat, np.int32).reshape(-1, width)

@@ -57,6 +57,18 @@ AK_INLINE float ak_sigmoid(float x) { return 1.0f / (1.0f + __expf(-x)); }
 AK_INLINE float ak_maximum(float a, float b) { return (a != a || b != b) ? (a + b) : (a > b ? a : b); }
 AK_INLINE float ak_minimum(float a, float b) { return (a != a || b != b) ? (a + b) : (a < b ? a : b); }
 
+// The value lane ^ 32 holds, through v_permlane32_swap (no LDS round trip). The swap exchanges the upper
+// half of its first operand with the lower half of its second; the lower half's partner is read from the
+// second result and the upper half's from the first, which is also right when the compiler gives both
+// operands one register (the swap then rotates it by 32 lanes and both results hold the partners).
+AK_INLINE float ak_xor32(float x) {
+  const unsigned b = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return __builtin_bit_cast(float, (__lane_id() < 32) ? r[1] : r[0]);
+}
+AK_INLINE float ak_xor32_max(float x) { return fmaxf(x, ak_xor32(x)); }
+AK_INLINE float ak_xor32_sum(float x) { return x + ak_xor32(x); }
+
 // 8x8 transpose of 16-bit elements held as 8 rows of 4 dwords: out[c] holds column c (8 elements).
 AK_INLINE void ak_transpose8x8_b16(const ak_u32x4 in[8], ak_u32x4 out[8]) {
 #pragma unroll

@@ -197,6 +197,7 @@ class _Gemm:
         self.subs = self.sub_m * self.sub_n
         self.tables: Dict[str, np.ndarray] = {}
         self.const_value: Optional[float] = None
+        self.split: Optional[Tuple[int, int, int]] = None  # (items cut, chunks per item, K slices per chunk)
 
     # ------------------------------------------------------------------ work items (host)
 
@@ -251,7 +252,47 @@ class _Gemm:
                      for t, s in items]
             consts = {keep}
         self.const_value = next(iter(consts)) if consts else None
-        return items, weights, groups
+        items3 = [(t, s, 0) for t, s in items]
+        if not sch.runtime:
+            items3, weights, groups = self._split_remainder(items3, weights, groups)
+        return items3, weights, groups
+
+    def _split_remainder(self, items, weights, groups):
+        """Balance the last round. With n equal compute items on G workgroups, n = q G + r and r <= G / 2,
+        the last round would leave most workgroups idle: r of the items are cut along the reduction into
+        `split` chunks each (r * split <= G). A chunk writes its f32 partial sums to a workspace slot, and a
+        fixup kernel adds a tile's partials in chunk order and applies the epilogue."""
+        hw, G = self.hw, gfx950.CUS
+        compute = [k for k, (_, c, _) in enumerate(items) if (c >> 16) == 0]
+        if not compute or len({weights[k] for k in compute}) != 1:
+            return items, weights, groups
+        r = len(compute) % G
+        T = int(round(weights[compute[0]])) - 1  # K slices per item
+        if r == 0 or 2 * r > G:
+            return items, weights, groups
+        split = 1
+        while (2 * split * r <= G and T % (2 * split) == 0 and (T // (2 * split)) % hw.stages == 0
+               and T // (2 * split) >= max(4, 2 * hw.stages)):
+            split *= 2
+        if split == 1:
+            return items, weights, groups
+        chosen = compute[-r:]
+        self.split = (r, split, T // split)
+        self.tables["split_items"] = np.array([items[k][:2] for k in chosen], np.int32).reshape(-1)
+        out, w_out, g_out = [], [], []
+        chosen_set = set(chosen)
+        for k, item in enumerate(items):
+            if k not in chosen_set:
+                out.append(item)
+                w_out.append(weights[k])
+                g_out.append(groups[k])
+        for p, k in enumerate(chosen):
+            t, c, _ = items[k]
+            for ch in range(split):
+                out.append((t, (c & 0xFFFF) | (3 << 16), p * split + ch))
+                w_out.append(T / split + 1)
+                g_out.append(groups[k])
+        return out, w_out, g_out
 
     def _constant_of(self, t: int, s: int) -> Optional[float]:
         blocks = self.sch.blocks_at(t)
@@ -298,7 +339,7 @@ class _Gemm:
         grid = max(1, min(len(items), gfx950.CUS))
         offsets, flat = work_lists(items, weights, groups, grid)
         self.tables["wg_items"] = offsets
-        self.tables["items"] = flat.reshape(-1) if flat.size else np.zeros(2, np.int32)
+        self.tables["items"] = flat.reshape(-1) if flat.size else np.zeros(3, np.int32)
         for name, t in sch.tables.items():
             if name in (STEP_TILE,):
                 continue
@@ -307,13 +348,20 @@ class _Gemm:
             self.tables["tile_steps"] = static_tile_steps(sch)
         args = self._args()
         source = self._source(args)
-        launch = Launch(self.name, args, (grid, 1, 1), (THREADS, 1, 1), 0)
+        launches = [Launch(self.name, args, (grid, 1, 1), (THREADS, 1, 1), 0)]
+        workspace = {}
+        if self.split:
+            r, split, _ = self.split
+            workspace["gm_part"] = r * split * hw.bm * hw.bn * 4
+            launches.append(Launch(f"{self.name}_fixup", args, (r * hw.bm * hw.bn // (4 * THREADS), 1, 1),
+                                   (THREADS, 1, 1), 0))
         inputs = [(spec.shape, spec.dtype) for spec in plan.inputs]
         prog = Program(
-            name=self.name, source=source, launches=[launch], outputs=[(m.out.shape, m.out.dtype)], inputs=inputs,
-            tables=dict(self.tables), lds_bytes=hw.lds,
+            name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)], inputs=inputs,
+            tables=dict(self.tables), workspace=workspace, lds_bytes=hw.lds,
             notes={"family": "gemm", "hw_tile": (hw.bm, hw.bn, hw.bk), "stages": hw.stages, "grid": grid,
-                   "items": len(items), "constant_items": sum(1 for _, s in items if (s >> 16) == 2)},
+                   "items": len(items), "constant_items": sum(1 for _, s, _ in items if (s >> 16) == 2),
+                   "split": self.split},
         )
         if sch.runtime:
             from .steps import attach_step_builder
@@ -335,6 +383,8 @@ class _Gemm:
             args.append(Arg("table", name, "const int* __restrict__", name))
         args.append(Arg("int", 2 * self._pitch(m.a), "int", "ak_pitch_a"))
         args.append(Arg("int", 2 * self._pitch(m.b), "int", "ak_pitch_b"))
+        if self.split:
+            args.append(Arg("workspace", "gm_part", "float* __restrict__", "gm_part"))
         if self.sch.runtime:
             args.append(Arg("workspace", "step_code", "const int* __restrict__", "rt_step_code"))
             args.append(Arg("workspace", "tile_steps", "const int* __restrict__", "rt_tile_steps"))
@@ -352,6 +402,7 @@ class _Gemm:
         mi, ni = wtm // MFMA, wtn // MFMA
         k16s = bk // 16
         kslices = m.tk // bk
+        split, split_slices = (self.split[1], self.split[2]) if self.split else (1, 0)
         kvar = m.kvar
         index = Index(plan, lambda v: f"lv_{v}")
         a_shape = plan.inputs[m.a.param].shape
@@ -485,7 +536,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             w("  }")
         w(f"""  const int q_begin = args.wg_items[blockIdx.x], q_end = args.wg_items[blockIdx.x + 1];
   for (int q = q_begin; q < q_end; ++q) {{
-    const int t = args.items[2 * q], code = args.items[2 * q + 1];
+    const int t = args.items[3 * q], code = args.items[3 * q + 1], slot = args.items[3 * q + 2];
     const int sub = code & 0xffff, kind = code >> 16;
     const int sm = sub / {self.sub_n}, sn = sub % {self.sub_n};
     {fill_block}
@@ -497,6 +548,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     }}
     {setup}
     int T = __builtin_amdgcn_readfirstlane(nsteps * {kslices});  // K slices (even; one value per wave)
+    int g0 = 0;  // the first K slice (a chunk of a tile cut along the reduction starts later)
+    if (kind == 3) {{ g0 = (slot % {split}) * {split_slices}; T = {split_slices}; }}
     asm volatile("" : "+s"(T));  // an opaque trip count: a known one makes the compiler spill in the loop
     const long long a_off = ({a_base}) + (long long)(sm * {bm}) * {lda};""")
         if nt:
@@ -507,17 +560,19 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
         (int)({a_numel}LL * 2 - a_off * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc((void*)({B} + b_off), (short)0,
         (int)({b_numel}LL * 2 - b_off * 2), 0x00020000);
+    // A tile's chunks are summed by the fixup kernel: only the first starts from the initial value.
+    const float acc_init = (kind == 3 && g0 != 0) ? 0.0f : {literal(m.init)};
     ak_f32x16 acc[{mi}][{ni}];
 #pragma unroll
     for (int i_ = 0; i_ < {mi}; ++i_)
 #pragma unroll
       for (int j_ = 0; j_ < {ni}; ++j_)
 #pragma unroll
-        for (int r_ = 0; r_ < 16; ++r_) acc[i_][j_][r_] = {literal(m.init)};
+        for (int r_ = 0; r_ < 16; ++r_) acc[i_][j_][r_] = acc_init;
     ak_bf16x8 fa[2][{mi}], fb[2][{ni}];
     // Slice g's loads into stage s: the slice's step and K offset (slices past the tile's last reload it).
     auto k_of = [&](int g) -> int {{
-      const int gg = g < T ? g : (T > 0 ? T - 1 : 0);
+      const int gg = g0 + (g < T ? g : (T > 0 ? T - 1 : 0));
       const int st_ = gg / {kslices};
       return {kval} + (gg % {kslices}) * {bk};
     }};""")
@@ -602,6 +657,19 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
         w(f"{ind}}}")
         w(f"{ind}AK_WAIT_VM(0);")
         w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+        if self.split:
+            w(f"""    if (kind == 3) {{  // a chunk: its f32 partial sums go to workspace slot `slot`, lane-contiguous
+      float* part = args.gm_part + (long long)slot * {bm * bn};
+#pragma unroll
+      for (int i_ = 0; i_ < {mi}; ++i_)
+#pragma unroll
+        for (int j_ = 0; j_ < {ni}; ++j_)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4)
+            *(ak_f32x4*)(part + ((((wave * {mi} + i_) * {ni} + j_) * 4 + g4) * 64 + lane) * 4) =
+                ak_f32x4{{acc[i_][j_][g4 * 4], acc[i_][j_][g4 * 4 + 1], acc[i_][j_][g4 * 4 + 2], acc[i_][j_][g4 * 4 + 3]}};
+      continue;
+    }}""")
         w(f"""    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
     // The lane index goes through an empty asm so the stores' addresses are computed here, not hoisted
     // above the K loop where they would take registers the loop needs.
@@ -629,6 +697,41 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
       }}
     }}
   }}
+}}""")
+        if self.split:
+            r, split, _ = self.split
+            per_item = bm * bn // (4 * THREADS)
+            w(f"""
+// The fixup of tiles cut along the reduction: each thread adds one float4 of the {split} chunks' partial sums
+// (in chunk order), then applies the epilogue to those four outputs.
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_fixup(const {self.name}_args args) {{
+  const int p = blockIdx.x / {per_item};
+  const int e = (blockIdx.x % {per_item}) * {THREADS} + threadIdx.x;
+  const int lane_e = e & 63, g4 = (e >> 6) & 3, j_ = (e >> 8) % {ni}, i_ = (e >> 8) / {ni} % {mi};
+  const int wave = (e >> 8) / {ni * mi}, wm = wave >> 1, wn = wave & 1;
+  const float* part = args.gm_part + (long long)p * {split * bm * bn} + e * 4;
+  ak_f32x4 sum = *(const ak_f32x4*)part;
+#pragma unroll
+  for (int c = 1; c < {split}; ++c) {{
+    const ak_f32x4 v = *(const ak_f32x4*)(part + (long long)c * {bm * bn});
+    sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
+  }}
+  const int t = args.split_items[2 * p], sub = args.split_items[2 * p + 1] & 0xffff;
+  const int sm = sub / {self.sub_n}, sn = sub % {self.sub_n};
+  {tile_decode}
+  const long long obase = {o_base};
+  const int er = sm * {bm} + wm * {wtm} + i_ * 32 + (lane_e & 31);
+  const int ec0 = sn * {bn} + wn * {wtn} + j_ * 32 + g4 * 8 + (lane_e >> 5) * 4;
+  float res[4];
+#pragma unroll
+  for (int e4 = 0; e4 < 4; ++e4) {{
+    const int ec = ec0 + e4;
+    const float acc_v = sum[e4];
+    (void)ec; (void)er;
+    {epi}
+    res[e4] = (float)({result});
+  }}
+  {_store4(O, "obase", ldo, out_bf16)}
 }}""")
         return "\n".join(L)
 

@@ -1,0 +1,32 @@
+"""Trace-region profiles on the CPU: summing per-workgroup region totals and classifying the bottleneck
+(the reference's profiling.py:95-220 and tests/test_profiling.py)."""
+
+import numpy as np
+
+from tilejax_amd.profiling import CLOCK_HZ, DMA_BOUND_SHARE, OVERHEAD_BOUND_SHARE, KernelProfile, summarize
+
+
+def test_summarize_averages_workgroups_and_calls():
+    # two workgroups, two calls summed: [wait, fill, out_wait, compute, steps] in 100 MHz ticks
+    stamps = np.array([[400, 100, 40, 1200, 8], [600, 100, 60, 1000, 8]])
+    p = summarize(stamps, "k", None, calls=2, device_s=20e-6, workgroups=2)
+    tick = 1 / CLOCK_HZ
+    assert p.regions and p.calls == 2 and p.steps == 8
+    assert np.isclose(p.wait_s, 250 * tick) and np.isclose(p.fill_s, 50 * tick)
+    assert np.isclose(p.out_wait_s, 25 * tick) and np.isclose(p.compute_s, 550 * tick)
+    assert np.isclose(p.exposed_wait_s, 200 * tick)
+    assert np.isclose(p.other_s, 20e-6 - (250 + 25 + 550) * tick)
+
+
+def test_bottleneck_thresholds():
+    def prof(wait=0.0, out=0.0, compute=10.0, fill=0.0, regions=True):
+        return KernelProfile("k", None, 1, 10.0, regions, 4, wait, fill, out, compute)
+
+    assert prof(regions=False).bottleneck is None
+    assert prof(wait=DMA_BOUND_SHARE * 10 + 0.1, compute=7.0).bottleneck == "dma"
+    # waits that only fill the pipeline aren't exposed
+    assert prof(wait=3.0, fill=3.0, compute=7.0).bottleneck == "compute"
+    assert prof(out=2.5, compute=7.0).bottleneck == "dma"
+    assert prof(compute=10 - OVERHEAD_BOUND_SHARE * 10 - 0.5).bottleneck == "overhead"
+    assert prof().bottleneck == "compute"
+    assert "bottleneck: compute" in str(prof())

@@ -43,7 +43,7 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
     name = _symbol(plan)
     found = gemm.match(plan)
     if found is not None:
-        return gemm.lower(plan, schedule, pipeline, found, name)
+        return gemm.lower(plan, schedule, pipeline, found, name, trace=trace)
     found = flash.match(plan)
     if found is not None:
         return flash.lower(plan, schedule, pipeline, found, name)

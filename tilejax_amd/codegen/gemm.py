@@ -43,6 +43,8 @@ __all__ = ["GemmMatch", "match", "lower"]
 
 THREADS = 256
 MFMA = 32  # 32x32x16 bf16 MFMA tiles
+TRACE = "ak_trace"  # per workgroup: input-wait, pipeline-fill, output, compute ticks (s_memrealtime) and steps
+TRACE_FIELDS = 5
 
 
 @dataclass
@@ -185,14 +187,16 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline) -> HwTile:
     return HwTile(bm, bn, bk, stages)
 
 
-def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, name: str) -> Program:
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, name: str, trace: bool = False) -> Program:
     hw = hardware_tile(m, pipeline)
-    return _Gemm(plan, sch, pipeline, m, hw, name).program()
+    return _Gemm(plan, sch, pipeline, m, hw, name, trace).program()
 
 
 class _Gemm:
-    def __init__(self, plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, hw: HwTile, name: str) -> None:
+    def __init__(self, plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, hw: HwTile, name: str,
+                 trace: bool = False) -> None:
         self.plan, self.sch, self.pipeline, self.m, self.hw, self.name = plan, sch, pipeline, m, hw, name
+        self.trace = trace
         self.sub_m, self.sub_n = m.tm // hw.bm, m.tn // hw.bn
         self.subs = self.sub_m * self.sub_n
         self.tables: Dict[str, np.ndarray] = {}
@@ -350,6 +354,8 @@ class _Gemm:
         source = self._source(args)
         launches = [Launch(self.name, args, (grid, 1, 1), (THREADS, 1, 1), 0)]
         workspace = {}
+        if self.trace:
+            workspace[TRACE] = grid * TRACE_FIELDS * 8
         if self.split:
             r, split, _ = self.split
             workspace["gm_part"] = r * split * hw.bm * hw.bn * 4
@@ -361,7 +367,8 @@ class _Gemm:
             tables=dict(self.tables), workspace=workspace, lds_bytes=hw.lds,
             notes={"family": "gemm", "hw_tile": (hw.bm, hw.bn, hw.bk), "stages": hw.stages, "grid": grid,
                    "items": len(items), "constant_items": sum(1 for _, s, _ in items if (s >> 16) == 2),
-                   "split": self.split},
+                   "split": self.split, "trace_workgroups": grid if self.trace else 0,
+                   "slices_per_step": m.tk // hw.bk * self.subs},
         )
         if sch.runtime:
             from .steps import attach_step_builder
@@ -385,6 +392,8 @@ class _Gemm:
         args.append(Arg("int", 2 * self._pitch(m.b), "int", "ak_pitch_b"))
         if self.split:
             args.append(Arg("workspace", "gm_part", "float* __restrict__", "gm_part"))
+        if self.trace:
+            args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
         if self.sch.runtime:
             args.append(Arg("workspace", "step_code", "const int* __restrict__", "rt_step_code"))
             args.append(Arg("workspace", "tile_steps", "const int* __restrict__", "rt_tile_steps"))
@@ -534,7 +543,14 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
                 w(f"    {{ const int n = wn * {wtn} + {j * 32} + 16 * (G & 1) + 4 * (s & 3);"
                   f" b_roff[{j}] = k * {bn * 2} + (((n >> 3) ^ {swb('k')}) << 4) + (n & 7) * 2; }}")
             w("  }")
+        trace_write = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
+                       f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_out; tr[3] = tr_comp - tr_wait; "
+                       f"tr[4] = tr_slices; }}" if self.trace else "")
+        trace_decl = ("unsigned long long tr_wait = 0, tr_fill = 0, tr_out = 0, tr_comp = 0, tr_slices = 0;"
+                      if self.trace else "")
+        now = "__builtin_amdgcn_s_memrealtime()"
         w(f"""  const int q_begin = args.wg_items[blockIdx.x], q_end = args.wg_items[blockIdx.x + 1];
+  {trace_decl}
   for (int q = q_begin; q < q_end; ++q) {{
     const int t = args.items[3 * q], code = args.items[3 * q + 1], slot = args.items[3 * q + 2];
     const int sub = code & 0xffff, kind = code >> 16;
@@ -627,10 +643,14 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             return out
 
         ind = "    "
+        if self.trace:
+            w(f"{ind}const unsigned long long tr_i0 = {now}; tr_slices += T;")
         for s in range(S):
             L.extend(issue(str(s), s, ind))
         w(f"{ind}AK_WAIT_VM({per_slice * (S - 1)});")
         w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+        if self.trace:
+            w(f"{ind}const unsigned long long tr_c0 = {now}; tr_fill += tr_c0 - tr_i0;")
         L.extend(reads(0, 0, 0, ind))
         w(f"{ind}for (int g = 0; g < T; g += {S}) {{")
         ind2 = ind + "  "
@@ -646,9 +666,13 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
                     # Last K16 of slice g + s: our reads of its stage are done, and (after the barrier) every
                     # wave's; slice g + s + 1 has landed. Refill this stage with slice g + s + S and read the
                     # next slice's first fragments while this slice's last MFMAs run.
+                    if self.trace:
+                        w(f"{ind2}  const unsigned long long tr_w0 = {now};")
                     w(f"{ind2}  AK_WAIT_LGKM0();")
                     w(f"{ind2}  AK_WAIT_VM({per_slice * (S - 2)});")
                     w(f'{ind2}  asm volatile("s_barrier" ::: "memory");')
+                    if self.trace:
+                        w(f"{ind2}  tr_wait += {now} - tr_w0;")
                     L.extend(issue(f"g + {s + S}", s, ind2 + "  "))
                     L.extend(reads((s + 1) % S, 0, cur ^ 1, ind2 + "  "))
                     L.extend(mfmas(cur, ind2 + "  "))
@@ -657,6 +681,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
         w(f"{ind}}}")
         w(f"{ind}AK_WAIT_VM(0);")
         w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+        if self.trace:
+            w(f"{ind}const unsigned long long tr_o0 = {now}; tr_comp += tr_o0 - tr_c0;")
         if self.split:
             w(f"""    if (kind == 3) {{  // a chunk: its f32 partial sums go to workspace slot `slot`, lane-contiguous
       float* part = args.gm_part + (long long)slot * {bm * bn};
@@ -668,6 +694,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
           for (int g4 = 0; g4 < 4; ++g4)
             *(ak_f32x4*)(part + ((((wave * {mi} + i_) * {ni} + j_) * 4 + g4) * 64 + lane) * 4) =
                 ak_f32x4{{acc[i_][j_][g4 * 4], acc[i_][j_][g4 * 4 + 1], acc[i_][j_][g4 * 4 + 2], acc[i_][j_][g4 * 4 + 3]}};
+      {"tr_out += " + now + " - tr_o0;" if self.trace else ""}
       continue;
     }}""")
         w(f"""    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
@@ -696,7 +723,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
         }}
       }}
     }}
+    {"tr_out += " + now + " - tr_o0;" if self.trace else ""}
   }}
+  {trace_write}
 }}""")
         if self.split:
             r, split, _ = self.split

@@ -86,6 +86,14 @@ class Program:
         outputs, _ = self._run(arrays, outputs, stream, self.launches)
         return outputs[0] if len(outputs) == 1 else tuple(outputs)
 
+    def run_traced(self, *arrays: torch.Tensor) -> Tuple[Any, Optional[torch.Tensor]]:
+        """One call of a program generated with trace regions: its outputs, and its trace buffer (per
+        workgroup: input-wait, fill, output and compute ticks of the 100 MHz clock, then steps), or None."""
+        outputs, workspace = self._run(arrays, None, None, self.launches)
+        trace = workspace.get("ak_trace")
+        result = outputs[0] if len(outputs) == 1 else tuple(outputs)
+        return result, (trace.view(torch.int64) if trace is not None else None)
+
     def step_tables(self, *arrays: torch.Tensor) -> Dict[str, torch.Tensor]:
         """Run only the device step-table builder (runtime masks) and return its tables as int32 tensors:
         step_tile, step_code, count (the reference's three) and tile_steps."""

@@ -25,6 +25,7 @@ __all__ = ["DMA_BOUND_SHARE", "OVERHEAD_BOUND_SHARE", "KernelProfile", "measure"
 DMA_BOUND_SHARE = 0.2
 OVERHEAD_BOUND_SHARE = 0.3
 CLOCK_HZ = 100e6  # s_memrealtime
+TRACE_FIELDS = 5  # per workgroup: wait, fill, out_wait, compute (ticks), steps
 
 
 @dataclass
@@ -103,16 +104,31 @@ def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile
 
     runtime.require_gpu()
     stream = runtime.current_stream()
+    program = lowered.program
+    workgroups = program.notes.get("trace_workgroups", 0) if lowered.trace else 0
     lowered.run(*inputs)
     torch.cuda.synchronize()
-    samples = []
+    samples, stamps = [], None
     for _ in range(runs):
         start, stop = runtime.Event(), runtime.Event()
         start.record(stream)
-        lowered.run(*inputs)
+        if workgroups:
+            _, trace = program.run_traced(*inputs)
+        else:
+            lowered.run(*inputs)
         stop.record(stream)
+        if workgroups:
+            torch.cuda.synchronize()
+            t = trace[: workgroups * TRACE_FIELDS].cpu()
+            stamps = t if stamps is None else stamps + t
         samples.append(start.elapsed_ms(stop) * 1e-3)
-    return KernelProfile(lowered.plan.nest.name, lowered.config, runs, statistics.median(samples), samples=samples)
+    device_s = statistics.median(samples)
+    if workgroups:
+        result = summarize(stamps.numpy(), lowered.plan.nest.name, lowered.config, runs, device_s, workgroups)
+        result.steps /= max(program.notes.get("slices_per_step", 1), 1)
+        result.samples = samples
+        return result
+    return KernelProfile(lowered.plan.nest.name, lowered.config, runs, device_s, samples=samples)
 
 
 def profile(kernel: Any, args: Sequence[Any], runs: int = 5) -> KernelProfile:
@@ -121,5 +137,5 @@ def profile(kernel: Any, args: Sequence[Any], runs: int = 5) -> KernelProfile:
 
     arrays, _ = kernel._split(tuple(args))
     config = kernel.lower(*args).config
-    lowered = kernel.lowered(kernel.signature(*arrays), config)
+    lowered = kernel.lowered(kernel.signature(*arrays), config, trace=True)
     return measure(lowered, [_tensor(a) for a in arrays], runs)

@@ -223,7 +223,7 @@ def _measure(kernel: Any, signature: Any, config: Config, inputs: Sequence[torch
     from .api import compare
 
     try:
-        lowered = kernel.lowered(signature, config)
+        lowered = kernel.lowered(signature, config, trace=True)  # trace regions: the profile's breakdown
         got = lowered.run(*inputs)
         torch.cuda.synchronize()
     except Exception as e:

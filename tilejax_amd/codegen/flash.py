@@ -377,35 +377,71 @@ class _Flash:
 
     # ------------------------------------------------------------------------------------------ program
 
+    def _split(self, items, weights):
+        """Split-KV for balance: items with more key blocks than a CU's share of all blocks (one workgroup
+        per CU at a time) are cut into chunks of consecutive blocks. A chunk runs the same online softmax
+        over its blocks and writes its (m, l, acc) to a workspace slot; the merge kernel combines a tile's
+        chunks. Returns the items (t, sub, block offset, blocks, per-wave counts, slot or -1), their weights
+        and the merge table rows (t, sub, first slot, chunks)."""
+        total = sum(it[3] for it in items)
+        share = max(1, -(-total // gfx950.CUS))
+        out, w_out, merges = [], [], []
+        slot = 0
+        for it, wt in zip(items, weights):
+            t, sub, off, cnt, waves = it
+            parts = -(-cnt // share) if cnt > share * 1.1 and len(items) < 2 * gfx950.CUS else 1
+            if parts == 1:
+                out.append((t, sub, off, cnt, waves, -1))
+                w_out.append(wt)
+                continue
+            bounds = [cnt * c // parts for c in range(parts + 1)]
+            merges.append((t, sub, slot, parts))
+            for c in range(parts):
+                b0, b1 = bounds[c], bounds[c + 1]
+                cw = [(min(max(f - b0, 0), b1 - b0), min(max(u - b0, 0), b1 - b0)) for f, u in waves]
+                out.append((t, sub, off + b0, b1 - b0, cw, slot))
+                w_out.append(sum(u for _, u in cw))
+                slot += 1
+        return out, w_out, merges
+
     def program(self) -> Program:
         plan, sch, m = self.plan, self.sch, self.m
         items, weights, blocks = self._items()
+        items, weights, merges = self._split(items, weights)
+        self.slots = sum(c for _, _, _, c in merges)
         order = sorted(range(len(items)), key=lambda i: (-weights[i], i))
         nw = self.nw
-        stride = 4 + 2 * nw
+        stride = 5 + 2 * nw
         table = np.zeros((max(len(items), 1), stride), np.int32)
         for row, i in enumerate(order):
-            t, sub, off, cnt, waves = items[i]
-            table[row, :4] = (t, sub, off, cnt)
+            t, sub, off, cnt, waves, slot = items[i]
+            table[row, :5] = (t, sub, off, cnt, slot)
             for wv, (full, upto) in enumerate(waves):
-                table[row, 4 + 2 * wv] = full
-                table[row, 5 + 2 * wv] = upto
+                table[row, 5 + 2 * wv] = full
+                table[row, 6 + 2 * wv] = upto
         kvtab = np.array(blocks, np.int32).reshape(-1) if blocks else np.zeros(2, np.int32)
         tables = {"fa_items": table.reshape(-1), "fa_blocks": kvtab}
+        if merges:
+            tables["fa_merge"] = np.array(merges, np.int32).reshape(-1)
         for name, t in sch.tables.items():
             if name.startswith("tile_") or name.startswith("fill_"):
                 tables[name] = t
         self.tables = tables
         args = self._args()
         source = self._source(args, stride)
-        launch = Launch(self.name, args, (max(len(items), 1), 1, 1), (64 * nw, 1, 1), 0)
+        launches = [Launch(self.name, args, (max(len(items), 1), 1, 1), (64 * nw, 1, 1), 0)]
+        workspace = {}
+        if merges:
+            workspace["fa_part"] = self.slots * self.bq * (m.dv + 2) * 4
+            per_item = self.bq * m.dv // 4 // 256
+            launches.append(Launch(f"{self.name}_merge", args, (len(merges) * per_item, 1, 1), (256, 1, 1), 0))
         flop = 2.0 * sum(w for w in weights) * 32 * self.bkv * (m.d + m.dv)
         return Program(
-            name=self.name, source=source, launches=[launch], outputs=[(m.out.shape, m.out.dtype)],
-            inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables,
+            name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
+            inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
             lds_bytes=2 * self.bkv * (m.d + m.dv) * 2,
             notes={"family": "flash", "block_q": self.bq, "block_kv": self.bkv, "waves": nw, "items": len(items),
-                   "executed_flop": flop},
+                   "executed_flop": flop, "split_items": len(merges), "chunks": self.slots},
         )
 
     def _args(self) -> List[Arg]:
@@ -420,6 +456,8 @@ class _Flash:
         args.append(Arg("output", 0, "ak_u16* __restrict__", m.out.name + "_out"))
         for name in self.tables:
             args.append(Arg("table", name, "const int* __restrict__", name))
+        if "fa_merge" in self.tables:
+            args.append(Arg("workspace", "fa_part", "float* __restrict__", "fa_part"))
         return args
 
     def _source(self, args: List[Arg], stride: int) -> str:
@@ -513,7 +551,9 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int* item = args.fa_items + blockIdx.x * {stride};
   const int t = ak_ldc(item, 0), sub = ak_ldc(item, 1), boff = ak_ldc(item, 2), nblk = ak_ldc(item, 3);
-  const int f_w = ak_ldc(item, 4 + 2 * wave), n_w = ak_ldc(item, 5 + 2 * wave);
+  const int slot = ak_ldc(item, 4);  // a chunk of a tile split along the keys: its workspace slot (else -1)
+  const int f_w = ak_ldc(item, 5 + 2 * wave), n_w = ak_ldc(item, 6 + 2 * wave);
+  (void)slot;
   {tile_decode}
   const int er = sub * {bq} + wave * 32 + (lane & 31);   // this lane's query row in the spec tile
   // Q^T fragments (srcB of S^T = K Q^T): row er, head dims 16 s + 8 (lane / 32) .. + 8
@@ -650,6 +690,19 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             w("      }")
             w("    }")
         w("  }")
+        if self.slots:
+            w(f"""  if (slot >= 0) {{  // a chunk: (m, l, acc) of its rows to the workspace, for the merge kernel
+    float* part = args.fa_part + (long long)slot * {bq * (DV + 2)};
+    const int lr = wave * 32 + (lane & 31);
+#pragma unroll
+    for (int dt = 0; dt < {dt_n}; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *(ak_f32x4*)(part + lr * {DV} + 32 * dt + g4 * 8 + (lane >> 5) * 4) =
+            ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};
+    if (lane < 32) {{ part[{bq * DV} + lr] = m_run; part[{bq * DV + bq} + lr] = l_run; }}
+    return;
+  }}""")
         w(f"""  // Output: lane = query row er, acc[dt][r] = head dim 32 dt + (r / 4) * 8 + (lane / 32) * 4 + r % 4.
   ak_u16* op = (ak_u16*){O} + ({o_base}) + (long long)er * {ldo};
 #pragma unroll
@@ -666,6 +719,41 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
       }}
       *(ak_u32x2*)(op + 32 * dt + g4 * 8 + (lane >> 5) * 4) = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
     }}
+}}""")
+        if self.slots:
+            per_item = bq * DV // 4 // 256
+            w(f"""
+// The merge of tiles split along the keys: each thread combines four output elements of one row over the
+// tile's chunks with the online softmax's own rule (weights exp(m_c - M)), then applies the epilogue.
+extern "C" __global__ void __launch_bounds__(256) {self.name}_merge(const {self.name}_args args) {{
+  const int p = blockIdx.x / {per_item};
+  const int e = (blockIdx.x % {per_item}) * 256 + threadIdx.x;
+  const int lr = e / {DV // 4}, d0 = (e % {DV // 4}) * 4;
+  const int t = ak_ldc(args.fa_merge, 4 * p), sub = ak_ldc(args.fa_merge, 4 * p + 1);
+  const int first = ak_ldc(args.fa_merge, 4 * p + 2), chunks = ak_ldc(args.fa_merge, 4 * p + 3);
+  {tile_decode}
+  float mx = -__builtin_inff();
+  for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, args.fa_part[(long long)(first + c) * {bq * (DV + 2)} + {bq * DV} + lr]);
+  float l_run = 0.f;
+  ak_f32x4 a = {{0.f, 0.f, 0.f, 0.f}};
+  for (int c = 0; c < chunks; ++c) {{
+    const float* part = args.fa_part + (long long)(first + c) * {bq * (DV + 2)};
+    const float w = ak_exp(part[{bq * DV} + lr] - mx);
+    l_run += w * part[{bq * DV + bq} + lr];
+    const ak_f32x4 v = *(const ak_f32x4*)(part + lr * {DV} + d0);
+    a[0] += w * v[0]; a[1] += w * v[1]; a[2] += w * v[2]; a[3] += w * v[3];
+  }}
+  const int er = sub * {bq} + lr; (void)er;
+  ak_u16* op = (ak_u16*){O} + ({o_base}) + (long long)er * {ldo} + d0;
+  float res[4];
+#pragma unroll
+  for (int e4 = 0; e4 < 4; ++e4) {{
+    const int ed = d0 + e4; (void)ed;
+    const float acc_v = a[e4];
+    {epi_lines}
+    res[e4] = (float)({out_expr});
+  }}
+  *(ak_u32x2*)op = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
 }}""")
         return "\n".join(L)
 

@@ -53,6 +53,7 @@ __all__ = ["FlashMatch", "match", "lower"]
 LOG2E = 1.4426950408889634
 RESCALE_SLACK = 8.0  # natural-log units: p stays below e^8 between rescales
 MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 once a row has a real score
+STAGES = 3  # LDS stages of K and V blocks: loads run two blocks ahead, one barrier per block
 
 
 @dataclass
@@ -439,7 +440,7 @@ class _Flash:
         return Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
             inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
-            lds_bytes=2 * self.bkv * (m.d + m.dv) * 2,
+            lds_bytes=STAGES * self.bkv * (m.d + m.dv) * 2,
             notes={"family": "flash", "block_q": self.bq, "block_kv": self.bkv, "waves": nw, "items": len(items),
                    "executed_flop": flop, "split_items": len(merges), "chunks": self.slots},
         )
@@ -542,7 +543,7 @@ class _Flash:
 // spec tile {m.rows} x {m.bk} (head dims {D}, {DV}); workgroup {bq} query rows in {nw} waves, key blocks of {bkv}.
 {PRELUDE}
 {struct}""")
-        for s in range(2):
+        for s in range(STAGES):
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
         w(f"""
@@ -672,21 +673,28 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             a(f"{ind}}}")
             return o
 
-        w("  if (nblk > 0) {")
-        L.extend(issue("0", 0, "    "))
-        w("  }")
-        w("  for (int b = 0; b < nblk; b += 2) {")
-        for s in range(2):
+        # K and V blocks stream through STAGES LDS stages, loaded STAGES - 1 blocks ahead. At the barrier that
+        # opens block b every wave has finished block b - 1 (its LDS reads waited for before the barrier),
+        # so block b + STAGES - 1 can go into that block's stage; one barrier per block.
+        per_block = ldk_n + ldv_n
+        for s in range(STAGES - 1):
+            w(f"  if ({s} < nblk) {{")
+            L.extend(issue(str(s), s, "    "))
+            w("  }")
+        w(f"  for (int b = 0; b < nblk; b += {STAGES}) {{")
+        for s in range(STAGES):
             w(f"    {{ const int b_ = b + {s};")
             w("      if (b_ < nblk) {")
-            w("        AK_WAIT_VM(0);")
-            w('        asm volatile("s_barrier" ::: "memory");')
-            w("        if (b_ + 1 < nblk) {")
-            L.extend(issue("b_ + 1", 1 - s, "          "))
-            w("        }")
-            L.extend(compute(s, "        "))
+            # Block b_ has landed; the (at most STAGES - 2) later blocks issued may still be in flight.
+            for ahead in range(STAGES - 2, 0, -1):
+                w(f"        {'if' if ahead == STAGES - 2 else 'else if'} (b_ + {ahead} < nblk) {{ AK_WAIT_VM({ahead * per_block}); }}")
+            w("        " + ("else " if STAGES > 2 else "") + "{ AK_WAIT_VM(0); }")
             w("        AK_WAIT_LGKM0();")
             w('        asm volatile("s_barrier" ::: "memory");')
+            w(f"        if (b_ + {STAGES - 1} < nblk) {{")
+            L.extend(issue(f"b_ + {STAGES - 1}", (s + STAGES - 1) % STAGES, "          "))
+            w("        }")
+            L.extend(compute(s, "        "))
             w("      }")
             w("    }")
         w("  }")

@@ -3,9 +3,15 @@
 `python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line. A step is one call of the
 generated kernel for the workload of BASELINE.json's metric: the dense 8192^3 bf16 matmul `x @ y`
 (examples/matmul.py of the reference, f32 accumulate, bf16 out), inputs ~N(0,1) from seeds 0 and 1,
-already resident in HBM. `value` is its TFLOP/s (2*M*N*K / time). The same line carries the causal
-matmul `tril(x @ y)` at the same size (its time over the dense time) and, once lowered, causal MHA
-(4, 16, 2048, 128), each timed the same way, plus:
+already resident in HBM. `value` is its TFLOP/s (2*M*N*K / time) at MatmulTiles(512, 512, 512). The same line
+carries the other BASELINE configurations in `legs`, each timed the same way:
+- dense at MatmulTiles(1024, 2048, 1024);
+- causal `tril(x @ y)` at the same size, with its time over the dense time;
+- causal MHA at (4, 16, 2048, 128) and (1, 16, 4096, 128);
+- the MoE grouped GEMM (16384 x 4096 x 14336, 8 experts);
+- paged GQA decode (64 sequences, HBM GB/s).
+
+It also carries:
 
 - `roofline`: the dense kernel's achieved TFLOP/s (algorithmic 2*8192^3 FLOP per launch over its mean
   launch time, from HIP events recorded on the stream the kernel runs on) against the 2.5 PFLOP/s bf16
@@ -105,7 +111,7 @@ def main() -> int:
     ap.add_argument("--tiles", default="512,512,512", help="dense matmul spec tiles tm,tn,tk")
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of legs to run: dense,causal,attention,moe,decode")
+    ap.add_argument("--only", default="", help="comma list of legs to run: dense,dense2,causal,attention,moe,decode")
     ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3; "
                     "default: profiles/traffic.json")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -152,6 +158,15 @@ def main() -> int:
     out["dense"] = {"tiles": [tiles.tm, tiles.tn, tiles.tk], "us": round(ms * 1e3, 2),
                     "tflops": round(tflops, 2), "hw": lowered.program.notes}
 
+    if "dense2" in legs or not args.only:
+        t2 = MatmulTiles(1024, 2048, 1024)
+        _log(f"dense matmul {N_DENSE}^3 tiles {t2}: lowering")
+        l2 = matmul.lower(x, y, t2)
+        ms2, _ = time_kernel(lambda: l2.run(x, y), args.steps, args.warmup)
+        _log(f"  {ms2 * 1e3:.1f} us/call, {flop / (ms2 * 1e-3) / 1e12:.1f} TFLOP/s")
+        out["dense_1024x2048x1024"] = {"tiles": [t2.tm, t2.tn, t2.tk], "us": round(ms2 * 1e3, 2),
+                                       "tflops": round(flop / (ms2 * 1e-3) / 1e12, 2)}
+
     if "causal" in legs:
         ct = MatmulTiles(*(int(v) for v in args.causal_tiles.split(",")))
         _log(f"causal matmul {N_DENSE}^3 tiles {ct}: lowering")
@@ -165,19 +180,20 @@ def main() -> int:
         try:
             from examples.causal_attention import AttentionBlocks, causal_attention
 
-            B, H, S, D = 4, 16, 2048, 128
-            gens = [torch.Generator().manual_seed(s) for s in (0, 1, 2)]
-            q, k, v = (torch.randn(B, H, S, D, generator=gg).to(torch.bfloat16) for gg in gens)
-            q = (q.float() * D**-0.5).to(torch.bfloat16)
-            q, k, v = q.to(dev), k.to(dev), v.to(dev)
-            blocks = AttentionBlocks(512, 512)
-            al = causal_attention.lower(q, k, v, blocks)
-            ams, _ = time_kernel(lambda: al.run(q, k, v), args.steps, args.warmup)
-            aflop = 2.0 * B * H * S * S * D  # algorithmic causal count (QK^T and PV over the lower triangle)
-            atf = aflop / (ams * 1e-3) / 1e12
-            _log(f"causal MHA {B}x{H}x{S}x{D}: {ams * 1e3:.1f} us, {atf:.1f} TFLOP/s")
-            out["attention"] = {"shape": [B, H, S, D], "blocks": [512, 512], "us": round(ams * 1e3, 2),
-                                "tflops": round(atf, 2), "frac_peak": round(atf / PEAK_TFLOPS, 4)}
+            for key, (B, H, S, D) in (("attention", (4, 16, 2048, 128)), ("attention_4096", (1, 16, 4096, 128))):
+                gens = [torch.Generator().manual_seed(s) for s in (0, 1, 2)]
+                q, k, v = (torch.randn(B, H, S, D, generator=gg).to(torch.bfloat16) for gg in gens)
+                q = (q.float() * D**-0.5).to(torch.bfloat16)
+                q, k, v = q.to(dev), k.to(dev), v.to(dev)
+                blocks = AttentionBlocks(512, 512)
+                al = causal_attention.lower(q, k, v, blocks)
+                ams, _ = time_kernel(lambda: al.run(q, k, v), args.steps, args.warmup)
+                aflop = 2.0 * B * H * S * S * D  # algorithmic causal count (QK^T and PV over the lower triangle)
+                atf = aflop / (ams * 1e-3) / 1e12
+                _log(f"causal MHA {B}x{H}x{S}x{D}: {ams * 1e3:.1f} us, {atf:.1f} TFLOP/s")
+                out[key] = {"shape": [B, H, S, D], "blocks": [512, 512], "us": round(ams * 1e3, 2),
+                            "tflops": round(atf, 2), "frac_peak": round(atf / PEAK_TFLOPS, 4)}
+                del q, k, v
         except Exception as e:  # not lowered yet: reported, not hidden
             _log(f"causal MHA: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
             out["attention"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}

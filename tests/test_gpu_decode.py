@@ -107,3 +107,24 @@ def test_baseline_config_sampled():
         s = torch.einsum("gqd,ngd->gqn", qq, kk)
         want = torch.einsum("gqn,ngd->gqd", torch.softmax(s, -1), vv).reshape(H, D)
         _close(got[b, 0], want)
+
+
+def test_decode_step_tables_bit_exact_at_baseline_size():
+    """The builder at BASELINE config 5's size (64 sequences x 512 pages: 512 mask words, written by 16
+    workgroups, each repeating the masks and the scan and writing its own words) against the reference's
+    table semantics."""
+    B, pages = 64, 512
+    g = torch.Generator().manual_seed(0)
+    lengths = torch.randint(128, 8193, (B,), generator=g, dtype=torch.int32)
+    lengths[5], lengths[9] = 0, 8192  # an empty sequence and a full one
+    ins = _inputs(B, 32, 8, 128, 16, pages, tuple(int(n) for n in lengths))
+    lowered = paged_gqa_decode.lower(*ins)
+    assert lowered.program.launches[0].grid[0] > 1
+    got = lowered.program.step_tables(*(t.cuda() for t in ins))
+    lens = [int(n) for n in lengths]
+    step_tile, step_code, count = oracle_schedule.runtime_tables(
+        [{"b": b} for b in range(B)], [("p", 0, 1, pages, lambda v: v["p"] * 16 >= lens[v["b"]])])
+    assert int(got["count"][0]) == count == sum(max(1, -(-n // 16)) for n in lens)
+    np.testing.assert_array_equal(got["step_tile"].cpu().numpy(), step_tile)
+    np.testing.assert_array_equal(got["step_code"].cpu().numpy(), step_code)
+    np.testing.assert_array_equal(got["tile_steps"].cpu().numpy(), np.cumsum([0] + [max(1, -(-n // 16)) for n in lens]))

@@ -7,9 +7,10 @@ none of whose blocks run keeps one empty step at block 0; each step gets its cod
 moved to the front in (t, kb) order and the rest follow in order (a stable partition); the count of kept
 steps is the third output.
 
-Here it is one workgroup of 1024 threads, generated from the mask expression: the waves evaluate the masks
-64 blocks per ballot into words kept in LDS, a block-wide scan turns the tiles' kept counts into offsets, and
-each wave writes one word's entries at ballot-prefix positions. Besides the reference's three outputs it writes `tile_steps`,
+Here it is a few workgroups of 1024 threads, generated from the mask expression. Every workgroup evaluates
+all the masks, 64 blocks per ballot, into words kept in LDS, and a block-wide scan turns the tiles' kept
+counts into offsets; this part is cheap and repeated, so no workgroup waits for another. Each workgroup then
+writes its own range of words' entries, a wave per word, at ballot-prefix positions. Besides the reference's three outputs it writes `tile_steps`,
 each pattern tile's first kept step (and the total at the end), which the kernels use to find a tile's steps
 without a search.
 """
@@ -54,6 +55,8 @@ def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg]) -> str
                           f"{MAX_WORDS * 64} (tile, block) pairs")
     waves = THREADS // 64
     rounds = -(-pt // waves)
+    groups = builder_groups(words)
+    wpg = -(-words // groups)  # words each workgroup writes
     return f"""
 {struct}
 // Step tables for `{plan.nest.name}`: {pt} pattern tiles x {count} blocks of `{phase.var}`, as {words} words of
@@ -120,10 +123,11 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {name}(const {name}_args
   }}
   __syncthreads();
   const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  const int w_end = ak_imin((int)(blockIdx.x + 1) * {wpg}, {words});
 #pragma unroll 4
-  for (int i = 0; i < {-(-words // waves)}; ++i) {{
-    const int w = wave + {waves} * i;
-    if (w >= {words}) break;
+  for (int i = 0; i < {-(-wpg // waves)}; ++i) {{
+    const int w = blockIdx.x * {wpg} + wave + {waves} * i;
+    if (w >= w_end) break;
     const int t = w / {nb}, wi = w % {nb}, k0 = wi * 64, kb = k0 + lane;
     int first = first_t[t], last = last_t[t], before = before_w[w];
     const int empty = first < 0;
@@ -141,12 +145,17 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {name}(const {name}_args
       args.rt_step_code[at] = code;
     }}
   }}
-  if (tid == 0) {{
+  if (blockIdx.x == 0 && tid == 0) {{
     args.rt_count[0] = total;
     args.rt_tile_steps[{pt}] = total;
   }}
 }}
 """
+
+
+def builder_groups(words: int) -> int:
+    """Workgroups of the builder: about 32 mask words (2048 table entries) each, at most 64."""
+    return max(1, min(64, -(-words // 32)))
 
 
 def attach_step_builder(prog: Program, plan: Plan, sch: Schedule, kernel_name: str) -> None:
@@ -164,5 +173,6 @@ def attach_step_builder(prog: Program, plan: Plan, sch: Schedule, kernel_name: s
         prog.workspace[ws] = 4 * n
         args.append(Arg("workspace", ws, "int* __restrict__", f"rt_{ws}"))
     prog.source += builder_source(plan, sch, name, args)
-    prog.launches.insert(0, Launch(name, args, (1, 1, 1), (THREADS, 1, 1), 0))
+    words = sch.pattern_tiles * -(-plan.phases[0].range.count // 64)
+    prog.launches.insert(0, Launch(name, args, (builder_groups(words), 1, 1), (THREADS, 1, 1), 0))
     prog.notes["step_builder"] = name

@@ -96,8 +96,9 @@ def summarize(stamps: Any, name: str, config: Any, calls: int, device_s: float, 
 
 
 def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile:
-    """Time a generated kernel: one warm-up call, then `runs` calls, each bracketed by HIP events on the
-    current stream; the median per call."""
+    """Time a generated kernel: one warm-up call, then `runs` calls back to back with HIP events between
+    them on the current stream; the median per call (with trace regions when the kernel was generated with
+    them)."""
     import torch
 
     from . import runtime
@@ -108,20 +109,23 @@ def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile
     workgroups = program.notes.get("trace_workgroups", 0) if lowered.trace else 0
     lowered.run(*inputs)
     torch.cuda.synchronize()
-    samples, stamps = [], None
-    for _ in range(runs):
-        start, stop = runtime.Event(), runtime.Event()
-        start.record(stream)
+    # The calls run back to back, with an event between consecutive ones, so the GPU stays busy while the
+    # host prepares the next launch and host time never counts as device time.
+    events = [runtime.Event() for _ in range(runs + 1)]
+    traces = []
+    events[0].record(stream)
+    for k in range(runs):
         if workgroups:
-            _, trace = program.run_traced(*inputs)
+            traces.append(program.run_traced(*inputs)[1])
         else:
             lowered.run(*inputs)
-        stop.record(stream)
-        if workgroups:
-            torch.cuda.synchronize()
-            t = trace[: workgroups * TRACE_FIELDS].cpu()
-            stamps = t if stamps is None else stamps + t
-        samples.append(start.elapsed_ms(stop) * 1e-3)
+        events[k + 1].record(stream)
+    torch.cuda.synchronize()
+    samples = [events[k].elapsed_ms(events[k + 1]) * 1e-3 for k in range(runs)]
+    stamps = None
+    for trace in traces:
+        t = trace[: workgroups * TRACE_FIELDS].cpu()
+        stamps = t if stamps is None else stamps + t
     device_s = statistics.median(samples)
     if workgroups:
         result = summarize(stamps.numpy(), lowered.plan.nest.name, lowered.config, runs, device_s, workgroups)

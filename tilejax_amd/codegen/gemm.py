@@ -41,7 +41,8 @@ from .program import Arg, Launch, Program, c_struct
 
 __all__ = ["GemmMatch", "match", "lower"]
 
-THREADS = 256
+THREADS = 256  # the fixup kernel's workgroup
+WAVE_GRID = (2, 2)  # waves of the matmul workgroup along M and N
 MFMA = 32  # 32x32x16 bf16 MFMA tiles
 TRACE = "ak_trace"  # per workgroup: input-wait, pipeline-fill, output, compute ticks (s_memrealtime) and steps
 TRACE_FIELDS = 5
@@ -352,7 +353,7 @@ class _Gemm:
             self.tables["tile_steps"] = static_tile_steps(sch)
         args = self._args()
         source = self._source(args)
-        launches = [Launch(self.name, args, (grid, 1, 1), (THREADS, 1, 1), 0)]
+        launches = [Launch(self.name, args, (grid, 1, 1), (64 * WAVE_GRID[0] * WAVE_GRID[1], 1, 1), 0)]
         workspace = {}
         if self.trace:
             workspace[TRACE] = grid * TRACE_FIELDS * 8
@@ -407,7 +408,9 @@ class _Gemm:
     def _source(self, args: List[Arg]) -> str:
         plan, sch, m, hw = self.plan, self.sch, self.m, self.hw
         bm, bn, bk, S = hw.bm, hw.bn, hw.bk, hw.stages
-        wtm, wtn = bm // 2, bn // 2
+        WM, WN = WAVE_GRID
+        T = 64 * WM * WN  # threads of the workgroup
+        wtm, wtn = bm // WM, bn // WN
         mi, ni = wtm // MFMA, wtn // MFMA
         k16s = bk // 16
         kslices = m.tk // bk
@@ -430,10 +433,10 @@ class _Gemm:
         nt = m.b_nt
         kca = bk // 8  # 16-byte chunks per K-contiguous row
         nc = bn // 8  # 16-byte chunks per N-contiguous row (B of `a @ b`)
-        a_ld = bm * bk // 8 // THREADS
-        b_ld = bn * bk // 8 // THREADS
+        a_ld = bm * bk // 8 // T
+        b_ld = bn * bk // 8 // T
         if a_ld < 1 or b_ld < 1 or (not nt and 64 % nc):
-            raise KernelError(f"matmul hardware tile {bm} x {bn} x {bk} is too small for a 256-thread workgroup")
+            raise KernelError(f"matmul hardware tile {bm} x {bn} x {bk} is too small for a {T}-thread workgroup")
 
         def swa(row: str) -> str:  # K-contiguous rows: chunk XOR, conflict-free ds_read_b128 (64 banks)
             return {8: f"((({row}) >> 1) & 7)", 4: f"((({row}) >> 2) & 3)", 2: f"((({row}) >> 3) & 1)"}[kca]
@@ -500,7 +503,7 @@ class _Gemm:
         if sch.fills:
             fill_decode = "\n      ".join(decode_fill(plan, sch, "t"))
             fill_block = (f"if (kind == 1) {{\n      {fill_decode}\n      const long long obase = {o_base};\n      "
-                          f"{_store_constant(bm, bn, out_bf16, O, 'obase', ldo, fill_value)}\n      continue;\n    }}")
+                          f"{_store_constant(bm, bn, out_bf16, O, 'obase', ldo, fill_value, T)}\n      continue;\n    }}")
         setup = "\n    ".join(steps_setup)
 
         L: List[str] = []
@@ -514,10 +517,10 @@ class _Gemm:
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sa{s}[{bm * bk}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sb{s}[{bn * bk}];")
         w(f"""
-extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
+extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS addresses stay in SGPRs
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / {WN}, wn = wave % {WN};
   // Each wave's buffer_load ... lds fills 1 KiB of a stage, lane l's 16 bytes at 16 l: the lane loads the
   // global chunk that belongs at that (swizzled) position.
   const int a_row = wave * {64 // kca} + lane / {kca};
@@ -559,7 +562,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     {tile_decode}
     const long long obase = {o_base};
     if (kind == 2) {{
-      {_store_constant(bm, bn, out_bf16, O, "obase", ldo, const_value)}
+      {_store_constant(bm, bn, out_bf16, O, "obase", ldo, const_value, T)}
       continue;
     }}
     {setup}
@@ -595,16 +598,16 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
 
         def issue(g: str, s: int, ind: str) -> List[str]:
             out = [f"{ind}{{ const int k0 = k_of({g});"]
-            rows_a = THREADS // kca
+            rows_a = T // kca
             for c in range(a_ld):
-                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, AK_LDS(&ak_sa{s}[({c * THREADS} + wave * 64) * 8]), "
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, AK_LDS(&ak_sa{s}[({c * T} + wave * 64) * 8]), "
                            f"16, a_voff, {c * rows_a}u * pa + (unsigned)k0 * 2u, 0, 0);")
             for c in range(b_ld):
                 if nt:
                     soff = f"{c * rows_a}u * pb + (unsigned)k0 * 2u"
                 else:
-                    soff = f"(unsigned)(k0 + {c * (THREADS // nc)}) * pb"
-                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, AK_LDS(&ak_sb{s}[({c * THREADS} + wave * 64) * 8]), "
+                    soff = f"(unsigned)(k0 + {c * (T // nc)}) * pb"
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, AK_LDS(&ak_sb{s}[({c * T} + wave * 64) * 8]), "
                            f"16, b_voff, {soff}, 0, 0);")
             out.append(f"{ind}}}")
             return out
@@ -685,15 +688,22 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             w(f"{ind}const unsigned long long tr_o0 = {now}; tr_comp += tr_o0 - tr_c0;")
         if self.split:
             w(f"""    if (kind == 3) {{  // a chunk: its f32 partial sums go to workspace slot `slot`, lane-contiguous
-      float* part = args.gm_part + (long long)slot * {bm * bn};
+      // The lane index goes through an empty asm, as in the epilogue: the stores' addresses are then computed
+      // here, not hoisted above the K loop where they would take the registers it needs.
+      int lane_p = lane;
+      asm volatile("" : "+v"(lane_p));
+      float* part = args.gm_part + (long long)slot * {bm * bn} + (wave * {mi * ni * 4 * 64} + lane_p) * 4;
+      // One accumulator tile at a time through VGPRs (the empty asm orders the copies).
 #pragma unroll
       for (int i_ = 0; i_ < {mi}; ++i_)
 #pragma unroll
-        for (int j_ = 0; j_ < {ni}; ++j_)
+        for (int j_ = 0; j_ < {ni}; ++j_) {{
+          ak_f32x16 t_ = acc[i_][j_];
+          asm volatile("" : "+v"(t_));
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4)
-            *(ak_f32x4*)(part + ((((wave * {mi} + i_) * {ni} + j_) * 4 + g4) * 64 + lane) * 4) =
-                ak_f32x4{{acc[i_][j_][g4 * 4], acc[i_][j_][g4 * 4 + 1], acc[i_][j_][g4 * 4 + 2], acc[i_][j_][g4 * 4 + 3]}};
+            *(ak_f32x4*)(part + ((i_ * {ni} + j_) * 4 + g4) * 256) = ak_f32x4{{t_[g4 * 4], t_[g4 * 4 + 1], t_[g4 * 4 + 2], t_[g4 * 4 + 3]}};
+        }}
       {"tr_out += " + now + " - tr_o0;" if self.trace else ""}
       continue;
     }}""")
@@ -737,7 +747,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_fixup(const 
   const int p = blockIdx.x / {per_item};
   const int e = (blockIdx.x % {per_item}) * {THREADS} + threadIdx.x;
   const int lane_e = e & 63, g4 = (e >> 6) & 3, j_ = (e >> 8) % {ni}, i_ = (e >> 8) / {ni} % {mi};
-  const int wave = (e >> 8) / {ni * mi}, wm = wave >> 1, wn = wave & 1;
+  const int wave = (e >> 8) / {ni * mi}, wm = wave / {WN}, wn = wave % {WN};
   const float* part = args.gm_part + (long long)p * {split * bm * bn} + e * 4;
   ak_f32x4 sum = *(const ak_f32x4*)part;
 #pragma unroll
@@ -776,19 +786,19 @@ def _store4(O: str, obase: str, ldo: int, bf16: bool) -> str:
     return f"*(ak_f32x4*)({O} + {obase} + (long long)er * {ldo} + ec0) = ak_f32x4{{res[0], res[1], res[2], res[3]}};"
 
 
-def _store_constant(bm: int, bn: int, bf16: bool, O: str, obase: str, ldo: int, value: str) -> str:
+def _store_constant(bm: int, bn: int, bf16: bool, O: str, obase: str, ldo: int, value: str, threads: int) -> str:
     """Source storing one value over the workgroup's hardware sub-tile (sm, sn)."""
     if bf16:
         return (
             f"{{ const unsigned w_ = ak_bf16_bits((float)({value})) * 0x10001u; const ak_u32x4 v_ = {{w_, w_, w_, w_}};\n"
-            f"        for (int c_ = tid; c_ < {bm * bn // 8}; c_ += {THREADS}) {{\n"
+            f"        for (int c_ = tid; c_ < {bm * bn // 8}; c_ += {threads}) {{\n"
             f"          const int r_ = c_ / {bn // 8}, k_ = c_ % {bn // 8};\n"
             f"          *(ak_u32x4*)((ak_u16*){O} + {obase} + (long long)(sm * {bm} + r_) * {ldo} + sn * {bn} + k_ * 8) = v_;\n"
             "        } }"
         )
     return (
         f"{{ const float f_ = (float)({value}); const ak_f32x4 v_ = {{f_, f_, f_, f_}};\n"
-        f"        for (int c_ = tid; c_ < {bm * bn // 4}; c_ += {THREADS}) {{\n"
+        f"        for (int c_ = tid; c_ < {bm * bn // 4}; c_ += {threads}) {{\n"
         f"          const int r_ = c_ / {bn // 4}, k_ = c_ % {bn // 4};\n"
         f"          *(ak_f32x4*)({O} + {obase} + (long long)(sm * {bm} + r_) * {ldo} + sn * {bn} + k_ * 4) = v_;\n"
         "        } }"

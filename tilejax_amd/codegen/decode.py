@@ -499,21 +499,40 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
   const int ts = args.rt_tile_steps[t], te = args.rt_tile_steps[t + 1];
   const int w0 = ts / per, w1 = (te - 1) / per;
   const int n = w1 - w0 + 1;
+  // The partials' loads go out four at a time (they are independent); the sums run in partial order.
   for (int r = threadIdx.x; r < {R}; r += {THREADS}) {{
+    const float* mp = args.dc_m + (t + w0) * {R} + r;
+    const float* lp = args.dc_l + (t + w0) * {R} + r;
     float mm = -__builtin_inff();
-    for (int k = 0; k < n; ++k) mm = fmaxf(mm, args.dc_m[(t + w0 + k) * {R} + r]);
-    float ls = 0.f;
-    for (int k = 0; k < n; ++k) {{
-      const float wk = ak_exp(args.dc_m[(t + w0 + k) * {R} + r] - mm);
-      dc_w[k][r] = wk;
-      ls += wk * args.dc_l[(t + w0 + k) * {R} + r];
+    int k = 0;
+    for (; k + 4 <= n; k += 4) {{
+      const float a0 = mp[k * {R}], a1 = mp[(k + 1) * {R}], a2 = mp[(k + 2) * {R}], a3 = mp[(k + 3) * {R}];
+      dc_w[k][r] = a0; dc_w[k + 1][r] = a1; dc_w[k + 2][r] = a2; dc_w[k + 3][r] = a3;
+      mm = fmaxf(fmaxf(fmaxf(fmaxf(mm, a0), a1), a2), a3);
     }}
+    for (; k < n; ++k) {{ const float a = mp[k * {R}]; dc_w[k][r] = a; mm = fmaxf(mm, a); }}
+    float ls = 0.f;
+    for (k = 0; k + 4 <= n; k += 4) {{
+      const float l0 = lp[k * {R}], l1 = lp[(k + 1) * {R}], l2 = lp[(k + 2) * {R}], l3 = lp[(k + 3) * {R}];
+      const float e0 = ak_exp(dc_w[k][r] - mm), e1 = ak_exp(dc_w[k + 1][r] - mm);
+      const float e2 = ak_exp(dc_w[k + 2][r] - mm), e3 = ak_exp(dc_w[k + 3][r] - mm);
+      dc_w[k][r] = e0; dc_w[k + 1][r] = e1; dc_w[k + 2][r] = e2; dc_w[k + 3][r] = e3;
+      ls += e0 * l0; ls += e1 * l1; ls += e2 * l2; ls += e3 * l3;
+    }}
+    for (; k < n; ++k) {{ const float e = ak_exp(dc_w[k][r] - mm); dc_w[k][r] = e; ls += e * lp[k * {R}]; }}
     dc_lsum[r] = ls;
   }}
   __syncthreads();
   auto dc_acc_at = [&](int r, int c) -> float {{
+    const float* ap = args.dc_acc + (long long)(t + w0) * {R * W} + r * {W} + c;
     float v = 0.f;
-    for (int k = 0; k < n; ++k) v += dc_w[k][r] * args.dc_acc[(long long)(t + w0 + k) * {R * W} + r * {W} + c];
+    int k = 0;
+    for (; k + 4 <= n; k += 4) {{
+      const float a0 = ap[(long long)k * {R * W}], a1 = ap[(long long)(k + 1) * {R * W}];
+      const float a2 = ap[(long long)(k + 2) * {R * W}], a3 = ap[(long long)(k + 3) * {R * W}];
+      v += dc_w[k][r] * a0; v += dc_w[k + 1][r] * a1; v += dc_w[k + 2][r] * a2; v += dc_w[k + 3][r] * a3;
+    }}
+    for (; k < n; ++k) v += dc_w[k][r] * ap[(long long)k * {R * W}];
     return v;
   }};
   ak_u16* op = args.{m.out.name}_out + ({o_base});

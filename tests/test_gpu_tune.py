@@ -62,3 +62,58 @@ def test_tuning_beats_small_default_tiles():
     assert small_matmul.lower(x, y).config == tuning.config
     scale = small_matmul(x, y).float().abs().max().item()
     assert small_matmul.verify(x, y) <= 1e-2 * scale  # (verify asserts the dtype tolerances itself)
+
+
+def _attention_inputs(shape, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(*shape, generator=g).to(torch.bfloat16) for _ in range(3))
+    q = (q.float() * shape[-1] ** -0.5).to(torch.bfloat16)
+    return q.cuda(), k.cuda(), v.cuda()
+
+
+@pytest.mark.parametrize("shape, blocks", [((2, 4, 1024, 128), (256, 256)), ((1, 16, 4096, 128), (512, 512))])
+def test_attention_profile_has_trace_regions(shape, blocks):
+    """The flash family's regions: the first block's wait is the fill, later waits and compute per block;
+    a traced build computes what the untraced one does."""
+    from examples.causal_attention import AttentionBlocks, causal_attention
+
+    q, k, v = _attention_inputs(shape)
+    tiles = AttentionBlocks(*blocks)
+    print(f"profile causal_attention {shape} {blocks}", flush=True)
+    p = autokernel.profile(causal_attention, q, k, v, tiles, runs=3)
+    print(p, flush=True)
+    assert p.calls == 3 and p.regions
+    assert 0 < p.compute_s < p.device_s and p.wait_s >= p.fill_s > 0
+    assert p.bottleneck in ("dma", "overhead", "compute")
+    plain = causal_attention.lower(q, k, v, tiles)
+    traced = causal_attention.lowered(causal_attention.signature(q, k, v), plain.config, trace=True)
+    out, trace = traced.program.run_traced(q, k, v)
+    assert trace is not None and torch.equal(out, plain.run(q, k, v))
+    # a workgroup's slices are the key blocks of its work item (the item table's block count column)
+    items = traced.program.tables["fa_items"].reshape(-1, 5 + 2 * traced.program.notes["waves"])
+    assert trace.view(-1, 5)[:, 4].sum().item() == int(items[:, 3].sum())
+
+
+def test_decode_profile_has_trace_regions():
+    """The decode family's regions over its attention kernel; slices are the step table's steps."""
+    from examples.decode import paged_gqa_decode
+
+    g = torch.Generator().manual_seed(5)
+    B, pages, P, W = 8, 64, 16, 1024
+    q = (torch.randn(B, 1, 32, 128, generator=g) * 128**-0.5).to(torch.bfloat16).cuda()
+    kp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    vp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    table = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32).cuda()
+    lengths = torch.tensor([0, 1, 17, 300, 512, 777, 1000, 1024], dtype=torch.int32).cuda()
+    print("profile paged_gqa_decode 8 sequences", flush=True)
+    p = autokernel.profile(paged_gqa_decode, q, kp, vp, table, lengths, runs=3)
+    print(p, flush=True)
+    assert p.calls == 3 and p.regions
+    assert 0 < p.compute_s < p.device_s and p.wait_s >= p.fill_s > 0
+    # one step per page in use, one empty step per empty sequence (the reference's table)
+    want = sum(-(-int(n) // P) for n in lengths.tolist()) + sum(1 for n in lengths.tolist() if n == 0)
+    assert p.steps == want
+    plain = paged_gqa_decode.lower(q, kp, vp, table, lengths)
+    traced = paged_gqa_decode.lowered(paged_gqa_decode.signature(q, kp, vp, table, lengths), plain.config, trace=True)
+    out, trace = traced.program.run_traced(q, kp, vp, table, lengths)
+    assert trace is not None and torch.equal(out, plain.run(q, kp, vp, table, lengths))

@@ -18,6 +18,16 @@ def test_summarize_averages_workgroups_and_calls():
     assert np.isclose(p.other_s, 20e-6 - (250 + 25 + 550) * tick)
 
 
+def test_summarize_divides_by_the_workgroups_that_run_side_by_side():
+    # four workgroups on two slots (each slot runs two in turn): a slot's time is the sum of its two
+    stamps = np.array([[100, 50, 10, 300, 2]] * 4)
+    p = summarize(stamps, "k", None, calls=1, device_s=10e-6, workgroups=4, slots=2)
+    tick = 1 / CLOCK_HZ
+    assert np.isclose(p.compute_s, 600 * tick) and np.isclose(p.wait_s, 200 * tick) and p.steps == 8
+    # no more slots than workgroups
+    assert np.isclose(summarize(stamps, "k", None, 1, 10e-6, 4, slots=16).compute_s, 300 * tick)
+
+
 def test_bottleneck_thresholds():
     def prof(wait=0.0, out=0.0, compute=10.0, fill=0.0, regions=True):
         return KernelProfile("k", None, 1, 10.0, regions, 4, wait, fill, out, compute)

@@ -46,10 +46,10 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
         return gemm.lower(plan, schedule, pipeline, found, name, trace=trace)
     found = flash.match(plan)
     if found is not None:
-        return flash.lower(plan, schedule, pipeline, found, name)
+        return flash.lower(plan, schedule, pipeline, found, name, trace=trace)
     found = decode.match(plan)
     if found is not None:
-        return decode.lower(plan, schedule, pipeline, found, name)
+        return decode.lower(plan, schedule, pipeline, found, name, trace=trace)
     raise KernelError(
         f"{plan.nest.name}: the gfx950 backend has no lowering for this loop nest's tile code yet "
         "(it lowers matmuls with pointwise epilogues and online-softmax attention)"

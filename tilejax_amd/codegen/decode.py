@@ -43,7 +43,7 @@ from .common import Index, strides, tile_base
 from .device import PRELUDE
 from .expr import ElementEmitter, literal
 from .flash import Softmax, _is, _strip, softmax_structure
-from .program import Arg, Launch, Program, c_struct
+from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 from .steps import attach_step_builder
 
 __all__ = ["DecodeMatch", "match", "lower"]
@@ -108,8 +108,9 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
 
 
 class _Decode:
-    def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str) -> None:
+    def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
+        self.trace = trace
         if m.rows != 32 or m.page != 16 or m.width % (32 * WAVES):
             raise KernelError(f"the gfx950 decode lowering takes 32 query rows, pages of 16 positions and widths "
                               f"that are multiples of {32 * WAVES} (got {m.rows}, {m.page}, {m.width})")
@@ -189,6 +190,9 @@ class _Decode:
         args.append(Arg("workspace", "dc_q", "ak_u16* __restrict__", "dc_q"))
         for ws in ("dc_m", "dc_l", "dc_acc"):
             args.append(Arg("workspace", ws, "float* __restrict__", ws))
+        if self.trace:
+            workspace[TRACE] = self.grid * TRACE_FIELDS * 8
+            args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
         struct = c_struct(f"{self.name}_args", args)
         source = "\n".join([f"// Generated by tilejax_amd for `{plan.nest.name}`: gfx950 split-KV decode attention.",
                             PRELUDE, struct, self._setup_source(), self._attention_source(), self._merge_source()])
@@ -199,7 +203,9 @@ class _Decode:
                       Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (THREADS, 1, 1), 0)],
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
             tables=tables, workspace=workspace, lds_bytes=self.lds,
-            notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page},
+            notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
+                   # trace regions cover the attention kernel; a slice is one step (one page) of the step table
+                   "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": 1},
         )
         attach_step_builder(prog, plan, sch, self.name)
         return prog
@@ -269,7 +275,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
   const int count = args.rt_count[0];
   const int per = (count + {self.grid - 1}) / {self.grid};
   const int g0 = blockIdx.x * per, n = ak_imin(g0 + per, count) - g0;
-  if (n <= 0) return;
+  {self._trace_start()}
+  if (n <= 0) {{ {self._trace_write("0")} return; }}
   // The range's steps, decoded once into LDS: tile, code, K and V page byte offsets. The loop then reads
   // them from LDS, so no global load other than the pages themselves sits in the vector memory queue.
   for (int j = tid; j < n; j += {THREADS}) {{
@@ -314,6 +321,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
   float m_run = {literal(m.sm.m_init)}, l_run = 0.f;
   int cur_t = -1;
   auto flush = [&](int t) {{
+    {f"const unsigned long long tr_f0 = {NOW};" if self.trace else ""}
     const int slot = t + blockIdx.x;
     const int row = lane & 31;
     if (wave == 0 && lane < 32) {{
@@ -326,6 +334,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4)
         *(ak_f32x4*)(ap + 32 * dt + 8 * g4) = ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};
+    {f"tr_out += {NOW} - tr_f0;" if self.trace else ""}
   }};
   auto start_tile = [&](int t) {{
     const ak_u16* qp = args.dc_q + (long long)t * {R * W} + cb + 8 * (lane >> 4);
@@ -372,10 +381,16 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a = o.append
             a(f"{ind}{{ const int j_ = {j};")
             a(f"{ind}  const int t = __builtin_amdgcn_readfirstlane(dc_st[j_][0]), code = __builtin_amdgcn_readfirstlane(dc_st[j_][1]);")
+            if self.trace:
+                a(f"{ind}  const unsigned long long tr_w0 = {NOW}, tr_o0 = tr_out;")
             a(f"{ind}  if (t != cur_t) {{ if (cur_t >= 0) flush(cur_t); start_tile(t); cur_t = t; AK_WAIT_VM(0); }}")
             a(f"{ind}  AK_WAIT_VM({wait_n});")
             # every wave is past step j - 1, so its V stage is free; every thread's part of V(j) has landed
             a(f'{ind}  asm volatile("s_barrier" ::: "memory");')
+            if self.trace:
+                # the first step's wait is the pipeline fill; a flush inside the wait is output time
+                a(f"{ind}  {{ const unsigned long long d_ = {NOW} - tr_w0 - (tr_out - tr_o0);"
+                  f" if (j_ == 0) tr_fill = d_; else tr_wait += d_; }}")
             o.extend(issue_v(f"j_ + {D - 1}", (u + D - 1) % D, ind + "  "))
             a(f"{ind}  const bool run = !(code & 4);")
             # partial S^T over this wave's columns
@@ -458,8 +473,25 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             ind = ind[:-2]
             w(f"{ind}}}")
         w("  flush(cur_t);")
+        if self.trace:
+            w(f"  {self._trace_write('n')}")
         w("}")
         return "\n".join(L)
+
+    def _trace_start(self) -> str:
+        if not self.trace:
+            return ""
+        return (f"unsigned long long tr_fill = 0, tr_wait = 0, tr_out = 0; "
+                f"const unsigned long long tr_i0 = {NOW};")
+
+    def _trace_write(self, steps: str) -> str:
+        """Wave 0 writes the workgroup's region totals: waits (fill included), fill, output, compute, steps."""
+        if not self.trace:
+            return ""
+        return (f"if (threadIdx.x == 0) {{ const unsigned long long tr_e = {NOW}; "
+                f"unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
+                f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_out; "
+                f"tr[3] = tr_e - tr_i0 - tr_fill - tr_wait - tr_out; tr[4] = (unsigned long long)({steps}); }}")
 
     def _merge_source(self) -> str:
         plan, sch, m = self.plan, self.sch, self.m
@@ -545,7 +577,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
 """
 
 
-def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: str) -> Program:
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: str, trace: bool = False) -> Program:
     if m.out.dtype.name != "bfloat16":
         raise KernelError("the gfx950 decode lowering stores bf16 outputs")
-    return _Decode(plan, sch, m, name).program()
+    return _Decode(plan, sch, m, name, trace).program()

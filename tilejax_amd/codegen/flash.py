@@ -46,7 +46,7 @@ from ..schedule import CODE_SHIFT, STEP_CODE, Schedule
 from .common import Index, decode_tile, static_tile_steps, strides, tile_base
 from .device import PRELUDE
 from .expr import Emitter, Interval, intervals, literal, nodes_between
-from .program import Arg, Launch, Program, c_struct
+from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 
 __all__ = ["FlashMatch", "match", "lower"]
 
@@ -54,6 +54,8 @@ LOG2E = 1.4426950408889634
 RESCALE_SLACK = 8.0  # natural-log units: p stays below e^8 between rescales
 MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 once a row has a real score
 STAGES = 3  # LDS stages of K and V blocks: loads run two blocks ahead, one barrier per block
+K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
+V_AHEAD = 4  # V fragments in flight ahead of the O MFMAs
 
 
 @dataclass
@@ -256,8 +258,10 @@ def _loop_window(op: Operand, var: str) -> Tuple[int, Any]:
 
 
 class _Flash:
-    def __init__(self, plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str) -> None:
+    def __init__(self, plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str,
+                 trace: bool = False) -> None:
         self.plan, self.sch, self.pipeline, self.m, self.name = plan, sch, pipeline, m, name
+        self.trace = trace
         if m.d % 32 or m.dv % 32 or m.d > 128 or m.dv > 128:
             raise KernelError(f"the gfx950 attention lowering takes head dims that are multiples of 32 up to 128 "
                               f"(got {m.d} and {m.dv})")
@@ -432,17 +436,25 @@ class _Flash:
         source = self._source(args, stride)
         launches = [Launch(self.name, args, (max(len(items), 1), 1, 1), (64 * nw, 1, 1), 0)]
         workspace = {}
+        if self.trace:
+            workspace[TRACE] = max(len(items), 1) * TRACE_FIELDS * 8
         if merges:
             workspace["fa_part"] = self.slots * self.bq * (m.dv + 2) * 4
             per_item = self.bq * m.dv // 4 // 256
             launches.append(Launch(f"{self.name}_merge", args, (len(merges) * per_item, 1, 1), (256, 1, 1), 0))
         flop = 2.0 * sum(w for w in weights) * 32 * self.bkv * (m.d + m.dv)
+        lds = STAGES * self.bkv * (m.d + m.dv) * 2
         return Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
             inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
-            lds_bytes=STAGES * self.bkv * (m.d + m.dv) * 2,
+            lds_bytes=lds,
             notes={"family": "flash", "block_q": self.bq, "block_kv": self.bkv, "waves": nw, "items": len(items),
-                   "executed_flop": flop, "split_items": len(merges), "chunks": self.slots},
+                   "executed_flop": flop, "split_items": len(merges), "chunks": self.slots,
+                   # the reference's step is (query tile, key block) of the spec; a workgroup's slice here is
+                   # one block of bkv keys for its bq rows
+                   "trace_workgroups": max(len(items), 1) if self.trace else 0,
+                   "trace_slots": min(max(len(items), 1), gfx950.CUS * max(1, gfx950.LDS_BYTES // lds)),
+                   "slices_per_step": (m.rows // self.bq) * (m.bk // self.bkv)},
         )
 
     def _args(self) -> List[Arg]:
@@ -459,6 +471,8 @@ class _Flash:
             args.append(Arg("table", name, "const int* __restrict__", name))
         if "fa_merge" in self.tables:
             args.append(Arg("workspace", "fa_part", "float* __restrict__", "fa_part"))
+        if self.trace:
+            args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
         return args
 
     def _source(self, args: List[Arg], stride: int) -> str:
@@ -595,6 +609,16 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
   float m_run = {literal(m.m_init)}, l_run = 0.f;""")
+        tr = self.trace
+        if tr:
+            # trace regions: the wait for block 0 is the pipeline fill; later blocks' waits (their loads and the
+            # barrier) are input waits; the rest of the loop is compute; the stores are output
+            w(f"  unsigned long long tr_fill = 0, tr_wait = 0;")
+            w(f"  const unsigned long long tr_i0 = {NOW};")
+        trace_write = (f"if (tid == 0) {{ const unsigned long long tr_e = {NOW}; "
+                       f"unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
+                       f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_e - tr_c1; "
+                       f"tr[3] = tr_c1 - tr_i0 - tr_fill - tr_wait; tr[4] = (unsigned long long)nblk; }}") if tr else ""
 
         def issue(b: str, s: int, ind: str) -> List[str]:
             out = [f"{ind}{{ const int* bp = args.fa_blocks + 2 * (boff + ({b}));",
@@ -619,25 +643,54 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             for t in range(kt):
                 a(f"{ind}  #pragma unroll")
                 a(f"{ind}  for (int r = 0; r < 16; ++r) st[{t}][r] = 0.f;")
-            for t in range(kt):
-                for sl in range(ds):
-                    a(f"{ind}  st[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const ak_bf16x8*)(ks + k_roff[{sl}] + {t * 32 * D * 2}), qf[{sl}], st[{t}], 0, 0, 0);")
-            a(f"{ind}  float mx = -__builtin_inff();")
-            a(f"{ind}  if (b_ < f_w) {{")
-            for t in range(kt):
-                a(f"{ind}    #pragma unroll")
-                a(f"{ind}    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[{t}][r]);")
-            a(f"{ind}  }} else {{")
+            # S^T = K Q^T: the key tiles' MFMA chains alternate (a chain's next MFMA waits for its last), and
+            # the K fragments are read K_AHEAD MFMAs ahead of use, so LDS latency stays hidden.
+            order = [(t, sl) for sl in range(ds) for t in range(kt)]
+            ahead = min(K_AHEAD, len(order))
+            a(f"{ind}  ak_bf16x8 kf[{len(order)}];")
+            for i, (t, sl) in enumerate(order[:ahead]):
+                a(f"{ind}  kf[{i}] = *(const ak_bf16x8*)(ks + k_roff[{sl}] + {t * 32 * D * 2});")
+            for i, (t, sl) in enumerate(order):
+                a(f"{ind}  st[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[{i}], qf[{sl}], st[{t}], 0, 0, 0);")
+                if i + ahead < len(order):
+                    t2, sl2 = order[i + ahead]
+                    a(f"{ind}  kf[{i + ahead}] = *(const ak_bf16x8*)(ks + k_roff[{sl2}] + {t2 * 32 * D * 2});")
+            # O^T += V^T P^T: the first V_AHEAD fragments (two transposed reads each) go out now, beside the
+            # S MFMAs and the softmax; the rest V_AHEAD MFMAs ahead of use.
+            v_order = [(kk, dt) for kk in range(ks) for dt in range(dt_n)]
+            v_ahead = min(V_AHEAD, len(v_order))
+
+            def v_read(i: int, ind: str) -> str:
+                kk, dt = v_order[i]
+                o1 = kk * 16 * DV * 2
+                return (f"{ind}  {{ const ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1}));"
+                        f" const ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1 + 8 * DV * 2}));"
+                        f" vf[{i}] = __builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)); }}")
+            a(f"{ind}  ak_bf16x8 vf[{len(v_order)}];")
+            for i in range(v_ahead):
+                a(v_read(i, ind))
+            a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, {ahead}, 0);")
+            for i in range(len(order)):
+                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
+                if i + ahead < len(order):
+                    a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);")
+            a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, {2 * v_ahead}, 0);")
+            # the mask's scores in place (blocks the mask keeps whole skip it); then one max for both
+            a(f"{ind}  if (b_ >= f_w) {{")
             for t in range(kt):
                 a(f"{ind}    #pragma unroll")
                 a(f"{ind}    for (int r = 0; r < 16; ++r) {{")
                 a(f"{ind}      const int ec = ec0 + {32 * t} + (r >> 2) * 8 + (r & 3); (void)ec;")
                 a(f"{ind}      const float sv = st[{t}][r];")
                 a(f"{ind}      {score_lines}")
-                a(f"{ind}      st[{t}][r] = (float)({score_expr}); mx = fmaxf(mx, st[{t}][r]);")
+                a(f"{ind}      st[{t}][r] = (float)({score_expr});")
                 a(f"{ind}    }}")
             a(f"{ind}  }}")
-            a(f"{ind}  mx = fmaxf(mx, __shfl_xor(mx, 32));")
+            a(f"{ind}  float mx = -__builtin_inff();")
+            for t in range(kt):
+                a(f"{ind}  #pragma unroll")
+                a(f"{ind}  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[{t}][r]);")
+            a(f"{ind}  mx = ak_xor32_max(mx);")
             a(f"{ind}  const float m_new = ak_maximum(m_run, mx);")
             # Lazy rescaling: the running max moves (and acc, l are rescaled) only when some row's new max
             # exceeds it by more than RESCALE_SLACK; otherwise p = exp(s - m_run) stays below e^slack and
@@ -662,14 +715,16 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                     a(f"{ind}      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[{t}][{8 * half} + r + 1], {LOG2E!r}f, mb));")
                     a(f"{ind}      ps += p0 + p1; pk[r >> 1] = ak_pack_bf16x2(p0, p1); }}")
                     a(f"{ind}    pf[{2 * t + half}] = __builtin_bit_cast(ak_bf16x8, (ak_u32x4){{pk[0], pk[1], pk[2], pk[3]}}); }}")
-            a(f"{ind}  ps += __shfl_xor(ps, 32);")
+            a(f"{ind}  ps = ak_xor32_sum(ps);")
             a(f"{ind}  l_run += ps;")
-            for kk in range(ks):
-                for dt in range(dt_n):
-                    o1 = kk * 16 * DV * 2
-                    a(f"{ind}  {{ ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1}));"
-                      f" ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1 + 8 * DV * 2}));")
-                    a(f"{ind}    acc[{dt}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pf[{kk}], acc[{dt}], 0, 0, 0); }}")
+            for i, (kk, dt) in enumerate(v_order):
+                a(f"{ind}  acc[{dt}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[{i}], pf[{kk}], acc[{dt}], 0, 0, 0);")
+                if i + v_ahead < len(v_order):
+                    a(v_read(i + v_ahead, ind))
+            for i in range(len(v_order)):
+                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
+                if i + v_ahead < len(v_order):
+                    a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);")
             a(f"{ind}}}")
             return o
 
@@ -685,12 +740,16 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
         for s in range(STAGES):
             w(f"    {{ const int b_ = b + {s};")
             w("      if (b_ < nblk) {")
+            if tr:
+                w(f"        const unsigned long long tr_w0 = {NOW};")
             # Block b_ has landed; the (at most STAGES - 2) later blocks issued may still be in flight.
             for ahead in range(STAGES - 2, 0, -1):
                 w(f"        {'if' if ahead == STAGES - 2 else 'else if'} (b_ + {ahead} < nblk) {{ AK_WAIT_VM({ahead * per_block}); }}")
             w("        " + ("else " if STAGES > 2 else "") + "{ AK_WAIT_VM(0); }")
             w("        AK_WAIT_LGKM0();")
             w('        asm volatile("s_barrier" ::: "memory");')
+            if tr:
+                w(f"        {{ const unsigned long long tr_w1 = {NOW}; if (b_ == 0) tr_fill = tr_w1 - tr_i0; else tr_wait += tr_w1 - tr_w0; }}")
             w(f"        if (b_ + {STAGES - 1} < nblk) {{")
             L.extend(issue(f"b_ + {STAGES - 1}", (s + STAGES - 1) % STAGES, "          "))
             w("        }")
@@ -698,6 +757,8 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             w("      }")
             w("    }")
         w("  }")
+        if tr:
+            w(f"  const unsigned long long tr_c1 = {NOW};")
         if self.slots:
             w(f"""  if (slot >= 0) {{  // a chunk: (m, l, acc) of its rows to the workspace, for the merge kernel
     float* part = args.fa_part + (long long)slot * {bq * (DV + 2)};
@@ -709,6 +770,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
         *(ak_f32x4*)(part + lr * {DV} + 32 * dt + g4 * 8 + (lane >> 5) * 4) =
             ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};
     if (lane < 32) {{ part[{bq * DV} + lr] = m_run; part[{bq * DV + bq} + lr] = l_run; }}
+    {trace_write}
     return;
   }}""")
         w(f"""  // Output: lane = query row er, acc[dt][r] = head dim 32 dt + (r / 4) * 8 + (lane / 32) * 4 + r % 4.
@@ -727,6 +789,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
       }}
       *(ak_u32x2*)(op + 32 * dt + g4 * 8 + (lane >> 5) * 4) = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
     }}
+  {trace_write}
 }}""")
         if self.slots:
             per_item = bq * DV // 4 // 256
@@ -766,7 +829,7 @@ extern "C" __global__ void __launch_bounds__(256) {self.name}_merge(const {self.
         return "\n".join(L)
 
 
-def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str) -> Program:
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str, trace: bool = False) -> Program:
     if m.out.dtype.name != "bfloat16":
         raise KernelError("the gfx950 attention lowering stores bf16 outputs")
-    return _Flash(plan, sch, pipeline, m, name).program()
+    return _Flash(plan, sch, pipeline, m, name, trace).program()

@@ -37,15 +37,13 @@ from ..schedule import CODE_SHIFT, FILL_TABLE, STEP_CODE, STEP_TILE, TILE_TABLE,
 from .common import Index, decode_fill, decode_tile, static_tile_steps, strides, tile_base, work_lists
 from .device import PRELUDE
 from .expr import Emitter, Interval, ctype, intervals, literal, nodes_between
-from .program import Arg, Launch, Program, c_struct
+from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 
 __all__ = ["GemmMatch", "match", "lower"]
 
 THREADS = 256  # the fixup kernel's workgroup
 WAVE_GRID = (2, 2)  # waves of the matmul workgroup along M and N
 MFMA = 32  # 32x32x16 bf16 MFMA tiles
-TRACE = "ak_trace"  # per workgroup: input-wait, pipeline-fill, output, compute ticks (s_memrealtime) and steps
-TRACE_FIELDS = 5
 
 
 @dataclass
@@ -551,7 +549,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                        f"tr[4] = tr_slices; }}" if self.trace else "")
         trace_decl = ("unsigned long long tr_wait = 0, tr_fill = 0, tr_out = 0, tr_comp = 0, tr_slices = 0;"
                       if self.trace else "")
-        now = "__builtin_amdgcn_s_memrealtime()"
+        now = NOW
         w(f"""  const int q_begin = args.wg_items[blockIdx.x], q_end = args.wg_items[blockIdx.x + 1];
   {trace_decl}
   for (int q = q_begin; q < q_end; ++q) {{

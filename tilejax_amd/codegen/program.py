@@ -18,7 +18,14 @@ import torch
 from .. import jaxlite, runtime
 from ..errors import KernelError
 
-__all__ = ["Arg", "Launch", "Program"]
+__all__ = ["Arg", "Launch", "Program", "TRACE", "TRACE_FIELDS", "NOW"]
+
+# A kernel generated with trace regions writes, per workgroup, TRACE_FIELDS 64-bit totals into the
+# workspace buffer TRACE: input-wait ticks (pipeline fill included), fill ticks, output ticks, compute ticks
+# (of the 100 MHz constant clock NOW reads), then the slices (units of streamed work) it processed.
+TRACE = "ak_trace"
+TRACE_FIELDS = 5
+NOW = "__builtin_amdgcn_s_memrealtime()"
 
 
 @dataclass(frozen=True)
@@ -90,7 +97,7 @@ class Program:
         """One call of a program generated with trace regions: its outputs, and its trace buffer (per
         workgroup: input-wait, fill, output and compute ticks of the 100 MHz clock, then steps), or None."""
         outputs, workspace = self._run(arrays, None, None, self.launches)
-        trace = workspace.get("ak_trace")
+        trace = workspace.get(TRACE)
         result = outputs[0] if len(outputs) == 1 else tuple(outputs)
         return result, (trace.view(torch.int64) if trace is not None else None)
 

@@ -15,9 +15,11 @@ waits exceed 20 % of the device time, "overhead" when time outside every region 
 from __future__ import annotations
 
 import statistics
+import time
 from dataclasses import dataclass, field
 from typing import Any, Dict, Optional, Sequence
 
+from .codegen.program import TRACE_FIELDS  # per workgroup: wait, fill, out_wait, compute (ticks), steps
 from .errors import KernelError
 
 __all__ = ["DMA_BOUND_SHARE", "OVERHEAD_BOUND_SHARE", "KernelProfile", "measure", "profile", "summarize"]
@@ -25,7 +27,6 @@ __all__ = ["DMA_BOUND_SHARE", "OVERHEAD_BOUND_SHARE", "KernelProfile", "measure"
 DMA_BOUND_SHARE = 0.2
 OVERHEAD_BOUND_SHARE = 0.3
 CLOCK_HZ = 100e6  # s_memrealtime
-TRACE_FIELDS = 5  # per workgroup: wait, fill, out_wait, compute (ticks), steps
 
 
 @dataclass
@@ -79,14 +80,16 @@ class KernelProfile:
         return "\n".join(lines)
 
 
-def summarize(stamps: Any, name: str, config: Any, calls: int, device_s: float, workgroups: int) -> KernelProfile:
+def summarize(stamps: Any, name: str, config: Any, calls: int, device_s: float, workgroups: int,
+              slots: int = 0) -> KernelProfile:
     """A profile from a trace buffer of per-workgroup region totals (in clock ticks): rows of
-    [wait, fill, out_wait, compute, steps], summed over `calls` calls; time per call is the mean over
-    workgroups (they run side by side)."""
+    [wait, fill, out_wait, compute, steps], summed over `calls` calls. Time per call is the total over
+    workgroups divided by the number that run side by side (`slots`, default all of them): with more
+    workgroups than that, a slot runs several in turn."""
     import numpy as np
 
     t = np.asarray(stamps, dtype=np.float64).reshape(workgroups, -1)
-    per = t.sum(axis=0) / max(workgroups, 1) / max(calls, 1)
+    per = t.sum(axis=0) / max(min(workgroups, slots or workgroups), 1) / max(calls, 1)
     ticks = 1.0 / CLOCK_HZ
     return KernelProfile(
         name=name, config=config, calls=calls, device_s=device_s, regions=True,
@@ -109,10 +112,19 @@ def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile
     workgroups = program.notes.get("trace_workgroups", 0) if lowered.trace else 0
     lowered.run(*inputs)
     torch.cuda.synchronize()
-    # The calls run back to back, with an event between consecutive ones, so the GPU stays busy while the
-    # host prepares the next launch and host time never counts as device time.
+    # The calls run back to back, with an event between consecutive ones. A spin kernel queued ahead of
+    # them holds the GPU for twice the host's launch time of all of them (measured on a second warm-up
+    # call), so every call is queued before the GPU reaches it and host time never counts as device time.
     events = [runtime.Event() for _ in range(runs + 1)]
     traces = []
+    start = time.perf_counter()
+    if workgroups:
+        program.run_traced(*inputs)
+    else:
+        lowered.run(*inputs)
+    host_s = time.perf_counter() - start
+    torch.cuda.synchronize()
+    runtime.spin(2.0 * runs * host_s + 1e-4, stream)
     events[0].record(stream)
     for k in range(runs):
         if workgroups:
@@ -128,7 +140,8 @@ def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile
         stamps = t if stamps is None else stamps + t
     device_s = statistics.median(samples)
     if workgroups:
-        result = summarize(stamps.numpy(), lowered.plan.nest.name, lowered.config, runs, device_s, workgroups)
+        result = summarize(stamps.numpy(), lowered.plan.nest.name, lowered.config, runs, device_s, workgroups,
+                           program.notes.get("trace_slots", 0))
         result.steps /= max(program.notes.get("slices_per_step", 1), 1)
         result.samples = samples
         return result

@@ -19,7 +19,7 @@ from typing import Any, Dict, List, Optional, Sequence, Tuple
 from . import gfx950
 from .errors import KernelError
 
-__all__ = ["Library", "compile_source", "library", "load", "Module"]
+__all__ = ["Library", "compile_source", "library", "load", "Module", "spin"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libak.so")
@@ -177,6 +177,32 @@ class Event:
             library().lib.ak_event_destroy(self.handle)
         except Exception:
             pass
+
+
+# A one-wave kernel that waits `ticks` of the 100 MHz constant clock, then exits: queued ahead of timed
+# calls, it holds the GPU while the host launches them all, so the host's launch time never shows up as
+# gaps between them.
+_SPIN_SOURCE = r"""
+extern "C" __global__ void __launch_bounds__(64) ak_spin(const unsigned long long ticks) {
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(32);
+}
+"""
+_SPIN: Dict[int, "Kernel"] = {}
+SPIN_MAX_S = 0.05
+
+
+def spin(seconds: float, stream: int) -> None:
+    """Queue a kernel on `stream` that keeps the GPU waiting for `seconds` (at most SPIN_MAX_S)."""
+    import struct
+
+    import torch
+
+    device = torch.cuda.current_device()
+    if device not in _SPIN:
+        _SPIN[device] = load(_SPIN_SOURCE, "ak_spin.hip").kernel("ak_spin")
+    ticks = int(min(max(seconds, 0.0), SPIN_MAX_S) * 100e6)
+    _SPIN[device].launch((1, 1, 1), (64, 1, 1), 0, struct.pack("<Q", ticks), stream)
 
 
 def current_stream() -> int:

@@ -615,7 +615,9 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             # barrier) are input waits; the rest of the loop is compute; the stores are output
             w(f"  unsigned long long tr_fill = 0, tr_wait = 0;")
             w(f"  const unsigned long long tr_i0 = {NOW};")
-        trace_write = (f"if (tid == 0) {{ const unsigned long long tr_e = {NOW}; "
+        # the last wave writes: its rows see every key block the tile visits, so its waits are for data
+        # (and the barrier), never for want of work
+        trace_write = (f"if (tid == {T - 64}) {{ const unsigned long long tr_e = {NOW}; "
                        f"unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
                        f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_e - tr_c1; "
                        f"tr[3] = tr_c1 - tr_i0 - tr_fill - tr_wait; tr[4] = (unsigned long long)nblk; }}") if tr else ""

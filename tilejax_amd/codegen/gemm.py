@@ -498,10 +498,14 @@ class _Gemm:
         const_value = literal(self.const_value if self.const_value is not None else 0.0, m.out.dtype)
         tile_decode = "\n    ".join(decode_tile(plan, sch, "t"))
         fill_block = ""
+        # a traced kernel counts the stores of filled and constant tiles as output time
+        tr_s0 = f"const unsigned long long tr_s0 = {NOW}; " if self.trace else ""
+        tr_s1 = f" tr_out += {NOW} - tr_s0;" if self.trace else ""
         if sch.fills:
             fill_decode = "\n      ".join(decode_fill(plan, sch, "t"))
             fill_block = (f"if (kind == 1) {{\n      {fill_decode}\n      const long long obase = {o_base};\n      "
-                          f"{_store_constant(bm, bn, out_bf16, O, 'obase', ldo, fill_value, T)}\n      continue;\n    }}")
+                          f"{tr_s0}{_store_constant(bm, bn, out_bf16, O, 'obase', ldo, fill_value, T)}{tr_s1}\n"
+                          f"      continue;\n    }}")
         setup = "\n    ".join(steps_setup)
 
         L: List[str] = []
@@ -560,7 +564,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
     {tile_decode}
     const long long obase = {o_base};
     if (kind == 2) {{
-      {_store_constant(bm, bn, out_bf16, O, "obase", ldo, const_value, T)}
+      {tr_s0}{_store_constant(bm, bn, out_bf16, O, "obase", ldo, const_value, T)}{tr_s1}
       continue;
     }}
     {setup}

@@ -53,7 +53,10 @@ __all__ = ["FlashMatch", "match", "lower"]
 LOG2E = 1.4426950408889634
 RESCALE_SLACK = 8.0  # natural-log units: p stays below e^8 between rescales
 MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 once a row has a real score
-STAGES = 3  # LDS stages of K and V blocks: loads run two blocks ahead, one barrier per block
+AHEAD = 2  # K and V blocks are loaded this many blocks ahead of use; one barrier per block
+# LDS stages of K and V: AHEAD + 1 would do; the ring of block-table entries the loop keeps (blocks b to
+# b + AHEAD + 1, at b modulo STAGES) takes AHEAD + 2, and one stage per ring slot keeps both static
+STAGES = AHEAD + 2
 K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
 V_AHEAD = 4  # V fragments in flight ahead of the O MFMAs
 
@@ -622,9 +625,14 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                        f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_e - tr_c1; "
                        f"tr[3] = tr_c1 - tr_i0 - tr_fill - tr_wait; tr[4] = (unsigned long long)nblk; }}") if tr else ""
 
-        def issue(b: str, s: int, ind: str) -> List[str]:
-            out = [f"{ind}{{ const int* bp = args.fa_blocks + 2 * (boff + ({b}));",
-                   f"{ind}  const int kpos = ak_ldc(bp, 0) + {self.kwin.offset} + ak_ldc(bp, 1), vpos = ak_ldc(bp, 0) + {self.vwin.offset} + ak_ldc(bp, 1);"]
+        # A block's table entry (key block start, column offset) is loaded into a ring of scalars one block
+        # before it is first needed, so no scalar load's latency follows a barrier.
+        def entry_load(x: str, r: int, ind: str) -> str:
+            return (f"{ind}{{ const int* bp = args.fa_blocks + 2 * (boff + ak_imin({x}, nblk - 1)); "
+                    f"bj[{r}] = ak_ldc(bp, 0); bc[{r}] = ak_ldc(bp, 1); }}")
+
+        def issue(r: int, s: int, ind: str) -> List[str]:
+            out = [f"{ind}{{ const int kpos = bj[{r}] + {self.kwin.offset} + bc[{r}], vpos = bj[{r}] + {self.vwin.offset} + bc[{r}];"]
             rows_k, rows_v = T // chk, T // chv
             for c in range(ldk_n):
                 out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, AK_LDS(&ak_sk{s}[({c * T} + wave * 64) * 8]), 16, k_voff, "
@@ -635,12 +643,38 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             out.append(f"{ind}}}")
             return out
 
+        v_order = [(kk, dt) for kk in range(ks) for dt in range(dt_n)]
+        v_ahead = min(V_AHEAD, len(v_order))
+
+        def v_read(i: int, ind: str) -> str:
+            kk, dt = v_order[i]
+            o1 = kk * 16 * DV * 2
+            return (f"{ind}  {{ const ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1}));"
+                    f" const ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1 + 8 * DV * 2}));"
+                    f" vf[{i}] = __builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)); }}")
+
+        def pv(ind: str) -> List[str]:
+            """O^T += V^T P^T from the V stage `vs` and `pf`: the first V_AHEAD fragments are in `vf`
+            already, the rest are read V_AHEAD MFMAs ahead of use."""
+            o: List[str] = []
+            a = o.append
+            for i, (kk, dt) in enumerate(v_order):
+                a(f"{ind}  acc[{dt}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[{i}], pf[{kk}], acc[{dt}], 0, 0, 0);")
+                if i + v_ahead < len(v_order):
+                    a(v_read(i + v_ahead, ind))
+            for i in range(len(v_order)):
+                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
+                if i + v_ahead < len(v_order):
+                    a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);")
+            return o
+
         def compute(s: int, ind: str) -> List[str]:
+            """Block b_ from stage s: S^T, the mask, the online softmax into `pf`, and O^T += V^T P^T."""
             o: List[str] = []
             a = o.append
             a(f"{ind}if (b_ < n_w) {{")
-            a(f"{ind}  const char* ks = (const char*)ak_sk{s}; const char* vs = (const char*)ak_sv{s};")
-            a(f"{ind}  const int lv_{jvar} = ak_ldc(args.fa_blocks, 2 * (boff + b_)), ec0 = ak_ldc(args.fa_blocks, 2 * (boff + b_) + 1) + (lane >> 5) * 4;")
+            a(f"{ind}  const char* ks = (const char*)ak_sk{s}; const char* vs = (const char*)ak_sv{s}; (void)vs;")
+            a(f"{ind}  const int lv_{jvar} = bj[{s}], ec0 = bc[{s}] + (lane >> 5) * 4;")
             a(f"{ind}  ak_f32x16 st[{kt}];")
             for t in range(kt):
                 a(f"{ind}  #pragma unroll")
@@ -657,17 +691,8 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                 if i + ahead < len(order):
                     t2, sl2 = order[i + ahead]
                     a(f"{ind}  kf[{i + ahead}] = *(const ak_bf16x8*)(ks + k_roff[{sl2}] + {t2 * 32 * D * 2});")
-            # O^T += V^T P^T: the first V_AHEAD fragments (two transposed reads each) go out now, beside the
-            # S MFMAs and the softmax; the rest V_AHEAD MFMAs ahead of use.
-            v_order = [(kk, dt) for kk in range(ks) for dt in range(dt_n)]
-            v_ahead = min(V_AHEAD, len(v_order))
-
-            def v_read(i: int, ind: str) -> str:
-                kk, dt = v_order[i]
-                o1 = kk * 16 * DV * 2
-                return (f"{ind}  {{ const ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1}));"
-                        f" const ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[{dt}] + {o1 + 8 * DV * 2}));"
-                        f" vf[{i}] = __builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)); }}")
+            # O^T += V^T P^T: its first V_AHEAD fragments (two transposed reads each) go out now, beside the
+            # S MFMAs and the softmax.
             a(f"{ind}  ak_bf16x8 vf[{len(v_order)}];")
             for i in range(v_ahead):
                 a(v_read(i, ind))
@@ -707,7 +732,6 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             # p = exp(s - m) as one fma and v_exp_f32 (2^x)
             a(f"{ind}  const float mb = -m_run * {LOG2E!r}f;")
             a(f"{ind}  float ps = 0.f;")
-            a(f"{ind}  ak_bf16x8 pf[{ks}];")
             for t in range(kt):
                 for half in range(2):
                     a(f"{ind}  {{ unsigned pk[4];")
@@ -719,42 +743,41 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                     a(f"{ind}    pf[{2 * t + half}] = __builtin_bit_cast(ak_bf16x8, (ak_u32x4){{pk[0], pk[1], pk[2], pk[3]}}); }}")
             a(f"{ind}  ps = ak_xor32_sum(ps);")
             a(f"{ind}  l_run += ps;")
-            for i, (kk, dt) in enumerate(v_order):
-                a(f"{ind}  acc[{dt}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[{i}], pf[{kk}], acc[{dt}], 0, 0, 0);")
-                if i + v_ahead < len(v_order):
-                    a(v_read(i + v_ahead, ind))
-            for i in range(len(v_order)):
-                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
-                if i + v_ahead < len(v_order):
-                    a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);")
+            o.extend(pv(ind))
             a(f"{ind}}}")
             return o
 
-        # K and V blocks stream through STAGES LDS stages, loaded STAGES - 1 blocks ahead. At the barrier that
-        # opens block b every wave has finished block b - 1 (its LDS reads waited for before the barrier),
-        # so block b + STAGES - 1 can go into that block's stage; one barrier per block.
+        # K and V blocks stream through STAGES LDS stages, loaded AHEAD blocks ahead. At the barrier that opens
+        # block b every wave has finished reading the stage block b + AHEAD goes into (that of block
+        # b + AHEAD - STAGES), so that load is issued right after it.
         per_block = ldk_n + ldv_n
-        for s in range(STAGES - 1):
+
+        w(f"  int bj[{STAGES}], bc[{STAGES}];  // table entries of blocks b .. b + {STAGES - 1}, at b mod {STAGES}")
+        for x in range(AHEAD + 1):
+            w(entry_load(str(x), x, "  "))
+        for s in range(AHEAD):
             w(f"  if ({s} < nblk) {{")
-            L.extend(issue(str(s), s, "    "))
+            L.extend(issue(s, s, "    "))
             w("  }")
+        w("  ak_bf16x8 pf[" + str(ks) + "];  // P^T of the block (srcB of O^T = V^T P^T)")
         w(f"  for (int b = 0; b < nblk; b += {STAGES}) {{")
         for s in range(STAGES):
             w(f"    {{ const int b_ = b + {s};")
             w("      if (b_ < nblk) {")
             if tr:
                 w(f"        const unsigned long long tr_w0 = {NOW};")
-            # Block b_ has landed; the (at most STAGES - 2) later blocks issued may still be in flight.
-            for ahead in range(STAGES - 2, 0, -1):
-                w(f"        {'if' if ahead == STAGES - 2 else 'else if'} (b_ + {ahead} < nblk) {{ AK_WAIT_VM({ahead * per_block}); }}")
-            w("        " + ("else " if STAGES > 2 else "") + "{ AK_WAIT_VM(0); }")
+            # Block b_ has landed; the (at most AHEAD - 1) later blocks issued may still be in flight.
+            for ahead in range(AHEAD - 1, 0, -1):
+                w(f"        {'if' if ahead == AHEAD - 1 else 'else if'} (b_ + {ahead} < nblk) {{ AK_WAIT_VM({ahead * per_block}); }}")
+            w("        " + ("else " if AHEAD > 1 else "") + "{ AK_WAIT_VM(0); }")
             w("        AK_WAIT_LGKM0();")
             w('        asm volatile("s_barrier" ::: "memory");')
             if tr:
                 w(f"        {{ const unsigned long long tr_w1 = {NOW}; if (b_ == 0) tr_fill = tr_w1 - tr_i0; else tr_wait += tr_w1 - tr_w0; }}")
-            w(f"        if (b_ + {STAGES - 1} < nblk) {{")
-            L.extend(issue(f"b_ + {STAGES - 1}", (s + STAGES - 1) % STAGES, "          "))
+            w(f"        if (b_ + {AHEAD} < nblk) {{")
+            L.extend(issue((s + AHEAD) % STAGES, (s + AHEAD) % STAGES, "          "))
             w("        }")
+            w(entry_load(f"b_ + {AHEAD + 1}", (s + AHEAD + 1) % STAGES, "        "))
             L.extend(compute(s, "        "))
             w("      }")
             w("    }")

@@ -92,6 +92,38 @@ def finish(acc, row_sum, shape, dtype):
     return out.reshape(shape).astype(dtype)
 
 
+@autokernel.tunable
+class DecodeTiles:
+    """Cache positions per step."""
+
+    block_kv: int = autokernel.choice(128, 256, 512, 1024, 2048, default=512)
+
+
+@autokernel.kernel
+def gqa_decode(q, k_cache, v_cache, lengths, tiles=DecodeTiles()):
+    """GQA decode attention over a contiguous cache: q (B, T, H, Dh), caches (B, S_max, Hkv * Dh)
+    (the reference's examples/decode.py:175-196)."""
+    B, T, H, Dh = q.shape
+    S, W = k_cache.shape[1], k_cache.shape[2]
+    Hkv, R = W // Dh, T * H
+    bk, dtype = min(tiles.block_kv, S), q.dtype
+    out = jnp.zeros((B, T, H, Dh), dtype)
+    for b in range(B):
+        token, group = row_index(R, H, Hkv)
+        qt = block_diagonal(query_rows(q[b, :, :, :]), group, Hkv, dtype)  # once per sequence
+        row_max = jnp.full((R, LANES), MASK_VALUE, jnp.float32)
+        row_sum = jnp.zeros((R, LANES), jnp.float32)
+        acc = jnp.zeros((R, W), jnp.float32)  # every kv head's values; a row keeps its own block
+        for j in range(0, S, bk):
+            if j >= lengths[b]:  # past the sequence's end: decided on the device, before the kernel runs
+                continue
+            s = qt @ k_cache[b, j : j + bk, :].T
+            ok = visible(token, bk, j, lengths[b], T)
+            row_max, row_sum, acc = online_softmax(s, v_cache[b, j : j + bk, :], ok, row_max, row_sum, acc)
+        out = out.at[b, :, :, :].set(finish(own_blocks(acc, group, Hkv), row_sum, (T, H, Dh), dtype))
+    return out
+
+
 @autokernel.kernel
 def paged_gqa_decode(q, k_pages, v_pages, block_tables, lengths):
     """GQA decode attention over a paged cache: q (B, T, H, Dh), pages (num_pages, page_size, Hkv * Dh),

@@ -188,3 +188,42 @@ def gqa_float64(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, b
             s = kk[:, g] @ qd[b, 0, h]
             out[b, 0, h] = (torch.softmax(s, 0) @ vv[:, g]).numpy()
     return out
+
+
+def contiguous_as_pages(cache: torch.Tensor, block: int):
+    """A contiguous cache (B, S, W) as pages of `block` positions (B * S / block, block, W) and the page
+    table (B, S / block) that lists sequence b's blocks in order: the paged spec over these pages reads
+    exactly what the contiguous spec reads, block for block."""
+    B, S, W = cache.shape
+    n = S // block
+    table = torch.arange(B * n, dtype=torch.int32).reshape(B, n)
+    return cache.reshape(B * n, block, W), table
+
+
+def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
+               block_kv: int = 512) -> torch.Tensor:
+    """examples/decode.py:175-196 of the reference (one new token, T = 1): the contiguous cache's blocks
+    of bk = min(block_kv, S) positions, skipped from lengths[b] on, are the paged spec's pages in order, so
+    this is `paged_gqa_decode` over `contiguous_as_pages` (same blocks, same online-softmax steps)."""
+    bk = min(block_kv, k_cache.shape[1])
+    kp, table = contiguous_as_pages(k_cache, bk)
+    vp, _ = contiguous_as_pages(v_cache, bk)
+    return paged_gqa_decode(q, kp, vp, table, lengths)
+
+
+def gqa_contiguous_float64(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           lengths: torch.Tensor) -> np.ndarray:
+    """GQA decode attention in float64 over a contiguous cache: softmax(q k[:n].T) v[:n] per head, with
+    n = lengths[b] (the reference's tests/test_decode.py:62-76 `_gqa`, T = 1); empty sequences give 0."""
+    B, T, H, Dh = q.shape
+    Hkv = k_cache.shape[2] // Dh
+    out = np.zeros((B, T, H, Dh))
+    kd, vd, qd = k_cache.double().cpu(), v_cache.double().cpu(), q.double().cpu()
+    for b, n in enumerate(lengths.cpu().tolist()):
+        if n == 0:
+            continue
+        kk, vv = kd[b, :n].reshape(n, Hkv, Dh), vd[b, :n].reshape(n, Hkv, Dh)
+        for h in range(H):
+            g = h // (H // Hkv)
+            out[b, 0, h] = (torch.softmax(kk[:, g] @ qd[b, 0, h], 0) @ vv[:, g]).numpy()
+    return out

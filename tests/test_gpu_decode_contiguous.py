@@ -1,0 +1,96 @@
+"""Parity of GQA decode over a contiguous cache (the reference's `gqa_decode`, examples/decode.py:175-196)
+with the CPU oracle on the same seeded inputs, with the paged kernel on the same cache cut into pages
+(bit for bit, as the reference's tests/test_decode.py:202-212 asserts), of its device step tables with the
+reference's table semantics, and at a BASELINE-sized cache with a float32 GPU reference on sampled
+sequences.
+
+Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want| (the paged tests'
+bound: the kernel merges per-workgroup partial softmaxes where the spec runs one pass).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from examples.decode import DecodeTiles, gqa_decode, paged_gqa_decode
+from oracle import kernels
+from oracle import schedule as oracle_schedule
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, S, lengths, H=32, Hkv=8, D=128, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, 1, H, D, generator=g) * D**-0.5).to(torch.bfloat16)
+    k = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16)
+    return q, k, v, torch.tensor(lengths, dtype=torch.int32)
+
+
+def _close(got, want):
+    got, want = got.float().cpu(), torch.as_tensor(want).float().cpu()
+    scale = want.abs().max().item()
+    bad = (got - want).abs() > 1e-2 * want.abs() + 1e-2 * scale
+    assert not bad.any(), f"{int(bad.sum())} of {want.numel()} differ; max |diff| {(got - want).abs().max().item()}"
+
+
+@pytest.mark.parametrize("block_kv", [128, 256, 512])
+def test_contiguous_decode_matches_oracle(block_kv):
+    # an empty sequence, one with just the new token, a partial last block and a full cache
+    ins = _inputs(4, 512, (0, 1, 300, 512))
+    print(f"contiguous decode block_kv={block_kv}", flush=True)
+    got = gqa_decode(*(t.cuda() for t in ins), DecodeTiles(block_kv))
+    torch.cuda.synchronize()
+    _close(got, kernels.gqa_decode(*ins, block_kv))
+    _close(got, kernels.gqa_contiguous_float64(*ins))
+    assert not got[0].float().any()  # the empty sequence
+
+
+def test_paged_equals_contiguous_bit_for_bit():
+    """The same cache as 128-position pages in a shuffled page table: the paged kernel reads exactly the
+    blocks the contiguous one reads, in the same order, so the outputs agree exactly."""
+    q, k, v, lengths = _inputs(4, 512, (0, 1, 300, 512), seed=1)
+    kp, table = kernels.contiguous_as_pages(k, 128)
+    vp, _ = kernels.contiguous_as_pages(v, 128)
+    perm = torch.randperm(kp.shape[0], generator=torch.Generator().manual_seed(2))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    table = inv[table.long()].to(torch.int32)
+    print("paged (128-position pages) vs contiguous (block_kv 128)", flush=True)
+    paged = paged_gqa_decode(q.cuda(), kp[perm].cuda(), vp[perm].cuda(), table.cuda(), lengths.cuda())
+    contiguous = gqa_decode(q.cuda(), k.cuda(), v.cuda(), lengths.cuda(), DecodeTiles(128))
+    assert torch.equal(paged, contiguous)
+
+
+def test_contiguous_decode_step_tables():
+    """The reference's count for lengths (0, 1, 300, 512) at block_kv 128 (tests/test_decode.py:195-199):
+    the empty sequence takes one empty step, then 1 + 3 + 4 blocks."""
+    lengths = (0, 1, 300, 512)
+    ins = _inputs(4, 512, lengths)
+    lowered = gqa_decode.lower(*ins, DecodeTiles(128))
+    got = lowered.program.step_tables(*(t.cuda() for t in ins))
+    step_tile, step_code, count = oracle_schedule.runtime_tables(
+        [{"b": b} for b in range(4)], [("j", 0, 128, 4, lambda v: v["j"] >= lengths[v["b"]])])
+    assert int(got["count"][0]) == count == 1 + 1 + 3 + 4
+    np.testing.assert_array_equal(got["step_tile"].cpu().numpy(), step_tile)
+    np.testing.assert_array_equal(got["step_code"].cpu().numpy(), step_code)
+
+
+def test_contiguous_decode_large_cache_sampled():
+    """64 sequences over an 8192-position cache (1 GiB per K and V, BASELINE config 5's shape without the
+    page table), lengths uniform in [128, 8192], block_kv 512; sampled sequences against float32 on the GPU."""
+    B, H, Hkv, D, S = 64, 32, 8, 128, 8192
+    g = torch.Generator().manual_seed(0)
+    lengths = torch.randint(128, S + 1, (B,), generator=g, dtype=torch.int32)
+    q = (torch.randn(B, 1, H, D, generator=g) * D**-0.5).to(torch.bfloat16).cuda()
+    k = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).cuda()
+    print("contiguous decode 64 x 8192, block_kv 512", flush=True)
+    got = gqa_decode(q, k, v, lengths.cuda(), DecodeTiles(512))
+    for b in range(0, B, 7):
+        n = int(lengths[b])
+        kk = k[b, :n].reshape(n, Hkv, D).float().permute(1, 2, 0).contiguous()  # (g, d, n)
+        vv = v[b, :n].reshape(n, Hkv, D).float().permute(1, 0, 2).contiguous()  # (g, n, d)
+        qq = q[b, 0].float().reshape(Hkv, H // Hkv, D)
+        want = torch.bmm(torch.softmax(torch.bmm(qq, kk), -1), vv).reshape(H, D)
+        _close(got[b, 0], want)

@@ -96,6 +96,40 @@ def test_gqa_float64_single_position_returns_its_value():
         np.testing.assert_allclose(out[b, 0, 0], vp[page, 0, :128].double().numpy(), rtol=1e-12)
 
 
+def _contiguous(B=4, H=8, Hkv=2, D=128, S=256, seed=0, lengths=(0, 1, 100, 256)):
+    q = (rand((B, 1, H, D), seed, torch.float32) * D**-0.5).to(BF)
+    k = rand((B, S, Hkv * D), seed + 1, BF)
+    v = rand((B, S, Hkv * D), seed + 2, BF)
+    return q, k, v, torch.tensor(lengths, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("block_kv", [64, 128, 512])
+def test_contiguous_decode_is_gqa_softmax(block_kv):
+    q, k, v, lengths = _contiguous()
+    got = kernels.gqa_decode(q, k, v, lengths, block_kv)
+    _close(got.double(), kernels.gqa_contiguous_float64(q, k, v, lengths))
+    assert not got[0].float().any()  # an empty sequence gives zeros
+
+
+def test_contiguous_float64_agrees_with_the_paged_one():
+    # the two float64 references, each from its own layout, on one cache
+    q, k, v, lengths = _contiguous()
+    kp, table = kernels.contiguous_as_pages(k, 32)
+    vp, _ = kernels.contiguous_as_pages(v, 32)
+    perm = torch.randperm(kp.shape[0], generator=torch.Generator().manual_seed(5))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    np.testing.assert_allclose(kernels.gqa_float64(q, kp[perm], vp[perm], inv[table.long()].to(torch.int32), lengths),
+                               kernels.gqa_contiguous_float64(q, k, v, lengths), rtol=1e-12, atol=1e-12)
+
+
+def test_contiguous_float64_catches_an_off_by_one_length():
+    q, k, v, lengths = _contiguous(lengths=(3, 50, 100, 200))
+    want = kernels.gqa_contiguous_float64(q, k, v, lengths)
+    wrong = kernels.gqa_contiguous_float64(q, k, v, lengths + 1)
+    assert np.abs(want - wrong).max() > 1e-3
+
+
 def test_grouped_matmul_routes_groups_to_their_experts():
     G, E, K, N = 64, 3, 128, 256
     xs = rand((4 * G, K), 0, BF)

@@ -1,9 +1,10 @@
-"""Lowering of runtime-masked online-softmax loop nests (decode attention over a paged cache) to gfx950.
+"""Lowering of runtime-masked online-softmax loop nests (decode attention over a KV cache) to gfx950.
 
-The family is the reference's `paged_gqa_decode` (examples/decode.py:199-223): per output tile (one
-sequence) some setup code computes the query rows once (`block_diagonal(query_rows(q[b]))`), then a
-reduction loop over the cache's pages, under a runtime mask (`p * P >= lengths[b]`) and reading each page
-through a runtime window (`k_pages[block_tables[b, p], :, :]`), runs the online softmax that
+The family is the reference's `paged_gqa_decode` (examples/decode.py:199-223) and `gqa_decode` over a
+contiguous cache (:175-196): per output tile (one sequence) some setup code computes the query rows once
+(`block_diagonal(query_rows(q[b]))`), then a reduction loop over the cache's pages or blocks, under a
+runtime mask (`p * P >= lengths[b]`, `j >= lengths[b]`) and reading each through a window (a runtime
+one, `k_pages[block_tables[b, p], :, :]`, or `k_cache[b, j : j + bk, :]`), runs the online softmax that
 `flash.softmax_structure` recognises, and the output is some epilogue of the accumulator and the row sum
 (`finish(own_blocks(acc))`). It computes exactly that, as four launches on one stream:
 
@@ -11,7 +12,8 @@ through a runtime window (`k_pages[block_tables[b, p], :, :]`), runs the online 
    order, compacted;
 2. a setup kernel materialises each tile's query rows (the setup code's value, per element) in a
    workspace, so the attention kernel reads them as plain loads;
-3. the attention kernel splits the compacted step list evenly over one workgroup per CU (a sequence's
+3. the attention kernel works in kernel steps of SUB = 16 positions (a table step of P positions is P / 16
+   of them, in order) and splits the compacted list of them evenly over one workgroup per CU (a sequence's
    pages may span several workgroups, a workgroup several short sequences). It decodes its range's steps
    (tile, code, page offsets) into LDS first, then streams pages with three in flight under each step's
    compute: K fragments HBM -> registers (`buffer_load_dwordx4`, four register sets), V rows HBM -> LDS
@@ -50,6 +52,7 @@ __all__ = ["DecodeMatch", "match", "lower"]
 
 THREADS = 256
 WAVES = 4
+SUB = 16  # key positions per kernel step: a spec step of P positions (a page, a cache block) is P / SUB of them
 DEPTH = 3  # K register sets and V LDS stages: pages fetched ahead of the step being computed
 
 
@@ -77,8 +80,10 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
         return None
     k = plan.operand(sm.qk.args[1].kwargs["operand"])
     v = plan.operand(sm.pv.args[1].kwargs["operand"])
-    if k.kind is not Kind.STREAM or v.kind is not Kind.STREAM or k.tile.dtype.name != "bfloat16" \
-            or v.tile.dtype.name != "bfloat16":
+    # K and V stream with the loop, or (a loop of one block) stay per tile; either way the kernel reads each
+    # step's window at the address its indices give
+    if k.kind not in (Kind.STREAM, Kind.TILE) or v.kind not in (Kind.STREAM, Kind.TILE) \
+            or k.tile.dtype.name != "bfloat16" or v.tile.dtype.name != "bfloat16":
         return None
     qn = sm.qk.args[0]
     seg0 = plan.scopes["seg0"]
@@ -111,20 +116,22 @@ class _Decode:
     def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
         self.trace = trace
-        if m.rows != 32 or m.page != 16 or m.width % (32 * WAVES):
-            raise KernelError(f"the gfx950 decode lowering takes 32 query rows, pages of 16 positions and widths "
-                              f"that are multiples of {32 * WAVES} (got {m.rows}, {m.page}, {m.width})")
+        if m.rows != 32 or m.page % SUB or m.width % (32 * WAVES):
+            raise KernelError(f"the gfx950 decode lowering takes 32 query rows, pages (or cache blocks) of a multiple "
+                              f"of {SUB} positions and widths that are multiples of {32 * WAVES} "
+                              f"(got {m.rows}, {m.page}, {m.width})")
+        self.sub = m.page // SUB  # kernel steps per spec step
         if sch.repeats != 1:
             raise KernelError("decode with parallel loops the runtime mask doesn't read is not lowered yet")
         self.grid = gfx950.CUS
         self.slots = self.grid + sch.pattern_tiles
-        self.max_per = -(-sch.pattern_steps // self.grid)  # most steps one workgroup takes
-        self.lds = DEPTH * m.page * m.width * 2 + WAVES * m.page * m.rows * 4 + 16 * self.max_per
+        self.max_per = -(-sch.pattern_steps * self.sub // self.grid)  # most kernel steps one workgroup takes
+        self.lds = DEPTH * SUB * m.width * 2 + WAVES * SUB * m.rows * 4 + 20 * self.max_per
         if self.lds > gfx950.LDS_BYTES:
             raise KernelError(f"decode over {sch.pattern_steps} pattern steps of {m.page} x {m.width} needs "
                               f"{self.lds} bytes of LDS per workgroup (gfx950 has {gfx950.LDS_BYTES})")
         self.phase = plan.phases[0].range
-        if (self.phase.count + 1) * m.rows * 4 > 96 * 1024:
+        if (min(self.grid, self.phase.count * self.sub) + 1) * m.rows * 4 > 96 * 1024:
             raise KernelError("too many pages per sequence for the merge kernel's LDS")
         self.index = Index(plan, lambda v: f"lv_{v}")
         self.seg0 = plan.scopes["seg0"]
@@ -204,8 +211,8 @@ class _Decode:
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
             tables=tables, workspace=workspace, lds_bytes=self.lds,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
-                   # trace regions cover the attention kernel; a slice is one step (one page) of the step table
-                   "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": 1},
+                   # trace regions cover the attention kernel; a slice is one kernel step, SUB positions
+                   "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": self.sub},
         )
         attach_step_builder(prog, plan, sch, self.name)
         return prog
@@ -234,7 +241,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
 
     def _attention_source(self) -> str:
         plan, sch, m = self.plan, self.sch, self.m
-        R, P, W = m.rows, m.page, m.width
+        R, P, W = m.rows, SUB, m.width
+        U = self.sub
         WQ = W // WAVES  # a wave's share of the width
         slabs = WQ // 32  # K = 32 slabs of S^T = K Q^T per wave
         dtiles = WQ // 32  # 32-wide tiles of acc^T per wave
@@ -267,12 +275,12 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
         for s in range(D):  # one array per stage: the compiler then keeps the other stages' loads in flight
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sv{s}[{P * W}];")
         w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{P}][{R}];")
-        w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][4];")
+        w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][5];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int count = args.rt_count[0];
+  const int count = args.rt_count[0] * {U};  // kernel steps: {U} of {P} positions per step of the table
   const int per = (count + {self.grid - 1}) / {self.grid};
   const int g0 = blockIdx.x * per, n = ak_imin(g0 + per, count) - g0;
   {self._trace_start()}
@@ -280,13 +288,15 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
   // The range's steps, decoded once into LDS: tile, code, K and V page byte offsets. The loop then reads
   // them from LDS, so no global load other than the pages themselves sits in the vector memory queue.
   for (int j = tid; j < n; j += {THREADS}) {{
-    const int t = args.rt_step_tile[g0 + j], code = args.rt_step_code[g0 + j];
+    const int x = g0 + j, js = x / {U}, su = x - js * {U};  // the table's step, and the part of its block
+    const int t = args.rt_step_tile[js], code = args.rt_step_code[js];
     {self._decode_tile("t")}
     const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step};
     dc_st[j][0] = t;
     dc_st[j][1] = code;
-    dc_st[j][2] = (int)(({k_base}) * 2);
-    dc_st[j][3] = (int)(({v_base}) * 2);
+    dc_st[j][2] = (int)(({k_base} + (long long)su * {P * ldk}) * 2);
+    dc_st[j][3] = (int)(({v_base} + (long long)su * {P * ldv}) * 2);
+    dc_st[j][4] = su;
   }}
   __syncthreads();
   const int cb = wave * {WQ};  // this wave's columns of the width
@@ -412,6 +422,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}  if (run) {{")
             a(f"{ind}    {self._decode_tile('t')}")
             a(f"{ind}    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step}; (void)lv_{jvar};")
+            a(f"{ind}    const int su = __builtin_amdgcn_readfirstlane(dc_st[j_][4]); (void)su;")
             a(f"{ind}    const char* vs = (const char*)dc_sv{u};")
             # an LDS-only barrier: the pages in flight stay in flight
             a(f"{ind}    AK_WAIT_LGKM0();")
@@ -422,8 +433,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}    float mx = -__builtin_inff();")
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int e = 0; e < 8; ++e) {{")
-            a(f"{ind}      const int ep = 8 * (lane >> 5) + e;")
-            a(f"{ind}      const float sv = dc_sp[0][ep][er] + dc_sp[1][ep][er] + dc_sp[2][ep][er] + dc_sp[3][ep][er];")
+            a(f"{ind}      const int el = 8 * (lane >> 5) + e;  // the position in this kernel step")
+            a(f"{ind}      const int ep = {P} * su + el;  // the position in the table step's block")
+            a(f"{ind}      const float sv = dc_sp[0][el][er] + dc_sp[1][el][er] + dc_sp[2][el][er] + dc_sp[3][el][er];")
             a(f"{ind}      sc[e] = (float)({score});")
             a(f"{ind}      mx = fmaxf(mx, sc[e]);")
             a(f"{ind}    }}")
@@ -496,7 +508,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     def _merge_source(self) -> str:
         plan, sch, m = self.plan, self.sch, self.m
         R, W = m.rows, m.width
-        maxs = self.phase.count + 1  # partials per tile: at most its steps (+1 for the division's edges)
+        U = self.sub
+        # partials per tile: at most its kernel steps or the grid (+1 for the division's edges)
+        maxs = min(self.grid, self.phase.count * U) + 1
         out_shape = m.out.tile.shape
         index = self.index
         o_base, o_str = tile_base(m.out.tile, m.out.shape, index, lambda v: f"lv_{v}")
@@ -526,9 +540,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
   __shared__ float dc_lsum[{R}];
   const int t = blockIdx.x;
   {self._decode_tile("t")}
-  const int count = args.rt_count[0];
+  const int count = args.rt_count[0] * {U};  // kernel steps, as the attention kernel divides them
   const int per = (count + {self.grid - 1}) / {self.grid};
-  const int ts = args.rt_tile_steps[t], te = args.rt_tile_steps[t + 1];
+  const int ts = args.rt_tile_steps[t] * {U}, te = args.rt_tile_steps[t + 1] * {U};
   const int w0 = ts / per, w1 = (te - 1) / per;
   const int n = w1 - w0 + 1;
   // The partials' loads go out four at a time (they are independent); the sums run in partial order.

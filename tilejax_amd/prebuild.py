@@ -51,6 +51,11 @@ def standard() -> Iterator[Tuple[object, tuple]]:
     for b, pages, n_pages in ((4, 64, 256), (5, 100, 500), (64, 512, 32768)):
         yield decode.paged_gqa_decode, (_bf16(b, 1, 32, 128), _bf16(n_pages, 16, 1024), _bf16(n_pages, 16, 1024),
                                         _i32(b, pages), _i32(b))
+    yield decode.paged_gqa_decode, (_bf16(4, 1, 32, 128), _bf16(16, 128, 1024), _bf16(16, 128, 1024), _i32(4, 4),
+                                    _i32(4))
+    for b, s, block in ((4, 512, 128), (4, 512, 256), (4, 512, 512), (64, 8192, 512)):
+        yield decode.gqa_decode, (_bf16(b, 1, 32, 128), _bf16(b, s, 1024), _bf16(b, s, 1024), _i32(b),
+                                  decode.DecodeTiles(block))
     try:
         from examples import causal_attention as ca
 

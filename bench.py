@@ -9,7 +9,8 @@ carries the other BASELINE configurations in `legs`, each timed the same way:
 - causal `tril(x @ y)` at the same size, with its time over the dense time;
 - causal MHA at (4, 16, 2048, 128) and (1, 16, 4096, 128);
 - the MoE grouped GEMM (16384 x 4096 x 14336, 8 experts);
-- paged GQA decode (64 sequences, HBM GB/s).
+- paged GQA decode (64 sequences, HBM GB/s), with step tables and with a cursor, and the same sequences
+  over a contiguous cache (the reference's gqa_decode).
 
 It also carries:
 
@@ -231,16 +232,43 @@ def main() -> int:
             kp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
             vp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
             ln = lengths.to(dev)
-            dl = paged_gqa_decode.lower(q, kp, vp, table, ln)
-            dms, _ = time_kernel(lambda: dl.run(q, kp, vp, table, ln), args.steps, args.warmup)
+            from tilejax_amd.tune import Config
+
+            dsig = paged_gqa_decode.signature(q, kp, vp, table, ln)
+            dl = paged_gqa_decode.lowered(dsig, paged_gqa_decode.default_config(dsig))
+            # the two ways of finding the steps: device step tables, or a cursor in the attention kernel
+            dc = paged_gqa_decode.lowered(paged_gqa_decode.signature(q, kp, vp, table, ln),
+                                          Config(dl.config.tunable, dl.config.pipeline, True))
+            tms, _ = time_kernel(lambda: dl.run(q, kp, vp, table, ln), args.steps, args.warmup)
+            cms, _ = time_kernel(lambda: dc.run(q, kp, vp, table, ln), args.steps, args.warmup)
+            dms = min(tms, cms)
             # the valid K and V rows, plus queries, outputs, the page table and the lengths
             dbytes = int(lengths.sum()) * Hkv * D * 2 * 2 + 2 * q.numel() * 2 + table.numel() * 4 + B * 4
             gbs = dbytes / (dms * 1e-3) / 1e9
-            _log(f"paged GQA decode 64 seqs, 32/8 heads, 16-token pages: {dms * 1e3:.1f} us, {gbs:.0f} GB/s")
+            _log(f"paged GQA decode 64 seqs, 32/8 heads, 16-token pages: {tms * 1e3:.1f} us with step tables, "
+                 f"{cms * 1e3:.1f} us with a cursor; {gbs:.0f} GB/s")
             out["decode"] = {"sequences": B, "heads": [H, Hkv], "page": P, "sum_lengths": int(lengths.sum()),
-                             "us": round(dms * 1e3, 2), "bytes": dbytes, "gbs": round(gbs, 1),
+                             "us": round(dms * 1e3, 2), "us_tables": round(tms * 1e3, 2),
+                             "us_cursor": round(cms * 1e3, 2), "bytes": dbytes, "gbs": round(gbs, 1),
                              "frac_hbm_peak": round(gbs / 8000.0, 4)}
             del kp, vp
+            # the contiguous cache (the reference's gqa_decode): the same 64 sequences over 8192 positions
+            from examples.decode import DecodeTiles, gqa_decode
+
+            S = pages * P
+            kc = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
+            vc = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
+            gl = gqa_decode.lower(q, kc, vc, ln, DecodeTiles(512))
+            gc = gqa_decode.lowered(gqa_decode.signature(q, kc, vc, ln), Config(DecodeTiles(512), gl.config.pipeline, True))
+            gms = min(time_kernel(lambda: gl.run(q, kc, vc, ln), args.steps, args.warmup)[0],
+                      time_kernel(lambda: gc.run(q, kc, vc, ln), args.steps, args.warmup)[0])
+            # whole 512-position blocks are read up to each sequence's end
+            blocks = int(sum(-(-int(n) // 512) for n in lengths)) * 512
+            gbytes = blocks * Hkv * D * 2 * 2 + 2 * q.numel() * 2 + B * 4
+            _log(f"contiguous GQA decode 64 x 8192, block_kv 512: {gms * 1e3:.1f} us, {gbytes / (gms * 1e-3) / 1e9:.0f} GB/s")
+            out["decode_contiguous"] = {"sequences": B, "cache": S, "block_kv": 512, "us": round(gms * 1e3, 2),
+                                        "bytes": gbytes, "gbs": round(gbytes / (gms * 1e-3) / 1e9, 1)}
+            del kc, vc
         except Exception as e:
             _log(f"decode: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
             out["decode"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}

@@ -28,6 +28,13 @@ def _inputs(B, H, Hkv, D, P, pages, lengths, seed=0):
     return q, k_pages, v_pages, table, torch.tensor(lengths, dtype=torch.int32)
 
 
+def _with_tables(kernel, ins):
+    """The kernel as built from device step tables (its default; called on GPU tensors without a schedule,
+    it is tuned, and tuning may choose a cursor)."""
+    signature = kernel.signature(*ins)
+    return kernel.lowered(signature, kernel.default_config(signature))
+
+
 def _close(got, want):
     got, want = got.float().cpu(), torch.as_tensor(want).float().cpu()
     scale = want.abs().max().item()
@@ -57,7 +64,7 @@ def test_paged_decode_against_float64():
 def test_decode_step_tables_are_bit_exact():
     lengths = (0, 1, 300, 1024)
     ins = _inputs(4, 32, 8, 128, 16, 64, lengths)
-    lowered = paged_gqa_decode.lower(*ins)
+    lowered = _with_tables(paged_gqa_decode, ins)
     got = lowered.program.step_tables(*(t.cuda() for t in ins))
     step_tile, step_code, count = oracle_schedule.runtime_tables(
         [{"b": b} for b in range(4)], [("p", 0, 1, 64, lambda v: v["p"] * 16 >= lengths[v["b"]])])
@@ -72,7 +79,7 @@ def test_decode_step_tables_ragged_words():
     lengths = (0, 5, 1600, 1023, 1025)
     ins = _inputs(5, 32, 8, 128, 16, 100, lengths, seed=4)
     print(f"decode step tables lengths={lengths}", flush=True)
-    lowered = paged_gqa_decode.lower(*ins)
+    lowered = _with_tables(paged_gqa_decode, ins)
     got = lowered.program.step_tables(*(t.cuda() for t in ins))
     step_tile, step_code, count = oracle_schedule.runtime_tables(
         [{"b": b} for b in range(5)], [("p", 0, 1, 100, lambda v: v["p"] * 16 >= lengths[v["b"]])])
@@ -118,7 +125,7 @@ def test_decode_step_tables_bit_exact_at_baseline_size():
     lengths = torch.randint(128, 8193, (B,), generator=g, dtype=torch.int32)
     lengths[5], lengths[9] = 0, 8192  # an empty sequence and a full one
     ins = _inputs(B, 32, 8, 128, 16, pages, tuple(int(n) for n in lengths))
-    lowered = paged_gqa_decode.lower(*ins)
+    lowered = _with_tables(paged_gqa_decode, ins)
     assert lowered.program.launches[0].grid[0] > 1
     got = lowered.program.step_tables(*(t.cuda() for t in ins))
     lens = [int(n) for n in lengths]
@@ -128,3 +135,36 @@ def test_decode_step_tables_bit_exact_at_baseline_size():
     np.testing.assert_array_equal(got["step_tile"].cpu().numpy(), step_tile)
     np.testing.assert_array_equal(got["step_code"].cpu().numpy(), step_code)
     np.testing.assert_array_equal(got["tile_steps"].cpu().numpy(), np.cumsum([0] + [max(1, -(-n // 16)) for n in lens]))
+
+
+def _cursor_run(kernel, ins):
+    """The kernel built with a cursor (its attention kernel finds its steps itself) and with tables."""
+    from tilejax_amd.tune import Config
+
+    plain = _with_tables(kernel, ins)
+    cursor = kernel.lowered(kernel.signature(*ins), Config(plain.config.tunable, plain.config.pipeline, True))
+    assert cursor.program.notes["cursor"] and len(cursor.program.launches) == len(plain.program.launches) - 1
+    dev = [t.cuda() for t in ins]
+    return plain.run(*dev), cursor.run(*dev)
+
+
+@pytest.mark.parametrize("lengths, pages", [((0, 1, 300, 1024), 64), ((0, 5, 1600, 1023, 1025), 100)])
+def test_cursor_equals_step_tables(lengths, pages):
+    """With a cursor each workgroup evaluates the mask and finds its own steps; it takes the same steps in
+    the same order as the device tables give, so the outputs agree bit for bit."""
+    ins = _inputs(len(lengths), 32, 8, 128, 16, pages, lengths, seed=6)
+    print(f"decode cursor vs tables lengths={lengths}", flush=True)
+    tables, cursor = _cursor_run(paged_gqa_decode, ins)
+    assert torch.equal(tables, cursor)
+    _close(cursor, kernels.paged_gqa_decode(*ins))
+
+
+def test_cursor_at_baseline_size():
+    B, pages = 64, 512
+    g = torch.Generator().manual_seed(0)
+    lengths = torch.randint(128, 8193, (B,), generator=g, dtype=torch.int32)
+    lengths[5], lengths[9] = 0, 8192
+    ins = _inputs(B, 32, 8, 128, 16, pages, tuple(int(n) for n in lengths))
+    print("decode cursor vs tables at 64 x 512 pages", flush=True)
+    tables, cursor = _cursor_run(paged_gqa_decode, ins)
+    assert torch.equal(tables, cursor)

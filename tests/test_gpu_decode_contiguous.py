@@ -94,3 +94,14 @@ def test_contiguous_decode_large_cache_sampled():
         qq = q[b, 0].float().reshape(Hkv, H // Hkv, D)
         want = torch.bmm(torch.softmax(torch.bmm(qq, kk), -1), vv).reshape(H, D)
         _close(got[b, 0], want)
+
+
+def test_contiguous_cursor_equals_step_tables():
+    from tilejax_amd.tune import Config
+
+    ins = _inputs(4, 512, (0, 1, 300, 512), seed=3)
+    dev = [t.cuda() for t in ins]
+    plain = gqa_decode.lower(*ins, DecodeTiles(128))
+    cursor = gqa_decode.lowered(gqa_decode.signature(*ins), Config(DecodeTiles(128), plain.config.pipeline, True))
+    print("contiguous decode cursor vs tables", flush=True)
+    assert torch.equal(plain.run(*dev), cursor.run(*dev))

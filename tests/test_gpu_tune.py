@@ -117,3 +117,21 @@ def test_decode_profile_has_trace_regions():
     traced = paged_gqa_decode.lowered(paged_gqa_decode.signature(q, kp, vp, table, lengths), plain.config, trace=True)
     out, trace = traced.program.run_traced(q, kp, vp, table, lengths)
     assert trace is not None and torch.equal(out, plain.run(q, kp, vp, table, lengths))
+
+
+def test_tuning_decode_tries_both_ways_of_finding_steps():
+    """A kernel with runtime masks may find its steps from device tables or with a cursor; tuning tries
+    both (the reference's tune.py:186-187) and keeps the faster."""
+    from examples.decode import paged_gqa_decode
+
+    g = torch.Generator().manual_seed(8)
+    B, pages, P, W = 16, 64, 16, 1024
+    q = (torch.randn(B, 1, 32, 128, generator=g) * 128**-0.5).to(torch.bfloat16).cuda()
+    kp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    vp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    table = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32).cuda()
+    lengths = torch.randint(0, pages * P + 1, (B,), generator=g, dtype=torch.int32).cuda()
+    print("tuning paged_gqa_decode 16 sequences", flush=True)
+    tuning = paged_gqa_decode.tuning(q, kp, vp, table, lengths)
+    print(tuning, flush=True)
+    assert {t.config.cursor for t in tuning.trials if t.profile is not None} == {False, True}

@@ -212,7 +212,9 @@ class Kernel:
         key = (signature, config, trace)
         if key not in self._lowered:
             plan, schedule = self.build(signature, config.tunable)
-            program = codegen.generate(plan, schedule, config.pipeline, trace=trace)
+            if config.cursor and not plan.either:
+                raise KernelError(f"{self.nest.name}: only a kernel with runtime masks finds its steps with a cursor")
+            program = codegen.generate(plan, schedule, config.pipeline, trace=trace, cursor=config.cursor)
             self._lowered[key] = Lowered(plan, schedule, config, program.source, trace, program)
         return self._lowered[key]
 

@@ -36,20 +36,25 @@ def default_pipeline(plan: Plan, schedule: Schedule) -> Pipeline:
     return Pipeline(2, 2)
 
 
-def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool = False) -> Program:
-    """The program for this plan, schedule and pipeline."""
+def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool = False,
+             cursor: bool = False) -> Program:
+    """The program for this plan, schedule and pipeline; with `cursor`, a kernel with runtime masks finds
+    its steps itself as it runs rather than from device-built step tables (the decode family)."""
     from . import decode, flash, gemm
 
     name = _symbol(plan)
     found = gemm.match(plan)
     if found is not None:
+        if cursor:
+            raise KernelError(f"{plan.nest.name}: the matmul family reads runtime masks from device step tables "
+                              "(no cursor)")
         return gemm.lower(plan, schedule, pipeline, found, name, trace=trace)
     found = flash.match(plan)
     if found is not None:
         return flash.lower(plan, schedule, pipeline, found, name, trace=trace)
     found = decode.match(plan)
     if found is not None:
-        return decode.lower(plan, schedule, pipeline, found, name, trace=trace)
+        return decode.lower(plan, schedule, pipeline, found, name, trace=trace, cursor=cursor)
     raise KernelError(
         f"{plan.nest.name}: the gfx950 backend has no lowering for this loop nest's tile code yet "
         "(it lowers matmuls with pointwise epilogues and online-softmax attention)"

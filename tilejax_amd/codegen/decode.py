@@ -113,9 +113,10 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
 
 
 class _Decode:
-    def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False) -> None:
+    def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False,
+                 cursor: bool = False) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
-        self.trace = trace
+        self.trace, self.cursor = trace, cursor
         if m.rows != 32 or m.page % SUB or m.width % (32 * WAVES):
             raise KernelError(f"the gfx950 decode lowering takes 32 query rows, pages (or cache blocks) of a multiple "
                               f"of {SUB} positions and widths that are multiples of {32 * WAVES} "
@@ -127,6 +128,10 @@ class _Decode:
         self.slots = self.grid + sch.pattern_tiles
         self.max_per = -(-sch.pattern_steps * self.sub // self.grid)  # most kernel steps one workgroup takes
         self.lds = DEPTH * SUB * m.width * 2 + WAVES * SUB * m.rows * 4 + 20 * self.max_per
+        # with a cursor the attention kernel evaluates the mask itself: a 64-block word per tile and word
+        self.words = sch.pattern_tiles * -(-plan.phases[0].range.count // 64)
+        if cursor:
+            self.lds += 8 * self.words + 4 * (sch.pattern_tiles + 1) + 4 * THREADS
         if self.lds > gfx950.LDS_BYTES:
             raise KernelError(f"decode over {sch.pattern_steps} pattern steps of {m.page} x {m.width} needs "
                               f"{self.lds} bytes of LDS per workgroup (gfx950 has {gfx950.LDS_BYTES})")
@@ -192,8 +197,13 @@ class _Decode:
             args.append(Arg("table", f"tv_{r.var}", "const int* __restrict__", f"tv_{r.var}"))
         workspace = {"dc_q": 2 * sch.pattern_tiles * R * W, "dc_m": 4 * self.slots * R, "dc_l": 4 * self.slots * R,
                      "dc_acc": 4 * self.slots * R * W}
-        for ws in ("step_tile", "step_code", "count", "tile_steps"):
+        # the step tables (device-built) or, with a cursor, only what the merge reads: the count and each
+        # tile's first step, which the attention kernel's workgroup 0 writes
+        for ws in (("count", "tile_steps") if self.cursor else ("step_tile", "step_code", "count", "tile_steps")):
             args.append(Arg("workspace", ws, "int* __restrict__", f"rt_{ws}"))
+        if self.cursor:
+            workspace["count"] = 4
+            workspace["tile_steps"] = 4 * (sch.pattern_tiles + 1)
         args.append(Arg("workspace", "dc_q", "ak_u16* __restrict__", "dc_q"))
         for ws in ("dc_m", "dc_l", "dc_acc"):
             args.append(Arg("workspace", ws, "float* __restrict__", ws))
@@ -211,10 +221,12 @@ class _Decode:
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
             tables=tables, workspace=workspace, lds_bytes=self.lds,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
+                   "cursor": self.cursor,
                    # trace regions cover the attention kernel; a slice is one kernel step, SUB positions
                    "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": self.sub},
         )
-        attach_step_builder(prog, plan, sch, self.name)
+        if not self.cursor:
+            attach_step_builder(prog, plan, sch, self.name)
         return prog
 
     def _decode_tile(self, t: str) -> str:
@@ -280,16 +292,17 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int count = args.rt_count[0] * {U};  // kernel steps: {U} of {P} positions per step of the table
+  {self._trace_start()}
+  {self._cursor_scan() if self.cursor else ""}
+  const int count = {"cs_start[" + str(sch.pattern_tiles) + "]" if self.cursor else "args.rt_count[0]"} * {U};  // kernel steps: {U} of {P} positions per table step
   const int per = (count + {self.grid - 1}) / {self.grid};
   const int g0 = blockIdx.x * per, n = ak_imin(g0 + per, count) - g0;
-  {self._trace_start()}
   if (n <= 0) {{ {self._trace_write("0")} return; }}
   // The range's steps, decoded once into LDS: tile, code, K and V page byte offsets. The loop then reads
   // them from LDS, so no global load other than the pages themselves sits in the vector memory queue.
   for (int j = tid; j < n; j += {THREADS}) {{
     const int x = g0 + j, js = x / {U}, su = x - js * {U};  // the table's step, and the part of its block
-    const int t = args.rt_step_tile[js], code = args.rt_step_code[js];
+    {self._cursor_step() if self.cursor else "const int t = args.rt_step_tile[js], code = args.rt_step_code[js];"}
     {self._decode_tile("t")}
     const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step};
     dc_st[j][0] = t;
@@ -490,6 +503,84 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
         w("}")
         return "\n".join(L)
 
+    def _cursor_scan(self) -> str:
+        """With a cursor: the runtime mask of every (tile, block), a ballot per 64 blocks into LDS words (each
+        wave takes every WAVES-th tile, decoding its loop values once); each tile's kept count (a tile with
+        no block running keeps one empty step, as the step tables do) and their exclusive scan, cs_start.
+        Workgroup 0 writes the count and the tiles' first steps for the merge kernel."""
+        plan, sch = self.plan, self.sch
+        phase = plan.phases[0].range
+        pt, count, nb = sch.pattern_tiles, phase.count, -(-phase.count // 64)
+        mask = Index(plan, lambda v: f"lv_{v}").expr(phase.mask)
+        per_t = -(-pt // THREADS)
+        return f"""__shared__ unsigned long long cs_run[{self.words}];
+  __shared__ int cs_start[{pt + 1}], cs_part[{THREADS}];
+  // (unrolled so that several tiles' loop values and index reads are in flight at once)
+#pragma unroll 8
+  for (int t = wave; t < {pt}; t += {WAVES}) {{
+    {self._decode_tile("t")}
+    for (int wi = 0; wi < {nb}; ++wi) {{
+      const int kb = wi * 64 + lane;
+      bool run = false;
+      if (kb < {count}) {{
+        const int lv_{phase.var} = {phase.start} + kb * {phase.step};
+        run = !({mask});
+      }}
+      const unsigned long long m_ = __ballot(run);
+      if (lane == 0) cs_run[t * {nb} + wi] = m_;
+    }}
+  }}
+  __syncthreads();
+  {{  // kept steps per tile, summed over runs of {per_t} tiles per thread, then a block-wide scan
+    const int t0 = tid * {per_t}, t1 = ak_imin(t0 + {per_t}, {pt});
+    int mine = 0;
+    for (int t = t0; t < t1; ++t) {{
+      int k = 0;
+      for (int wi = 0; wi < {nb}; ++wi) k += __popcll(cs_run[t * {nb} + wi]);
+      cs_start[t] = k ? k : 1;
+      mine += k ? k : 1;
+    }}
+    cs_part[tid] = mine;
+    __syncthreads();
+    for (int d = 1; d < {THREADS}; d <<= 1) {{
+      const int add = tid >= d ? cs_part[tid - d] : 0;
+      __syncthreads();
+      cs_part[tid] += add;
+      __syncthreads();
+    }}
+    int at = cs_part[tid] - mine;
+    for (int t = t0; t < t1; ++t) {{ const int k = cs_start[t]; cs_start[t] = at; at += k; }}
+    if (tid == {THREADS - 1}) cs_start[{pt}] = cs_part[{THREADS - 1}];
+    __syncthreads();
+    if (blockIdx.x == 0) {{
+      for (int t = tid; t <= {pt}; t += {THREADS}) args.rt_tile_steps[t] = cs_start[t];
+      if (tid == 0) args.rt_count[0] = cs_start[{pt}];
+    }}
+  }}"""
+
+    def _cursor_step(self) -> str:
+        """With a cursor: table step js's tile (the last tile starting at or before it) and block (the
+        tile's (js - start)-th running block, or block 0 of a tile with none: an empty step), as the code
+        the step tables would hold (the kernel reads its block and its empty flag)."""
+        sch = self.sch
+        pt, nb = sch.pattern_tiles, -(-self.plan.phases[0].range.count // 64)
+        radix = sch.phase_radix * sch.iterations
+        return f"""int t = 0;
+    {{ int hi = {pt - 1};
+      while (t < hi) {{ const int mid = (t + hi + 1) >> 1; if (cs_start[mid] <= js) t = mid; else hi = mid - 1; }} }}
+    int code = 4;  // an empty step at block 0, unless a running block is found
+    {{ int r = js - cs_start[t];
+      for (int wi = 0; wi < {nb}; ++wi) {{
+        unsigned long long w_ = cs_run[t * {nb} + wi];
+        const int c = __popcll(w_);
+        if (r < c) {{
+          for (; r > 0; --r) w_ &= w_ - 1;
+          code = ((wi * 64 + __ffsll((long long)w_) - 1) * {radix}) << {CODE_SHIFT};
+          break;
+        }}
+        r -= c;
+      }} }}"""
+
     def _trace_start(self) -> str:
         if not self.trace:
             return ""
@@ -591,7 +682,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
 """
 
 
-def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: str, trace: bool = False) -> Program:
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: str, trace: bool = False,
+          cursor: bool = False) -> Program:
     if m.out.dtype.name != "bfloat16":
         raise KernelError("the gfx950 decode lowering stores bf16 outputs")
-    return _Decode(plan, sch, m, name, trace).program()
+    return _Decode(plan, sch, m, name, trace, cursor).program()

@@ -190,11 +190,14 @@ class Plan:
 
     @property
     def cursor(self) -> bool:
+        """Must the kernel find its steps as it runs (runtime loop bounds)? Not lowered by this backend."""
         return False
 
     @property
     def either(self) -> bool:
-        return False
+        """May the kernel find its steps either way: from step tables the device makes of its runtime masks
+        before it runs, or with a cursor as it runs (src/autokernel/plan.py:318-322)? Tuning tries both."""
+        return self.runtime and not self.cursor
 
     def operand(self, name: str) -> Operand:
         return next(op for op in self.operands if op.name == name)

@@ -15,6 +15,7 @@ Tuning needs a GPU; without one the defaults are used (and `kernel(...)` raises 
 from __future__ import annotations
 
 import dataclasses
+import itertools
 import math
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any, Callable, Dict, List, Optional, Sequence, Tuple
@@ -39,17 +40,19 @@ MIN_GAIN = 0.01
 
 @dataclass(frozen=True)
 class Config:
-    """A schedule: the kernel's tunable (None if it has none) and its buffering."""
+    """A schedule: the kernel's tunable (None if it has none), its buffering, and whether a kernel with
+    runtime masks finds its steps with a cursor as it runs (src/autokernel/tune.py:57-72)."""
 
     tunable: Any
     pipeline: Pipeline
     cursor: bool = False
 
     def __str__(self) -> str:
+        rest = f"{self.pipeline}, steps found as it runs" if self.cursor else str(self.pipeline)
         if self.tunable is None:
-            return str(self.pipeline)
+            return rest
         fields = ", ".join(f"{k}={getattr(self.tunable, k)!r}" for k in choices(self.tunable))
-        return f"{type(self.tunable).__name__}({fields}), {self.pipeline}"
+        return f"{type(self.tunable).__name__}({fields}), {rest}"
 
 
 @dataclass
@@ -147,7 +150,14 @@ def proposals(kernel: Any, signature: Any, trial: Trial) -> List[Config]:
         buffering.append(dataclasses.replace(pipe, output_buffers=pipe.output_buffers + 1))
     if not prof.regions and pipe.input_buffers < MAX_INPUT_BUFFERS:
         buffering.append(dataclasses.replace(pipe, input_buffers=pipe.input_buffers + 1))
-    moves = [Config(config.tunable, p) for p in buffering]
+    moves = [Config(config.tunable, p, config.cursor) for p in buffering]
+    if plan.either:  # the other way of finding the steps (src/autokernel/tune.py:186-187), where it lowers
+        other = dataclasses.replace(config, cursor=not config.cursor)
+        try:
+            kernel.lowered(signature, other)
+            moves.insert(0, other)
+        except KernelError:
+            pass
     near: List[Tuple[_Stats, Config]] = []
     for tunable in neighbours(config.tunable) if config.tunable is not None else ():
         try:
@@ -156,7 +166,7 @@ def proposals(kernel: Any, signature: Any, trial: Trial) -> List[Config]:
             continue
         if _loop_steps(plan) == loops:
             continue
-        near.append((_stats(plan, schedule), Config(tunable, pipe)))
+        near.append((_stats(plan, schedule), Config(tunable, pipe, config.cursor)))
     if prof.bottleneck == "dma":
         near = sorted((n for n in near if (n[0].bytes, n[0].steps) < (here.bytes, here.steps)),
                       key=lambda n: (n[0].bytes, n[0].steps))
@@ -181,19 +191,21 @@ def _smaller(kernel: Any, signature: Any, config: Config) -> List[Config]:
 
 
 def _other_kernels(kernel: Any, signature: Any, start: Config) -> List[Config]:
-    """The bufferings of `start` whose generated kernels differ from its own."""
+    """The bufferings of `start` (and the other way of finding steps, where a kernel may take either) whose
+    generated kernels differ from its own."""
     here = kernel.lowered(signature, start).source
     found = []
-    for n in range(1, MAX_INPUT_BUFFERS + 1):
-        for m in range(1, MAX_OUTPUT_BUFFERS + 1):
-            config = Config(start.tunable, Pipeline(n, m))
-            if config == start:
-                continue
-            try:
-                if kernel.lowered(signature, config).source != here:
-                    found.append(config)
-            except KernelError:
-                continue
+    plan, _ = kernel.build(signature, start.tunable)
+    cursors = (False, True) if plan.either else (start.cursor,)
+    for n, m, cursor in itertools.product(range(1, MAX_INPUT_BUFFERS + 1), range(1, MAX_OUTPUT_BUFFERS + 1), cursors):
+        config = Config(start.tunable, Pipeline(n, m), cursor)
+        if config == start:
+            continue
+        try:
+            if kernel.lowered(signature, config).source != here:
+                found.append(config)
+        except KernelError:
+            continue
     return found
 
 

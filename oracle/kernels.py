@@ -227,3 +227,32 @@ def gqa_contiguous_float64(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
             g = h // (H // Hkv)
             out[b, 0, h] = (torch.softmax(kk[:, g] @ qd[b, 0, h], 0) @ vv[:, g]).numpy()
     return out
+
+
+def rmsnorm_matmul(x: torch.Tensor, gamma: torch.Tensor, w: torch.Tensor, tm: int = 512, tn: int = 512,
+                   tk: int = 512, eps: float = 1e-6) -> torch.Tensor:
+    """examples/rmsnorm_matmul.py:33-46 of the reference: per output tile, over tk-deep blocks of the model
+    dim, acc += bf16(x * gamma) @ w (f32 accumulation) and each row's sum of squares of x (f32); then
+    out = bf16(acc * rsqrt(sum_sq / D + eps))."""
+    M, D = x.shape
+    N = w.shape[1]
+    tm, tn, tk = min(tm, M), min(tn, N), min(tk, D)
+    xf, gf, wf = _f32(x), _f32(gamma), _f32(w)
+    out = torch.zeros((M, N), dtype=x.dtype)
+    for i in range(0, M, tm):
+        for j in range(0, N, tn):
+            acc = torch.zeros((tm, tn), dtype=torch.float32)
+            sum_sq = torch.zeros((tm, 1), dtype=torch.float32)
+            for k in range(0, D, tk):
+                xk = xf[i:i + tm, k:k + tk]
+                sum_sq += (xk * xk).sum(dim=1, keepdim=True)
+                acc += (xk * gf[0:1, k:k + tk]).to(x.dtype).float() @ wf[k:k + tk, j:j + tn]
+            out[i:i + tm, j:j + tn] = (acc * torch.rsqrt(sum_sq / D + eps)).to(x.dtype)
+    return out
+
+
+def rmsnorm_matmul_float64(x: torch.Tensor, gamma: torch.Tensor, w: torch.Tensor, eps: float = 1e-6) -> np.ndarray:
+    """rmsnorm(x) @ w in float64: x / sqrt(mean(x^2, axis=-1) + eps) * gamma, then @ w."""
+    xd, gd, wd = x.double().cpu(), gamma.double().cpu(), w.double().cpu()
+    normed = xd / torch.sqrt((xd * xd).mean(dim=1, keepdim=True) + eps) * gd
+    return (normed @ wd).numpy()

@@ -1,0 +1,66 @@
+"""Parity of RMSNorm fused with the projection after it (the reference's examples/rmsnorm_matmul.py) with
+the CPU oracle on the same seeded inputs, and at a larger size with a float32 GPU reference.
+
+The kernel runs a row pass (each row's sum of squares, and bf16(x * gamma), the matmul's left operand)
+and then the matmul, whose epilogue scales each row by rsqrt(sum_sq / D + eps).
+
+Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want| (2 bf16 ulp): the
+sum of squares is added in another order than the spec's tk-deep blocks, and the products in MFMA order.
+"""
+
+import pytest
+import torch
+
+from examples.rmsnorm_matmul import NormMatmulTiles, rmsnorm_matmul
+from oracle import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(m, d, n, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(1, d, generator=g)).to(torch.bfloat16)
+    w = (torch.randn(d, n, generator=g) / d**0.5).to(torch.bfloat16)
+    return x, gamma, w
+
+
+def _close(got, want):
+    got, want = got.float().cpu(), torch.as_tensor(want).float().cpu()
+    scale = want.abs().max().item()
+    bad = (got - want).abs() > 1e-2 * want.abs() + 1e-2 * scale
+    assert not bad.any(), f"{int(bad.sum())} of {want.numel()} differ; max |diff| {(got - want).abs().max().item()}"
+
+
+@pytest.mark.parametrize("m,d,n,tiles", [
+    (1024, 1024, 512, NormMatmulTiles(512, 512, 512)),
+    (512, 768, 256, NormMatmulTiles(256, 256, 256)),
+    (256, 512, 512, NormMatmulTiles(128, 128, 128)),
+])
+def test_rmsnorm_matmul_matches_oracle(m, d, n, tiles):
+    x, gamma, w = _inputs(m, d, n)
+    print(f"rmsnorm_matmul {m}x{d}x{n} {tiles}", flush=True)
+    got = rmsnorm_matmul(x.cuda(), gamma.cuda(), w.cuda(), tiles)
+    torch.cuda.synchronize()
+    _close(got, kernels.rmsnorm_matmul(x, gamma, w, tiles.tm, tiles.tn, tiles.tk))
+    _close(got, kernels.rmsnorm_matmul_float64(x, gamma, w))
+
+
+def test_rmsnorm_matmul_verify_against_the_spec():
+    x, gamma, w = _inputs(512, 512, 512, seed=2)
+    tiles = NormMatmulTiles(256, 256, 256)
+    print("rmsnorm_matmul verify", flush=True)
+    err = rmsnorm_matmul.verify(x.cuda(), gamma.cuda(), w.cuda(), tiles)
+    assert err <= 1e-2 * 4  # the outputs are O(1): within a few bf16 ulp of the spec's own evaluation
+
+
+def test_rmsnorm_matmul_large():
+    """4096 x 4096 x 4096 at the default tiles against float32 on the GPU."""
+    x, gamma, w = _inputs(4096, 4096, 4096, seed=1)
+    x, gamma, w = x.cuda(), gamma.cuda(), w.cuda()
+    print("rmsnorm_matmul 4096^3", flush=True)
+    got = rmsnorm_matmul(x, gamma, w, NormMatmulTiles())
+    xf = x.float()
+    normed = (xf * torch.rsqrt((xf * xf).mean(dim=1, keepdim=True) + 1e-6) * gamma.float())
+    want = normed @ w.float()
+    _close(got, want)

@@ -130,6 +130,37 @@ def test_contiguous_float64_catches_an_off_by_one_length():
     assert np.abs(want - wrong).max() > 1e-3
 
 
+@pytest.mark.parametrize("tiles", [(128, 128, 128), (256, 128, 512)])
+def test_rmsnorm_matmul_is_normalized_projection(tiles):
+    x = rand((256, 512), 0, BF)
+    gamma = (1 + 0.1 * rand((1, 512), 1, torch.float32)).to(BF)
+    w = (rand((512, 256), 2, torch.float32) / 16).to(BF)
+    got = kernels.rmsnorm_matmul(x, gamma, w, *tiles)
+    _close(got.double(), kernels.rmsnorm_matmul_float64(x, gamma, w))
+
+
+def test_rmsnorm_float64_is_the_plain_normalization():
+    # rows of one repeated value v normalize to sign(v) (times gamma): mean(x^2) = v^2
+    x = torch.full((4, 64), 3.0, dtype=torch.float64)
+    x[1] = -0.5
+    gamma = torch.ones((1, 64), dtype=torch.float64)
+    w = torch.eye(64, dtype=torch.float64)
+    got = kernels.rmsnorm_matmul_float64(x, gamma, w, eps=0.0)
+    np.testing.assert_allclose(got[0], np.ones(64), rtol=1e-12)
+    np.testing.assert_allclose(got[1], -np.ones(64), rtol=1e-12)
+
+
+def test_rmsnorm_matmul_check_catches_a_planted_eps():
+    # small activations (mean square 1e-4): the oracle run with a wrong eps fails the float64 comparison
+    x = (rand((128, 256), 3, torch.float32) * 0.01).to(BF)
+    gamma = torch.ones((1, 256), dtype=BF)
+    w = (rand((256, 128), 4, torch.float32) / 16).to(BF)
+    want = kernels.rmsnorm_matmul_float64(x, gamma, w)
+    _close(kernels.rmsnorm_matmul(x, gamma, w, 128, 128, 128).double(), want)
+    with pytest.raises(AssertionError):
+        _close(kernels.rmsnorm_matmul(x, gamma, w, 128, 128, 128, eps=1e-3).double(), want)
+
+
 def test_grouped_matmul_routes_groups_to_their_experts():
     G, E, K, N = 64, 3, 128, 256
     xs = rand((4 * G, K), 0, BF)

@@ -68,6 +68,13 @@ AK_INLINE float ak_xor32(float x) {
 }
 AK_INLINE float ak_xor32_max(float x) { return fmaxf(x, ak_xor32(x)); }
 AK_INLINE float ak_xor32_sum(float x) { return x + ak_xor32(x); }
+// The sum over the wave's 64 lanes, in every lane.
+AK_INLINE float ak_wave_sum(float x) {
+  x += ak_xor32(x);
+#pragma unroll
+  for (int d = 16; d >= 1; d >>= 1) x += __shfl_xor(x, d);
+  return x;
+}
 
 // 8x8 transpose of 16-bit elements held as 8 rows of 4 dwords: out[c] holds column c (8 elements).
 AK_INLINE void ak_transpose8x8_b16(const ak_u32x4 in[8], ak_u32x4 out[8]) {

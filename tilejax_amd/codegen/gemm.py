@@ -36,7 +36,7 @@ from ..plan import Kind, Operand, Output, Plan
 from ..schedule import CODE_SHIFT, FILL_TABLE, STEP_CODE, STEP_TILE, TILE_TABLE, Schedule
 from .common import Index, decode_fill, decode_tile, static_tile_steps, strides, tile_base, work_lists
 from .device import PRELUDE
-from .expr import Emitter, Interval, ctype, intervals, literal, nodes_between
+from .expr import ElementEmitter, Emitter, Interval, ctype, intervals, literal, nodes_between
 from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 
 __all__ = ["GemmMatch", "match", "lower"]
@@ -59,24 +59,94 @@ class GemmMatch:
     init: float
     out: Output
     value: Any  # the stored value (Node, or a number)
+    # A row prologue: the left operand is a pointwise function of its load and k-wise row vectors (`a_expr`,
+    # None for a plain load), and other carried values are row sums of such functions (`side`: (name, summand,
+    # initial value)), which the epilogue may read (the reference's examples/rmsnorm_matmul.py:33-46).
+    a_expr: Optional[Node] = None
+    side: Tuple[Tuple[str, Node, float], ...] = ()
 
 
 def _is(node: Any, op: str) -> bool:
     return isinstance(node, Node) and node.op == op
 
 
-def _dot_of_loads(plan: Plan, node: Node) -> Optional[Tuple[Operand, Operand, bool]]:
+_POINTWISE = {"astype", "multiply", "add", "subtract", "divide", "negative", "maximum", "minimum", "full"}
+
+
+def _row_prologue(plan: Plan, expr: Any, x: Optional[Node] = None) -> Optional[Node]:
+    """The one 2-D load a pointwise bf16 or f32 expression is a function of, besides loads of k-wise row
+    vectors ((1, n) tiles) and constants; None if it is anything else. With `x`, that load must be `x`."""
+    if not isinstance(expr, Node):
+        return None
+    loads = []
+    for n in nodes_between(expr):
+        if n.op == "load":
+            loads.append(n)
+        elif n.op not in _POINTWISE:
+            return None
+    main = [n for n in loads if len(n.shape) == 2 and n.shape[0] != 1]
+    if len({id(n) for n in main}) != 1 or (x is not None and main[0] is not x):
+        return None
+    if any(len(n.shape) != 2 or (n.shape[0] != 1 and n is not main[0]) for n in loads):
+        return None
+    return main[0]
+
+
+def _dot_of_loads(plan: Plan, node: Node) -> Optional[Tuple[Operand, Operand, bool, Optional[Node], Optional[Node]]]:
+    """(a's operand, b's operand, `a @ b.T`, a's expression if it isn't a plain load, a's load)."""
     if not (_is(node, "dot") or _is(node, "dot_nt")) or node.dtype.name != "float32":
         return None
     a, b = node.args[0], node.args[1]
-    if not (_is(a, "load") and _is(b, "load")):
+    a_expr = None
+    if not _is(a, "load"):
+        x = _row_prologue(plan, a)
+        if x is None or a.dtype.name != "bfloat16" or a.shape != x.shape:
+            return None
+        a_expr, a = a, x
+    if not _is(b, "load"):
         return None
     opa, opb = plan.operand(a.kwargs["operand"]), plan.operand(b.kwargs["operand"])
     if opa.tile.dtype.name != "bfloat16" or opb.tile.dtype.name != "bfloat16":
         return None
     if len(opa.tile.shape) != 2 or len(opb.tile.shape) != 2:
         return None
-    return opa, opb, node.op == "dot_nt"
+    return opa, opb, node.op == "dot_nt", a_expr, a
+
+
+_UNIFORM_OPS = _POINTWISE | {"rsqrt", "sqrt", "exp", "log", "reciprocal", "square", "tanh", "sigmoid"}
+
+
+def _column_uniform(node: Node, side: set) -> bool:
+    """Is `node` the same in every column: built pointwise from row sums (`side`) and constants only?"""
+    for n in nodes_between(node):
+        if n.op == "carried":
+            if n.kwargs["name"] not in side:
+                return False
+        elif n.op not in _UNIFORM_OPS:
+            return False
+    return True
+
+
+def _side_sum(plan: Plan, name: str, x: Node) -> Optional[Tuple[str, Node, float]]:
+    """A carried value whose update is `c + jnp.sum(h, axis=1, keepdims=True)`, h a row-prologue function of
+    the left operand's load, from a constant: (name, h, initial value)."""
+    body, seg0 = plan.scopes["body0"], plan.scopes["seg0"]
+    new, init = body.values.get(name), seg0.values.get(name)
+    leaf = body.carried_in.get(name)
+    if not (isinstance(new, jaxlite.Sym) and _is(new.node, "add")) or leaf is None:
+        return None
+    u, v = new.node.args
+    red = v if u is leaf else u if v is leaf else None
+    if not (_is(red, "reduce_sum") and red.kwargs.get("axis") in (1, -1) and red.kwargs.get("keepdims")):
+        return None
+    h = red.args[0]
+    if _row_prologue(plan, h, x) is None:
+        return None
+    if isinstance(init, jaxlite.Sym) and _is(init.node, "full"):
+        return name, h, float(init.node.kwargs["value"])
+    if isinstance(init, (int, float)):
+        return name, h, float(init)
+    return None
 
 
 def match(plan: Plan) -> Optional[GemmMatch]:
@@ -89,23 +159,29 @@ def match(plan: Plan) -> Optional[GemmMatch]:
     last = plan.scopes["last"]
     value = last.stores.get(out.name)
     root = value.node if isinstance(value, jaxlite.Sym) else None
+    side: List[Tuple[str, Node, float]] = []
     if plan.phases:
-        if set(plan.carried) != {name for name in plan.carried} or len(plan.carried) != 1:
-            return None
-        (acc,) = plan.carried
         body, seg0 = plan.scopes["body0"], plan.scopes["seg0"]
-        new = body.values.get(acc)
-        init = seg0.values.get(acc)
-        if not (isinstance(new, jaxlite.Sym) and _is(new.node, "add")):
-            return None
-        x, y = new.node.args
-        leaf = body.carried_in.get(acc)
-        dot = y if x is leaf else x if y is leaf else None
-        if dot is None:
-            return None
-        found = _dot_of_loads(plan, dot)
+        found = None
+        for acc in plan.carried:  # the carried value a matmul accumulates into
+            new = body.values.get(acc)
+            if not (isinstance(new, jaxlite.Sym) and _is(new.node, "add")):
+                continue
+            x, y = new.node.args
+            leaf = body.carried_in.get(acc)
+            dot = y if x is leaf else x if y is leaf else None
+            found = _dot_of_loads(plan, dot) if isinstance(dot, Node) else None
+            if found is not None:
+                break
         if found is None:
             return None
+        init = seg0.values.get(acc)
+        for name in plan.carried:  # every other carried value: a row sum of the left operand's prologue
+            if name != acc:
+                got = _side_sum(plan, name, found[4])
+                if got is None:
+                    return None
+                side.append(got)
         if isinstance(init, jaxlite.Sym) and _is(init.node, "full"):
             init_value = float(init.node.kwargs["value"])
         elif isinstance(init, (int, float)):
@@ -128,7 +204,7 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         if found is None:
             return None
         acc_leaf, init_value, kvar = dots[0], 0.0, None
-    opa, opb, nt = found
+    opa, opb, nt, a_expr, _ = found
     tm, tk = opa.tile.shape
     tn, tkb = (opb.tile.shape if nt else opb.tile.shape[::-1])
     if tkb != tk or tuple(out.tile.shape) != (tm, tn):
@@ -149,7 +225,7 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         return None
     if out.dtype.name not in ("bfloat16", "float32"):
         return None
-    return GemmMatch(opa, opb, nt, kvar, tm, tn, tk, acc_leaf, init_value, out, value)
+    return GemmMatch(opa, opb, nt, kvar, tm, tn, tk, acc_leaf, init_value, out, value, a_expr, tuple(side))
 
 
 @dataclass(frozen=True)
@@ -201,6 +277,31 @@ class _Gemm:
         self.tables: Dict[str, np.ndarray] = {}
         self.const_value: Optional[float] = None
         self.split: Optional[Tuple[int, int, int]] = None  # (items cut, chunks per item, K slices per chunk)
+        self.prologue = m.a_expr is not None or bool(m.side)
+        if self.prologue:
+            self._check_prologue()
+
+    def _check_prologue(self) -> None:
+        """A row prologue runs as its own pass over the left operand's whole array: its rows are the output's
+        rows and its columns the reduction, every block of which the loop visits."""
+        plan, sch, m = self.plan, self.sch, self.m
+        shape = plan.inputs[m.a.param].shape
+        wins = [w for w in m.a.tile.windows if w.size is not None]
+        if len(shape) != 2 or len(wins) != 2 or len(m.a.tile.windows) != 2:
+            raise KernelError("a matmul's row prologue is lowered for a 2-D left operand only")
+        rows, cols = wins
+        if sch.runtime or (plan.phases and plan.phases[0].range.mask is not None):
+            raise KernelError("a matmul's row prologue is lowered for unmasked reduction loops only")
+        if rows.offset != 0 or cols.offset != 0 or shape[1] % 8:
+            raise KernelError("a matmul's row prologue needs windows from the array's start and rows of a "
+                              "multiple of 8 elements")
+        if plan.phases:
+            r = plan.phases[0].range
+            if not (r.start == 0 and r.step == m.tk and r.count * m.tk == shape[1]):
+                raise KernelError("a matmul's row prologue needs a reduction loop over the whole row")
+        elif m.tk != shape[1]:
+            raise KernelError("a matmul's row prologue needs a reduction loop over the whole row")
+        self.rows_n, self.cols_n = shape
 
     # ------------------------------------------------------------------ work items (host)
 
@@ -353,6 +454,12 @@ class _Gemm:
         source = self._source(args)
         launches = [Launch(self.name, args, (grid, 1, 1), (64 * WAVE_GRID[0] * WAVE_GRID[1], 1, 1), 0)]
         workspace = {}
+        if self.prologue:
+            source += self._rows_source()
+            workspace["rn_a"] = self.rows_n * self.cols_n * 2
+            for name, _, _ in m.side:
+                workspace[f"rn_{name}"] = self.rows_n * 4
+            launches.insert(0, Launch(f"{self.name}_rows", args, (-(-self.rows_n // 4), 1, 1), (THREADS, 1, 1), 0))
         if self.trace:
             workspace[TRACE] = grid * TRACE_FIELDS * 8
         if self.split:
@@ -393,10 +500,62 @@ class _Gemm:
             args.append(Arg("workspace", "gm_part", "float* __restrict__", "gm_part"))
         if self.trace:
             args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
+        if self.prologue:
+            args.append(Arg("workspace", "rn_a", "ak_u16* __restrict__", "rn_a"))
+            for name, _, _ in m.side:
+                args.append(Arg("workspace", f"rn_{name}", "float* __restrict__", f"rn_{name}"))
         if self.sch.runtime:
             args.append(Arg("workspace", "step_code", "const int* __restrict__", "rt_step_code"))
             args.append(Arg("workspace", "tile_steps", "const int* __restrict__", "rt_tile_steps"))
         return args
+
+    def _rows_source(self) -> str:
+        """The row prologue's pass: one wave per row of the left operand, eight columns a lane at a time. It
+        writes the operand the matmul reads (the prologue's bf16 value per element) and each row sum, a
+        lane's partial sums added across the wave."""
+        plan, m = self.plan, self.m
+        zero = Index(plan, lambda v: "0")
+
+        def leaves(n: Node, idx: Tuple[str, ...]) -> Optional[str]:
+            if n.op == "load":
+                op = plan.operand(n.kwargs["operand"])
+                shape = plan.inputs[op.param].shape
+                base, st = tile_base(op.tile, shape, zero, lambda v: "0")
+                flat = " + ".join(f"(long long)({i}) * {s_}" for i, s_ in zip(idx, st)) or "0"
+                if op.tile.dtype.name != "bfloat16":
+                    raise KernelError("a matmul's row prologue reads bf16 operands")
+                return f"ak_bf16_to_f32(((const ak_u16*)args.{op.tile.array})[({base}) + {flat}])"
+            return None
+
+        em = ElementEmitter(leaves)
+        a_node = m.a_expr
+        if a_node is None:  # (only row sums: the operand is copied as it is)
+            a_node = next(n for n in nodes_between(m.side[0][1]) if n.op == "load")
+        D = self.cols_n
+        sums = "".join(f" float rs_{k} = 0.f;" for k in range(len(m.side)))
+        adds = "\n".join(f"        rs_{k} += (float)({em.at(h, ('r', 'c'))}) + (float)({em.at(h, ('r', 'c + 1'))});"
+                          for k, (_, h, _) in enumerate(m.side))
+        outs = "\n".join(f"  rs_{k} = ak_wave_sum(rs_{k}); if (lane == 0) args.rn_{name}[r] = rs_{k};"
+                          for k, (name, _, _) in enumerate(m.side))
+        return f"""
+// The row prologue of `{plan.nest.name}`: rows {self.rows_n} x {D}, one wave per row.
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {self.name}_args args) {{
+  const int r = blockIdx.x * {THREADS // 64} + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (r >= {self.rows_n}) return;
+ {sums}
+  for (int c0 = lane * 8; c0 < {D}; c0 += 512) {{
+    unsigned pk[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {{
+      const int c = c0 + e;
+      pk[e >> 1] = ak_pack_bf16x2((float)({em.at(a_node, ('r', 'c'))}), (float)({em.at(a_node, ('r', 'c + 1'))}));
+{adds}
+    }}
+    *(ak_u32x4*)(args.rn_a + (long long)r * {D} + c0) = ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}};
+  }}
+{outs}
+}}
+"""
 
     def _pitch(self, op: Operand) -> int:
         """Elements between consecutive rows of an operand tile (its first sliced dim's stride)."""
@@ -483,6 +642,14 @@ class _Gemm:
                 ix = plan.index(n.kwargs["array"])
                 flat = " + ".join(f"({em.value(i)}) * {s}" for i, s in zip(n.args, strides(ix.shape))) or "0"
                 return f"args.{ix.name}[{flat}]"
+            if n.op == "tile" and isinstance(n.args[0], Node) and _column_uniform(n.args[0], {x[0] for x in m.side}):
+                return em.emit(n.args[0])  # tiling a row statistic along the columns repeats each row's value
+            if n.op == "carried" and any(n.kwargs["name"] == name for name, _, _ in m.side):
+                # a row sum: the same for every column; the tile's rows are the left operand's
+                name, _, init = next(x for x in m.side if x[0] == n.kwargs["name"])
+                rows = [w for w in m.a.tile.windows if w.size is not None][0]
+                row = f"(lv_{rows.loop}) + er" if rows.loop else "er"
+                return f"({literal(init, n.dtype)} + args.rn_{name}[{row}])"
             if n.op in ("carried", "load"):
                 raise KernelError("the matmul epilogue reads only the accumulator, positions and loop values")
             return None
@@ -492,7 +659,9 @@ class _Gemm:
         epi = "\n              ".join(em.lines)
         out_bf16 = m.out.dtype.name == "bfloat16"
         struct = c_struct(f"{self.name}_args", args)
-        A, B, O = f"args.{m.a.tile.array}", f"args.{m.b.tile.array}", f"args.{m.out.name}_out"
+        # with a row prologue the left operand is its pass's output, laid out as the operand's array
+        A = "args.rn_a" if self.prologue else f"args.{m.a.tile.array}"
+        B, O = f"args.{m.b.tile.array}", f"args.{m.out.name}_out"
         a_numel, b_numel = int(np.prod(a_shape)), int(np.prod(b_shape))
         fill_value = literal(m.out.fill if m.out.fill is not None else 0, m.out.dtype)
         const_value = literal(self.const_value if self.const_value is not None else 0.0, m.out.dtype)

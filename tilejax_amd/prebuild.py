@@ -46,6 +46,13 @@ def standard() -> Iterator[Tuple[object, tuple]]:
                                    ((1024, 512, 1024, 4, 4), GT(512, 512)), ((2048, 1024, 512, 4, 8), GT(512, 256)),
                                    ((16384, 4096, 14336, 8, 64), GT(512, 512))):
         yield moe.grouped_matmul, (_bf16(m, k), _bf16(e, k, n), _i32(g), tiles)
+    from examples import rmsnorm_matmul as rm
+
+    R = rm.NormMatmulTiles
+    for (m, d, n), tiles in (((1024, 1024, 512), R(512, 512, 512)), ((512, 768, 256), R(256, 256, 256)),
+                             ((256, 512, 512), R(128, 128, 128)), ((512, 512, 512), R(256, 256, 256)),
+                             ((4096, 4096, 4096), R())):
+        yield rm.rmsnorm_matmul, (_bf16(m, d), _bf16(1, d), _bf16(d, n), tiles)
     from examples import decode
 
     for b, pages, n_pages in ((4, 64, 256), (5, 100, 500), (64, 512, 32768)):

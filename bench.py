@@ -7,6 +7,7 @@ already resident in HBM. `value` is its TFLOP/s (2*M*N*K / time) at MatmulTiles(
 carries the other BASELINE configurations in `legs`, each timed the same way:
 - dense at MatmulTiles(1024, 2048, 1024);
 - causal `tril(x @ y)` at the same size, with its time over the dense time;
+- RMSNorm fused with the same matmul (`rmsnorm_matmul`, the reference's examples/rmsnorm_matmul.py);
 - causal MHA at (4, 16, 2048, 128) and (1, 16, 4096, 128);
 - the MoE grouped GEMM (16384 x 4096 x 14336, 8 experts);
 - paged GQA decode (64 sequences, HBM GB/s), with step tables and with a cursor, and the same sequences
@@ -112,7 +113,8 @@ def main() -> int:
     ap.add_argument("--tiles", default="512,512,512", help="dense matmul spec tiles tm,tn,tk")
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list of legs to run: dense,dense2,causal,attention,moe,decode")
+    ap.add_argument("--only", default="",
+                    help="comma list of legs to run: dense,dense2,causal,rmsnorm,attention,moe,decode")
     ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3; "
                     "default: profiles/traffic.json")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -139,7 +141,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    legs = set(args.only.split(",")) if args.only else {"dense", "causal", "attention", "moe", "decode"}
+    legs = set(args.only.split(",")) if args.only else {"dense", "causal", "rmsnorm", "attention", "moe", "decode"}
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
     x = torch.randn(N_DENSE, N_DENSE, generator=g).to(torch.bfloat16).to(dev)
@@ -176,6 +178,21 @@ def main() -> int:
         _log(f"  {cms * 1e3:.1f} us/call = {cms / ms:.3f} x dense")
         out["causal"] = {"tiles": [ct.tm, ct.tn, ct.tk], "us": round(cms * 1e3, 2), "vs_dense": round(cms / ms, 4),
                          "tflops_dense_equiv": round(flop / (cms * 1e-3) / 1e12, 2)}
+
+    if "rmsnorm" in legs:
+        try:
+            from examples.rmsnorm_matmul import NormMatmulTiles, rmsnorm_matmul
+
+            g = torch.Generator().manual_seed(2)
+            gamma = (1 + 0.1 * torch.randn(1, N_DENSE, generator=g)).to(torch.bfloat16).to(dev)
+            rl = rmsnorm_matmul.lower(x, gamma, y, NormMatmulTiles(tiles.tm, tiles.tn, tiles.tk))
+            rms_, _ = time_kernel(lambda: rl.run(x, gamma, y), args.steps, args.warmup)
+            _log(f"RMSNorm + matmul {N_DENSE}^3: {rms_ * 1e3:.1f} us = {rms_ / ms:.3f} x dense")
+            out["rmsnorm_matmul"] = {"shape": [N_DENSE] * 3, "us": round(rms_ * 1e3, 2), "vs_dense": round(rms_ / ms, 4),
+                                     "tflops": round(flop / (rms_ * 1e-3) / 1e12, 2)}
+        except Exception as e:  # reported, not hidden
+            _log(f"RMSNorm + matmul: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
+            out["rmsnorm_matmul"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
 
     if "attention" in legs:
         try:

@@ -51,7 +51,7 @@ def standard() -> Iterator[Tuple[object, tuple]]:
     R = rm.NormMatmulTiles
     for (m, d, n), tiles in (((1024, 1024, 512), R(512, 512, 512)), ((512, 768, 256), R(256, 256, 256)),
                              ((256, 512, 512), R(128, 128, 128)), ((512, 512, 512), R(256, 256, 256)),
-                             ((4096, 4096, 4096), R())):
+                             ((4096, 4096, 4096), R()), ((8192, 8192, 8192), R())):
         yield rm.rmsnorm_matmul, (_bf16(m, d), _bf16(1, d), _bf16(d, n), tiles)
     from examples import decode
 

@@ -53,10 +53,14 @@ __all__ = ["FlashMatch", "match", "lower"]
 LOG2E = 1.4426950408889634
 RESCALE_SLACK = 8.0  # natural-log units: p stays below e^8 between rescales
 MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 once a row has a real score
-AHEAD = 2  # K and V blocks are loaded this many blocks ahead of use; one barrier per block
-# LDS stages of K and V: AHEAD + 1 would do; the ring of block-table entries the loop keeps (blocks b to
-# b + AHEAD + 1, at b modulo STAGES) takes AHEAD + 2, and one stage per ring slot keeps both static
-STAGES = AHEAD + 2
+# Workgroups of 4 waves (128 query rows) with two LDS stages (64 KiB): two workgroups share a CU, and as
+# they keep no step with each other, one's MFMA work runs beside the other's softmax. Measured against one
+# workgroup of 8 waves (256 rows) and four stages: equal at (4, 16, 2048, 128), 5 % faster at
+# (1, 16, 4096, 128).
+AHEAD = 1  # K and V blocks are loaded this many blocks ahead of use; one barrier per block
+STAGES = AHEAD + 1  # LDS stages of K and V (at least AHEAD + 1)
+RING = AHEAD + 2  # block-table entries kept in scalars: blocks b .. b + AHEAD + 1, at b modulo RING
+WAVES = 4  # waves per workgroup (None: 8 for tiles of a multiple of 256 query rows, else 4)
 K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
 V_AHEAD = 4  # V fragments in flight ahead of the O MFMAs
 
@@ -268,7 +272,7 @@ class _Flash:
         if m.d % 32 or m.dv % 32 or m.d > 128 or m.dv > 128:
             raise KernelError(f"the gfx950 attention lowering takes head dims that are multiples of 32 up to 128 "
                               f"(got {m.d} and {m.dv})")
-        self.nw = 8 if m.rows % 256 == 0 else 4 if m.rows % 128 == 0 else 0
+        self.nw = WAVES or (8 if m.rows % 256 == 0 else 4 if m.rows % 128 == 0 else 0)
         if not self.nw:
             raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of 128 rows (got {m.rows})")
         self.bq = 32 * self.nw
@@ -564,7 +568,7 @@ class _Flash:
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
         w(f"""
-extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_args args) {{
+extern "C" __global__ void __launch_bounds__({T}, {max(1, 8 // nw)}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int* item = args.fa_items + blockIdx.x * {stride};
@@ -668,13 +672,14 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                     a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);")
             return o
 
-        def compute(s: int, ind: str) -> List[str]:
+        def compute(s: int, ind: str, r: Optional[int] = None) -> List[str]:
             """Block b_ from stage s: S^T, the mask, the online softmax into `pf`, and O^T += V^T P^T."""
             o: List[str] = []
             a = o.append
             a(f"{ind}if (b_ < n_w) {{")
             a(f"{ind}  const char* ks = (const char*)ak_sk{s}; const char* vs = (const char*)ak_sv{s}; (void)vs;")
-            a(f"{ind}  const int lv_{jvar} = bj[{s}], ec0 = bc[{s}] + (lane >> 5) * 4;")
+            r = s if r is None else r
+            a(f"{ind}  const int lv_{jvar} = bj[{r}], ec0 = bc[{r}] + (lane >> 5) * 4;")
             a(f"{ind}  ak_f32x16 st[{kt}];")
             for t in range(kt):
                 a(f"{ind}  #pragma unroll")
@@ -752,7 +757,8 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
         # b + AHEAD - STAGES), so that load is issued right after it.
         per_block = ldk_n + ldv_n
 
-        w(f"  int bj[{STAGES}], bc[{STAGES}];  // table entries of blocks b .. b + {STAGES - 1}, at b mod {STAGES}")
+        unroll = STAGES * RING // math.gcd(STAGES, RING)  # loop positions: stage p % STAGES, ring slot p % RING
+        w(f"  int bj[{RING}], bc[{RING}];  // table entries of blocks b .. b + {RING - 1}, at b mod {RING}")
         for x in range(AHEAD + 1):
             w(entry_load(str(x), x, "  "))
         for s in range(AHEAD):
@@ -760,9 +766,10 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             L.extend(issue(s, s, "    "))
             w("  }")
         w("  ak_bf16x8 pf[" + str(ks) + "];  // P^T of the block (srcB of O^T = V^T P^T)")
-        w(f"  for (int b = 0; b < nblk; b += {STAGES}) {{")
-        for s in range(STAGES):
-            w(f"    {{ const int b_ = b + {s};")
+        w(f"  for (int b = 0; b < nblk; b += {unroll}) {{")
+        for p_ in range(unroll):
+            s, r_ = p_ % STAGES, p_ % RING
+            w(f"    {{ const int b_ = b + {p_};")
             w("      if (b_ < nblk) {")
             if tr:
                 w(f"        const unsigned long long tr_w0 = {NOW};")
@@ -775,10 +782,10 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             if tr:
                 w(f"        {{ const unsigned long long tr_w1 = {NOW}; if (b_ == 0) tr_fill = tr_w1 - tr_i0; else tr_wait += tr_w1 - tr_w0; }}")
             w(f"        if (b_ + {AHEAD} < nblk) {{")
-            L.extend(issue((s + AHEAD) % STAGES, (s + AHEAD) % STAGES, "          "))
+            L.extend(issue((r_ + AHEAD) % RING, (s + AHEAD) % STAGES, "          "))
             w("        }")
-            w(entry_load(f"b_ + {AHEAD + 1}", (s + AHEAD + 1) % STAGES, "        "))
-            L.extend(compute(s, "        "))
+            w(entry_load(f"b_ + {AHEAD + 1}", (r_ + AHEAD + 1) % RING, "        "))
+            L.extend(compute(s, "        ", r_))
             w("      }")
             w("    }")
         w("  }")

@@ -61,6 +61,7 @@ AHEAD = 1  # K and V blocks are loaded this many blocks ahead of use; one barrie
 STAGES = AHEAD + 1  # LDS stages of K and V (at least AHEAD + 1)
 RING = AHEAD + 2  # block-table entries kept in scalars: blocks b .. b + AHEAD + 1, at b modulo RING
 WAVES = 4  # waves per workgroup (None: 8 for tiles of a multiple of 256 query rows, else 4)
+BKV = 64  # keys per block (a multiple of 32)
 K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
 V_AHEAD = 4  # V fragments in flight ahead of the O MFMAs
 
@@ -276,9 +277,9 @@ class _Flash:
         if not self.nw:
             raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of 128 rows (got {m.rows})")
         self.bq = 32 * self.nw
-        self.bkv = 64
+        self.bkv = BKV
         if m.bk % self.bkv:
-            raise KernelError(f"the gfx950 attention lowering needs key blocks of a multiple of 64 (got {m.bk})")
+            raise KernelError(f"the gfx950 attention lowering needs key blocks of a multiple of {self.bkv} (got {m.bk})")
         if plan.runtime or sch.runtime:
             raise KernelError("attention with runtime masks is lowered by the decode path, not this one")
         self.jr = plan.phases[0].range
@@ -491,6 +492,7 @@ class _Flash:
         chk, chv = D // 8, DV // 8
         ldk_n = bkv * D // 8 // T
         ldv_n = bkv * DV // 8 // T
+        vo_n = max(1, 16 // (T // chk)) if chk >= 16 else 1
         if ldk_n < 1 or ldv_n < 1 or 64 % chk or 64 % chv:
             raise KernelError("attention block too small for the workgroup")
         index = Index(plan, lambda v: f"lv_{v}")
@@ -568,7 +570,7 @@ class _Flash:
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
         w(f"""
-extern "C" __global__ void __launch_bounds__({T}, {max(1, 8 // nw)}) {self.name}(const {self.name}_args args) {{
+extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int* item = args.fa_items + blockIdx.x * {stride};
@@ -593,7 +595,12 @@ extern "C" __global__ void __launch_bounds__({T}, {max(1, 8 // nw)}) {self.name}
       (int)({v_numel}LL * 2 - v_off * 2), 0x00020000);
   // K rows XOR-swizzled for ds_read_b128 (chunk ^ row & 15), V rows for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2)
   const int k_row = (wave * 64 + lane) / {chk}, v_row = (wave * 64 + lane) / {chv};
-  const unsigned k_voff = (unsigned)(k_row * {ldk * 2} + (((lane % {chk}) ^ (k_row & {min(15, chk - 1)})) * 16));
+  // A load step covers {T // chk} K rows; with fewer than 16 the swizzle (row & 15) differs between steps, so
+  // the lanes keep one offset per step position modulo 16 rows.
+  unsigned k_voff[{vo_n}];
+#pragma unroll
+  for (int p = 0; p < {vo_n}; ++p)
+    k_voff[p] = (unsigned)(k_row * {ldk * 2} + (((lane % {chk}) ^ ((p * {T // chk} + k_row) & {min(15, chk - 1)})) * 16));
   const unsigned v_voff = (unsigned)(v_row * {ldv * 2} + (((lane % {chv}) ^ (((v_row & 3) << 2) & {chv - 1})) * 16));
   int k_roff[{ds}];
 #pragma unroll
@@ -639,7 +646,7 @@ extern "C" __global__ void __launch_bounds__({T}, {max(1, 8 // nw)}) {self.name}
             out = [f"{ind}{{ const int kpos = bj[{r}] + {self.kwin.offset} + bc[{r}], vpos = bj[{r}] + {self.vwin.offset} + bc[{r}];"]
             rows_k, rows_v = T // chk, T // chv
             for c in range(ldk_n):
-                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, AK_LDS(&ak_sk{s}[({c * T} + wave * 64) * 8]), 16, k_voff, "
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, AK_LDS(&ak_sk{s}[({c * T} + wave * 64) * 8]), 16, k_voff[{c % vo_n}], "
                            f"(unsigned)((kpos + {c * rows_k}) * {kstride_j * 2}), 0, 0);")
             for c in range(ldv_n):
                 out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, AK_LDS(&ak_sv{s}[({c * T} + wave * 64) * 8]), 16, v_voff, "

@@ -33,6 +33,7 @@ __all__ = [
     "Tuning",
     "choice",
     "compare",
+    "enable_profiling",
     "kernel",
     "profile",
     "tunable",
@@ -46,10 +47,10 @@ def __getattr__(name: str) -> Any:
         from . import tune
 
         return getattr(tune, name)
-    if name == "KernelProfile":
-        from .profiling import KernelProfile
+    if name in ("KernelProfile", "enable_profiling"):
+        from . import profiling
 
-        return KernelProfile
+        return getattr(profiling, name)
     raise AttributeError(name)
 
 

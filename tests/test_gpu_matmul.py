@@ -102,3 +102,20 @@ def test_split_chunks_start_from_the_initial_value_once():
     torch.cuda.synchronize()
     want = k.reference(x, y)
     assert torch.allclose(got.cpu(), want, rtol=1e-4, atol=1e-3), (got.cpu() - want).abs().max()
+
+
+def test_four_input_buffers_take_half_depth_slices():
+    """Four input buffers don't fit as 64-deep slices of a 256 x 256 tile; the kernel then streams 32-deep
+    slices through four LDS stages, and computes the same."""
+    from tilejax_amd.pipeline import Pipeline
+    from tilejax_amd.tune import Config
+
+    x, y = _inputs(1024, 1024, 1024, seed=5)
+    tiles = MatmulTiles(512, 512, 512)
+    lowered = matmul.lowered(matmul.signature(x, y), Config(tiles, Pipeline(4, 2)))
+    assert lowered.program.notes["hw_tile"][2] == 32 and lowered.program.notes["stages"] == 4
+    print("matmul 1024^3, four 32-deep stages", flush=True)
+    got = lowered.run(x.cuda(), y.cuda())
+    _close(got, kernels.matmul(x, y, 512, 512, 512))
+    plain = matmul.lowered(matmul.signature(x, y), Config(tiles, Pipeline(2, 2))).run(x.cuda(), y.cuda())
+    assert torch.equal(got, plain)  # the same K order, so the same bits

@@ -253,12 +253,18 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline) -> HwTile:
     if m.tk % 64 and m.tk != 32:
         raise KernelError(f"the gfx950 matmul lowering needs a reduction block of 32 or a multiple of 64 (got {m.tk})")
     bk = 64 if m.tk % 128 == 0 else 32 if m.tk % 64 == 0 else 16
-    kslices = m.tk // bk
-    stages = 2
-    for s in range(max(2, pipeline.input_buffers), 1, -1):
-        if kslices % s == 0 and s * (bm + bn) * bk * 2 <= gfx950.LDS_BUDGET:
-            stages = s
-            break
+
+    def deepest(bk_: int) -> int:
+        kslices = m.tk // bk_
+        for s in range(max(2, pipeline.input_buffers), 1, -1):
+            if kslices % s == 0 and s * (bm + bn) * bk_ * 2 <= gfx950.LDS_BUDGET:
+                return s
+        return 2
+
+    stages = deepest(bk)
+    # More buffers than 64-deep slices can have in LDS: slices half as deep, so loads run further ahead.
+    if pipeline.input_buffers > stages and bk == 64 and deepest(32) > stages:
+        bk, stages = 32, deepest(32)
     return HwTile(bm, bn, bk, stages)
 
 

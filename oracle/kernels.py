@@ -128,9 +128,11 @@ def grouped_matmul(xs: torch.Tensor, w: torch.Tensor, group_expert: torch.Tensor
 
 def paged_gqa_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, block_tables: torch.Tensor,
                      lengths: torch.Tensor) -> torch.Tensor:
-    """examples/decode.py:199-223 (one new token, T = 1): each query head h attends its kv head
-    h // (H / Hkv) over positions < lengths[b], pages read through block_tables[b, p] (clamped); scores in
-    f32, p rounded to bf16 before `p @ v`; empty sequences give zeros."""
+    """examples/decode.py:199-223: query head h of new token t attends its kv head h // (H / Hkv) over the
+    positions `visible` gives (decode.py:92-99: < lengths[b] for one new token; with T of them, token t sits
+    at lengths[b] - T + t and sees the positions up to it), pages read through block_tables[b, p]
+    (clamped) while p * P < lengths[b]; scores in f32, p rounded to bf16 before `p @ v`, one online-softmax
+    step per page; empty sequences give zeros."""
     B, T, H, Dh = q.shape
     P, W = k_pages.shape[1], k_pages.shape[2]
     Hkv = W // Dh
@@ -145,30 +147,31 @@ def paged_gqa_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tens
         pages = [min(max(int(tables[b, p]), 0), n_pages - 1) for p in range(tables.shape[1]) if p * P < L]
         if not pages:
             continue
-        kk = torch.cat([kf[p] for p in pages])[:, :].reshape(-1, Hkv, Dh)
-        vv = torch.cat([vf[p] for p in pages])[:, :].reshape(-1, Hkv, Dh)
-        for h in range(H):
-            g = h // group
-            row_max = torch.tensor(MASK_VALUE)
-            row_sum = torch.tensor(0.0)
-            acc = torch.zeros(Dh)
-            for n, page in enumerate(pages):
-                s = (kf[page].reshape(P, Hkv, Dh)[:, g] @ qf[b, 0, h])
-                pos = n * P + torch.arange(P)
-                s = torch.where(pos < L, s, torch.tensor(MASK_VALUE))
-                m_new = torch.maximum(row_max, s.max())
-                p = torch.exp(s - m_new)
-                alpha = torch.exp(row_max - m_new)
-                row_sum = alpha * row_sum + p.sum()
-                acc = alpha * acc + p.to(q.dtype).float() @ vf[page].reshape(P, Hkv, Dh)[:, g]
-                row_max = m_new
-            out[b, 0, h] = (acc / torch.clamp(row_sum, min=1e-30)).to(q.dtype)
+        for t in range(T):
+            for h in range(H):
+                g = h // group
+                row_max = torch.tensor(MASK_VALUE)
+                row_sum = torch.tensor(0.0)
+                acc = torch.zeros(Dh)
+                for n, page in enumerate(pages):
+                    s = (kf[page].reshape(P, Hkv, Dh)[:, g] @ qf[b, t, h])
+                    pos = n * P + torch.arange(P)
+                    ok = pos < L if T == 1 else pos <= L - T + t
+                    s = torch.where(ok, s, torch.tensor(MASK_VALUE))
+                    m_new = torch.maximum(row_max, s.max())
+                    p = torch.exp(s - m_new)
+                    alpha = torch.exp(row_max - m_new)
+                    row_sum = alpha * row_sum + p.sum()
+                    acc = alpha * acc + p.to(q.dtype).float() @ vf[page].reshape(P, Hkv, Dh)[:, g]
+                    row_max = m_new
+                out[b, t, h] = (acc / torch.clamp(row_sum, min=1e-30)).to(q.dtype)
     return out
 
 
 def gqa_float64(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, block_tables: torch.Tensor,
                 lengths: torch.Tensor) -> np.ndarray:
-    """GQA decode attention in float64 over the pages (tests/test_decode.py:62-76 of the reference)."""
+    """GQA decode attention in float64 over the pages (tests/test_decode.py:62-76 of the reference): token t
+    of sequence b sits at position lengths[b] - T + t and sees the positions up to it."""
     B, T, H, Dh = q.shape
     P, W = k_pages.shape[1], k_pages.shape[2]
     Hkv = W // Dh
@@ -183,10 +186,12 @@ def gqa_float64(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, b
         npages = -(-L // P)
         kk = torch.cat([kd[int(tables[b, p])] for p in range(npages)])[:L].reshape(L, Hkv, Dh)
         vv = torch.cat([vd[int(tables[b, p])] for p in range(npages)])[:L].reshape(L, Hkv, Dh)
-        for h in range(H):
-            g = h // (H // Hkv)
-            s = kk[:, g] @ qd[b, 0, h]
-            out[b, 0, h] = (torch.softmax(s, 0) @ vv[:, g]).numpy()
+        for t in range(T):
+            seen = L - T + t + 1
+            for h in range(H):
+                g = h // (H // Hkv)
+                s = kk[:seen, g] @ qd[b, t, h]
+                out[b, t, h] = (torch.softmax(s, 0) @ vv[:seen, g]).numpy()
     return out
 
 
@@ -202,7 +207,7 @@ def contiguous_as_pages(cache: torch.Tensor, block: int):
 
 def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, lengths: torch.Tensor,
                block_kv: int = 512) -> torch.Tensor:
-    """examples/decode.py:175-196 of the reference (one new token, T = 1): the contiguous cache's blocks
+    """examples/decode.py:175-196 of the reference: the contiguous cache's blocks
     of bk = min(block_kv, S) positions, skipped from lengths[b] on, are the paged spec's pages in order, so
     this is `paged_gqa_decode` over `contiguous_as_pages` (same blocks, same online-softmax steps)."""
     bk = min(block_kv, k_cache.shape[1])
@@ -213,8 +218,9 @@ def gqa_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, le
 
 def gqa_contiguous_float64(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            lengths: torch.Tensor) -> np.ndarray:
-    """GQA decode attention in float64 over a contiguous cache: softmax(q k[:n].T) v[:n] per head, with
-    n = lengths[b] (the reference's tests/test_decode.py:62-76 `_gqa`, T = 1); empty sequences give 0."""
+    """GQA decode attention in float64 over a contiguous cache: softmax(q k[:seen].T) v[:seen] per head, token t
+    seeing lengths[b] - T + t + 1 positions (the reference's tests/test_decode.py:62-76 `_gqa`); empty
+    sequences give 0."""
     B, T, H, Dh = q.shape
     Hkv = k_cache.shape[2] // Dh
     out = np.zeros((B, T, H, Dh))
@@ -223,9 +229,11 @@ def gqa_contiguous_float64(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         if n == 0:
             continue
         kk, vv = kd[b, :n].reshape(n, Hkv, Dh), vd[b, :n].reshape(n, Hkv, Dh)
-        for h in range(H):
-            g = h // (H // Hkv)
-            out[b, 0, h] = (torch.softmax(kk[:, g] @ qd[b, 0, h], 0) @ vv[:, g]).numpy()
+        for t in range(T):
+            seen = n - T + t + 1
+            for h in range(H):
+                g = h // (H // Hkv)
+                out[b, t, h] = (torch.softmax(kk[:seen, g] @ qd[b, t, h], 0) @ vv[:seen, g]).numpy()
     return out
 
 

@@ -168,3 +168,26 @@ def test_cursor_at_baseline_size():
     print("decode cursor vs tables at 64 x 512 pages", flush=True)
     tables, cursor = _cursor_run(paged_gqa_decode, ins)
     assert torch.equal(tables, cursor)
+
+
+@pytest.mark.parametrize("cursor", [False, True])
+def test_paged_decode_with_new_tokens(cursor):
+    """Two new tokens per sequence (32 query rows: 2 tokens x 16 heads, 4 kv heads): token t sits at
+    lengths[b] - 2 + t and sees the positions up to it (the reference's tests/test_decode.py:215-221)."""
+    from tilejax_amd.tune import Config
+
+    g = torch.Generator().manual_seed(11)
+    B, T, H, Hkv, D, P, pages = 4, 2, 16, 4, 128, 16, 32
+    q = (torch.randn(B, T, H, D, generator=g) * D**-0.5).to(torch.bfloat16)
+    kp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16)
+    vp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16)
+    table = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32)
+    lengths = torch.tensor([2, 17, 300, 512], dtype=torch.int32)
+    ins = (q, kp, vp, table, lengths)
+    print(f"paged decode, two new tokens, cursor={cursor}", flush=True)
+    plain = _with_tables(paged_gqa_decode, ins)
+    lowered = paged_gqa_decode.lowered(paged_gqa_decode.signature(*ins),
+                                       Config(plain.config.tunable, plain.config.pipeline, cursor))
+    got = lowered.run(*(t.cuda() for t in ins))
+    _close(got, kernels.paged_gqa_decode(*ins))
+    _close(got, kernels.gqa_float64(*ins))

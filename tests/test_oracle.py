@@ -78,6 +78,21 @@ def test_paged_decode_is_gqa_softmax():
     assert not got[0].float().any()  # an empty sequence gives zeros
 
 
+def test_paged_decode_with_new_tokens_is_gqa_softmax():
+    # two new tokens per sequence: token t sees the positions up to lengths[b] - 2 + t
+    B, T, H, Hkv, D, P, pages = 3, 2, 8, 2, 128, 16, 8
+    q = (rand((B, T, H, D), 7, torch.float32) * D**-0.5).to(BF)
+    kp = rand((B * pages, P, Hkv * D), 8, BF)
+    vp = rand((B * pages, P, Hkv * D), 9, BF)
+    table = torch.randperm(B * pages, generator=torch.Generator().manual_seed(1)).reshape(B, pages).to(torch.int32)
+    lengths = torch.tensor([2, 64, 100], dtype=torch.int32)
+    got = kernels.paged_gqa_decode(q, kp, vp, table, lengths)
+    want = kernels.gqa_float64(q, kp, vp, table, lengths)
+    _close(got.double(), want)
+    # the first token of a sequence of two sees one position: its value row
+    np.testing.assert_allclose(want[0, 0, 0], vp[int(table[0, 0]), 0, :D].double().numpy(), rtol=1e-12)
+
+
 def test_paged_decode_is_independent_of_the_page_layout():
     q, kp, vp, table, lengths = _paged()
     got = kernels.paged_gqa_decode(q, kp, vp, table, lengths)

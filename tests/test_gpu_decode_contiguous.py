@@ -105,3 +105,21 @@ def test_contiguous_cursor_equals_step_tables():
     cursor = gqa_decode.lowered(gqa_decode.signature(*ins), Config(DecodeTiles(128), plain.config.pipeline, True))
     print("contiguous decode cursor vs tables", flush=True)
     assert torch.equal(plain.run(*dev), cursor.run(*dev))
+
+
+@pytest.mark.parametrize("t, heads, kv_heads, block_kv", [(1, 8, 2, 128), (1, 4, 4, 256), (3, 8, 2, 128)])
+def test_few_query_rows(t, heads, kv_heads, block_kv):
+    """The reference's own cases (tests/test_decode.py:176-191): fewer than 32 query rows (t * heads), the
+    kernels' rows past them zero; an empty sequence, one with just the new tokens, a partial block, a full
+    cache."""
+    g = torch.Generator().manual_seed(4)
+    q = (torch.randn(4, t, heads, 128, generator=g) * 128**-0.5).to(torch.bfloat16)
+    k = torch.randn(4, 512, kv_heads * 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(4, 512, kv_heads * 128, generator=g).to(torch.bfloat16)
+    lengths = torch.tensor([0, t, 300, 512], dtype=torch.int32)
+    print(f"contiguous decode t={t} heads={heads}/{kv_heads} block_kv={block_kv}", flush=True)
+    got = gqa_decode(q.cuda(), k.cuda(), v.cuda(), lengths.cuda(), DecodeTiles(block_kv))
+    torch.cuda.synchronize()
+    _close(got, kernels.gqa_decode(q, k, v, lengths, block_kv))
+    _close(got, kernels.gqa_contiguous_float64(q, k, v, lengths))
+    assert not got[0].float().any()

@@ -52,6 +52,7 @@ __all__ = ["DecodeMatch", "match", "lower"]
 
 THREADS = 256
 WAVES = 4
+RP = 32  # query rows the kernels work on: a spec's R <= 32 rows, the rest zero
 SUB = 16  # key positions per kernel step: a spec step of P positions (a page, a cache block) is P / SUB of them
 DEPTH = 3  # K register sets and V LDS stages: pages fetched ahead of the step being computed
 
@@ -117,8 +118,8 @@ class _Decode:
                  cursor: bool = False) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
         self.trace, self.cursor = trace, cursor
-        if m.rows != 32 or m.page % SUB or m.width % (32 * WAVES):
-            raise KernelError(f"the gfx950 decode lowering takes 32 query rows, pages (or cache blocks) of a multiple "
+        if m.rows > RP or m.page % SUB or m.width % (32 * WAVES):
+            raise KernelError(f"the gfx950 decode lowering takes up to {RP} query rows, pages (or cache blocks) of a multiple "
                               f"of {SUB} positions and widths that are multiples of {32 * WAVES} "
                               f"(got {m.rows}, {m.page}, {m.width})")
         self.sub = m.page // SUB  # kernel steps per spec step
@@ -127,7 +128,7 @@ class _Decode:
         self.grid = gfx950.CUS
         self.slots = self.grid + sch.pattern_tiles
         self.max_per = -(-sch.pattern_steps * self.sub // self.grid)  # most kernel steps one workgroup takes
-        self.lds = DEPTH * SUB * m.width * 2 + WAVES * SUB * m.rows * 4 + 20 * self.max_per
+        self.lds = DEPTH * SUB * m.width * 2 + WAVES * SUB * RP * 4 + 20 * self.max_per
         # with a cursor the attention kernel evaluates the mask itself: a 64-block word per tile and word
         self.words = sch.pattern_tiles * -(-plan.phases[0].range.count // 64)
         if cursor:
@@ -136,14 +137,14 @@ class _Decode:
             raise KernelError(f"decode over {sch.pattern_steps} pattern steps of {m.page} x {m.width} needs "
                               f"{self.lds} bytes of LDS per workgroup (gfx950 has {gfx950.LDS_BYTES})")
         self.phase = plan.phases[0].range
-        if (min(self.grid, self.phase.count * self.sub) + 1) * m.rows * 4 > 96 * 1024:
+        if (min(self.grid, self.phase.count * self.sub) + 1) * RP * 4 > 96 * 1024:
             raise KernelError("too many pages per sequence for the merge kernel's LDS")
         self.index = Index(plan, lambda v: f"lv_{v}")
         self.seg0 = plan.scopes["seg0"]
         # The setup and merge kernels split each tile's elements over `chunks` workgroups (grid y), enough for
         # about four workgroups per CU over all tiles, each thread keeping at least one element.
         want = -(-4 * gfx950.CUS // sch.pattern_tiles)
-        self.setup_chunks = max(1, min(m.rows * m.width // THREADS, want))
+        self.setup_chunks = max(1, min(RP * m.width // THREADS, want))
         self.merge_chunks = max(1, min(math.prod(m.out.tile.shape) // THREADS, want))
 
     # -------------------------------------------------------------------------------- element emitters
@@ -195,8 +196,8 @@ class _Decode:
         for r in sch.inner:
             tables[f"tv_{r.var}"] = np.asarray(sch.tile_values[r.var], np.int32)
             args.append(Arg("table", f"tv_{r.var}", "const int* __restrict__", f"tv_{r.var}"))
-        workspace = {"dc_q": 2 * sch.pattern_tiles * R * W, "dc_m": 4 * self.slots * R, "dc_l": 4 * self.slots * R,
-                     "dc_acc": 4 * self.slots * R * W}
+        workspace = {"dc_q": 2 * sch.pattern_tiles * RP * W, "dc_m": 4 * self.slots * RP, "dc_l": 4 * self.slots * RP,
+                     "dc_acc": 4 * self.slots * RP * W}
         # the step tables (device-built) or, with a cursor, only what the merge reads: the count and each
         # tile's first step, which the attention kernel's workgroup 0 writes
         for ws in (("count", "tile_steps") if self.cursor else ("step_tile", "step_code", "count", "tile_steps")):
@@ -242,11 +243,11 @@ class _Decode:
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const {self.name}_args args) {{
   const int t = blockIdx.x;
   {self._decode_tile("t")}
-  ak_u16* dst = args.dc_q + (long long)t * {R * W};
-  const int e1 = ak_imin((int)(blockIdx.y + 1) * {-(-R * W // self.setup_chunks)}, {R * W});
-  for (int e = blockIdx.y * {-(-R * W // self.setup_chunks)} + threadIdx.x; e < e1; e += {THREADS}) {{
+  ak_u16* dst = args.dc_q + (long long)t * {RP * W};
+  const int e1 = ak_imin((int)(blockIdx.y + 1) * {-(-RP * W // self.setup_chunks)}, {RP * W});
+  for (int e = blockIdx.y * {-(-RP * W // self.setup_chunks)} + threadIdx.x; e < e1; e += {THREADS}) {{
     const int qr = e / {W}, qc = e % {W};
-    dst[e] = (ak_u16)ak_bf16_bits((float)({expr}));
+    dst[e] = qr < {R} ? (ak_u16)ak_bf16_bits((float)({expr})) : (ak_u16)0;  // rows past R are zero
   }}
 }}
 """
@@ -286,7 +287,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
         w = L.append
         for s in range(D):  # one array per stage: the compiler then keeps the other stages' loads in flight
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sv{s}[{P * W}];")
-        w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{P}][{R}];")
+        w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{P}][{RP}];")
         w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][5];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
@@ -348,10 +349,10 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     const int slot = t + blockIdx.x;
     const int row = lane & 31;
     if (wave == 0 && lane < 32) {{
-      args.dc_m[slot * {R} + row] = m_run;
-      args.dc_l[slot * {R} + row] = l_run;
+      args.dc_m[slot * {RP} + row] = m_run;
+      args.dc_l[slot * {RP} + row] = l_run;
     }}
-    float* ap = args.dc_acc + (long long)slot * {R * W} + row * {W} + cb + (lane >> 5) * 4;
+    float* ap = args.dc_acc + (long long)slot * {RP * W} + row * {W} + cb + (lane >> 5) * 4;
 #pragma unroll
     for (int dt = 0; dt < {dtiles}; ++dt)
 #pragma unroll
@@ -360,7 +361,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     {f"tr_out += {NOW} - tr_f0;" if self.trace else ""}
   }};
   auto start_tile = [&](int t) {{
-    const ak_u16* qp = args.dc_q + (long long)t * {R * W} + cb + 8 * (lane >> 4);
+    const ak_u16* qp = args.dc_q + (long long)t * {RP * W} + cb + 8 * (lane >> 4);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -441,14 +442,15 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}    AK_WAIT_LGKM0();")
             a(f'{ind}    asm volatile("s_barrier" ::: "memory");')
             # softmax: lane = query row er, positions 8 (lane / 32) + e
-            a(f"{ind}    const int er = lane & 31;")
+            # the lane's row; the mask sees rows past R (zero queries, never stored) as row R - 1
+            a(f"{ind}    const int lr = lane & 31, er = {'lr' if m.rows == RP else f'ak_imin(lr, {m.rows - 1})'};")
             a(f"{ind}    float sc[8];")
             a(f"{ind}    float mx = -__builtin_inff();")
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int e = 0; e < 8; ++e) {{")
             a(f"{ind}      const int el = 8 * (lane >> 5) + e;  // the position in this kernel step")
             a(f"{ind}      const int ep = {P} * su + el;  // the position in the table step's block")
-            a(f"{ind}      const float sv = dc_sp[0][el][er] + dc_sp[1][el][er] + dc_sp[2][el][er] + dc_sp[3][el][er];")
+            a(f"{ind}      const float sv = dc_sp[0][el][lr] + dc_sp[1][el][lr] + dc_sp[2][el][lr] + dc_sp[3][el][lr];")
             a(f"{ind}      sc[e] = (float)({score});")
             a(f"{ind}      mx = fmaxf(mx, sc[e]);")
             a(f"{ind}    }}")
@@ -638,38 +640,38 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
   const int n = w1 - w0 + 1;
   // The partials' loads go out four at a time (they are independent); the sums run in partial order.
   for (int r = threadIdx.x; r < {R}; r += {THREADS}) {{
-    const float* mp = args.dc_m + (t + w0) * {R} + r;
-    const float* lp = args.dc_l + (t + w0) * {R} + r;
+    const float* mp = args.dc_m + (t + w0) * {RP} + r;
+    const float* lp = args.dc_l + (t + w0) * {RP} + r;
     float mm = -__builtin_inff();
     int k = 0;
     for (; k + 4 <= n; k += 4) {{
-      const float a0 = mp[k * {R}], a1 = mp[(k + 1) * {R}], a2 = mp[(k + 2) * {R}], a3 = mp[(k + 3) * {R}];
+      const float a0 = mp[k * {RP}], a1 = mp[(k + 1) * {RP}], a2 = mp[(k + 2) * {RP}], a3 = mp[(k + 3) * {RP}];
       dc_w[k][r] = a0; dc_w[k + 1][r] = a1; dc_w[k + 2][r] = a2; dc_w[k + 3][r] = a3;
       mm = fmaxf(fmaxf(fmaxf(fmaxf(mm, a0), a1), a2), a3);
     }}
-    for (; k < n; ++k) {{ const float a = mp[k * {R}]; dc_w[k][r] = a; mm = fmaxf(mm, a); }}
+    for (; k < n; ++k) {{ const float a = mp[k * {RP}]; dc_w[k][r] = a; mm = fmaxf(mm, a); }}
     float ls = 0.f;
     for (k = 0; k + 4 <= n; k += 4) {{
-      const float l0 = lp[k * {R}], l1 = lp[(k + 1) * {R}], l2 = lp[(k + 2) * {R}], l3 = lp[(k + 3) * {R}];
+      const float l0 = lp[k * {RP}], l1 = lp[(k + 1) * {RP}], l2 = lp[(k + 2) * {RP}], l3 = lp[(k + 3) * {RP}];
       const float e0 = ak_exp(dc_w[k][r] - mm), e1 = ak_exp(dc_w[k + 1][r] - mm);
       const float e2 = ak_exp(dc_w[k + 2][r] - mm), e3 = ak_exp(dc_w[k + 3][r] - mm);
       dc_w[k][r] = e0; dc_w[k + 1][r] = e1; dc_w[k + 2][r] = e2; dc_w[k + 3][r] = e3;
       ls += e0 * l0; ls += e1 * l1; ls += e2 * l2; ls += e3 * l3;
     }}
-    for (; k < n; ++k) {{ const float e = ak_exp(dc_w[k][r] - mm); dc_w[k][r] = e; ls += e * lp[k * {R}]; }}
+    for (; k < n; ++k) {{ const float e = ak_exp(dc_w[k][r] - mm); dc_w[k][r] = e; ls += e * lp[k * {RP}]; }}
     dc_lsum[r] = ls;
   }}
   __syncthreads();
   auto dc_acc_at = [&](int r, int c) -> float {{
-    const float* ap = args.dc_acc + (long long)(t + w0) * {R * W} + r * {W} + c;
+    const float* ap = args.dc_acc + (long long)(t + w0) * {RP * W} + r * {W} + c;
     float v = 0.f;
     int k = 0;
     for (; k + 4 <= n; k += 4) {{
-      const float a0 = ap[(long long)k * {R * W}], a1 = ap[(long long)(k + 1) * {R * W}];
-      const float a2 = ap[(long long)(k + 2) * {R * W}], a3 = ap[(long long)(k + 3) * {R * W}];
+      const float a0 = ap[(long long)k * {RP * W}], a1 = ap[(long long)(k + 1) * {RP * W}];
+      const float a2 = ap[(long long)(k + 2) * {RP * W}], a3 = ap[(long long)(k + 3) * {RP * W}];
       v += dc_w[k][r] * a0; v += dc_w[k + 1][r] * a1; v += dc_w[k + 2][r] * a2; v += dc_w[k + 3][r] * a3;
     }}
-    for (; k < n; ++k) v += dc_w[k][r] * ap[(long long)k * {R * W}];
+    for (; k < n; ++k) v += dc_w[k][r] * ap[(long long)k * {RP * W}];
     return v;
   }};
   ak_u16* op = args.{m.out.name}_out + ({o_base});

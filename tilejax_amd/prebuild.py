@@ -63,6 +63,9 @@ def standard() -> Iterator[Tuple[object, tuple]]:
     for b, s, block in ((4, 512, 128), (4, 512, 256), (4, 512, 512), (64, 8192, 512)):
         yield decode.gqa_decode, (_bf16(b, 1, 32, 128), _bf16(b, s, 1024), _bf16(b, s, 1024), _i32(b),
                                   decode.DecodeTiles(block))
+    for t, h, kv, block in ((1, 8, 2, 128), (1, 4, 4, 256), (3, 8, 2, 128)):
+        yield decode.gqa_decode, (_bf16(4, t, h, 128), _bf16(4, 512, kv * 128), _bf16(4, 512, kv * 128), _i32(4),
+                                  decode.DecodeTiles(block))
     try:
         from examples import causal_attention as ca
 

@@ -32,6 +32,8 @@ def _close(got, want):
 @pytest.mark.parametrize("shape,blocks", [
     ((1, 2, 512, 128), AttentionBlocks(128, 128)),
     ((2, 2, 512, 128), AttentionBlocks(256, 128)),
+    ((2, 2, 512, 128), AttentionBlocks(128, 128)),  # the reference's block shapes, tests/test_examples.py:80-88
+    ((2, 2, 512, 128), AttentionBlocks(128, 256)),
     ((1, 2, 1024, 128), AttentionBlocks(256, 256)),
     ((1, 1, 1024, 128), AttentionBlocks(512, 512)),
 ])

@@ -1,7 +1,11 @@
 """Parity of the generated gfx950 matmul kernels with the CPU oracle (same seeded inputs).
 
 Tolerance: bf16 outputs within 2 bf16 ulp of the oracle (rtol 1e-2 of |want| plus an absolute floor of
-1e-2 of the output's scale), as the north star asks; the two differ only in f32 summation order.
+1e-2 of the output's scale), as the north star asks; the two differ only in f32 summation order. f32
+operands (`@` at full precision) are multiplied as three bf16 products of their high and low parts, each
+within about 3 * 2^-16 of the exact product: the outputs are checked against float64 within rtol 1e-4 of
+|want| plus 1e-4 of the output's scale (the reference's f32 tolerance, tests/test_examples.py:27-32, with a
+tighter absolute floor).
 """
 
 import pytest
@@ -119,3 +123,56 @@ def test_four_input_buffers_take_half_depth_slices():
     _close(got, kernels.matmul(x, y, 512, 512, 512))
     plain = matmul.lowered(matmul.signature(x, y), Config(tiles, Pipeline(2, 2))).run(x.cuda(), y.cuda())
     assert torch.equal(got, plain)  # the same K order, so the same bits
+
+
+def _inputs_f32(m, k, n, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(m, k, generator=g), torch.randn(k, n, generator=torch.Generator().manual_seed(seed + 1))
+
+
+def _close_f32(got, want):
+    got, want = got.double().cpu(), torch.as_tensor(want).double().cpu()
+    scale = want.abs().max().item()
+    bad = (got - want).abs() > 1e-4 * want.abs() + 1e-4 * scale
+    assert not bad.any(), f"{int(bad.sum())} of {want.numel()} differ; max |diff| {(got - want).abs().max().item()}"
+
+
+@pytest.mark.parametrize("m,k,n,tiles", [
+    (256, 384, 256, MatmulTiles(128, 128, 128)),  # three reduction steps
+    (256, 384, 256, MatmulTiles(256, 128, 512)),  # one reduction step: no accumulator
+    (256, 384, 256, MatmulTiles(256, 256, 128)),
+    (1024, 1024, 1024, MatmulTiles(512, 512, 512)),
+])
+def test_matmul_f32_operands(m, k, n, tiles):
+    """The reference's f32 cases (tests/test_examples.py:18-32): `@` of f32 operands against float64."""
+    x, y = _inputs_f32(m, k, n)
+    print(f"matmul f32 {m}x{k}x{n} {tiles}", flush=True)
+    lowered = matmul.lower(x, y, tiles)
+    assert lowered.program.notes["f32_operands"]
+    got = lowered.run(x.cuda(), y.cuda())
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32
+    _close_f32(got, x.double() @ y.double())
+
+
+def test_matmul_one_reduction_step_bf16():
+    """tk covering the whole reduction: the loop of one step joins the tile code, and no value is carried."""
+    x, y = _inputs(256, 384, 256, seed=4)
+    tiles = MatmulTiles(256, 128, 512)
+    assert not matmul.lower(x, y, tiles).plan.carried
+    print(f"matmul bf16 one step {tiles}", flush=True)
+    got = matmul(x.cuda(), y.cuda(), tiles)
+    torch.cuda.synchronize()
+    _close(got, kernels.matmul(x, y, tiles.tm, tiles.tn, tiles.tk))
+
+
+def test_causal_matmul_f32_operands():
+    """tests/test_examples.py:55-63 of the reference in f32: tril(x @ y) against float64, above the diagonal
+    exactly the fill."""
+    x, y = _inputs_f32(512, 256, 512, seed=2)
+    tiles = MatmulTiles(128, 128, 128)
+    print(f"causal f32 {tiles}", flush=True)
+    got = causal_matmul(x.cuda(), y.cuda(), tiles)
+    torch.cuda.synchronize()
+    _close_f32(got, torch.tril(x.double() @ y.double()))
+    assert not got.cpu().triu(1).any()

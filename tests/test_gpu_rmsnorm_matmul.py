@@ -6,6 +6,9 @@ and then the matmul, whose epilogue scales each row by rsqrt(sum_sq / D + eps).
 
 Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want| (2 bf16 ulp): the
 sum of squares is added in another order than the spec's tk-deep blocks, and the products in MFMA order.
+f32 inputs (the left operand's prologue then stays f32, and the products take its high and low bf16
+parts): within rtol 1e-4 plus 1e-4 of the largest |want| of float64, the reference's f32 tolerance
+(tests/test_examples.py:136-152).
 """
 
 import pytest
@@ -44,6 +47,36 @@ def test_rmsnorm_matmul_matches_oracle(m, d, n, tiles):
     torch.cuda.synchronize()
     _close(got, kernels.rmsnorm_matmul(x, gamma, w, tiles.tm, tiles.tn, tiles.tk))
     _close(got, kernels.rmsnorm_matmul_float64(x, gamma, w))
+
+
+def test_rmsnorm_matmul_whole_model_dim_in_one_step():
+    """tk = D (tests/test_examples.py:141 of the reference): no carried values; each row's sum of squares is
+    a sum over the whole row in the tile's epilogue, which the row pass computes."""
+    x, gamma, w = _inputs(256, 512, 512, seed=6)
+    tiles = NormMatmulTiles(128, 256, 512)
+    lowered = rmsnorm_matmul.lower(x, gamma, w, tiles)
+    assert not lowered.plan.carried
+    print(f"rmsnorm_matmul one step {tiles}", flush=True)
+    got = lowered.run(x.cuda(), gamma.cuda(), w.cuda())
+    torch.cuda.synchronize()
+    _close(got, kernels.rmsnorm_matmul(x, gamma, w, tiles.tm, tiles.tn, tiles.tk))
+    _close(got, kernels.rmsnorm_matmul_float64(x, gamma, w))
+
+
+@pytest.mark.parametrize("tiles", [NormMatmulTiles(128, 128, 128), NormMatmulTiles(256, 128, 512)])
+def test_rmsnorm_matmul_f32(tiles):
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(256, 512, generator=g)
+    gamma = 1 + 0.1 * torch.randn(1, 512, generator=g)
+    w = torch.randn(512, 512, generator=g) / 512**0.5
+    print(f"rmsnorm_matmul f32 {tiles}", flush=True)
+    got = rmsnorm_matmul(x.cuda(), gamma.cuda(), w.cuda(), tiles)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32
+    want = torch.as_tensor(kernels.rmsnorm_matmul_float64(x, gamma, w))
+    scale = want.abs().max().item()
+    diff = (got.double().cpu() - want).abs()
+    assert not (diff > 1e-4 * want.abs() + 1e-4 * scale).any(), diff.max().item()
 
 
 def test_rmsnorm_matmul_verify_against_the_spec():

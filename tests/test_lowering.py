@@ -1,0 +1,63 @@
+"""What the gfx950 lowering builds for a loop nest, checked on the CPU (no kernel runs): the passes and
+workspaces f32 operands and one-step reductions take, and the error for what isn't lowered."""
+
+import pytest
+
+from examples.causal_attention import AttentionBlocks, causal_attention
+from examples.matmul import MatmulTiles, matmul
+from examples.rmsnorm_matmul import NormMatmulTiles, rmsnorm_matmul
+from tilejax_amd import jaxlite
+from tilejax_amd.errors import KernelError
+
+F32, BF16 = jaxlite.float32, jaxlite.bfloat16
+
+
+def _symbols(lowered):
+    return [launch.symbol for launch in lowered.program.launches]
+
+
+def test_f32_operands_take_their_bf16_parts():
+    lowered = matmul.lower(((256, 384), F32), ((384, 256), F32), MatmulTiles(128, 128, 128))
+    prog = lowered.program
+    assert prog.notes["f32_operands"]
+    assert _symbols(lowered) == ["tj_matmul_parts_b", "tj_matmul_parts_a", "tj_matmul"]
+    # three bf16 slices for each of the operand's: 2 bytes x 3 per element
+    assert prog.workspace == {"x3_a": 6 * 256 * 384, "x3_b": 6 * 384 * 256}
+    # three reduction steps of 128: 2 slices of 64 each, so 6 slices of the parts per step
+    assert prog.notes["slices_per_step"] == 6
+
+
+def test_bf16_operands_read_the_arrays_themselves():
+    lowered = matmul.lower(((256, 384), BF16), ((384, 256), BF16), MatmulTiles(128, 128, 128))
+    assert not lowered.program.notes["f32_operands"]
+    assert _symbols(lowered) == ["tj_matmul"] and not lowered.program.workspace
+
+
+def test_one_reduction_step_is_lowered():
+    """tk = K: the loop of one step joins the tile code (its variable bound to its start), nothing is
+    carried, and the lowering reads the k window at that value."""
+    lowered = matmul.lower(((256, 384), BF16), ((384, 256), BF16), MatmulTiles(256, 128, 512))
+    assert not lowered.plan.carried and not lowered.plan.phases
+    assert _symbols(lowered) == ["tj_matmul"]
+
+
+def test_one_step_rmsnorm_sums_rows_in_the_row_pass():
+    lowered = rmsnorm_matmul.lower(((256, 512), BF16), ((1, 512), BF16), ((512, 512), BF16),
+                                   NormMatmulTiles(128, 256, 512))
+    assert not lowered.plan.carried
+    assert _symbols(lowered)[:2] == ["tj_rmsnorm_matmul_rows", "tj_rmsnorm_matmul"]
+    sums = [k for k in lowered.program.workspace if k.startswith("rn__sum")]
+    assert len(sums) == 1 and lowered.program.workspace[sums[0]] == 4 * 256
+
+
+def test_f32_rmsnorm_writes_the_left_operands_parts_in_its_row_pass():
+    lowered = rmsnorm_matmul.lower(((256, 512), F32), ((1, 512), F32), ((512, 512), F32),
+                                   NormMatmulTiles(128, 128, 128))
+    assert _symbols(lowered)[:3] == ["tj_rmsnorm_matmul_rows", "tj_rmsnorm_matmul_parts_b", "tj_rmsnorm_matmul"]
+    assert lowered.program.workspace["rn_a"] == 6 * 256 * 512 and "x3_a" not in lowered.program.workspace
+
+
+def test_f32_attention_is_not_lowered():
+    spec = ((1, 1, 256, 128), F32)
+    with pytest.raises(KernelError, match="no lowering"):
+        causal_attention.lower(spec, spec, spec, AttentionBlocks(128, 128))

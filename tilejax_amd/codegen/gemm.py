@@ -51,7 +51,7 @@ class GemmMatch:
     a: Operand
     b: Operand
     b_nt: bool  # `a @ b.T`: b's tile is (tn, tk), K-contiguous
-    kvar: Optional[str]  # the reduction loop's variable (None: one step per tile)
+    kvar: Optional[str]  # the reduction loop's variable (None: no reduction loop)
     tm: int
     tn: int
     tk: int
@@ -64,12 +64,14 @@ class GemmMatch:
     # initial value)), which the epilogue may read (the reference's examples/rmsnorm_matmul.py:33-46).
     a_expr: Optional[Node] = None
     side: Tuple[Tuple[str, Node, float], ...] = ()
+    k0: int = 0  # the value of a reduction loop of one step (not among the plan's phases)
 
 
 def _is(node: Any, op: str) -> bool:
     return isinstance(node, Node) and node.op == op
 
 
+_OPERAND_TYPES = ("bfloat16", "float32")  # operand types `@` takes: bf16, or f32 as three bf16 products
 _POINTWISE = {"astype", "multiply", "add", "subtract", "divide", "negative", "maximum", "minimum", "full"}
 
 
@@ -100,31 +102,52 @@ def _dot_of_loads(plan: Plan, node: Node) -> Optional[Tuple[Operand, Operand, bo
     a_expr = None
     if not _is(a, "load"):
         x = _row_prologue(plan, a)
-        if x is None or a.dtype.name != "bfloat16" or a.shape != x.shape:
+        if x is None or a.dtype.name not in _OPERAND_TYPES or a.shape != x.shape:
             return None
         a_expr, a = a, x
     if not _is(b, "load"):
         return None
     opa, opb = plan.operand(a.kwargs["operand"]), plan.operand(b.kwargs["operand"])
-    if opa.tile.dtype.name != "bfloat16" or opb.tile.dtype.name != "bfloat16":
+    if opa.tile.dtype.name not in _OPERAND_TYPES or opb.tile.dtype.name not in _OPERAND_TYPES:
         return None
     if len(opa.tile.shape) != 2 or len(opb.tile.shape) != 2:
         return None
     return opa, opb, node.op == "dot_nt", a_expr, a
 
 
+def _is_f32(m: "GemmMatch") -> bool:
+    """Does the product read f32 operands (`@` at HIGHEST precision, src/autokernel/mxu.py:21-43)?"""
+    a_type = (m.a_expr.dtype if m.a_expr is not None else m.a.tile.dtype).name
+    return "float32" in (a_type, m.b.tile.dtype.name)
+
+
 _UNIFORM_OPS = _POINTWISE | {"rsqrt", "sqrt", "exp", "log", "reciprocal", "square", "tanh", "sigmoid"}
 
 
 def _column_uniform(node: Node, side: set) -> bool:
-    """Is `node` the same in every column: built pointwise from row sums (`side`) and constants only?"""
-    for n in nodes_between(node):
+    """Is `node` the same in every column: built pointwise from row sums (`side`: carried values, or the
+    sums `_row_sum_name` names) and constants only?"""
+    stack, seen = [node], set()
+    while stack:
+        n = stack.pop()
+        if n.id in seen:
+            continue
+        seen.add(n.id)
         if n.op == "carried":
             if n.kwargs["name"] not in side:
                 return False
-        elif n.op not in _UNIFORM_OPS:
+            continue
+        if n.op == "reduce_sum" and _row_sum_name(n) in side:
+            continue
+        if n.op not in _UNIFORM_OPS:
             return False
+        stack.extend(n.inputs())
     return True
+
+
+def _row_sum_name(n: Node) -> str:
+    """The name a row sum in a one-step tile's epilogue goes by (a carried value's, in a loop)."""
+    return f"_sum{n.id}"
 
 
 def _side_sum(plan: Plan, name: str, x: Node) -> Optional[Tuple[str, Node, float]]:
@@ -204,6 +227,13 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         if found is None:
             return None
         acc_leaf, init_value, kvar = dots[0], 0.0, None
+        # a reduction of one step: the row sums a loop would carry are sums of the whole row, inline
+        for n in nodes_between(root):
+            if n.op == "reduce_sum":
+                if not (n.kwargs.get("axis") in (1, -1) and n.kwargs.get("keepdims")
+                        and _row_prologue(plan, n.args[0], found[4]) is not None):
+                    return None
+                side.append((_row_sum_name(n), n.args[0], 0.0))
     opa, opb, nt, a_expr, _ = found
     tm, tk = opa.tile.shape
     tn, tkb = (opb.tile.shape if nt else opb.tile.shape[::-1])
@@ -221,11 +251,16 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         return None
     if kvar is not None and (arow[1].loop != kvar or bk.loop != kvar):
         return None
+    k0 = 0
     if kvar is None and (arow[1].loop is not None or bk.loop is not None):
-        return None
+        # a reduction loop of one step joins the code around it, its variable bound to its start
+        one = {r.var: r.start for r in plan.reductions if r.count == 1 and r.mask is None}
+        if arow[1].loop != bk.loop or arow[1].loop not in one:
+            return None
+        kvar, k0 = arow[1].loop, one[arow[1].loop]
     if out.dtype.name not in ("bfloat16", "float32"):
         return None
-    return GemmMatch(opa, opb, nt, kvar, tm, tn, tk, acc_leaf, init_value, out, value, a_expr, tuple(side))
+    return GemmMatch(opa, opb, nt, kvar, tm, tn, tk, acc_leaf, init_value, out, value, a_expr, tuple(side), k0)
 
 
 @dataclass(frozen=True)
@@ -284,8 +319,16 @@ class _Gemm:
         self.const_value: Optional[float] = None
         self.split: Optional[Tuple[int, int, int]] = None  # (items cut, chunks per item, K slices per chunk)
         self.prologue = m.a_expr is not None or bool(m.side)
+        # f32 operands: each goes to HBM as bf16 parts, x = hi + lo (hi = bf16(x), lo = bf16(x - hi)), and the
+        # kernel sums hi_a hi_b + hi_a lo_b + lo_a hi_b in f32, a product within about 2^-16 of x y, on the
+        # bf16 MFMAs (the f32 ones run at a sixteenth of their rate). The parts array has three BK-deep
+        # slices for each of the operand's: (hi, hi, lo) for the left operand, (hi, lo, hi) for the right.
+        self.x3 = _is_f32(m)
+        self.kx = 3 if self.x3 else 1
         if self.prologue:
             self._check_prologue()
+        if self.x3:
+            self._check_parts()
 
     def _check_prologue(self) -> None:
         """A row prologue runs as its own pass over the left operand's whole array: its rows are the output's
@@ -309,13 +352,85 @@ class _Gemm:
             raise KernelError("a matmul's row prologue needs a reduction loop over the whole row")
         self.rows_n, self.cols_n = shape
 
+    def _kdim(self, role: str) -> int:
+        """The dim of the left ("a") or right ("b") operand's array that the reduction walks."""
+        shape = self.plan.inputs[(self.m.a if role == "a" else self.m.b).param].shape
+        return len(shape) - 1 if role == "a" or self.m.b_nt else len(shape) - 2
+
+    def _shape(self, role: str) -> Tuple[int, ...]:
+        """The array the kernel reads for an operand: its own, or with f32 operands its bf16 parts, whose
+        reduction dim is three times as long."""
+        shape = tuple(self.plan.inputs[(self.m.a if role == "a" else self.m.b).param].shape)
+        if not self.x3:
+            return shape
+        kd = self._kdim(role)
+        return shape[:kd] + (3 * shape[kd],) + shape[kd + 1:]
+
+    def _check_parts(self) -> None:
+        """f32 operands: every reduction block the kernel reads starts on a BK-slice boundary of the array, so
+        slice j of the operand is slices 3j..3j+2 of its parts."""
+        plan, m, bk = self.plan, self.m, self.hw.bk
+        for role, op in (("a", m.a), ("b", m.b)):
+            shape = plan.inputs[op.param].shape
+            kd = self._kdim(role)
+            kwin = [w for w in op.tile.windows if w.size is not None][1 if role == "a" or m.b_nt else 0]
+            if shape[kd] % bk or kwin.offset % bk or shape[-1] % 8:
+                raise KernelError(f"the gfx950 matmul lowering takes f32 operands whose reduction dim and windows "
+                                  f"are multiples of {bk} and whose rows are multiples of 8 elements")
+        if plan.phases:
+            r = plan.phases[0].range
+            if r.start % bk or r.step % bk:
+                raise KernelError(f"the gfx950 matmul lowering takes f32 operands with reduction blocks on "
+                                  f"multiples of {bk}")
+
+    def _parts_source(self, role: str) -> str:
+        """The pass that writes an f32 (or bf16) operand's bf16 parts: each thread takes 8 consecutive
+        elements, splits each into hi = bf16(x) and lo = bf16(x - hi) (0 for a bf16 operand, or where hi isn't
+        finite), and stores the three parts its slice's copies hold."""
+        op = self.m.a if role == "a" else self.m.b
+        spec = self.plan.inputs[op.param]
+        shape, kd, bk = tuple(spec.shape), self._kdim(role), self.hw.bk
+        K, inner, numel = shape[kd], int(np.prod(shape[kd + 1:])), int(np.prod(shape))
+        parts = ("hi", "hi", "lo") if role == "a" else ("hi", "lo", "hi")
+        if spec.dtype.name == "float32":
+            load = (f"const ak_f32x4 u0 = *(const ak_f32x4*)(args.{op.tile.array} + flat), "
+                    f"u1 = *(const ak_f32x4*)(args.{op.tile.array} + flat + 4);\n"
+                    "  const float v[8] = {u0[0], u0[1], u0[2], u0[3], u1[0], u1[1], u1[2], u1[3]};")
+        else:
+            load = (f"const ak_u32x4 u = *(const ak_u32x4*)((const ak_u16*)args.{op.tile.array} + flat);\n"
+                    "  float v[8];\n"
+                    "#pragma unroll\n"
+                    "  for (int e = 0; e < 8; ++e) v[e] = ak_bf16_to_f32((ak_u16)(u[e >> 1] >> (16 * (e & 1))));")
+        stores = "\n".join(f"  *(ak_u32x4*)(args.x3_{role} + o + {c * bk * inner}LL) = {p};" for c, p in enumerate(parts))
+        return f"""
+// The bf16 parts of `{op.tile.array}` ({"x".join(map(str, shape))}, {spec.dtype.name}) for the f32 matmul: for each {bk}-deep
+// slice of dim {kd}, the slices ({", ".join(parts)}).
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}(const {self.name}_args args) {{
+  const long long e8 = (long long)blockIdx.x * {THREADS} + threadIdx.x;
+  if (e8 >= {numel // 8}) return;
+  const long long flat = e8 * 8, kk = flat / {inner};
+  const int k = (int)(kk % {K});
+  const long long o = ((kk / {K}) * {3 * K} + 3 * (k / {bk}) * {bk} + k % {bk}) * {inner} + flat % {inner};
+  {load}
+  unsigned h2[4], l2[4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {{
+    const float h0 = ak_round_bf16(v[e]), h1 = ak_round_bf16(v[e + 1]);
+    h2[e >> 1] = ak_pack_bf16x2(h0, h1);
+    l2[e >> 1] = ak_pack_bf16x2(__builtin_isfinite(h0) ? v[e] - h0 : 0.f, __builtin_isfinite(h1) ? v[e + 1] - h1 : 0.f);
+  }}
+  const ak_u32x4 hi = {{h2[0], h2[1], h2[2], h2[3]}}, lo = {{l2[0], l2[1], l2[2], l2[3]}};
+{stores}
+}}
+"""
+
     # ------------------------------------------------------------------ work items (host)
 
     def _items(self) -> Tuple[List[Tuple[int, int]], List[float], List[int]]:
         """Every (tile or fill, sub-tile | kind << 16), its weight (k slices) and locality group."""
         plan, sch, m, hw = self.plan, self.sch, self.m, self.hw
         items, weights, groups = [], [], []
-        kslices = m.tk // hw.bk
+        kslices = m.tk // hw.bk * self.kx
         steps_of = None
         if sch.step_tables and not sch.runtime:
             offsets = static_tile_steps(sch)
@@ -460,9 +575,16 @@ class _Gemm:
         source = self._source(args)
         launches = [Launch(self.name, args, (grid, 1, 1), (64 * WAVE_GRID[0] * WAVE_GRID[1], 1, 1), 0)]
         workspace = {}
+        if self.x3:
+            for role in ("b",) if self.prologue else ("a", "b"):
+                source += self._parts_source(role)
+                workspace[f"x3_{role}"] = 2 * int(np.prod(self._shape(role)))
+                groups8 = int(np.prod(self.plan.inputs[(m.a if role == "a" else m.b).param].shape)) // 8
+                launches.insert(0, Launch(f"{self.name}_parts_{role}", args, (-(-groups8 // THREADS), 1, 1),
+                                          (THREADS, 1, 1), 0))
         if self.prologue:
             source += self._rows_source()
-            workspace["rn_a"] = self.rows_n * self.cols_n * 2
+            workspace["rn_a"] = self.rows_n * self.cols_n * 2 * self.kx
             for name, _, _ in m.side:
                 workspace[f"rn_{name}"] = self.rows_n * 4
             launches.insert(0, Launch(f"{self.name}_rows", args, (-(-self.rows_n // 4), 1, 1), (THREADS, 1, 1), 0))
@@ -480,7 +602,7 @@ class _Gemm:
             notes={"family": "gemm", "hw_tile": (hw.bm, hw.bn, hw.bk), "stages": hw.stages, "grid": grid,
                    "items": len(items), "constant_items": sum(1 for _, s, _ in items if (s >> 16) == 2),
                    "split": self.split, "trace_workgroups": grid if self.trace else 0,
-                   "slices_per_step": m.tk // hw.bk * self.subs},
+                   "slices_per_step": m.tk // hw.bk * self.kx * self.subs, "f32_operands": self.x3},
         )
         if sch.runtime:
             from .steps import attach_step_builder
@@ -500,12 +622,15 @@ class _Gemm:
         args.append(Arg("output", 0, f"{_cstore(m.out.dtype)}* __restrict__", m.out.name + "_out"))
         for name in self.tables:
             args.append(Arg("table", name, "const int* __restrict__", name))
-        args.append(Arg("int", 2 * self._pitch(m.a), "int", "ak_pitch_a"))
-        args.append(Arg("int", 2 * self._pitch(m.b), "int", "ak_pitch_b"))
+        args.append(Arg("int", 2 * self._pitch("a"), "int", "ak_pitch_a"))
+        args.append(Arg("int", 2 * self._pitch("b"), "int", "ak_pitch_b"))
         if self.split:
             args.append(Arg("workspace", "gm_part", "float* __restrict__", "gm_part"))
         if self.trace:
             args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
+        if self.x3:
+            for role in ("b",) if self.prologue else ("a", "b"):
+                args.append(Arg("workspace", f"x3_{role}", "ak_u16* __restrict__", f"x3_{role}"))
         if self.prologue:
             args.append(Arg("workspace", "rn_a", "ak_u16* __restrict__", "rn_a"))
             for name, _, _ in m.side:
@@ -528,8 +653,10 @@ class _Gemm:
                 shape = plan.inputs[op.param].shape
                 base, st = tile_base(op.tile, shape, zero, lambda v: "0")
                 flat = " + ".join(f"(long long)({i}) * {s_}" for i, s_ in zip(idx, st)) or "0"
+                if op.tile.dtype.name == "float32":
+                    return f"args.{op.tile.array}[({base}) + {flat}]"
                 if op.tile.dtype.name != "bfloat16":
-                    raise KernelError("a matmul's row prologue reads bf16 operands")
+                    raise KernelError("a matmul's row prologue reads bf16 or f32 operands")
                 return f"ak_bf16_to_f32(((const ak_u16*)args.{op.tile.array})[({base}) + {flat}])"
             return None
 
@@ -543,6 +670,21 @@ class _Gemm:
                           for k, (_, h, _) in enumerate(m.side))
         outs = "\n".join(f"  rs_{k} = ak_wave_sum(rs_{k}); if (lane == 0) args.rn_{name}[r] = rs_{k};"
                           for k, (name, _, _) in enumerate(m.side))
+        if self.x3:  # the operand's bf16 parts: slices (hi, hi, lo) for each of its BK-deep slices
+            bk = self.hw.bk
+            value = (f"const float v0 = {em.at(a_node, ('r', 'c'))}, v1 = {em.at(a_node, ('r', 'c + 1'))};\n"
+                     "      const float h0 = ak_round_bf16(v0), h1 = ak_round_bf16(v1);\n"
+                     "      pk[e >> 1] = ak_pack_bf16x2(h0, h1);\n"
+                     "      pl[e >> 1] = ak_pack_bf16x2(__builtin_isfinite(h0) ? v0 - h0 : 0.f, "
+                     "__builtin_isfinite(h1) ? v1 - h1 : 0.f);")
+            store = (f"ak_u16* dst = args.rn_a + (long long)r * {3 * D} + 3 * (c0 / {bk}) * {bk} + c0 % {bk};\n"
+                     "    *(ak_u32x4*)dst = ak_u32x4{pk[0], pk[1], pk[2], pk[3]};\n"
+                     f"    *(ak_u32x4*)(dst + {bk}) = ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}};\n"
+                     f"    *(ak_u32x4*)(dst + {2 * bk}) = ak_u32x4{{pl[0], pl[1], pl[2], pl[3]}};")
+        else:
+            value = (f"pk[e >> 1] = ak_pack_bf16x2((float)({em.at(a_node, ('r', 'c'))}), "
+                     f"(float)({em.at(a_node, ('r', 'c + 1'))}));")
+            store = f"*(ak_u32x4*)(args.rn_a + (long long)r * {D} + c0) = ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}};"
         return f"""
 // The row prologue of `{plan.nest.name}`: rows {self.rows_n} x {D}, one wave per row.
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {self.name}_args args) {{
@@ -550,23 +692,25 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
   if (r >= {self.rows_n}) return;
  {sums}
   for (int c0 = lane * 8; c0 < {D}; c0 += 512) {{
-    unsigned pk[4];
+    unsigned pk[4], pl[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {{
       const int c = c0 + e;
-      pk[e >> 1] = ak_pack_bf16x2((float)({em.at(a_node, ('r', 'c'))}), (float)({em.at(a_node, ('r', 'c + 1'))}));
+      {value}
 {adds}
     }}
-    *(ak_u32x4*)(args.rn_a + (long long)r * {D} + c0) = ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}};
+    (void)pl;
+    {store}
   }}
 {outs}
 }}
 """
 
-    def _pitch(self, op: Operand) -> int:
-        """Elements between consecutive rows of an operand tile (its first sliced dim's stride)."""
-        shape = self.plan.inputs[op.param].shape
-        return [s for w, s in zip(op.tile.windows, strides(shape)) if w.size is not None][0]
+    def _pitch(self, role: str) -> int:
+        """Elements between consecutive rows of an operand tile (its first sliced dim's stride) in the array
+        the kernel reads."""
+        op = self.m.a if role == "a" else self.m.b
+        return [s for w, s in zip(op.tile.windows, strides(self._shape(role))) if w.size is not None][0]
 
     def _source(self, args: List[Arg]) -> str:
         plan, sch, m, hw = self.plan, self.sch, self.m, self.hw
@@ -576,12 +720,11 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         wtm, wtn = bm // WM, bn // WN
         mi, ni = wtm // MFMA, wtn // MFMA
         k16s = bk // 16
-        kslices = m.tk // bk
+        kslices = m.tk // bk * self.kx  # K slices per step (with f32 operands, of the parts arrays)
         split, split_slices = (self.split[1], self.split[2]) if self.split else (1, 0)
         kvar = m.kvar
         index = Index(plan, lambda v: f"lv_{v}")
-        a_shape = plan.inputs[m.a.param].shape
-        b_shape = plan.inputs[m.b.param].shape
+        a_shape, b_shape = self._shape("a"), self._shape("b")
         no_k = lambda v: "0" if v == kvar else f"lv_{v}"  # the reduction loop's offset goes per slice
         a_base, a_str = tile_base(m.a.tile, a_shape, index, no_k)
         b_base, b_str = tile_base(m.b.tile, b_shape, index, no_k)
@@ -611,7 +754,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         phase = plan.phases[0].range if plan.phases else None
         if phase is None:
             steps_setup = ["const int nsteps = 1;"]
-            kval = "0"
+            kval = str(m.k0)
         elif not sch.step_tables:
             steps_setup = [f"const int nsteps = {phase.count};"]
             kval = f"({phase.start} + st_ * {phase.step})"
@@ -625,6 +768,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
             ]
             kval = (f"({phase.start} + (({codes}[sbeg + st_] >> {CODE_SHIFT}) / {sch.iterations} / "
                     f"{sch.phase_radix}) * {phase.step})")
+        if self.x3:  # the parts arrays hold three slices for each of the operand's
+            kval = f"(3 * {kval})"
 
         # The epilogue, per accumulator element.
         def leaf(n: Node) -> Optional[str]:
@@ -650,9 +795,10 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
                 return f"args.{ix.name}[{flat}]"
             if n.op == "tile" and isinstance(n.args[0], Node) and _column_uniform(n.args[0], {x[0] for x in m.side}):
                 return em.emit(n.args[0])  # tiling a row statistic along the columns repeats each row's value
-            if n.op == "carried" and any(n.kwargs["name"] == name for name, _, _ in m.side):
+            sided = n.kwargs["name"] if n.op == "carried" else _row_sum_name(n) if n.op == "reduce_sum" else None
+            if sided is not None and any(sided == name for name, _, _ in m.side):
                 # a row sum: the same for every column; the tile's rows are the left operand's
-                name, _, init = next(x for x in m.side if x[0] == n.kwargs["name"])
+                name, _, init = next(x for x in m.side if x[0] == sided)
                 rows = [w for w in m.a.tile.windows if w.size is not None][0]
                 row = f"(lv_{rows.loop}) + er" if rows.loop else "er"
                 return f"({literal(init, n.dtype)} + args.rn_{name}[{row}])"
@@ -666,8 +812,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         out_bf16 = m.out.dtype.name == "bfloat16"
         struct = c_struct(f"{self.name}_args", args)
         # with a row prologue the left operand is its pass's output, laid out as the operand's array
-        A = "args.rn_a" if self.prologue else f"args.{m.a.tile.array}"
-        B, O = f"args.{m.b.tile.array}", f"args.{m.out.name}_out"
+        A = "args.rn_a" if self.prologue else "args.x3_a" if self.x3 else f"args.{m.a.tile.array}"
+        B = "args.x3_b" if self.x3 else f"args.{m.b.tile.array}"
+        O = f"args.{m.out.name}_out"
         a_numel, b_numel = int(np.prod(a_shape)), int(np.prod(b_shape))
         fill_value = literal(m.out.fill if m.out.fill is not None else 0, m.out.dtype)
         const_value = literal(self.const_value if self.const_value is not None else 0.0, m.out.dtype)

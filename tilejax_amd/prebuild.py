@@ -21,6 +21,10 @@ def _bf16(*shape: int) -> Tuple[Tuple[int, ...], jaxlite.DType]:
     return (tuple(shape), jaxlite.bfloat16)
 
 
+def _f32(*shape: int) -> Tuple[Tuple[int, ...], jaxlite.DType]:
+    return (tuple(shape), jaxlite.float32)
+
+
 def _i32(*shape: int) -> Tuple[Tuple[int, ...], jaxlite.DType]:
     return (tuple(shape), jaxlite.int32)
 
@@ -39,6 +43,11 @@ def standard() -> Iterator[Tuple[object, tuple]]:
     for n, tiles in ((8192, T(512, 512, 512)), (1024, T(256, 256, 256)), (512, T(128, 128, 128))):
         yield cm.causal_matmul, (_bf16(n, n), _bf16(n, n), tiles)
     yield mm.matmul, (_bf16(512, 256), _bf16(256, 512), T(256, 256, 128))
+    yield mm.matmul, (_bf16(256, 384), _bf16(384, 256), T(256, 128, 512))
+    for tiles in (T(128, 128, 128), T(256, 128, 512), T(256, 256, 128)):  # f32 operands
+        yield mm.matmul, (_f32(256, 384), _f32(384, 256), tiles)
+    yield mm.matmul, (_f32(1024, 1024), _f32(1024, 1024), T(512, 512, 512))
+    yield cm.causal_matmul, (_f32(512, 256), _f32(256, 512), T(128, 128, 128))
     from examples import moe
 
     GT = moe.GroupTiles
@@ -53,6 +62,9 @@ def standard() -> Iterator[Tuple[object, tuple]]:
                              ((256, 512, 512), R(128, 128, 128)), ((512, 512, 512), R(256, 256, 256)),
                              ((4096, 4096, 4096), R()), ((8192, 8192, 8192), R())):
         yield rm.rmsnorm_matmul, (_bf16(m, d), _bf16(1, d), _bf16(d, n), tiles)
+    yield rm.rmsnorm_matmul, (_bf16(256, 512), _bf16(1, 512), _bf16(512, 512), R(128, 256, 512))
+    for tiles in (R(128, 128, 128), R(256, 128, 512)):
+        yield rm.rmsnorm_matmul, (_f32(256, 512), _f32(1, 512), _f32(512, 512), tiles)
     from examples import decode
 
     for b, pages, n_pages in ((4, 64, 256), (5, 100, 500), (64, 512, 32768)):
@@ -73,6 +85,7 @@ def standard() -> Iterator[Tuple[object, tuple]]:
         for shape, blocks in (((4, 16, 2048, 128), A(512, 512)), ((1, 16, 4096, 128), A(512, 512)),
                               ((2, 4, 512, 128), A(128, 128)), ((1, 2, 1024, 128), A(256, 256)),
                               ((1, 2, 512, 128), A(128, 128)), ((2, 2, 512, 128), A(256, 128)),
+                              ((2, 2, 512, 128), A(128, 128)), ((2, 2, 512, 128), A(128, 256)),
                               ((1, 1, 1024, 128), A(512, 512))):
             yield ca.causal_attention, (_bf16(*shape), _bf16(*shape), _bf16(*shape), blocks)
     except ImportError:

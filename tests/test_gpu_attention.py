@@ -4,7 +4,8 @@ reference on the GPU (the attention kernel is floating point).
 
 Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the output's largest magnitude (about
 2 bf16 ulp): the kernel and the oracle differ in f32 summation order and in where the online softmax
-rescales (the kernel steps through 64-key blocks, the spec through its own blocks).
+rescales (the kernel steps through 64-key blocks, the spec through its own blocks). f32 q, k, v run on
+the vector ALUs in f32: within 1e-4 of float64 (the reference's own tolerance, tests/test_examples.py:97-101).
 """
 
 import pytest
@@ -71,3 +72,21 @@ def test_verify_against_the_spec_reference():
     q, k, v = _inputs(1, 2, 512, 128, seed=3)
     err = causal_attention.verify(q.cuda(), k.cuda(), v.cuda(), AttentionBlocks(128, 128))
     assert err < 0.1
+
+
+@pytest.mark.parametrize("shape,blocks", [
+    ((1, 1, 256, 128), AttentionBlocks(128, 128)),  # tests/test_examples.py:97-101 of the reference
+    ((2, 2, 512, 128), AttentionBlocks(256, 128)),
+    ((1, 2, 512, 128), AttentionBlocks(128, 256)),
+])
+def test_causal_attention_f32(shape, blocks):
+    gens = [torch.Generator().manual_seed(20 + i) for i in range(3)]
+    q, k, v = (torch.randn(*shape, generator=g) for g in gens)
+    q = q * shape[-1] ** -0.5
+    print(f"attention f32 {shape} {blocks}", flush=True)
+    got = causal_attention(q.cuda(), k.cuda(), v.cuda(), blocks)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.float32
+    want = torch.as_tensor(kernels.attention_float64(q, k, v))
+    diff = (got.double().cpu() - want).abs()
+    assert diff.max().item() < 1e-4, diff.max().item()

@@ -2,7 +2,9 @@
 with the CPU oracle, and of the device step-table builder with the reference's table semantics restated in
 oracle/schedule.py: bit-exact tables, counts and codes.
 
-Tolerance for the matmul: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want|.
+Tolerance for the matmul: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want|; f32
+operands (three bf16 products of their parts) within rtol 1e-4 plus 1e-4 of the largest |want| of float64,
+the reference's f32 tolerance for its grouped kernels (tests/test_moe.py:252-275).
 """
 
 import numpy as np
@@ -45,6 +47,24 @@ def test_grouped_matmul_matches_oracle(experts, tiles):
     for g, e in enumerate(experts):
         if e < 0:
             assert not got[g * 256:(g + 1) * 256].float().any()
+
+
+def test_grouped_matmul_f32_operands():
+    experts = [2, -1, 0, 9]
+    g = torch.Generator().manual_seed(4)
+    xs, w = torch.randn(1024, 512, generator=g), torch.randn(4, 512, 1024, generator=g) * 0.02
+    ge = torch.tensor(experts, dtype=torch.int32)
+    tiles = GroupTiles(512, 256)
+    print(f"grouped matmul f32 experts={experts} {tiles}", flush=True)
+    got = grouped_matmul(xs.cuda(), w.cuda(), ge.cuda(), tiles)
+    torch.cuda.synchronize()
+    want = torch.zeros(1024, 1024, dtype=torch.float64)
+    for grp, e in enumerate(experts):
+        if e >= 0:
+            rows = slice(grp * 256, (grp + 1) * 256)
+            want[rows] = xs[rows].double() @ w[min(e, 3)].double()
+    diff = (got.double().cpu() - want).abs()
+    assert not (diff > 1e-4 * want.abs() + 1e-4 * want.abs().max()).any(), diff.max().item()
 
 
 def test_device_step_tables_are_bit_exact():

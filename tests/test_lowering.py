@@ -57,7 +57,26 @@ def test_f32_rmsnorm_writes_the_left_operands_parts_in_its_row_pass():
     assert lowered.program.workspace["rn_a"] == 6 * 256 * 512 and "x3_a" not in lowered.program.workspace
 
 
-def test_f32_attention_is_not_lowered():
+def test_f32_attention_runs_on_the_vector_alus():
     spec = ((1, 1, 256, 128), F32)
+    lowered = causal_attention.lower(spec, spec, spec, AttentionBlocks(128, 128))
+    assert lowered.program.notes["f32_operands"] and "mfma" not in lowered.source
+    assert _symbols(lowered) == ["tj_causal_attention"]
+
+
+def test_what_no_family_takes_is_a_kernel_error():
+    from tests.helpers import make_kernel
+
+    k = make_kernel('''
+        def row_sums(x):
+            M, N = x.shape
+            out = jnp.zeros((M, 128), jnp.float32)
+            for i in range(0, M, 128):
+                acc = jnp.zeros((128, 128), jnp.float32)
+                for j in range(0, N, 128):
+                    acc += x[i : i + 128, j : j + 128]
+                out = out.at[i : i + 128, :].set(acc)
+            return out
+    ''')
     with pytest.raises(KernelError, match="no lowering"):
-        causal_attention.lower(spec, spec, spec, AttentionBlocks(128, 128))
+        k.lower(((256, 512), F32))

@@ -200,8 +200,9 @@ def softmax_structure(plan: Plan) -> Optional[Softmax]:
     got = _either(_pair(scaled, "multiply"), lambda x: _strip(x) is alpha)
     if got is None or got[1] is not acc_in:
         return None
-    p16 = pv.args[0]
-    if not (_is(p16, "astype") and p16.args[0] is p and p16.dtype.name == "bfloat16"):
+    p16 = pv.args[0]  # p.astype(v.dtype): bf16 (or p itself, f32, where the cast changes nothing)
+    if not ((_is(p16, "astype") and p16.args[0] is p and p16.dtype.name in ("bfloat16", "float32"))
+            or (p16 is p and p.dtype.name == "float32")):
         return None
     # The score is pointwise in S: everything between S and it is elementwise on positions and loop values.
     stack, seen = [score], set()
@@ -234,7 +235,9 @@ def match(plan: Plan) -> Optional[FlashMatch]:
     q, k, v = (plan.operand(n.kwargs["operand"]) for n in (qk.args[0], qk.args[1], pv.args[1]))
     if q.kind is not Kind.TILE or k.kind is not Kind.STREAM or v.kind is not Kind.STREAM:
         return None
-    if any(op.tile.dtype.name != "bfloat16" for op in (q, k, v)):
+    if len({op.tile.dtype.name for op in (q, k, v)}) != 1 or q.tile.dtype.name not in ("bfloat16", "float32"):
+        return None
+    if (q.tile.dtype.name == "float32") != (pv.args[0].dtype.name == "float32"):
         return None
     phase = plan.phases[0].range
     last = plan.scopes["last"]
@@ -868,7 +871,214 @@ extern "C" __global__ void __launch_bounds__(256) {self.name}_merge(const {self.
         return "\n".join(L)
 
 
+class _FlashF32(_Flash):
+    """f32 q, k and v (`@` at full precision): a plain f32 kernel on the vector ALUs, for the parity of the
+    spec's f32 form rather than speed. One thread per query row (128 per workgroup), the key blocks of the
+    bf16 kernel's work items staged through LDS (K, V and the block's scores), per 64-key block the row max,
+    then exp and the sums, in f32 throughout."""
+
+    THREADS = 128
+
+    def __init__(self, plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str,
+                 trace: bool = False) -> None:
+        self.plan, self.sch, self.pipeline, self.m, self.name = plan, sch, pipeline, m, name
+        self.trace = trace
+        if m.d % 4 or m.dv % 4 or m.d > 128 or m.dv > 128:
+            raise KernelError(f"the gfx950 f32 attention lowering takes head dims that are multiples of 4 up to 128 "
+                              f"(got {m.d} and {m.dv})")
+        self.nw = 4  # rows in groups of 32 for the block lists' mask classes: 128 rows per work item
+        self.bq = 128
+        self.bkv = BKV
+        if m.rows % self.bq or m.bk % self.bkv:
+            raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of {self.bq} rows "
+                              f"and key blocks of a multiple of {self.bkv} (got {m.rows} and {m.bk})")
+        if plan.runtime or sch.runtime:
+            raise KernelError("attention with runtime masks is lowered by the decode path, not this one")
+        self.jr = plan.phases[0].range
+        self.kdim, self.kwin = _loop_window(m.k, m.jvar)
+        self.vdim, self.vwin = _loop_window(m.v, m.jvar)
+
+    def program(self) -> Program:
+        plan, m = self.plan, self.m
+        items, weights, blocks = self._items()
+        order = sorted(range(len(items)), key=lambda i: (-weights[i], i))
+        table = np.zeros((max(len(items), 1), 4), np.int32)
+        for row, i in enumerate(order):
+            t, sub, off, cnt, _ = items[i]
+            table[row] = (t, sub, off, cnt)
+        kvtab = np.array(blocks, np.int32).reshape(-1) if blocks else np.zeros(2, np.int32)
+        self.tables = {"fa_items": table.reshape(-1), "fa_blocks": kvtab}
+        for name, t in self.sch.tables.items():
+            if name.startswith("tile_") or name.startswith("fill_"):
+                self.tables[name] = t
+        args = self._args()
+        grid = max(len(items), 1)
+        workspace = {TRACE: grid * TRACE_FIELDS * 8} if self.trace else {}
+        lds = 4 * self.bkv * (m.d + m.dv + self.THREADS)
+        return Program(
+            name=self.name, source=self._source32(args), launches=[Launch(self.name, args, (grid, 1, 1),
+                                                                          (self.THREADS, 1, 1), 0)],
+            outputs=[(m.out.shape, m.out.dtype)], inputs=[(s_.shape, s_.dtype) for s_ in plan.inputs],
+            tables=self.tables, workspace=workspace, lds_bytes=lds,
+            notes={"family": "flash", "f32_operands": True, "block_q": self.bq, "block_kv": self.bkv,
+                   "items": len(items), "trace_workgroups": grid if self.trace else 0,
+                   "trace_slots": min(grid, gfx950.CUS * max(1, gfx950.LDS_BYTES // lds)),
+                   "slices_per_step": (m.rows // self.bq) * (m.bk // self.bkv)})
+
+    def _args(self) -> List[Arg]:
+        plan, m = self.plan, self.m
+        args = []
+        for k, name in enumerate(plan.nest.params):
+            if any(ix.name == name for ix in plan.indices):
+                args.append(Arg("input", k, "const int* __restrict__", name))
+            else:
+                args.append(Arg("input", k, "const float* __restrict__", name))
+        out_t = "float" if m.out.dtype.name == "float32" else "ak_u16"
+        args.append(Arg("output", 0, f"{out_t}* __restrict__", m.out.name + "_out"))
+        for name in self.tables:
+            args.append(Arg("table", name, "const int* __restrict__", name))
+        if self.trace:
+            args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
+        return args
+
+    def _source32(self, args: List[Arg]) -> str:
+        plan, sch, m = self.plan, self.sch, self.m
+        D, DV, bkv, T = m.d, m.dv, self.bkv, self.THREADS
+        index = Index(plan, lambda v: f"lv_{v}")
+        jvar = m.jvar
+        no_j = lambda v: "0" if v == jvar else f"lv_{v}"
+        q_shape, k_shape, v_shape = (plan.inputs[op.param].shape for op in (m.q, m.k, m.v))
+        q_base, q_str = tile_base(m.q.tile, q_shape, index, lambda v: f"lv_{v}")
+        k_base, k_str = tile_base(m.k.tile, k_shape, index, no_j)
+        v_base, v_str = tile_base(m.v.tile, v_shape, index, no_j)
+        o_base, o_str = tile_base(m.out.tile, m.out.shape, index, lambda v: f"lv_{v}")
+        if q_str[-1] != 1 or k_str[-1] != 1 or v_str[-1] != 1 or o_str[-1] != 1:
+            raise KernelError("the gfx950 attention lowering reads rows whose last dim is contiguous")
+        ldq, ldo = q_str[0], o_str[0]
+        kstride_j, vstride_j = strides(k_shape)[self.kdim], strides(v_shape)[self.vdim]
+
+        def sleaf(n: Node) -> Optional[str]:
+            if n is m.scores:
+                return "sv"
+            if n.op == "iota":
+                dim = n.kwargs["dimension"]
+                return "er" if dim == len(n.shape) - 2 else "ec" if dim == len(n.shape) - 1 else "0"
+            if n.op == "loop":
+                return f"lv_{n.kwargs['var']}"
+            if n.op == "full":
+                return literal(n.kwargs["value"], n.dtype)
+            if n.op == "index":
+                ix = plan.index(n.kwargs["array"])
+                flat = " + ".join(f"({sem.value(i)}) * {s_}" for i, s_ in zip(n.args, strides(ix.shape))) or "0"
+                return f"args.{ix.name}[{flat}]"
+            return None
+
+        sem = Emitter(sleaf, (m.rows, m.bk), prefix="sc")
+        score_expr = sem.emit(m.score)
+        score_lines = " ".join(sem.lines)
+
+        def eleaf(n: Node) -> Optional[str]:
+            if n is m.acc_leaf:
+                return "acc_v"
+            if _strip(n) is m.sum_leaf:
+                return "l_run"
+            if n.op == "iota":
+                dim = n.kwargs["dimension"]
+                return "er" if dim == len(n.shape) - 2 else "ed" if dim == len(n.shape) - 1 else "0"
+            if n.op == "loop":
+                return f"lv_{n.kwargs['var']}"
+            if n.op == "full":
+                return literal(n.kwargs["value"], n.dtype)
+            if n.op in ("carried", "load"):
+                raise KernelError("the attention epilogue reads only the accumulator and the row sum")
+            return None
+
+        eem = Emitter(eleaf, m.out.tile.shape, prefix="e")
+        out_expr = eem.emit(m.value.node)
+        epi_lines = "\n      ".join(eem.lines)
+        store = ("op[ed] = res;" if m.out.dtype.name == "float32"
+                 else "op[ed] = (ak_u16)ak_bf16_bits(res);")
+        tile_decode = "\n  ".join(decode_tile(plan, sch, "t"))
+        Q, K, V, O = (f"args.{m.q.tile.array}", f"args.{m.k.tile.array}", f"args.{m.v.tile.array}",
+                      f"args.{m.out.name}_out")
+        tr0 = f"const unsigned long long tr_0 = {NOW};" if self.trace else ""
+        tr1 = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; tr[0] = 0; "
+               f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = nblk; }}" if self.trace else "")
+        return f"""// Generated by tilejax_amd for `{plan.nest.name}`: f32 attention on the vector ALUs.
+// spec tile {m.rows} x {m.bk} (head dims {D}, {DV}); {T} query rows per workgroup, key blocks of {bkv}.
+{PRELUDE}
+{c_struct(f"{self.name}_args", args)}
+extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_args args) {{
+  __shared__ float ks[{bkv * D}], vs[{bkv * DV}], ss[{bkv * T}];
+  const int tid = threadIdx.x;
+  {tr0}
+  const int* item = args.fa_items + blockIdx.x * 4;
+  const int t = item[0], sub = item[1], boff = item[2], nblk = item[3];
+  {tile_decode}
+  const int er = sub * {T} + tid;  // this thread's query row in the spec tile
+  float q[{D}], acc[{DV}];
+  const float* qp = {Q} + ({q_base}) + (long long)er * {ldq};
+#pragma unroll
+  for (int d = 0; d < {D}; ++d) q[d] = qp[d];
+#pragma unroll
+  for (int d = 0; d < {DV}; ++d) acc[d] = 0.f;
+  float m_run = {literal(m.m_init)}, l_run = 0.f;
+  const long long k_off = {k_base}, v_off = {v_base};
+  for (int b = 0; b < nblk; ++b) {{
+    const int lv_{jvar} = args.fa_blocks[2 * (boff + b)], bc = args.fa_blocks[2 * (boff + b) + 1];
+    const int kpos = lv_{jvar} + {self.kwin.offset} + bc, vpos = lv_{jvar} + {self.vwin.offset} + bc;
+    __syncthreads();  // the previous block's reads are done
+    for (int e = tid; e < {bkv * D // 4}; e += {T}) {{
+      const int r = e / {D // 4}, c = e % {D // 4};
+      *(ak_f32x4*)(ks + 4 * e) = *(const ak_f32x4*)({K} + k_off + (long long)(kpos + r) * {kstride_j} + 4 * c);
+    }}
+    for (int e = tid; e < {bkv * DV // 4}; e += {T}) {{
+      const int r = e / {DV // 4}, c = e % {DV // 4};
+      *(ak_f32x4*)(vs + 4 * e) = *(const ak_f32x4*)({V} + v_off + (long long)(vpos + r) * {vstride_j} + 4 * c);
+    }}
+    __syncthreads();
+    float mx = m_run;
+    for (int key = 0; key < {bkv}; ++key) {{
+      float sv = 0.f;
+#pragma unroll
+      for (int d = 0; d < {D}; ++d) sv = __builtin_fmaf(q[d], ks[key * {D} + d], sv);
+      const int ec = bc + key;
+      {score_lines}
+      const float sc = {score_expr};
+      ss[key * {T} + tid] = sc;
+      mx = ak_maximum(mx, sc);
+    }}
+    const float alpha = ak_exp(m_run - mx);
+    float lsum = 0.f;
+#pragma unroll
+    for (int d = 0; d < {DV}; ++d) acc[d] *= alpha;
+    for (int key = 0; key < {bkv}; ++key) {{
+      const float p = ak_exp(ss[key * {T} + tid] - mx);
+      lsum += p;
+#pragma unroll
+      for (int d = 0; d < {DV}; ++d) acc[d] = __builtin_fmaf(p, vs[key * {DV} + d], acc[d]);
+    }}
+    l_run = alpha * l_run + lsum;
+    m_run = mx;
+  }}
+  auto* op = {O} + ({o_base}) + (long long)er * {ldo};
+#pragma unroll
+  for (int ed = 0; ed < {DV}; ++ed) {{
+    const float acc_v = acc[ed];
+    {epi_lines}
+    const float res = (float)({out_expr});
+    {store}
+  }}
+  {tr1}
+}}
+"""
+
+
 def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str, trace: bool = False) -> Program:
+    if m.q.tile.dtype.name == "float32":
+        if m.out.dtype.name not in ("float32", "bfloat16"):
+            raise KernelError("the gfx950 attention lowering stores f32 or bf16 outputs")
+        return _FlashF32(plan, sch, pipeline, m, name, trace).program()
     if m.out.dtype.name != "bfloat16":
         raise KernelError("the gfx950 attention lowering stores bf16 outputs")
     return _Flash(plan, sch, pipeline, m, name, trace).program()

@@ -55,6 +55,7 @@ def standard() -> Iterator[Tuple[object, tuple]]:
                                    ((1024, 512, 1024, 4, 4), GT(512, 512)), ((2048, 1024, 512, 4, 8), GT(512, 256)),
                                    ((16384, 4096, 14336, 8, 64), GT(512, 512))):
         yield moe.grouped_matmul, (_bf16(m, k), _bf16(e, k, n), _i32(g), tiles)
+    yield moe.grouped_matmul, (_f32(1024, 512), _f32(4, 512, 1024), _i32(4), GT(512, 256))
     from examples import rmsnorm_matmul as rm
 
     R = rm.NormMatmulTiles
@@ -88,6 +89,9 @@ def standard() -> Iterator[Tuple[object, tuple]]:
                               ((2, 2, 512, 128), A(128, 128)), ((2, 2, 512, 128), A(128, 256)),
                               ((1, 1, 1024, 128), A(512, 512))):
             yield ca.causal_attention, (_bf16(*shape), _bf16(*shape), _bf16(*shape), blocks)
+        for shape, blocks in (((1, 1, 256, 128), A(128, 128)), ((2, 2, 512, 128), A(256, 128)),
+                              ((1, 2, 512, 128), A(128, 256))):
+            yield ca.causal_attention, (_f32(*shape), _f32(*shape), _f32(*shape), blocks)
     except ImportError:
         pass
 

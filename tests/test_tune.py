@@ -2,6 +2,7 @@
 (the reference's tests/test_tune.py:51-120). Timing and testing candidates on the GPU is in test_gpu_tune.py."""
 
 import pytest
+import torch
 from helpers import make_kernel, spec
 
 import tilejax_amd as autokernel
@@ -106,3 +107,44 @@ def test_proposals_follow_the_bottleneck():
     # After a failure: two buffers, then the neighbours that build.
     failed = Trial(Config(Tiles(), Pipeline(3, 2)), error="out of LDS")
     assert proposals(k, sig, failed)[0] == Config(Tiles(), Pipeline(2, 2))
+
+
+# --------------------------------------------------------------------------------- testing candidates
+
+
+def test_the_reference_runs_the_fewest_iterations():
+    """The reference's tests/test_tune.py:159-164: the tuner evaluates the reference at the defaults or the
+    largest choices, whichever plans with fewer loop iterations."""
+    from tilejax_amd.tune import _reference_config
+
+    k = make_kernel(SOURCE, Tiles=Tiles)
+    sig = k.signature(spec(256, 256), spec(256, 128))
+    assert _reference_config(k, sig, k.default_config(sig)) == Tiles()  # tm=512 doesn't divide 256 rows
+    sig = k.signature(spec(1024, 512), spec(512, 128))
+    assert _reference_config(k, sig, k.default_config(sig)) == Tiles(tm=512, tk=512)
+    plain = make_kernel(SOURCE.replace("t=Tiles()", "").replace("t.tm", "128").replace("t.tk", "128"))
+    sig = plain.signature(spec(256, 256), spec(256, 128))
+    assert _reference_config(plain, sig, plain.default_config(sig)) is None
+
+
+def test_random_inputs():
+    from tilejax_amd.tune import random_inputs
+
+    a, b, c = random_inputs((((8, 128), jaxlite.bfloat16), ((4,), jaxlite.int32), ((64,), jaxlite.int32)),
+                            bounds={2: 5}, device="cpu")
+    assert a.dtype == torch.bfloat16 and b.dtype == torch.int32 and c.dtype == torch.int32
+    assert int(b.abs().max()) <= 8 and float(a.float().std()) > 0.5
+    assert int(c.min()) >= 0 and int(c.max()) <= 5  # an index array: from 0 to the furthest loop value
+
+
+def test_a_kernel_without_a_tunable_tunes_its_buffering():
+    """The reference's tests/test_tune.py:146-156: with nothing to choose in the tiles, exposed input waits
+    propose one more input buffer."""
+    k = make_kernel(SOURCE.replace("t=Tiles()", "").replace("t.tm", "128").replace("t.tk", "128"))
+    bf = jaxlite.bfloat16
+    sig = k.signature(spec(256, 256, dtype=bf), spec(256, 128, dtype=bf))
+    start = k.default_config(sig)
+    assert start.tunable is None and str(start) == f"{start.pipeline}"
+    dma = Trial(start, profile(start, seconds=10.0, wait=5.0))
+    bigger = Pipeline(start.pipeline.input_buffers + 1, start.pipeline.output_buffers)
+    assert proposals(k, sig, dma)[0] == Config(None, bigger)

@@ -231,6 +231,25 @@ def _index_bounds(kernel: Any, signature: Any, start: Config) -> Dict[int, int]:
     return {ix.param: furthest for ix in plan.indices}
 
 
+def _reference_config(kernel: Any, signature: Any, start: Config) -> Any:
+    """The tunable the reference is evaluated with while tuning (src/autokernel/tune.py:289-304 of the
+    reference): the defaults, or every field at its largest choice where that plans with fewer loop
+    iterations, since the reference runs the loop nest eagerly. None for a kernel without a tunable."""
+    if start.tunable is None:
+        return None
+    largest = dataclasses.replace(start.tunable, **{k: v[-1] for k, v in choices(start.tunable).items()})
+    best, fewest = start.tunable, math.inf
+    for tunable in (start.tunable, largest):
+        try:
+            plan, _ = kernel.build(signature, tunable)
+        except KernelError:
+            continue
+        iterations = math.prod(r.count for r in plan.loops)
+        if iterations < fewest:
+            best, fewest = tunable, iterations
+    return best
+
+
 def _measure(kernel: Any, signature: Any, config: Config, inputs: Sequence[torch.Tensor], want: Any) -> Trial:
     from .api import compare
 
@@ -265,7 +284,7 @@ def tune(kernel: Any, signature: Any, arrays: Optional[Sequence[Any]] = None, bu
         inputs = list(arrays)
     else:
         inputs = random_inputs(signature, _index_bounds(kernel, signature, start))
-    args = [start.tunable] if start.tunable is not None else []
-    want = kernel.reference(*inputs, *args)
+    ref = _reference_config(kernel, signature, start)
+    want = kernel.reference(*inputs, *([ref] if ref is not None else []))
     return search(start, lambda c: _measure(kernel, signature, c, inputs, want),
                   lambda t: proposals(kernel, signature, t), budget)

@@ -396,8 +396,8 @@ class _Flash:
     def _split(self, items, weights):
         """Split-KV for balance: items with more key blocks than a CU's share of all blocks (one workgroup
         per CU at a time) are cut into chunks of consecutive blocks. A chunk runs the same online softmax
-        over its blocks and writes its (m, l, acc) to a workspace slot; the tile's last chunk to finish (a
-        per-tile count in the program's state) merges them. Returns the items (t, sub, block offset, blocks, per-wave counts, slot or -1), their weights
+        over its blocks and writes its (m, l, acc) to a workspace slot; the merge kernel combines a tile's
+        chunks. Returns the items (t, sub, block offset, blocks, per-wave counts, slot or -1), their weights
         and the merge table rows (t, sub, first slot, chunks)."""
         total = sum(it[3] for it in items)
         share = max(1, -(-total // gfx950.CUS))
@@ -439,10 +439,6 @@ class _Flash:
         tables = {"fa_items": table.reshape(-1), "fa_blocks": kvtab}
         if merges:
             tables["fa_merge"] = np.array(merges, np.int32).reshape(-1)
-            owner = np.zeros(self.slots, np.int32)  # slot -> its tile's row of fa_merge
-            for p_, (_, _, first, parts) in enumerate(merges):
-                owner[first:first + parts] = p_
-            tables["fa_slot_merge"] = owner
         for name, t in sch.tables.items():
             if name.startswith("tile_") or name.startswith("fill_"):
                 tables[name] = t
@@ -450,17 +446,18 @@ class _Flash:
         args = self._args()
         source = self._source(args, stride)
         launches = [Launch(self.name, args, (max(len(items), 1), 1, 1), (64 * nw, 1, 1), 0)]
-        workspace, state = {}, {}
+        workspace = {}
         if self.trace:
             workspace[TRACE] = max(len(items), 1) * TRACE_FIELDS * 8
         if merges:
             workspace["fa_part"] = self.slots * self.bq * (m.dv + 2) * 4
-            state["fa_count"] = 4 * len(merges)  # chunks of each split tile done so far in this call
+            per_item = self.bq * m.dv // 4 // 256
+            launches.append(Launch(f"{self.name}_merge", args, (len(merges) * per_item, 1, 1), (256, 1, 1), 0))
         flop = 2.0 * sum(w for w in weights) * 32 * self.bkv * (m.d + m.dv)
         lds = STAGES * self.bkv * (m.d + m.dv) * 2
         return Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
-            inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace, state=state,
+            inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
             lds_bytes=lds,
             notes={"family": "flash", "block_q": self.bq, "block_kv": self.bkv, "waves": nw, "items": len(items),
                    "executed_flop": flop, "split_items": len(merges), "chunks": self.slots,
@@ -485,7 +482,6 @@ class _Flash:
             args.append(Arg("table", name, "const int* __restrict__", name))
         if "fa_merge" in self.tables:
             args.append(Arg("workspace", "fa_part", "float* __restrict__", "fa_part"))
-            args.append(Arg("state", "fa_count", "int* __restrict__", "fa_count"))
         if self.trace:
             args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
         return args
@@ -578,7 +574,6 @@ class _Flash:
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.name}_args args) {{
-  {"__shared__ int ak_merge;  // the split tile this workgroup merges, or -1" if self.slots else ""}
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int* item = args.fa_items + blockIdx.x * {stride};
@@ -807,7 +802,7 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
         if tr:
             w(f"  const unsigned long long tr_c1 = {NOW};")
         if self.slots:
-            w(f"""  if (slot >= 0) {{  // a chunk: (m, l, acc) of its rows to the workspace; the tile's last chunk merges
+            w(f"""  if (slot >= 0) {{  // a chunk: (m, l, acc) of its rows to the workspace, for the merge kernel
     float* part = args.fa_part + (long long)slot * {bq * (DV + 2)};
     const int lr = wave * 32 + (lane & 31);
 #pragma unroll
@@ -817,49 +812,6 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
         *(ak_f32x4*)(part + lr * {DV} + 32 * dt + g4 * 8 + (lane >> 5) * 4) =
             ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};
     if (lane < 32) {{ part[{bq * DV} + lr] = m_run; part[{bq * DV + bq} + lr] = l_run; }}
-    // Count the chunk done (its writes made visible first). The chunk that brings the count to the tile's
-    // number of chunks merges them and sets the count back to zero for the next call: no chunk waits.
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {{
-      const int p_ = ak_ldc(args.fa_slot_merge, slot), n_ = ak_ldc(args.fa_merge, 4 * p_ + 3);
-      const int done = atomicAdd(args.fa_count + p_, 1);
-      ak_merge = done == n_ - 1 ? p_ : -1;
-      if (done == n_ - 1) atomicExch(args.fa_count + p_, 0);
-    }}
-    __syncthreads();
-    const int pm = ak_merge;
-    if (pm >= 0) {{
-      __threadfence();  // the other chunks' writes
-      const int first = ak_ldc(args.fa_merge, 4 * pm + 2), chunks = ak_ldc(args.fa_merge, 4 * pm + 3);
-      // four output elements of one row a thread at a time, over the chunks in order with the online
-      // softmax's own rule (weights exp(m_c - M)), then the epilogue
-      for (int e = tid; e < {bq * DV // 4}; e += {T}) {{
-        const int mr = e / {DV // 4}, d0 = (e % {DV // 4}) * 4;
-        float mx = -__builtin_inff();
-        for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, args.fa_part[(long long)(first + c) * {bq * (DV + 2)} + {bq * DV} + mr]);
-        float l_run = 0.f;
-        ak_f32x4 a = {{0.f, 0.f, 0.f, 0.f}};
-        for (int c = 0; c < chunks; ++c) {{
-          const float* pp = args.fa_part + (long long)(first + c) * {bq * (DV + 2)};
-          const float wgt = ak_exp(pp[{bq * DV} + mr] - mx);
-          l_run += wgt * pp[{bq * DV + bq} + mr];
-          const ak_f32x4 v = *(const ak_f32x4*)(pp + mr * {DV} + d0);
-          a[0] += wgt * v[0]; a[1] += wgt * v[1]; a[2] += wgt * v[2]; a[3] += wgt * v[3];
-        }}
-        const int er = sub * {bq} + mr; (void)er;
-        ak_u16* op = (ak_u16*){O} + ({o_base}) + (long long)er * {ldo} + d0;
-        float res[4];
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {{
-          const int ed = d0 + e4; (void)ed;
-          const float acc_v = a[e4];
-          {epi_lines}
-          res[e4] = (float)({out_expr});
-        }}
-        *(ak_u32x2*)op = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
-      }}
-    }}
     {trace_write}
     return;
   }}""")
@@ -880,6 +832,41 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
       *(ak_u32x2*)(op + 32 * dt + g4 * 8 + (lane >> 5) * 4) = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
     }}
   {trace_write}
+}}""")
+        if self.slots:
+            per_item = bq * DV // 4 // 256
+            w(f"""
+// The merge of tiles split along the keys: each thread combines four output elements of one row over the
+// tile's chunks with the online softmax's own rule (weights exp(m_c - M)), then applies the epilogue.
+extern "C" __global__ void __launch_bounds__(256) {self.name}_merge(const {self.name}_args args) {{
+  const int p = blockIdx.x / {per_item};
+  const int e = (blockIdx.x % {per_item}) * 256 + threadIdx.x;
+  const int lr = e / {DV // 4}, d0 = (e % {DV // 4}) * 4;
+  const int t = ak_ldc(args.fa_merge, 4 * p), sub = ak_ldc(args.fa_merge, 4 * p + 1);
+  const int first = ak_ldc(args.fa_merge, 4 * p + 2), chunks = ak_ldc(args.fa_merge, 4 * p + 3);
+  {tile_decode}
+  float mx = -__builtin_inff();
+  for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, args.fa_part[(long long)(first + c) * {bq * (DV + 2)} + {bq * DV} + lr]);
+  float l_run = 0.f;
+  ak_f32x4 a = {{0.f, 0.f, 0.f, 0.f}};
+  for (int c = 0; c < chunks; ++c) {{
+    const float* part = args.fa_part + (long long)(first + c) * {bq * (DV + 2)};
+    const float w = ak_exp(part[{bq * DV} + lr] - mx);
+    l_run += w * part[{bq * DV + bq} + lr];
+    const ak_f32x4 v = *(const ak_f32x4*)(part + lr * {DV} + d0);
+    a[0] += w * v[0]; a[1] += w * v[1]; a[2] += w * v[2]; a[3] += w * v[3];
+  }}
+  const int er = sub * {bq} + lr; (void)er;
+  ak_u16* op = (ak_u16*){O} + ({o_base}) + (long long)er * {ldo} + d0;
+  float res[4];
+#pragma unroll
+  for (int e4 = 0; e4 < 4; ++e4) {{
+    const int ed = d0 + e4; (void)ed;
+    const float acc_v = a[e4];
+    {epi_lines}
+    res[e4] = (float)({out_expr});
+  }}
+  *(ak_u32x2*)op = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
 }}""")
         return "\n".join(L)
 

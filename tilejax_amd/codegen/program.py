@@ -32,8 +32,8 @@ NOW = "__builtin_amdgcn_s_memrealtime()"
 class Arg:
     """One kernel argument: a pointer to an input, output, table or workspace buffer, or an int."""
 
-    kind: str  # "input", "output", "table", "workspace", "state", "int"
-    key: Any  # input/output position, table/workspace/state name, or the int's value
+    kind: str  # "input", "output", "table", "workspace", "int"
+    key: Any  # input/output position, table/workspace name, or the int's value
     ctype: str  # the C type of the struct field
     name: str
 
@@ -56,14 +56,10 @@ class Program:
     inputs: List[Tuple[Tuple[int, ...], jaxlite.DType]]
     tables: Dict[str, np.ndarray] = field(default_factory=dict)
     workspace: Dict[str, int] = field(default_factory=dict)  # name -> bytes (uninitialised: launches write before reading)
-    # name -> bytes of device memory zeroed once per device and kept: counters the kernels leave at zero when a
-    # call ends (calls of one program that overlap on a device, on two streams, would share them)
-    state: Dict[str, int] = field(default_factory=dict)
     lds_bytes: int = 0
     notes: Dict[str, Any] = field(default_factory=dict)  # what the lowering chose (hardware tiles, ...)
     _modules: Dict[int, runtime.Module] = field(default_factory=dict, repr=False)
     _tables: Dict[int, Dict[str, torch.Tensor]] = field(default_factory=dict, repr=False)
-    _state: Dict[int, Dict[str, torch.Tensor]] = field(default_factory=dict, repr=False)
 
     def module(self, device: int) -> runtime.Module:
         if device not in self._modules:
@@ -77,13 +73,6 @@ class Program:
             self._tables[key] = {name: torch.from_numpy(np.ascontiguousarray(t)).to(device)
                                  for name, t in self.tables.items()}
         return self._tables[key]
-
-    def device_state(self, device: torch.device) -> Dict[str, torch.Tensor]:
-        key = device.index or 0
-        if key not in self._state:
-            self._state[key] = {name: torch.zeros(max(n, 4), dtype=torch.uint8, device=device)
-                                for name, n in self.state.items()}
-        return self._state[key]
 
     def check_inputs(self, arrays: Sequence[torch.Tensor]) -> None:
         if len(arrays) != len(self.inputs):
@@ -129,7 +118,6 @@ class Program:
             outputs = [torch.empty(shape, dtype=dt.torch, device=device) for shape, dt in self.outputs]
         tables = self.device_tables(device)
         workspace = {name: torch.empty(max(n, 4), dtype=torch.uint8, device=device) for name, n in self.workspace.items()}
-        workspace.update(self.device_state(device))
         module = self.module(device.index or 0)
         stream = runtime.current_stream() if stream is None else stream
         for launch in launches:
@@ -152,7 +140,7 @@ def pack(args: Sequence[Arg], arrays: Sequence[torch.Tensor], outputs: Sequence[
             pointers.append(outputs[a.key].data_ptr())
         elif a.kind == "table":
             pointers.append(tables[a.key].data_ptr())
-        elif a.kind in ("workspace", "state"):
+        elif a.kind == "workspace":
             pointers.append(workspace[a.key].data_ptr())
         else:
             raise KernelError(f"unknown argument kind {a.kind}")

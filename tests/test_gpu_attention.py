@@ -90,3 +90,16 @@ def test_causal_attention_f32(shape, blocks):
     want = torch.as_tensor(kernels.attention_float64(q, k, v))
     diff = (got.double().cpu() - want).abs()
     assert diff.max().item() < 1e-4, diff.max().item()
+
+
+def test_split_tiles_call_after_call():
+    """(1, 2, 1024, 128) at 256 x 256 blocks cuts its longest tiles into chunks, which the merge kernel
+    combines; three calls in a row give the same bits."""
+    q, k, v = (t.cuda() for t in _inputs(1, 2, 1024, 128, seed=9))
+    lowered = causal_attention.lower(q, k, v, AttentionBlocks(256, 256))
+    assert lowered.program.notes["split_items"] > 0
+    print("attention (1, 2, 1024, 128) split, three calls", flush=True)
+    outs = [lowered.run(q, k, v) for _ in range(3)]
+    torch.cuda.synchronize()
+    _close(outs[0], kernels.causal_attention(q.cpu(), k.cpu(), v.cpu(), 256, 256))
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])

@@ -6,8 +6,8 @@ and then the matmul, whose epilogue scales each row by rsqrt(sum_sq / D + eps).
 
 Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want| (2 bf16 ulp): the
 sum of squares is added in another order than the spec's tk-deep blocks, and the products in MFMA order.
-f32 inputs (the left operand's prologue then stays f32, and the products take its high and low bf16
-parts): within rtol 1e-4 plus 1e-4 of the largest |want| of float64, the reference's f32 tolerance
+f32 inputs (the left operand's prologue then stays f32, and the products take its three bf16 parts):
+within rtol 1e-4 plus 1e-4 of float64, the reference's f32 tolerance
 (tests/test_examples.py:136-152).
 """
 
@@ -76,7 +76,7 @@ def test_rmsnorm_matmul_f32(tiles):
     want = torch.as_tensor(kernels.rmsnorm_matmul_float64(x, gamma, w))
     scale = want.abs().max().item()
     diff = (got.double().cpu() - want).abs()
-    assert not (diff > 1e-4 * want.abs() + 1e-4 * scale).any(), diff.max().item()
+    assert not (diff > 1e-4 * want.abs() + 1e-4).any(), diff.max().item()
 
 
 def test_rmsnorm_matmul_verify_against_the_spec():
@@ -97,3 +97,41 @@ def test_rmsnorm_matmul_large():
     normed = (xf * torch.rsqrt((xf * xf).mean(dim=1, keepdim=True) + 1e-6) * gamma.float())
     want = normed @ w.float()
     _close(got, want)
+
+
+TWO_PASS = """
+def two_pass(x, w):
+    M, D = x.shape
+    out = jnp.zeros((M, 256))
+    for i in range(0, M, 128):
+        sum_sq = jnp.zeros((128, 128))
+        for k in range(0, D, 128):
+            xk = x[i : i + 128, k : k + 128]
+            sum_sq += xk * xk
+        scale = jax.lax.rsqrt(jnp.sum(sum_sq, axis=1, keepdims=True) / D + 1e-6)
+        acc = jnp.zeros((128, 256))
+        for k2 in range(0, D, 128):
+            acc += (x[i : i + 128, k2 : k2 + 128] * scale) @ w[k2 : k2 + 128, :]
+        out = out.at[i : i + 128, :].set(acc)
+    return out
+"""
+
+
+def test_two_reduction_loops_per_tile():
+    """The reference's tests/test_codegen.py:580-611: a first loop sums each row's squares (a tile summed
+    elementwise), the code between the loops turns them into a row scale, and the second loop multiplies the
+    scaled rows. The row pass computes the sums and the scale, then writes the operand's parts (f32)."""
+    from tests.helpers import make_kernel
+
+    kernel = make_kernel(TWO_PASS)
+    g = torch.Generator().manual_seed(12)
+    x, w = torch.randn(256, 384, generator=g), torch.randn(384, 256, generator=g)
+    lowered = kernel.lower(x, w)
+    assert [p.range.var for p in lowered.plan.phases] == ["k", "k2"] and lowered.steps == 2 * 6
+    print("two_pass f32 256x384x256", flush=True)
+    got = lowered.run(x.cuda(), w.cuda())
+    torch.cuda.synchronize()
+    xd = x.double()
+    want = xd / torch.sqrt((xd * xd).mean(dim=1, keepdim=True) + 1e-6) @ w.double()
+    diff = (got.double().cpu() - want).abs()
+    assert not (diff > 1e-4 * want.abs() + 1e-4).any(), diff.max().item()  # test_codegen.py:604

@@ -20,11 +20,11 @@ def test_f32_operands_take_their_bf16_parts():
     lowered = matmul.lower(((256, 384), F32), ((384, 256), F32), MatmulTiles(128, 128, 128))
     prog = lowered.program
     assert prog.notes["f32_operands"]
-    assert _symbols(lowered) == ["tj_matmul_parts_b", "tj_matmul_parts_a", "tj_matmul"]
-    # three bf16 slices for each of the operand's: 2 bytes x 3 per element
-    assert prog.workspace == {"x3_a": 6 * 256 * 384, "x3_b": 6 * 384 * 256}
-    # three reduction steps of 128: 2 slices of 64 each, so 6 slices of the parts per step
-    assert prog.notes["slices_per_step"] == 6
+    assert _symbols(lowered)[:3] == ["tj_matmul_parts_b", "tj_matmul_parts_a", "tj_matmul"]
+    # six bf16 slices for each of the operand's: 2 bytes x 6 per element
+    assert prog.workspace["x3_a"] == 12 * 256 * 384 and prog.workspace["x3_b"] == 12 * 384 * 256
+    # three reduction steps of 128: 2 slices of 64 each, so 12 slices of the parts per step
+    assert prog.notes["slices_per_step"] == 12
 
 
 def test_bf16_operands_read_the_arrays_themselves():
@@ -54,7 +54,7 @@ def test_f32_rmsnorm_writes_the_left_operands_parts_in_its_row_pass():
     lowered = rmsnorm_matmul.lower(((256, 512), F32), ((1, 512), F32), ((512, 512), F32),
                                    NormMatmulTiles(128, 128, 128))
     assert _symbols(lowered)[:3] == ["tj_rmsnorm_matmul_rows", "tj_rmsnorm_matmul_parts_b", "tj_rmsnorm_matmul"]
-    assert lowered.program.workspace["rn_a"] == 6 * 256 * 512 and "x3_a" not in lowered.program.workspace
+    assert lowered.program.workspace["rn_a"] == 12 * 256 * 512 and "x3_a" not in lowered.program.workspace
 
 
 def test_f32_attention_runs_on_the_vector_alus():
@@ -80,3 +80,13 @@ def test_what_no_family_takes_is_a_kernel_error():
     ''')
     with pytest.raises(KernelError, match="no lowering"):
         k.lower(((256, 512), F32))
+
+
+def test_two_reduction_loops_lower_to_a_row_pass_and_the_matmul():
+    from tests.test_gpu_rmsnorm_matmul import TWO_PASS
+    from tests.helpers import make_kernel
+
+    k = make_kernel(TWO_PASS)
+    lowered = k.lower(((256, 384), F32), ((384, 256), F32))
+    assert _symbols(lowered)[:3] == ["tj_two_pass_rows", "tj_two_pass_parts_b", "tj_two_pass"]
+    assert "ps_0 = ak_wave_sum(ps_0)" in lowered.source and "st_0" in lowered.source

@@ -44,6 +44,14 @@ AK_INLINE unsigned ak_bf16_bits(float x) { return ak_pack_bf16x2(x, 0.0f) & 0xff
 AK_INLINE float ak_round_bf16(float x) { return __builtin_bit_cast(float, ak_bf16_bits(x) << 16); }
 AK_INLINE float ak_bf16_to_f32(unsigned short b) { return __builtin_bit_cast(float, (unsigned)b << 16); }
 AK_INLINE float ak_round_f16(float x) { return (float)(_Float16)x; }
+// x as three bf16 parts, x = p1 + p2 + p3 to within about 2^-24 |x|: p1 = bf16(x), p2 = bf16(x - p1),
+// p3 = bf16(x - p1 - p2) (the differences are exact in f32). Parts after one that isn't finite are 0.
+AK_INLINE void ak_split3(float x, float& p1, float& p2, float& p3) {
+  p1 = ak_round_bf16(x);
+  const float r1 = __builtin_isfinite(p1) ? x - p1 : 0.0f;
+  p2 = ak_round_bf16(r1);
+  p3 = ak_round_bf16(r1 - p2);
+}
 
 // Elementwise functions with the tile code's meaning.
 AK_INLINE float ak_exp(float x) { return __expf(x); }

@@ -65,25 +65,39 @@ class GemmMatch:
     a_expr: Optional[Node] = None
     side: Tuple[Tuple[str, Node, float], ...] = ()
     k0: int = 0  # the value of a reduction loop of one step (not among the plan's phases)
+    # A first reduction loop before the matmul's (the reference's tests/test_codegen.py:580-611): carried row
+    # sums of row-prologue functions of the left operand's array (`pre`: (name, summand, "tile" for a tile
+    # summed elementwise and read through jnp.sum(axis=1), "row" for a (rows, 1) sum)), and the row statistics
+    # the code between the loops computes from them and the matmul's prologue reads (`stats`: (name, value)).
+    pre: Tuple[Tuple[str, Node, str], ...] = ()
+    stats: Tuple[Tuple[str, Node], ...] = ()
+    mphase: int = 0  # the matmul's reduction loop
 
 
 def _is(node: Any, op: str) -> bool:
     return isinstance(node, Node) and node.op == op
 
 
-_OPERAND_TYPES = ("bfloat16", "float32")  # operand types `@` takes: bf16, or f32 as three bf16 products
+_OPERAND_TYPES = ("bfloat16", "float32")  # operand types `@` takes: bf16, or f32 as six bf16 products
+# f32 operands as bf16 parts x = x1 + x2 + x3: the BK-deep slices each slice of an operand becomes, so that
+# slice by slice the products are a1 b1 + a1 b2 + a2 b1 + a1 b3 + a2 b2 + a3 b1 (every pair of parts whose
+# product is above about 2^-24 of a b)
+F32_PARTS = {"a": (1, 1, 2, 1, 2, 3), "b": (1, 2, 1, 3, 2, 1)}
 _POINTWISE = {"astype", "multiply", "add", "subtract", "divide", "negative", "maximum", "minimum", "full"}
 
 
-def _row_prologue(plan: Plan, expr: Any, x: Optional[Node] = None) -> Optional[Node]:
+def _row_prologue(plan: Plan, expr: Any, x: Optional[Node] = None, stats: frozenset = frozenset()) -> Optional[Node]:
     """The one 2-D load a pointwise bf16 or f32 expression is a function of, besides loads of k-wise row
-    vectors ((1, n) tiles) and constants; None if it is anything else. With `x`, that load must be `x`."""
+    vectors ((1, n) tiles), row statistics (carried values named in `stats`) and constants; None if it is
+    anything else. With `x`, that load must be `x`."""
     if not isinstance(expr, Node):
         return None
     loads = []
     for n in nodes_between(expr):
         if n.op == "load":
             loads.append(n)
+        elif n.op == "carried" and n.kwargs["name"] in stats:
+            continue
         elif n.op not in _POINTWISE:
             return None
     main = [n for n in loads if len(n.shape) == 2 and n.shape[0] != 1]
@@ -94,14 +108,15 @@ def _row_prologue(plan: Plan, expr: Any, x: Optional[Node] = None) -> Optional[N
     return main[0]
 
 
-def _dot_of_loads(plan: Plan, node: Node) -> Optional[Tuple[Operand, Operand, bool, Optional[Node], Optional[Node]]]:
+def _dot_of_loads(plan: Plan, node: Node, stats: frozenset = frozenset()
+                  ) -> Optional[Tuple[Operand, Operand, bool, Optional[Node], Optional[Node]]]:
     """(a's operand, b's operand, `a @ b.T`, a's expression if it isn't a plain load, a's load)."""
     if not (_is(node, "dot") or _is(node, "dot_nt")) or node.dtype.name != "float32":
         return None
     a, b = node.args[0], node.args[1]
     a_expr = None
     if not _is(a, "load"):
-        x = _row_prologue(plan, a)
+        x = _row_prologue(plan, a, stats=stats)
         if x is None or a.dtype.name not in _OPERAND_TYPES or a.shape != x.shape:
             return None
         a_expr, a = a, x
@@ -150,10 +165,10 @@ def _row_sum_name(n: Node) -> str:
     return f"_sum{n.id}"
 
 
-def _side_sum(plan: Plan, name: str, x: Node) -> Optional[Tuple[str, Node, float]]:
+def _side_sum(plan: Plan, name: str, x: Node, mp: int = 0) -> Optional[Tuple[str, Node, float]]:
     """A carried value whose update is `c + jnp.sum(h, axis=1, keepdims=True)`, h a row-prologue function of
     the left operand's load, from a constant: (name, h, initial value)."""
-    body, seg0 = plan.scopes["body0"], plan.scopes["seg0"]
+    body, seg0 = plan.scopes[f"body{mp}"], plan.scopes["seg0" if mp == 0 else f"end{mp - 1}"]
     new, init = body.values.get(name), seg0.values.get(name)
     leaf = body.carried_in.get(name)
     if not (isinstance(new, jaxlite.Sym) and _is(new.node, "add")) or leaf is None:
@@ -172,10 +187,72 @@ def _side_sum(plan: Plan, name: str, x: Node) -> Optional[Tuple[str, Node, float
     return None
 
 
+def _first_pass(plan: Plan) -> Optional[Tuple[List[Tuple[str, Node, str]], Dict[str, Node], str]]:
+    """A first reduction loop of row sums, before the matmul's: (its sums, the row statistics computed from
+    them between the loops and carried into the matmul's loop, the array they read); None if it is anything
+    else. Each sum is `c + h` (a tile summed elementwise, read afterwards only through jnp.sum(c, axis=1,
+    keepdims=True)) or `c + jnp.sum(h, axis=1, keepdims=True)`, from zero, h a row-prologue function of one
+    load."""
+    body, seg0, end, body1 = (plan.scopes[k] for k in ("body0", "seg0", "end0", "body1"))
+    pre: List[Tuple[str, Node, str]] = []
+    arrays = set()
+    for name, leaf in body.carried_in.items():
+        new = body.values.get(name)
+        if not (isinstance(new, jaxlite.Sym) and _is(new.node, "add")):
+            return None
+        u, v = new.node.args
+        h = v if u is leaf else u if v is leaf else None
+        kind = "tile"
+        if _is(h, "reduce_sum"):
+            if not (h.kwargs.get("axis") in (1, -1) and h.kwargs.get("keepdims")):
+                return None
+            h, kind = h.args[0], "row"
+        x = _row_prologue(plan, h)
+        init = seg0.values.get(name)
+        zero = (isinstance(init, jaxlite.Sym) and _is(init.node, "full") and float(init.node.kwargs["value"]) == 0.0) \
+            or (isinstance(init, (int, float)) and float(init) == 0.0)
+        if x is None or not zero or (kind == "tile" and h.shape != new.node.shape):
+            return None
+        arrays.add(plan.operand(x.kwargs["operand"]).tile.array)
+        pre.append((name, h, kind))
+    if len(arrays) != 1:
+        return None
+    kinds = {name: kind for name, _, kind in pre}
+    stats: Dict[str, Node] = {}
+    for name, leaf in body1.carried_in.items():
+        got = end.values.get(name)
+        if name in kinds or not isinstance(got, jaxlite.Sym) or body1.values.get(name) is None:
+            continue
+        if not (isinstance(body1.values[name], jaxlite.Sym) and body1.values[name].node is leaf):
+            continue  # updated in the matmul's loop: not a statistic
+        stack, ok = [got.node], True
+        while stack and ok:
+            n = stack.pop()
+            if n.op == "carried":
+                ok = kinds.get(n.kwargs["name"]) == "row"
+            elif n.op == "reduce_sum" and _is(n.args[0], "carried") and kinds.get(n.args[0].kwargs["name"]) == "tile":
+                ok = n.kwargs.get("axis") in (1, -1) and bool(n.kwargs.get("keepdims"))
+            elif n.op in _UNIFORM_OPS:
+                stack.extend(n.inputs())
+            else:
+                ok = False
+        if ok:
+            stats[name] = got.node
+    return pre, stats, next(iter(arrays))
+
+
 def match(plan: Plan) -> Optional[GemmMatch]:
     """The matmul this loop nest is, or None."""
-    if len(plan.outputs) != 1 or len(plan.phases) > 1:
+    if len(plan.outputs) != 1 or len(plan.phases) > 2:
         return None
+    mp = len(plan.phases) - 1 if plan.phases else 0
+    pre: List[Tuple[str, Node, str]] = []
+    stats: Dict[str, Node] = {}
+    if mp == 1:
+        first = _first_pass(plan)
+        if first is None:
+            return None
+        pre, stats, pre_array = first
     out = plan.outputs[0]
     if len(out.tile.shape) != 2:
         return None
@@ -184,24 +261,26 @@ def match(plan: Plan) -> Optional[GemmMatch]:
     root = value.node if isinstance(value, jaxlite.Sym) else None
     side: List[Tuple[str, Node, float]] = []
     if plan.phases:
-        body, seg0 = plan.scopes["body0"], plan.scopes["seg0"]
+        body, seg0 = plan.scopes[f"body{mp}"], plan.scopes["seg0" if mp == 0 else f"end{mp - 1}"]
         found = None
-        for acc in plan.carried:  # the carried value a matmul accumulates into
+        for acc in body.carried_in:  # the carried value a matmul accumulates into
             new = body.values.get(acc)
             if not (isinstance(new, jaxlite.Sym) and _is(new.node, "add")):
                 continue
             x, y = new.node.args
             leaf = body.carried_in.get(acc)
             dot = y if x is leaf else x if y is leaf else None
-            found = _dot_of_loads(plan, dot) if isinstance(dot, Node) else None
+            found = _dot_of_loads(plan, dot, frozenset(stats)) if isinstance(dot, Node) else None
             if found is not None:
                 break
         if found is None:
             return None
+        if pre and plan.operand(found[4].kwargs["operand"]).tile.array != pre_array:
+            return None
         init = seg0.values.get(acc)
         for name in plan.carried:  # every other carried value: a row sum of the left operand's prologue
-            if name != acc:
-                got = _side_sum(plan, name, found[4])
+            if name != acc and name not in stats and not any(name == p_[0] for p_ in pre):
+                got = _side_sum(plan, name, found[4], mp)
                 if got is None:
                     return None
                 side.append(got)
@@ -214,9 +293,7 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         acc_leaf = last.carried_in.get(acc)
         if acc_leaf is None or root is None:
             return None
-        kvar = plan.phases[0].range.var
-        if plan.phases[0].range.mask is not None and plan.phases[0].range.runtime is False and False:
-            return None
+        kvar = plan.phases[mp].range.var
     else:
         if root is None:
             return None
@@ -260,7 +337,10 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         kvar, k0 = arow[1].loop, one[arow[1].loop]
     if out.dtype.name not in ("bfloat16", "float32"):
         return None
-    return GemmMatch(opa, opb, nt, kvar, tm, tn, tk, acc_leaf, init_value, out, value, a_expr, tuple(side), k0)
+    if pre and a_expr is None:
+        a_expr = found[4]  # (the row pass writes the operand: its first loop reads the same array)
+    return GemmMatch(opa, opb, nt, kvar, tm, tn, tk, acc_leaf, init_value, out, value, a_expr, tuple(side), k0,
+                     tuple(pre), tuple(stats.items()), mp)
 
 
 @dataclass(frozen=True)
@@ -318,13 +398,12 @@ class _Gemm:
         self.tables: Dict[str, np.ndarray] = {}
         self.const_value: Optional[float] = None
         self.split: Optional[Tuple[int, int, int]] = None  # (items cut, chunks per item, K slices per chunk)
-        self.prologue = m.a_expr is not None or bool(m.side)
-        # f32 operands: each goes to HBM as bf16 parts, x = hi + lo (hi = bf16(x), lo = bf16(x - hi)), and the
-        # kernel sums hi_a hi_b + hi_a lo_b + lo_a hi_b in f32, a product within about 2^-16 of x y, on the
-        # bf16 MFMAs (the f32 ones run at a sixteenth of their rate). The parts array has three BK-deep
-        # slices for each of the operand's: (hi, hi, lo) for the left operand, (hi, lo, hi) for the right.
+        self.prologue = m.a_expr is not None or bool(m.side) or bool(m.pre)
+        # f32 operands: each goes to HBM as three bf16 parts (ak_split3), and the kernel sums the six products
+        # of F32_PARTS in f32 on the bf16 MFMAs, within a few 2^-24 of x y; the f32 MFMAs would run at a
+        # sixteenth of the bf16 rate. The parts array has six BK-deep slices for each of the operand's.
         self.x3 = _is_f32(m)
-        self.kx = 3 if self.x3 else 1
+        self.kx = len(F32_PARTS["a"]) if self.x3 else 1
         if self.prologue:
             self._check_prologue()
         if self.x3:
@@ -339,15 +418,18 @@ class _Gemm:
         if len(shape) != 2 or len(wins) != 2 or len(m.a.tile.windows) != 2:
             raise KernelError("a matmul's row prologue is lowered for a 2-D left operand only")
         rows, cols = wins
-        if sch.runtime or (plan.phases and plan.phases[0].range.mask is not None):
+        if sch.runtime or any(ph.range.mask is not None for ph in plan.phases):
             raise KernelError("a matmul's row prologue is lowered for unmasked reduction loops only")
         if rows.offset != 0 or cols.offset != 0 or shape[1] % 8:
             raise KernelError("a matmul's row prologue needs windows from the array's start and rows of a "
                               "multiple of 8 elements")
         if plan.phases:
-            r = plan.phases[0].range
+            r = plan.phases[m.mphase].range
             if not (r.start == 0 and r.step == m.tk and r.count * m.tk == shape[1]):
                 raise KernelError("a matmul's row prologue needs a reduction loop over the whole row")
+            first = plan.phases[0].range
+            if m.pre and not (first.start == 0 and first.count * first.step == shape[1]):
+                raise KernelError("a matmul's first reduction loop must walk the whole row")
         elif m.tk != shape[1]:
             raise KernelError("a matmul's row prologue needs a reduction loop over the whole row")
         self.rows_n, self.cols_n = shape
@@ -359,12 +441,12 @@ class _Gemm:
 
     def _shape(self, role: str) -> Tuple[int, ...]:
         """The array the kernel reads for an operand: its own, or with f32 operands its bf16 parts, whose
-        reduction dim is three times as long."""
+        reduction dim is kx times as long."""
         shape = tuple(self.plan.inputs[(self.m.a if role == "a" else self.m.b).param].shape)
         if not self.x3:
             return shape
         kd = self._kdim(role)
-        return shape[:kd] + (3 * shape[kd],) + shape[kd + 1:]
+        return shape[:kd] + (self.kx * shape[kd],) + shape[kd + 1:]
 
     def _check_parts(self) -> None:
         """f32 operands: every reduction block the kernel reads starts on a BK-slice boundary of the array, so
@@ -385,13 +467,14 @@ class _Gemm:
 
     def _parts_source(self, role: str) -> str:
         """The pass that writes an f32 (or bf16) operand's bf16 parts: each thread takes 8 consecutive
-        elements, splits each into hi = bf16(x) and lo = bf16(x - hi) (0 for a bf16 operand, or where hi isn't
-        finite), and stores the three parts its slice's copies hold."""
+        elements, splits each into three bf16 parts (the second and third 0 for a bf16 operand) and stores the
+        parts its slice's copies hold (F32_PARTS)."""
         op = self.m.a if role == "a" else self.m.b
         spec = self.plan.inputs[op.param]
         shape, kd, bk = tuple(spec.shape), self._kdim(role), self.hw.bk
         K, inner, numel = shape[kd], int(np.prod(shape[kd + 1:])), int(np.prod(shape))
-        parts = ("hi", "hi", "lo") if role == "a" else ("hi", "lo", "hi")
+        parts = tuple(f"p{i}" for i in F32_PARTS[role])
+        kx = self.kx
         if spec.dtype.name == "float32":
             load = (f"const ak_f32x4 u0 = *(const ak_f32x4*)(args.{op.tile.array} + flat), "
                     f"u1 = *(const ak_f32x4*)(args.{op.tile.array} + flat + 4);\n"
@@ -401,7 +484,7 @@ class _Gemm:
                     "  float v[8];\n"
                     "#pragma unroll\n"
                     "  for (int e = 0; e < 8; ++e) v[e] = ak_bf16_to_f32((ak_u16)(u[e >> 1] >> (16 * (e & 1))));")
-        stores = "\n".join(f"  *(ak_u32x4*)(args.x3_{role} + o + {c * bk * inner}LL) = {p};" for c, p in enumerate(parts))
+        stores = "\n".join(f"  *(ak_u32x4*)(args.x3_{role} + o + {c * bk * inner}LL) = {p_};" for c, p_ in enumerate(parts))
         return f"""
 // The bf16 parts of `{op.tile.array}` ({"x".join(map(str, shape))}, {spec.dtype.name}) for the f32 matmul: for each {bk}-deep
 // slice of dim {kd}, the slices ({", ".join(parts)}).
@@ -410,16 +493,17 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
   if (e8 >= {numel // 8}) return;
   const long long flat = e8 * 8, kk = flat / {inner};
   const int k = (int)(kk % {K});
-  const long long o = ((kk / {K}) * {3 * K} + 3 * (k / {bk}) * {bk} + k % {bk}) * {inner} + flat % {inner};
+  const long long o = ((kk / {K}) * {kx * K} + {kx} * (k / {bk}) * {bk} + k % {bk}) * {inner} + flat % {inner};
   {load}
-  unsigned h2[4], l2[4];
+  unsigned q1[4], q2[4], q3[4];
 #pragma unroll
   for (int e = 0; e < 8; e += 2) {{
-    const float h0 = ak_round_bf16(v[e]), h1 = ak_round_bf16(v[e + 1]);
-    h2[e >> 1] = ak_pack_bf16x2(h0, h1);
-    l2[e >> 1] = ak_pack_bf16x2(__builtin_isfinite(h0) ? v[e] - h0 : 0.f, __builtin_isfinite(h1) ? v[e + 1] - h1 : 0.f);
+    float a1, a2, a3, b1, b2, b3;
+    ak_split3(v[e], a1, a2, a3);
+    ak_split3(v[e + 1], b1, b2, b3);
+    q1[e >> 1] = ak_pack_bf16x2(a1, b1); q2[e >> 1] = ak_pack_bf16x2(a2, b2); q3[e >> 1] = ak_pack_bf16x2(a3, b3);
   }}
-  const ak_u32x4 hi = {{h2[0], h2[1], h2[2], h2[3]}}, lo = {{l2[0], l2[1], l2[2], l2[3]}};
+  const ak_u32x4 p1 = {{q1[0], q1[1], q1[2], q1[3]}}, p2 = {{q2[0], q2[1], q2[2], q2[3]}}, p3 = {{q3[0], q3[1], q3[2], q3[3]}};
 {stores}
 }}
 """
@@ -437,7 +521,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             codes = sch.tables[STEP_CODE]
             steps_of = [int(offsets[t + 1] - offsets[t]) - int(np.sum((codes[offsets[t]:offsets[t + 1]] & 4) != 0))
                         for t in range(sch.pattern_tiles)]
-        per_tile = sch.steps_per_tile if not sch.step_tables else None
+        per_tile = (plan.phases[m.mphase].range.count if plan.phases else 1) if not sch.step_tables else None
         out_cols = [w for w in m.out.tile.windows if w.size is not None][1]
         col_loop = out_cols.loop
         consts: set = set()
@@ -643,11 +727,20 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
     def _rows_source(self) -> str:
         """The row prologue's pass: one wave per row of the left operand, eight columns a lane at a time. It
         writes the operand the matmul reads (the prologue's bf16 value per element) and each row sum, a
-        lane's partial sums added across the wave."""
+        lane's partial sums added across the wave. With a first reduction loop, the wave first sums that
+        loop's row sums over the whole row and computes the row statistics the operand reads."""
         plan, m = self.plan, self.m
         zero = Index(plan, lambda v: "0")
+        pre_k = {name: k for k, (name, _, _) in enumerate(m.pre)}
+        stat_k = {name: k for k, (name, _) in enumerate(m.stats)}
 
         def leaves(n: Node, idx: Tuple[str, ...]) -> Optional[str]:
+            if n.op == "carried" and n.kwargs["name"] in stat_k:
+                return f"st_{stat_k[n.kwargs['name']]}"
+            if n.op == "carried" and n.kwargs["name"] in pre_k:  # a (rows, 1) sum
+                return f"ps_{pre_k[n.kwargs['name']]}"
+            if n.op == "reduce_sum" and _is(n.args[0], "carried") and n.args[0].kwargs["name"] in pre_k:
+                return f"ps_{pre_k[n.args[0].kwargs['name']]}"  # a tile summed elementwise, then along its rows
             if n.op == "load":
                 op = plan.operand(n.kwargs["operand"])
                 shape = plan.inputs[op.param].shape
@@ -670,36 +763,47 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
                           for k, (_, h, _) in enumerate(m.side))
         outs = "\n".join(f"  rs_{k} = ak_wave_sum(rs_{k}); if (lane == 0) args.rn_{name}[r] = rs_{k};"
                           for k, (name, _, _) in enumerate(m.side))
-        if self.x3:  # the operand's bf16 parts: slices (hi, hi, lo) for each of its BK-deep slices
-            bk = self.hw.bk
+        first = ""
+        if m.pre:
+            first = ("  // the first reduction loop's sums over the whole row, then the row statistics\n"
+                     + "".join(f"  float ps_{k} = 0.f;\n" for k in range(len(m.pre)))
+                     + f"  for (int c0 = lane * 8; c0 < {self.cols_n}; c0 += 512) {{\n#pragma unroll\n"
+                     + "    for (int e = 0; e < 8; ++e) {\n      const int c = c0 + e;\n"
+                     + "".join(f"      ps_{k} += (float)({em.at(h, ('r', 'c'))});\n" for k, (_, h, _) in enumerate(m.pre))
+                     + "    }\n  }\n"
+                     + "".join(f"  ps_{k} = ak_wave_sum(ps_{k});\n" for k in range(len(m.pre)))
+                     + "".join(f"  const float st_{k} = (float)({em.at(v, ('r', '0'))});\n"
+                               for k, (_, v) in enumerate(m.stats)))
+        if self.x3:  # the operand's bf16 parts: for each of its BK-deep slices, the slices F32_PARTS names
+            bk, kx = self.hw.bk, self.kx
             value = (f"const float v0 = {em.at(a_node, ('r', 'c'))}, v1 = {em.at(a_node, ('r', 'c + 1'))};\n"
-                     "      const float h0 = ak_round_bf16(v0), h1 = ak_round_bf16(v1);\n"
-                     "      pk[e >> 1] = ak_pack_bf16x2(h0, h1);\n"
-                     "      pl[e >> 1] = ak_pack_bf16x2(__builtin_isfinite(h0) ? v0 - h0 : 0.f, "
-                     "__builtin_isfinite(h1) ? v1 - h1 : 0.f);")
-            store = (f"ak_u16* dst = args.rn_a + (long long)r * {3 * D} + 3 * (c0 / {bk}) * {bk} + c0 % {bk};\n"
-                     "    *(ak_u32x4*)dst = ak_u32x4{pk[0], pk[1], pk[2], pk[3]};\n"
-                     f"    *(ak_u32x4*)(dst + {bk}) = ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}};\n"
-                     f"    *(ak_u32x4*)(dst + {2 * bk}) = ak_u32x4{{pl[0], pl[1], pl[2], pl[3]}};")
+                     "      float a1, a2, a3, b1, b2, b3;\n"
+                     "      ak_split3(v0, a1, a2, a3);\n"
+                     "      ak_split3(v1, b1, b2, b3);\n"
+                     "      q1[e >> 1] = ak_pack_bf16x2(a1, b1); q2[e >> 1] = ak_pack_bf16x2(a2, b2); "
+                     "q3[e >> 1] = ak_pack_bf16x2(a3, b3);")
+            store = (f"ak_u16* dst = args.rn_a + (long long)r * {kx * D} + {kx} * (c0 / {bk}) * {bk} + c0 % {bk};\n"
+                     + "\n".join(f"    *(ak_u32x4*)(dst + {c * bk}) = ak_u32x4{{q{i}[0], q{i}[1], q{i}[2], q{i}[3]}};"
+                                  for c, i in enumerate(F32_PARTS["a"])))
         else:
-            value = (f"pk[e >> 1] = ak_pack_bf16x2((float)({em.at(a_node, ('r', 'c'))}), "
+            value = (f"q1[e >> 1] = ak_pack_bf16x2((float)({em.at(a_node, ('r', 'c'))}), "
                      f"(float)({em.at(a_node, ('r', 'c + 1'))}));")
-            store = f"*(ak_u32x4*)(args.rn_a + (long long)r * {D} + c0) = ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}};"
+            store = f"*(ak_u32x4*)(args.rn_a + (long long)r * {D} + c0) = ak_u32x4{{q1[0], q1[1], q1[2], q1[3]}};"
         return f"""
 // The row prologue of `{plan.nest.name}`: rows {self.rows_n} x {D}, one wave per row.
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {self.name}_args args) {{
   const int r = blockIdx.x * {THREADS // 64} + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (r >= {self.rows_n}) return;
- {sums}
+{first} {sums}
   for (int c0 = lane * 8; c0 < {D}; c0 += 512) {{
-    unsigned pk[4], pl[4];
+    unsigned q1[4], q2[4], q3[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {{
       const int c = c0 + e;
       {value}
 {adds}
     }}
-    (void)pl;
+    (void)q2; (void)q3;
     {store}
   }}
 {outs}
@@ -751,7 +855,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
             return f"(((({k}) & 3) << 2) & {nc - 1})"
 
         # How a tile's steps are found: `nsteps` and the reduction loop's value at step `st_`.
-        phase = plan.phases[0].range if plan.phases else None
+        phase = plan.phases[m.mphase].range if plan.phases else None
         if phase is None:
             steps_setup = ["const int nsteps = 1;"]
             kval = str(m.k0)
@@ -768,8 +872,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
             ]
             kval = (f"({phase.start} + (({codes}[sbeg + st_] >> {CODE_SHIFT}) / {sch.iterations} / "
                     f"{sch.phase_radix}) * {phase.step})")
-        if self.x3:  # the parts arrays hold three slices for each of the operand's
-            kval = f"(3 * {kval})"
+        if self.x3:  # the parts arrays hold kx slices for each of the operand's
+            kval = f"({self.kx} * {kval})"
 
         # The epilogue, per accumulator element.
         def leaf(n: Node) -> Optional[str]:

@@ -4,7 +4,7 @@
 generated kernel for the workload of BASELINE.json's metric: the dense 8192^3 bf16 matmul `x @ y`
 (examples/matmul.py of the reference, f32 accumulate, bf16 out), inputs ~N(0,1) from seeds 0 and 1,
 already resident in HBM. `value` is its TFLOP/s (2*M*N*K / time) at MatmulTiles(512, 512, 512). The same line
-carries the other BASELINE configurations in `legs`, each timed the same way:
+carries the other BASELINE.json configurations in `legs`, each timed the same way:
 - dense at MatmulTiles(1024, 2048, 1024);
 - causal `tril(x @ y)` at the same size, with its time over the dense time;
 - RMSNorm fused with the same matmul (`rmsnorm_matmul`, the reference's examples/rmsnorm_matmul.py);

@@ -2,7 +2,7 @@
 
     out[b, t, h] = softmax(q[b, t, h] @ K[b, kv(h), :n].T) @ V[b, kv(h), :n],   n = lengths[b]
 
-The spec of BASELINE config 5, the reference's `paged_gqa_decode` (examples/decode.py:199-223, with the
+The spec of BASELINE.json config 5, the reference's `paged_gqa_decode` (examples/decode.py:199-223, with the
 helpers at :92-172) in this package's JAX stand-in: the cache is vLLM's paged layout (kv_cache.py), pages
 (num_pages, page_size, Hkv * Dh) with sequence b's i-th page at `block_tables[b, i]`; the reduction loop
 walks a sequence's pages under the runtime mask `p * P >= lengths[b]`, reading the page through a runtime

@@ -1,6 +1,6 @@
 """Grouped matmul with runtime expert windows: each group of G rows of `xs` through its expert's weights.
 
-The spec of BASELINE config 4, in the form the reference's grouped kernels take
+The spec of BASELINE.json config 4, in the form the reference's grouped kernels take
 (examples/moe.py:167-187 `expert_ffn`: the runtime mask `tile_expert[i // G] < 0` and the runtime window
 `w[tile_expert[i // G], ...]`; the single-matrix grouped form of tests/test_index_arrays.py:109-125):
 tokens arrive sorted by expert in groups of G rows, `group_expert[g]` names group g's expert (or -1 for an

@@ -1,7 +1,7 @@
 """Parity of GQA decode over a contiguous cache (the reference's `gqa_decode`, examples/decode.py:175-196)
 with the CPU oracle on the same seeded inputs, with the paged kernel on the same cache cut into pages
 (bit for bit, as the reference's tests/test_decode.py:202-212 asserts), of its device step tables with the
-reference's table semantics, and at a BASELINE-sized cache with a float32 GPU reference on sampled
+reference's table semantics, and at a cache the size of BASELINE.json config 5 with a float32 GPU reference on sampled
 sequences.
 
 Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want| (the paged tests'
@@ -77,7 +77,7 @@ def test_contiguous_decode_step_tables():
 
 
 def test_contiguous_decode_large_cache_sampled():
-    """64 sequences over an 8192-position cache (1 GiB per K and V, BASELINE config 5's shape without the
+    """64 sequences over an 8192-position cache (1 GiB per K and V, BASELINE.json config 5's shape without the
     page table), lengths uniform in [128, 8192], block_kv 512; sampled sequences against float32 on the GPU."""
     B, H, Hkv, D, S = 64, 32, 8, 128, 8192
     g = torch.Generator().manual_seed(0)

@@ -1,4 +1,4 @@
-"""Parity of the grouped matmul with runtime expert windows (BASELINE config 4's spec, examples/moe.py)
+"""Parity of the grouped matmul with runtime expert windows (BASELINE.json config 4's spec, examples/moe.py)
 with the CPU oracle, and of the device step-table builder with the reference's table semantics restated in
 oracle/schedule.py: bit-exact tables, counts and codes.
 
@@ -84,7 +84,7 @@ def test_device_step_tables_are_bit_exact():
 
 
 def test_baseline_config_against_torch():
-    """BASELINE config 4: 16384 tokens x 4096 -> 14336, 8 experts, groups of 256 with seeded multinomial
+    """BASELINE.json config 4: 16384 tokens x 4096 -> 14336, 8 experts, groups of 256 with seeded multinomial
     counts, sorted by expert; checked per group against a float32 product on the GPU."""
     g = torch.Generator().manual_seed(0)
     counts = torch.multinomial(torch.full((8,), 1 / 8), 64, replacement=True, generator=g).bincount(minlength=8)

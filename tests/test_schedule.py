@@ -101,7 +101,7 @@ def test_causal_matmul_counts():
     sch = schedule_of(causal_matmul, spec(512, 256, dtype=bf), spec(256, 512, dtype=bf),
                       tunable=MatmulTiles(tm=128, tn=128, tk=128))
     assert (sch.tiles, sch.total_tiles, sch.steps) == (10, 16, 20)
-    # The BASELINE config: 8192^3 at 512^3 tiles runs 136 of 256 tiles, 2176 steps, 120 fills.
+    # The BASELINE.json config: 8192^3 at 512^3 tiles runs 136 of 256 tiles, 2176 steps, 120 fills.
     sch = schedule_of(causal_matmul, spec(8192, 8192, dtype=bf), spec(8192, 8192, dtype=bf),
                       tunable=MatmulTiles(512, 512, 512))
     assert (sch.tiles, sch.total_tiles, sch.steps, sch.fills) == (136, 256, 2176, 120)
@@ -118,7 +118,7 @@ def test_causal_attention_skips_future_blocks():
         inner, lambda v: False, [("j", 0, 128, 4, lambda v: v["j"] > v["i"] + 128 - 1)])
     np.testing.assert_array_equal(sch.tables[STEP_TILE], step_tile)
     np.testing.assert_array_equal(sch.tables[STEP_CODE], step_code)
-    # The BASELINE shape at 512^2 blocks: a 10-step pattern repeated over the 64 (b, h) pairs.
+    # BASELINE.json config 3 at 512^2 blocks: a 10-step pattern repeated over the 64 (b, h) pairs.
     sch = schedule_of(causal_attention, *[spec(4, 16, 2048, 128, dtype=bf)] * 3, tunable=AttentionBlocks(512, 512))
     assert (sch.steps, sch.repeats, len(sch.tables[STEP_TILE])) == (640, 64, 10)
 

@@ -1,5 +1,5 @@
 """Parity of the generated gfx950 flash-attention kernels with the CPU oracle (oracle/kernels.py, the spec's
-loop nest with f32 accumulation) on the same seeded inputs, and at the BASELINE shape with a float32 torch
+loop nest with f32 accumulation) on the same seeded inputs, and at BASELINE.json config 3's shapes with a float32 torch
 reference on the GPU (the attention kernel is floating point).
 
 Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the output's largest magnitude (about

@@ -1,6 +1,6 @@
-"""Parity of paged GQA decode (BASELINE config 5's spec, examples/decode.py) with the CPU oracle on the
+"""Parity of paged GQA decode (BASELINE.json config 5's spec, examples/decode.py) with the CPU oracle on the
 same seeded inputs, of its device step tables with the reference's table semantics (bit-exact), and at
-the BASELINE size with a float32 GPU reference on sampled sequences.
+the size of BASELINE.json config 5 with a float32 GPU reference on sampled sequences.
 
 Tolerance: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want|; the kernel merges
 per-workgroup partial softmaxes (the online softmax's own rescaling rule) where the spec runs one pass, so
@@ -93,7 +93,7 @@ def test_decode_step_tables_ragged_words():
 
 
 def test_baseline_config_sampled():
-    """BASELINE config 5: 64 sequences, 32 q heads / 8 kv heads, head dim 128, 16-token pages, a seeded
+    """BASELINE.json config 5: 64 sequences, 32 q heads / 8 kv heads, head dim 128, 16-token pages, a seeded
     random page table over 32768 pages, lengths uniform in [128, 8192]; sequences checked against a float32
     GPU computation of the same softmax."""
     B, H, Hkv, D, P, pages = 64, 32, 8, 128, 16, 512
@@ -117,7 +117,7 @@ def test_baseline_config_sampled():
 
 
 def test_decode_step_tables_bit_exact_at_baseline_size():
-    """The builder at BASELINE config 5's size (64 sequences x 512 pages: 512 mask words, written by 16
+    """The builder at BASELINE.json config 5's size (64 sequences x 512 pages: 512 mask words, written by 16
     workgroups, each repeating the masks and the scan and writing its own words) against the reference's
     table semantics."""
     B, pages = 64, 512

@@ -90,3 +90,14 @@ def test_two_reduction_loops_lower_to_a_row_pass_and_the_matmul():
     lowered = k.lower(((256, 384), F32), ((384, 256), F32))
     assert _symbols(lowered)[:3] == ["tj_two_pass_rows", "tj_two_pass_parts_b", "tj_two_pass"]
     assert "ps_0 = ak_wave_sum(ps_0)" in lowered.source and "st_0" in lowered.source
+
+
+def test_a_first_loop_over_another_array_is_not_lowered():
+    from tests.helpers import make_kernel
+    from tests.test_gpu_rmsnorm_matmul import TWO_PASS
+
+    other = TWO_PASS.replace("def two_pass(x, w):", "def two_pass(x, z, w):").replace(
+        "xk = x[i : i + 128, k : k + 128]", "xk = z[i : i + 128, k : k + 128]")
+    k = make_kernel(other)
+    with pytest.raises(KernelError, match="no lowering"):
+        k.lower(((256, 384), F32), ((256, 384), F32), ((384, 256), F32))

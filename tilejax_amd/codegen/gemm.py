@@ -430,6 +430,15 @@ class _Gemm:
             first = plan.phases[0].range
             if m.pre and not (first.start == 0 and first.count * first.step == shape[1]):
                 raise KernelError("a matmul's first reduction loop must walk the whole row")
+            for _, h, _ in m.pre:  # the first loop reads the operand's rows where the matmul does
+                for n in nodes_between(h):
+                    if n.op != "load" or len(n.shape) != 2 or n.shape[0] == 1:
+                        continue
+                    w0 = [w for w in plan.operand(n.kwargs["operand"]).tile.windows if w.size is not None]
+                    if len(w0) != 2 or (w0[0].loop, w0[0].offset) != (rows.loop, rows.offset) or w0[1].offset != 0 \
+                            or w0[1].loop != first.var:
+                        raise KernelError("a matmul's first reduction loop must read the rows the matmul reads, "
+                                          "block by block along the row")
         elif m.tk != shape[1]:
             raise KernelError("a matmul's row prologue needs a reduction loop over the whole row")
         self.rows_n, self.cols_n = shape

@@ -101,3 +101,29 @@ def test_a_first_loop_over_another_array_is_not_lowered():
     k = make_kernel(other)
     with pytest.raises(KernelError, match="no lowering"):
         k.lower(((256, 384), F32), ((256, 384), F32), ((384, 256), F32))
+
+
+def test_the_f32_part_pairs_give_products_to_f32_accuracy():
+    """The slices F32_PARTS lays out, multiplied pairwise as the kernel's MFMAs do, give each product of
+    f32 operands to within a few 2^-24 (three bf16 parts each, split as ak_split3 does: each part the bf16
+    rounding of what the earlier parts leave). A table that dropped a pair or doubled one would be off by
+    2^-16 or more."""
+    import torch
+
+    from tilejax_amd.codegen.gemm import F32_PARTS
+
+    def split3(x):
+        p1 = x.bfloat16().float()
+        p2 = (x - p1).bfloat16().float()
+        p3 = (x - p1 - p2).bfloat16().float()
+        return {1: p1, 2: p2, 3: p3}
+
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(100000, generator=g) * torch.exp(torch.randn(100000, generator=g) * 4)
+    b = torch.randn(100000, generator=g) * torch.exp(torch.randn(100000, generator=g) * 4)
+    pa, pb = split3(a), split3(b)
+    assert len(F32_PARTS["a"]) == len(F32_PARTS["b"]) == 6
+    got = sum(pa[i].double() * pb[j].double() for i, j in zip(F32_PARTS["a"], F32_PARTS["b"]))
+    exact = a.double() * b.double()
+    rel = ((got - exact).abs() / exact.abs()).max().item()
+    assert rel < 8 * 2.0**-24, rel

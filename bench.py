@@ -113,14 +113,15 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     # Each leg starts after host work (lowering, input set-up) that leaves the GPU idle, and the clock then
-    # takes some tens of milliseconds of load to return to its sustained level (a leg's first calls run up
-    # to 25 % slower): 50 untimed calls cover that for every leg.
-    ap.add_argument("--warmup", type=int, default=50)
+    # takes some tens of milliseconds of load to return to its sustained level: 200 untimed calls cover
+    # that for every leg. (The first leg of a process has still measured up to 10 % slower than the same
+    # kernel later in the process, with 200 or 1000 warm-up calls alike.)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--tiles", default="512,512,512", help="dense matmul spec tiles tm,tn,tk")
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="",
-                    help="comma list of legs to run: dense,dense2,causal,rmsnorm,attention,moe,decode")
+                    help="comma list of legs to run: dense,library,dense2,causal,rmsnorm,attention,moe,decode")
     ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3; "
                     "default: profiles/traffic.json")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -166,6 +167,14 @@ def main() -> int:
     _log(f"  {ms * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_TFLOPS:.1f}% of peak)")
     out["dense"] = {"tiles": [tiles.tm, tiles.tn, tiles.tk], "us": round(ms * 1e3, 2),
                     "tflops": round(tflops, 2), "hw": lowered.program.notes}
+
+    if "library" in legs or not args.only:
+        # the vendor library on the same inputs, for comparison: torch.matmul (hipBLASLt), bf16 out
+        _log(f"torch.matmul {N_DENSE}^3 (hipBLASLt)")
+        msl, _ = time_kernel(lambda: torch.matmul(x, y), args.steps, args.warmup)
+        out["dense_library"] = {"what": "torch.matmul(x, y), hipBLASLt", "us": round(msl * 1e3, 2),
+                                "tflops": round(flop / (msl * 1e-3) / 1e12, 2)}
+        _log(f"  {msl * 1e3:.1f} us/call, {flop / (msl * 1e-3) / 1e12:.1f} TFLOP/s")
 
     if "dense2" in legs or not args.only:
         t2 = MatmulTiles(1024, 2048, 1024)

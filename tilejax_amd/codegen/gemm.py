@@ -18,7 +18,8 @@ BK-deep slices that stream through `stages` LDS stages:
   reads this one; the barrier for a slice sits one K16 step before it, so the next slice's first fragments
   load under this slice's last MFMAs (`v_mfma_f32_32x32x16_bf16`, f32 accumulators in AGPRs), and
   `sched_group_barrier` hints interleave each MFMA with an LDS read or a global load;
-- the epilogue is computed per element where the accumulator lives and stored as packed bf16.
+- the epilogue is computed per element where the accumulator lives; for bf16 outputs a lane and lane ^ 32
+  exchange halves so each stores 8 consecutive outputs (16 bytes), and a row's stores fill whole lines.
 """
 
 from __future__ import annotations
@@ -1144,15 +1145,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
       {"tr_out += " + now + " - tr_o0;" if self.trace else ""}
       continue;
     }}""")
-        w(f"""    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
-    // The lane index goes through an empty asm so the stores' addresses are computed here, not hoisted
-    // above the K loop where they would take registers the loop needs.
-    int lane_e = lane;
-    asm volatile("" : "+v"(lane_e));
-#pragma unroll
-    for (int i_ = 0; i_ < {mi}; ++i_) {{
-      const int er = sm * {bm} + wm * {wtm} + i_ * 32 + (lane_e & 31);
-#pragma unroll
+        old_loop = f"""#pragma unroll
       for (int j_ = 0; j_ < {ni}; ++j_) {{
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {{
@@ -1169,7 +1162,48 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
           {_store4(O, "obase", ldo, out_bf16)}
         }}
       }}
-    }}
+    }}"""
+        paired_loop = f"""#pragma unroll
+      for (int j_ = 0; j_ < {ni}; ++j_) {{
+#pragma unroll
+        for (int p2 = 0; p2 < 2; ++p2) {{
+          // groups 2 p2 and 2 p2 + 1, then one exchange with lane ^ 32: each lane stores 8 consecutive
+          // outputs (16 bytes), the lower half-wave columns 16 p2 .. + 7, the upper 16 p2 + 8 .. + 15
+          unsigned pk[2][2];
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {{
+            const int g4 = 2 * p2 + h2;
+            const int ec0 = sn * {bn} + wn * {wtn} + j_ * 32 + g4 * 8 + (lane_e >> 5) * 4;
+            float res[4];
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {{
+              const int ec = ec0 + e4;
+              const float acc_v = acc[i_][j_][g4 * 4 + e4];
+              (void)ec; (void)er;
+              {epi}
+              res[e4] = (float)({result});
+            }}
+            pk[h2][0] = ak_pack_bf16x2(res[0], res[1]);
+            pk[h2][1] = ak_pack_bf16x2(res[2], res[3]);
+          }}
+          const bool up = lane_e >= 32;
+          const unsigned r0 = __shfl_xor(up ? pk[0][0] : pk[1][0], 32), r1 = __shfl_xor(up ? pk[0][1] : pk[1][1], 32);
+          const ak_u32x4 v = up ? ak_u32x4{{r0, r1, pk[1][0], pk[1][1]}} : ak_u32x4{{pk[0][0], pk[0][1], r0, r1}};
+          const int ec8 = sn * {bn} + wn * {wtn} + j_ * 32 + 16 * p2 + (up ? 8 : 0);
+          *(ak_u32x4*)((ak_u16*){O} + obase + (long long)er * {ldo} + ec8) = v;
+        }}
+      }}
+    }}"""
+        EPILOGUE_LOOP = paired_loop if out_bf16 and ldo % 8 == 0 else old_loop  # (16-byte aligned rows)
+        w(f"""    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
+    // The lane index goes through an empty asm so the stores' addresses are computed here, not hoisted
+    // above the K loop where they would take registers the loop needs.
+    int lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
+#pragma unroll
+    for (int i_ = 0; i_ < {mi}; ++i_) {{
+      const int er = sm * {bm} + wm * {wtm} + i_ * 32 + (lane_e & 31);
+{EPILOGUE_LOOP}
     {"tr_out += " + now + " - tr_o0;" if self.trace else ""}
   }}
   {trace_write}

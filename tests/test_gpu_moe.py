@@ -2,7 +2,8 @@
 with the CPU oracle, and of the device step-table builder with the reference's table semantics restated in
 oracle/schedule.py: bit-exact tables, counts and codes.
 
-Tolerance for the matmul: bf16 outputs within rtol 1e-2 of |want| plus 1e-2 of the largest |want|; f32
+Tolerance for the matmul (tests/tolerance.py): bf16 outputs within 2 bf16 ulp of the expected value plus the
+f32 summation floor 2 * K * 2^-24 * (|xs| @ |w_e|) of each group's product; f32
 operands (six bf16 products of their parts) within rtol 1e-4 plus 1e-4 of float64,
 the reference's f32 tolerance for its grouped kernels (tests/test_moe.py:252-275).
 """
@@ -14,6 +15,7 @@ import torch
 from examples.moe import GroupTiles, grouped_matmul
 from oracle import kernels
 from oracle import schedule as oracle_schedule
+from tests.tolerance import check_bf16, matmul_floor
 
 pytestmark = pytest.mark.gpu
 
@@ -25,11 +27,15 @@ def _inputs(M, K, N, E, experts, seed=0):
     return xs, w, torch.tensor(experts, dtype=torch.int32)
 
 
-def _close(got, want):
-    got, want = got.float().cpu(), want.float().cpu()
-    scale = want.abs().max().item()
-    bad = (got - want).abs() > 1e-2 * want.abs() + 1e-2 * scale
-    assert not bad.any(), f"{int(bad.sum())} of {want.numel()} differ; max |diff| {(got - want).abs().max().item()}"
+def _floor(xs, w, experts):
+    """Each group's f32 summation floor through its (clamped) expert; zero for unused groups."""
+    G = xs.shape[0] // len(experts)
+    floor = torch.zeros(xs.shape[0], w.shape[2], dtype=torch.float32, device=xs.device)
+    for g, e in enumerate(experts):
+        if e >= 0:
+            rows = slice(g * G, (g + 1) * G)
+            floor[rows] = matmul_floor(xs[rows], w[min(e, w.shape[0] - 1)])
+    return floor
 
 
 @pytest.mark.parametrize("experts,tiles", [
@@ -43,7 +49,8 @@ def test_grouped_matmul_matches_oracle(experts, tiles):
     print(f"grouped matmul experts={experts} {tiles}", flush=True)
     got = grouped_matmul(xs.cuda(), w.cuda(), ge.cuda(), tiles)
     torch.cuda.synchronize()
-    _close(got, kernels.grouped_matmul(xs, w, ge, tiles.tn, tiles.tk))
+    check_bf16(f"grouped matmul experts={experts}", got.cpu(), kernels.grouped_matmul(xs, w, ge, tiles.tn, tiles.tk),
+               _floor(xs, w, experts))
     for g, e in enumerate(experts):
         if e < 0:
             assert not got[g * 256:(g + 1) * 256].float().any()
@@ -85,7 +92,7 @@ def test_device_step_tables_are_bit_exact():
 
 def test_baseline_config_against_torch():
     """16384 tokens x 4096 -> 14336, 8 experts, groups of 256 with seeded multinomial
-    counts, sorted by expert; checked per group against a float32 product on the GPU."""
+    counts, sorted by expert; every group checked against a float32 product on the GPU."""
     g = torch.Generator().manual_seed(0)
     counts = torch.multinomial(torch.full((8,), 1 / 8), 64, replacement=True, generator=g).bincount(minlength=8)
     ge = torch.repeat_interleave(torch.arange(8), counts).to(torch.int32)
@@ -93,8 +100,13 @@ def test_baseline_config_against_torch():
     w = (torch.randn(8, 4096, 14336, generator=g) * 0.02).to(torch.bfloat16).cuda()
     print("grouped matmul 16384x4096x14336, 8 experts", flush=True)
     got = grouped_matmul(xs, w, ge.cuda(), GroupTiles(512, 512))
-    for grp in range(0, 64, 9):
+    torch.backends.cuda.matmul.allow_tf32 = False
+    worst = 0.0
+    for grp in range(64):
         e = int(ge[grp])
         rows = slice(grp * 256, (grp + 1) * 256)
         want = xs[rows].float() @ w[e].float()
-        _close(got[rows], want)
+        report = check_bf16(f"MoE group {grp} (expert {e})", got[rows], want.to(torch.bfloat16),
+                            matmul_floor(xs[rows], w[e]))
+        worst = max(worst, report["bound_use"])
+    print(f"MoE config 4: largest bound use over all 64 groups {worst:.3f}", flush=True)

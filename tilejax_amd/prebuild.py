@@ -40,7 +40,8 @@ def standard() -> Iterator[Tuple[object, tuple]]:
     for n, tiles in ((8192, T(512, 512, 512)), (1024, T(512, 512, 512)), (8192, T(1024, 2048, 1024)),
                      (512, T(256, 256, 128)), (1024, T(256, 256, 256))):
         yield mm.matmul, (_bf16(n, n), _bf16(n, n), tiles)
-    for n, tiles in ((8192, T(512, 512, 512)), (1024, T(256, 256, 256)), (512, T(128, 128, 128))):
+    for n, tiles in ((8192, T(512, 512, 512)), (1024, T(256, 256, 256)), (512, T(128, 128, 128)),
+                     (8192, T(1024, 2048, 1024)), (2048, T(256, 256, 256))):
         yield cm.causal_matmul, (_bf16(n, n), _bf16(n, n), tiles)
     yield mm.matmul, (_bf16(512, 256), _bf16(256, 512), T(256, 256, 128))
     yield mm.matmul, (_bf16(256, 384), _bf16(384, 256), T(256, 128, 512))
@@ -68,7 +69,7 @@ def standard() -> Iterator[Tuple[object, tuple]]:
         yield rm.rmsnorm_matmul, (_f32(256, 512), _f32(1, 512), _f32(512, 512), tiles)
     from examples import decode
 
-    for b, pages, n_pages in ((4, 64, 256), (5, 100, 500), (64, 512, 32768)):
+    for b, pages, n_pages in ((4, 64, 256), (5, 100, 500), (64, 512, 32768), (8, 128, 1024), (4, 32, 128)):
         yield decode.paged_gqa_decode, (_bf16(b, 1, 32, 128), _bf16(n_pages, 16, 1024), _bf16(n_pages, 16, 1024),
                                         _i32(b, pages), _i32(b))
     yield decode.paged_gqa_decode, (_bf16(4, 1, 32, 128), _bf16(16, 128, 1024), _bf16(16, 128, 1024), _i32(4, 4),
@@ -84,6 +85,8 @@ def standard() -> Iterator[Tuple[object, tuple]]:
 
         A = ca.AttentionBlocks
         for shape, blocks in (((4, 16, 2048, 128), A(512, 512)), ((1, 16, 4096, 128), A(512, 512)),
+                              ((4, 16, 2048, 128), A(256, 256)), ((1, 16, 4096, 128), A(256, 256)),
+                              ((4, 16, 2048, 128), A(1024, 1024)), ((1, 16, 4096, 128), A(1024, 1024)),
                               ((2, 4, 512, 128), A(128, 128)), ((1, 2, 1024, 128), A(256, 256)),
                               ((1, 2, 512, 128), A(128, 128)), ((2, 2, 512, 128), A(256, 128)),
                               ((2, 2, 512, 128), A(128, 128)), ((2, 2, 512, 128), A(128, 256)),

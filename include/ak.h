@@ -70,6 +70,26 @@ int ak_event_elapsed_ms(void* start, void* stop, float* ms);
 int ak_event_destroy(void* event);
 int ak_stream_synchronize(void* stream);
 
+/* Bytes of the library's own scratch array on each device: the most ak_launch_scratch can lay out. */
+#define AK_SCRATCH_BYTES (64u << 20)
+/* The most argument bytes ak_launch_scratch takes (it patches a copy held on the stack). */
+#define AK_SCRATCH_MAX_ARGS 4096u
+
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): ak_launch, with the kernel's workspace
+ * buffers (partial results, step tables, staging) placed in the library's own scratch array of
+ * AK_SCRATCH_BYTES on the current device instead of buffers the caller allocated. For each i < count, the
+ * 8-byte pointer field at byte fields[i] of the argument struct is set to scratch + offsets[i], a buffer of
+ * sizes[i] bytes (offsets 256-aligned, offsets[i] + sizes[i] <= AK_SCRATCH_BYTES, else an error and nothing
+ * is launched). Inputs and outputs are still the caller's. The array is set up on a device's first call and
+ * kept until the process ends; it keeps the last call's contents (nothing is cleared: the generated kernels
+ * write every workspace byte they read). Every call on one device shares that device's array, so calls that
+ * overlap in time on one device (two streams, two threads) race. Allocates nothing: no hipMalloc, hipFree
+ * or allocating library routine. */
+int ak_launch_scratch(ak_kernel* kernel, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t by,
+                      uint32_t bz, uint32_t lds_bytes, const void* args, size_t args_size, const size_t* fields,
+                      const uint64_t* offsets, const uint64_t* sizes, size_t count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,6 +101,44 @@ class Program:
         result = outputs[0] if len(outputs) == 1 else tuple(outputs)
         return result, (trace.view(torch.int64) if trace is not None else None)
 
+    def scratch_layout(self) -> Dict[str, Tuple[int, int]]:
+        """Where each workspace buffer sits in the library's scratch array: name -> (offset, bytes), offsets
+        256-aligned in name order. KernelError if they don't fit."""
+        layout, at = {}, 0
+        for name in sorted(self.workspace):
+            n = max(self.workspace[name], 4)
+            layout[name] = (at, n)
+            at += -(-n // runtime.SCRATCH_ALIGN) * runtime.SCRATCH_ALIGN
+        if at > runtime.SCRATCH_BYTES:
+            raise KernelError(f"{self.name}: its workspace takes {at} bytes, more than the {runtime.SCRATCH_BYTES} "
+                              "bytes of the library's scratch array: call it with a workspace allocated per call")
+        return layout
+
+    def run_no_alloc(self, *arrays: torch.Tensor, outputs: Sequence[torch.Tensor],
+                     stream: Optional[int] = None) -> None:
+        """One call that allocates no device memory: the caller's outputs, and every workspace buffer placed in
+        the library's scratch array (ak_launch_scratch). The kernel's constant tables are uploaded on a
+        device's first call (once), as for ordinary calls. Calls that overlap on one GPU share its scratch
+        array and race."""
+        runtime.require_gpu()
+        self.check_inputs(arrays)
+        device = arrays[0].device
+        if len(outputs) != len(self.outputs):
+            raise KernelError(f"{self.name} has {len(self.outputs)} outputs, {len(outputs)} given")
+        for k, (t, (shape, dt)) in enumerate(zip(outputs, self.outputs)):
+            if tuple(t.shape) != shape or t.dtype != dt.torch or t.device != device or not t.is_contiguous():
+                raise KernelError(f"{self.name}: output {k} must be a contiguous {shape} {dt.name} tensor on {device}")
+        layout = self.scratch_layout()
+        tables = self.device_tables(device)
+        module = self.module(device.index or 0)
+        stream = runtime.current_stream() if stream is None else stream
+        for launch in self.launches:
+            placeholders = {name: _Null() for name in self.workspace}
+            args = pack(launch.args, arrays, outputs, tables, placeholders)
+            pointer_args = [a for a in launch.args if a.kind != "int"]
+            placed = [(8 * i, *layout[a.key]) for i, a in enumerate(pointer_args) if a.kind == "workspace"]
+            module.kernel(launch.symbol).launch_scratch(launch.grid, launch.block, launch.lds, args, stream, placed)
+
     def step_tables(self, *arrays: torch.Tensor) -> Dict[str, torch.Tensor]:
         """Run only the device step-table builder (runtime masks) and return its tables as int32 tensors:
         step_tile, step_code, count (the reference's three) and tile_steps."""
@@ -124,6 +162,14 @@ class Program:
             args = pack(launch.args, arrays, outputs, tables, workspace)
             module.kernel(launch.symbol).launch(launch.grid, launch.block, launch.lds, args, stream)
         return outputs, workspace
+
+
+class _Null:
+    """A workspace buffer not allocated here: its pointer field is packed as 0 and filled in by the library."""
+
+    @staticmethod
+    def data_ptr() -> int:
+        return 0
 
 
 def pack(args: Sequence[Arg], arrays: Sequence[torch.Tensor], outputs: Sequence[torch.Tensor],

@@ -6,6 +6,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -16,6 +17,11 @@ struct ak_module {
 struct ak_kernel {
   hipFunction_t function;
 };
+
+// The workspace of ak_launch_scratch: one array per device (each GPU holds its own copy once the library's
+// code object is loaded there). Host code never uses its name as an address: the per-device pointer comes
+// from hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) unsigned char scratch[AK_SCRATCH_BYTES];
 
 namespace {
 
@@ -30,6 +36,27 @@ int hip_fail(const char* what, hipError_t e) {
   return fail(std::string(what) + ": " + hipGetErrorName(e) + ": " + hipGetErrorString(e));
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[kMaxDevices] = {};
+
+int scratch_pointer(void** out) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return hip_fail("hipGetDevice", e);
+  if (device < 0 || device >= kMaxDevices) return fail("ak_launch_scratch: device index out of range");
+  std::lock_guard<std::mutex> hold(scratch_mutex);
+  if (!scratch_ptr[device]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail("hipGetSymbolAddress(scratch)", e);
+    if (!p) return fail("hipGetSymbolAddress(scratch) gave a null address");
+    scratch_ptr[device] = p;
+  }
+  *out = scratch_ptr[device];
+  return 0;
+}
+
 std::vector<const char*> split_options(const char* opts) {
   std::vector<const char*> out;
   if (!opts) return out;
@@ -41,7 +68,7 @@ std::vector<const char*> split_options(const char* opts) {
 
 extern "C" {
 
-int ak_version(void) { return (1 << 16) | 0; }
+int ak_version(void) { return (1 << 16) | 1; }
 
 const char* ak_last_error(void) { return last_error.c_str(); }
 
@@ -141,6 +168,45 @@ int ak_launch(ak_kernel* kernel, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t
   if (gx == 0 || gy == 0 || gz == 0 || bx == 0 || by == 0 || bz == 0) return fail("ak_launch: empty grid or block");
   size_t size = args_size;
   void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(args), HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+                    HIP_LAUNCH_PARAM_END};
+  hipError_t e = hipModuleLaunchKernel(kernel->function, gx, gy, gz, bx, by, bz, lds_bytes,
+                                       static_cast<hipStream_t>(stream), nullptr, args_size ? config : nullptr);
+  if (e != hipSuccess) return hip_fail("hipModuleLaunchKernel", e);
+  return 0;
+}
+
+int ak_launch_scratch(ak_kernel* kernel, uint32_t gx, uint32_t gy, uint32_t gz, uint32_t bx, uint32_t by,
+                      uint32_t bz, uint32_t lds_bytes, const void* args, size_t args_size, const size_t* fields,
+                      const uint64_t* offsets, const uint64_t* sizes, size_t count, void* stream) {
+  last_error.clear();
+  if (!kernel) return fail("ak_launch_scratch: null kernel");
+  if (gx == 0 || gy == 0 || gz == 0 || bx == 0 || by == 0 || bz == 0)
+    return fail("ak_launch_scratch: empty grid or block");
+  if (args_size > AK_SCRATCH_MAX_ARGS) return fail("ak_launch_scratch: argument struct larger than 4096 bytes");
+  if (args_size && !args) return fail("ak_launch_scratch: null arguments");
+  if (count && (!fields || !offsets || !sizes)) return fail("ak_launch_scratch: null workspace description");
+  for (size_t i = 0; i < count; ++i) {
+    if (fields[i] % 8 || fields[i] + 8 > args_size)
+      return fail("ak_launch_scratch: workspace field " + std::to_string(i) + " is not a pointer field of the arguments");
+    if (offsets[i] % 256) return fail("ak_launch_scratch: workspace offset " + std::to_string(offsets[i]) +
+                                      " is not 256-byte aligned");
+    if (offsets[i] > AK_SCRATCH_BYTES || sizes[i] > AK_SCRATCH_BYTES - offsets[i])
+      return fail("ak_launch_scratch: workspace of " + std::to_string(sizes[i]) + " bytes at offset " +
+                  std::to_string(offsets[i]) + " exceeds the scratch array of " + std::to_string(AK_SCRATCH_BYTES) +
+                  " bytes");
+  }
+  unsigned char patched[AK_SCRATCH_MAX_ARGS];
+  if (args_size) std::memcpy(patched, args, args_size);
+  if (count) {
+    void* base = nullptr;
+    if (scratch_pointer(&base)) return 1;
+    for (size_t i = 0; i < count; ++i) {
+      void* p = static_cast<unsigned char*>(base) + offsets[i];
+      std::memcpy(patched + fields[i], &p, sizeof p);
+    }
+  }
+  size_t size = args_size;
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, patched, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
                     HIP_LAUNCH_PARAM_END};
   hipError_t e = hipModuleLaunchKernel(kernel->function, gx, gy, gz, bx, by, bz, lds_bytes,
                                        static_cast<hipStream_t>(stream), nullptr, args_size ? config : nullptr);

@@ -51,12 +51,15 @@ class Library:
         L.ak_get_kernel.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(vp)]
         L.ak_kernel_info.argtypes = [vp] + [ctypes.POINTER(i32)] * 4
         L.ak_launch.argtypes = [vp, u32, u32, u32, u32, u32, u32, u32, vp, sz, vp]
+        L.ak_launch_scratch.argtypes = [vp, u32, u32, u32, u32, u32, u32, u32, vp, sz, ctypes.POINTER(sz),
+                                         ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64), sz, vp]
         L.ak_event_create.argtypes = [ctypes.POINTER(vp)]
         L.ak_event_record.argtypes = [vp, vp]
         L.ak_event_elapsed_ms.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_float)]
         L.ak_event_destroy.argtypes = [vp]
         L.ak_stream_synchronize.argtypes = [vp]
         for name in ("ak_compile", "ak_module_load", "ak_module_free", "ak_get_kernel", "ak_kernel_info", "ak_launch",
+                     "ak_launch_scratch",
                      "ak_event_create", "ak_event_record", "ak_event_elapsed_ms", "ak_event_destroy",
                      "ak_stream_synchronize"):
             getattr(L, name).restype = i32
@@ -131,6 +134,29 @@ class Kernel:
         lib.check(lib.lib.ak_launch(self.handle, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds,
                                     ctypes.cast(buf, ctypes.c_void_p), len(args), ctypes.c_void_p(stream)),
                   f"launching {self.symbol}")
+
+
+    def launch_scratch(self, grid: Tuple[int, int, int], block: Tuple[int, int, int], lds: int, args: bytes,
+                       stream: int, placed: Sequence[Tuple[int, int, int]]) -> None:
+        """Launch with the workspace pointer fields of `args` placed in the library's scratch array:
+        `placed` lists (byte offset of the field in args, offset in the scratch array, bytes). Allocates
+        nothing on the device (include/ak.h, ak_launch_scratch)."""
+        lib = library()
+        buf = ctypes.create_string_buffer(args, len(args))
+        n = len(placed)
+        fields = (ctypes.c_size_t * max(n, 1))(*(p[0] for p in placed))
+        offsets = (ctypes.c_uint64 * max(n, 1))(*(p[1] for p in placed))
+        sizes = (ctypes.c_uint64 * max(n, 1))(*(p[2] for p in placed))
+        lib.check(lib.lib.ak_launch_scratch(self.handle, grid[0], grid[1], grid[2], block[0], block[1], block[2],
+                                            lds, ctypes.cast(buf, ctypes.c_void_p), len(args), fields, offsets,
+                                            sizes, n, ctypes.c_void_p(stream)),
+                  f"launching {self.symbol} on the library's scratch")
+
+
+# The library's scratch array per device (include/ak.h AK_SCRATCH_BYTES), and the alignment of each
+# workspace buffer placed in it.
+SCRATCH_BYTES = 64 << 20
+SCRATCH_ALIGN = 256
 
 
 class Module:

@@ -69,6 +69,33 @@ def time_kernel(run, steps: int, warmup: int):
     return events[0].elapsed_ms(events[-1]) / steps, per
 
 
+def check_dense(got, x, y) -> dict:
+    """The timed kernel's output against a float32 product on the GPU: every element within 2 bf16 ulp of
+    it plus twice the f32 summation bound K * 2^-24 * (|x| @ |y|). Raises if not; returns the largest error
+    in ulps and the largest share of the bound used."""
+    import torch
+
+    allow = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    worst_ulp, worst_use = 0.0, 0.0
+    try:
+        for r in range(0, x.shape[0], 2048):
+            xs = x[r:r + 2048]
+            want = (xs.float() @ y.float()).to(torch.bfloat16).float()
+            floor = 2.0 * x.shape[1] * 2.0 ** -24 * (xs.float().abs() @ y.float().abs())
+            ulp = torch.exp2(torch.floor(torch.log2(want.abs().clamp(min=2.0 ** -126))) - 7)
+            err = (got[r:r + 2048].float() - want).abs()
+            use = float((err / (2 * ulp + floor)).max())
+            if not use <= 1.0:
+                raise AssertionError(f"dense {x.shape[0]}^3: rows {r}.. differ from a float32 product beyond 2 bf16 ulp "
+                                     f"plus the f32 summation floor (bound use {use:.3g})")
+            worst_use = max(worst_use, use)
+            worst_ulp = max(worst_ulp, float((err / ulp)[want.abs() >= want.abs().mean()].max()))
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = allow
+    return {"ulp_max_typical": round(worst_ulp, 3), "bound_use": round(worst_use, 4)}
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The oracle (oracle/kernels.matmul: the loop nest over 512^3 tiles, f32 accumulation) on a band of
     512 rows of the 8192^3 workload (x[:512] @ y, 1/16 of the FLOPs), repeated until `budget_s`."""
@@ -161,12 +188,14 @@ def main() -> int:
     _log(f"dense matmul {N_DENSE}^3 tiles {tiles}: lowering")
     lowered = matmul.lower(x, y, tiles)
     _log(f"  hardware: {lowered.program.notes}")
+    check = check_dense(lowered.run(x, y), x, y)
+    _log(f"  checked against a float32 product: {check}")
     ms, per = time_kernel(lambda: lowered.run(x, y), args.steps, args.warmup)
     tflops = flop / (ms * 1e-3) / 1e12
     launch_ms = statistics.mean(per)
     _log(f"  {ms * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_TFLOPS:.1f}% of peak)")
     out["dense"] = {"tiles": [tiles.tm, tiles.tn, tiles.tk], "us": round(ms * 1e3, 2),
-                    "tflops": round(tflops, 2), "hw": lowered.program.notes}
+                    "tflops": round(tflops, 2), "hw": lowered.program.notes, "check": check}
 
     if "library" in legs or not args.only:
         # the vendor library on the same inputs, for comparison: torch.matmul (hipBLASLt), bf16 out

@@ -404,10 +404,10 @@ class Array:
         return abs(self)
 
     def __matmul__(self, o: Any) -> "Array":
-        return matmul(self, o)
+        return _at_operator(self, o)
 
     def __rmatmul__(self, o: Any) -> "Array":
-        return matmul(o, self)
+        return _at_operator(o, self)
 
     def __and__(self, o: Any) -> "Array":
         return bitwise_and(self, o)
@@ -932,6 +932,52 @@ def dot_general(x: Any, y: Any, dimension_numbers: Any, preferred_element_type: 
     if rc == (1,):
         return matmul_nt(xx, y, preferred_element_type=preferred_element_type)
     return matmul(xx, y, preferred_element_type=preferred_element_type)
+
+
+# --------------------------------------------------------------------------------------------- `@` on matrix units
+
+_MATRIX_UNITS: List[int] = [0]
+
+
+@contextlib.contextmanager
+def matrix_units() -> Iterator[None]:
+    """Inside the block, the `@` operator means what a kernel's matrix units compute (the reference's
+    src/autokernel/mxu.py:21-43): operands of different types are promoted to a common one, the product
+    accumulates in f32 (i32 for integers) and stays f32 (f32 operands at full precision), and `a @ b.T` of
+    two matrices contracts both last dims. Outside it `@` is plain JAX: `bf16 @ bf16` rounds to bf16. Only
+    the operator changes: `jnp.matmul` and `jnp.dot` keep their meaning either way. `kernel.reference` and
+    the planner's trace run the loop nest inside this block; `kernel.fn` runs outside it."""
+    _MATRIX_UNITS[0] += 1
+    try:
+        yield
+    finally:
+        _MATRIX_UNITS[0] -= 1
+
+
+def _transposed_matrix(v: Any) -> Optional["Sym"]:
+    """For a traced `m.T` of a matrix m, m itself (so the product reads it transposed in place)."""
+    if not (isinstance(v, Sym) and v.node.op == "transpose" and v.ndim == 2):
+        return None
+    axes = v.node.args[1] if len(v.node.args) > 1 else v.node.kwargs.get("axes")
+    src = v.node.args[0]
+    if axes not in (None, (1, 0), [1, 0]) or not isinstance(src, Node) or len(src.shape) != 2:
+        return None
+    return Sym(torch.empty(src.shape, dtype=src.dtype.torch, device="meta"), src)
+
+
+def _at_operator(a: Any, b: Any) -> Array:
+    if not _MATRIX_UNITS[0]:
+        return matmul(a, b)
+    ta, tb = asarray(a) if not isinstance(a, Array) else a, asarray(b) if not isinstance(b, Array) else b
+    if ta.dtype != tb.dtype:
+        common = promote_types(ta.dtype, tb.dtype)
+        ta, tb = ta.astype(common), tb.astype(common)
+    acc = int32 if ta.dtype.kind in "iu" else float32
+    if ta.ndim == 2:
+        source = _transposed_matrix(tb)
+        if source is not None:
+            return matmul_nt(ta, source, preferred_element_type=acc)
+    return matmul(ta, tb, preferred_element_type=acc)
 
 
 # --------------------------------------------------------------------------------------------- activations

@@ -22,11 +22,13 @@ import itertools
 from dataclasses import dataclass, field
 from typing import Any, Callable, Dict, List, Mapping, Optional, Sequence, Set, Tuple
 
-from . import jaxlite, mxu
+import numpy as np
+
+from . import jaxlite
 from .errors import KernelError
 from .jaxlite import DType, Node, Sym
 from .parse import Loop, Nest
-from .tilecode import as_store, assigned, element_reads, first_reads, flatten, reads, subscript_dims
+from .syntax import bound, element_reads, in_order, index_dims, store_of, used, used_before_bound
 
 __all__ = ["Carried", "Index", "Kind", "Operand", "Output", "Phase", "Plan", "Range", "Scope", "Spec", "Tile",
            "Window", "make_plan"]
@@ -222,328 +224,396 @@ def make_plan(nest: Nest, fn: Callable, inputs: Sequence[Spec], tunable: Any = N
     return _Planner(nest, fn, tuple(inputs), tunable).plan()
 
 
+class _Env:
+    """Where plan-time code runs: the function's globals and closure, the tunable, and the inputs as meta
+    arrays (shapes and dtypes, no data). Every failure becomes a KernelError naming the line."""
+
+    def __init__(self, nest: Nest, fn: Callable, inputs: Tuple[Spec, ...], tunable: Any) -> None:
+        self.nest = nest
+        scope: Dict[str, Any] = {"__builtins__": builtins}
+        scope.update(fn.__globals__)
+        scope.update(inspect.getclosurevars(fn).nonlocals)
+        with jaxlite.default_device("meta"):
+            scope.update({name: jaxlite.zeros(s.shape, s.dtype) for name, s in zip(nest.params, inputs)})
+        if nest.tunable:
+            scope[nest.tunable] = tunable
+        self.scope = scope
+
+    def eval(self, node: ast.expr, values: Optional[Mapping[str, Any]] = None) -> Any:
+        return evaluate(self.nest, self.scope, node, values)
+
+    def run(self, stmt: ast.stmt) -> None:
+        try:
+            with jaxlite.default_device("meta"):
+                exec(compile(ast.Module([stmt], []), self.nest.filename, "exec"), self.scope)
+        except KernelError:
+            raise
+        except Exception as e:
+            raise self.nest.error(f"the prologue runs on the inputs' shapes and dtypes, and failed: {e!r}", stmt) from e
+
+    def integer(self, node: ast.expr, text: str) -> int:
+        value = self.eval(node)
+        if not isinstance(value, int):
+            raise self.nest.error(f"{text}: tile bounds are ints when planning, not {value!r}", node)
+        return int(value)
+
+
+def _allocation(env: _Env, name: str, call: ast.expr) -> Tuple[Tuple[int, ...], DType, Any]:
+    """An output's (shape, dtype, fill) from its allocation, `jnp.zeros(shape, dtype)` or `jnp.full(...)`."""
+    nest = env.nest
+    usage = f"allocate output `{name}` with jnp.zeros(shape, dtype) or jnp.full(shape, value, dtype)"
+    if isinstance(call, ast.Name) and call.id in nest.params:
+        raise nest.error(f"outputs updated in place (`{name} = {call.id}`) are not lowered by the gfx950 backend yet", call)
+    maker = env.eval(call.func) if isinstance(call, ast.Call) else None
+    if maker is not jaxlite.zeros and maker is not jaxlite.full:
+        raise nest.error(usage, call)
+    args = [env.eval(a) for a in call.args]  # type: ignore[attr-defined]
+    kwargs = {k.arg: env.eval(k.value) for k in call.keywords if k.arg}  # type: ignore[attr-defined]
+    try:
+        with jaxlite.default_device("meta"):
+            made = maker(*args, **kwargs)
+    except Exception as e:
+        raise nest.error(f"{usage}: {e!r}", call) from e
+    if maker is jaxlite.zeros:
+        fill: Any = 0
+    else:
+        fill = args[1] if len(args) > 1 else kwargs.get("fill_value")
+    if not isinstance(fill, (int, float, bool)):
+        raise nest.error(f"output `{name}` is filled with a scalar constant, not {type(fill).__name__}", call)
+    return tuple(made.shape), made.dtype, fill
+
+
+def _loop_range(env: _Env, loop: Loop, parallel: bool, indices: Mapping[str, Any]) -> Range:
+    """A loop's iterations, evaluated when planning: a nonempty `range` of whole steps from a multiple of its
+    step; `runtime` when its mask reads index-array elements."""
+    nest = env.nest
+    computed = bound(nest.tile)
+    if loop.mask is not None and element_reads(loop.mask, computed):
+        raise nest.error("a mask can't read values the tile code computes (it is evaluated before the kernel runs)",
+                         loop.mask)
+    if any(element_reads(b, indices) for b in loop.bounds):
+        raise nest.error("loops with runtime bounds (a cursor) are not lowered by the gfx950 backend yet", loop.node)
+    values = [env.eval(b) for b in loop.bounds]
+    if any(not isinstance(v, int) for v in values):
+        raise nest.error(f"loop bounds are ints when planning, got {values}", loop.node)
+    start, stop, step = (0, values[0], 1) if len(values) == 1 else (*values, 1)[:3]
+    if step <= 0:
+        raise nest.error(f"`{loop.var}` steps by {step}: loops count up", loop.node)
+    span = range(start, stop, step)
+    problems = [
+        (len(span) == 0, f"`{loop.var}` loops over {span}, which is empty"),
+        ((stop - start) % step != 0, f"`{loop.var}` loops over {span}: the range must be a whole number of steps of {step}"),
+        (start % step != 0, f"`{loop.var}` loops over {span}: it must start at a multiple of its step"),
+    ]
+    for bad, message in problems:
+        if bad:
+            raise nest.error(message, loop.node)
+    runtime = loop.mask is not None and bool(element_reads(loop.mask, indices))
+    if runtime and parallel:
+        raise nest.error("a tile mask can't read index arrays: mask the reduction loop's steps instead", loop.mask)
+    return Range(loop.var, start, step, len(span), loop.mask, runtime)
+
+
+class _Windows:
+    """Reads the index expressions of tile reads and stores into Windows. A dim's index is one of:
+    `v : v + n` (a loop variable v, n an int: moves with v), `v` (an integer index moving with v), constants
+    (`a : b`, `:`, an int), or an element of an index array (`w[ids[e], ...]`: chosen when the kernel runs).
+    Every window is checked to stay inside its dim for every value its loop takes."""
+
+    def __init__(self, env: _Env, ranges: Mapping[str, Range], indices: Mapping[str, Any]) -> None:
+        self.env, self.ranges, self.indices = env, ranges, indices
+
+    def _fail(self, text: str, node: ast.AST) -> KernelError:
+        return self.env.nest.error(
+            f"{text}: each index is `v:v + size` or `v` for a loop variable v, `:`, constants (`start:stop`, an int), "
+            "or an element of an index array (`w[ids[e], :]`)", node)
+
+    def _loop_name(self, node: Optional[ast.expr]) -> Optional[str]:
+        return node.id if isinstance(node, ast.Name) and node.id in self.ranges else None
+
+    def window(self, index: ast.expr, dim: int, text: str) -> Window:
+        movers = used(index) & set(self.ranges)
+        if isinstance(index, ast.Subscript) and isinstance(index.value, ast.Name) and index.value.id in self.indices:
+            if any(isinstance(d, ast.Slice) for d in index_dims(index)):
+                raise self.env.nest.error(f"{text}: windows gathered through index-array slices are not lowered yet",
+                                          index)
+            return Window(None, 0, None, index, frozenset(movers))
+        if isinstance(index, ast.Slice):
+            return self._slice(index, dim, text, movers)
+        var = self._loop_name(index)
+        if var is not None:
+            return self._inside(Window(var, 0, None), dim, text, index)
+        if movers:
+            raise self._fail(text, index)
+        return self._inside(Window(None, self.env.integer(index, text), None), dim, text, index)
+
+    def _slice(self, index: ast.Slice, dim: int, text: str, movers: Set[str]) -> Window:
+        if index.step is not None:
+            raise self._fail(text, index)
+        lo, hi = index.lower, index.upper
+        var = self._loop_name(lo)
+        if var is not None:
+            ok = (isinstance(hi, ast.BinOp) and isinstance(hi.op, ast.Add) and self._loop_name(hi.left) == var
+                  and not used(hi.right) & set(self.ranges))
+            if not ok:
+                raise self._fail(text, index)
+            return self._inside(Window(var, 0, self.env.integer(hi.right, text)), dim, text, index)  # type: ignore[union-attr]
+        if movers:
+            raise self._fail(text, index)
+        first = self.env.integer(lo, text) if lo is not None else 0
+        stop = self.env.integer(hi, text) if hi is not None else dim
+        return self._inside(Window(None, first, stop - first), dim, text, index)
+
+    def _inside(self, w: Window, dim: int, text: str, node: ast.AST) -> Window:
+        if w.size is not None and w.size <= 0:
+            raise self.env.nest.error(f"{text}: a slice takes at least one element", node)
+        width = w.size if w.size is not None else 1
+        lowest, highest = w.offset, w.offset + width
+        if w.loop:
+            r = self.ranges[w.loop]
+            lowest, highest = lowest + r.value(0), highest + r.value(r.count - 1)
+        if lowest < 0 or highest > dim:
+            raise self.env.nest.error(f"{text}: reads elements {lowest} to {highest - 1} of a dim of {dim}", node)
+        return w
+
+    def tile(self, array: str, shape: Tuple[int, ...], dt: DType, index: Sequence[ast.expr], node: ast.AST) -> Tile:
+        text = f"{array}[{', '.join(ast.unparse(i) for i in index)}]"
+        if len(index) != len(shape):
+            raise self.env.nest.error(f"{text}: index every one of {array}'s {len(shape)} dims", node)
+        windows = tuple(self.window(i, d, text) for i, d in zip(index, shape))
+        kept = [w.size is not None for w in windows]
+        if True not in kept:
+            raise self.env.nest.error(f"{text}: a tile keeps at least one dim (slice it, `v:v + 1`)", node)
+        if False in kept[kept.index(True):]:
+            raise self.env.nest.error(f"{text}: integer indices go before every sliced dim", node)
+        return Tile(array, windows, dt, text)
+
+
 class _Planner:
     def __init__(self, nest: Nest, fn: Callable, inputs: Tuple[Spec, ...], tunable: Any) -> None:
-        self.nest, self.fn, self.inputs = nest, fn, inputs
-        closure = inspect.getclosurevars(fn).nonlocals
-        self.env: Dict[str, Any] = {"__builtins__": builtins, **fn.__globals__, **closure}
-        with jaxlite.default_device("meta"):
-            for name, spec in zip(nest.params, inputs):
-                self.env[name] = jaxlite.zeros(spec.shape, spec.dtype)
-        if nest.tunable:
-            self.env[nest.tunable] = tunable
-        self.tunable = tunable
+        self.nest, self.fn, self.inputs, self.tunable = nest, fn, inputs, tunable
+        self.envs = _Env(nest, fn, inputs, tunable)
+        self.env = self.envs.scope
         self.ranges: Dict[str, Range] = {}
+        self.indices: Dict[str, Index] = {}
 
     def error(self, message: str, node: Optional[ast.AST] = None) -> KernelError:
         return self.nest.error(message, node)
 
     def eval(self, node: ast.expr, values: Optional[Mapping[str, Any]] = None) -> Any:
-        return evaluate(self.nest, self.env, node, values)
+        return self.envs.eval(node, values)
 
     def plan(self) -> Plan:
-        outputs = self._prologue()
-        indices = self._index_arrays()
-        self.indices = {ix.name: ix for ix in indices}
-        parallel = tuple(self._range(loop) for loop in self.nest.parallel)
-        reductions = tuple(self._range(loop) for loop in self.nest.reductions)
-        self.ranges = {r.var: r for r in (*parallel, *reductions)}
+        nest = self.nest
+        if nest.repeats:
+            raise self.error("repeat loops (a loop around reduction loops) are not lowered by the gfx950 backend yet",
+                             nest.repeats[0].loop.node)
+        allocated = self._run_prologue()
+        self.indices = {ix.name: ix for ix in self._index_arrays()}
+        parallel = tuple(_loop_range(self.envs, loop, True, self.indices) for loop in nest.parallel)
+        reductions = tuple(_loop_range(self.envs, loop, False, self.indices) for loop in nest.reductions)
+        self.ranges = {r.var: r for r in parallel + reductions}
         self._check_element_bounds()
-        phases, segments, bound = self._phases(reductions)
-        operands, by_node = self._operands(phases, segments)
+        windows = _Windows(self.envs, self.ranges, self.indices)
+        self.windows = windows
+        phases, segments, bound_vars = self._phases(reductions)
+        operands, by_node = self._operands(phases, windows)
         self.operands = operands
-        output_tiles = {name: self._output_tile(name, *outputs[name][:2], parallel) for name in self.nest.outputs}
-        for name in self.nest.outputs:
-            if self.nest.stored_in[name] is not None:
-                raise self.error("outputs stored per step are not lowered by the gfx950 backend yet",
-                                 self.nest.stores[name].node)
+        out_tiles = {name: self._output_tile(name, *allocated[name][:2], parallel, windows) for name in nest.outputs}
+        per_step = [name for name in nest.outputs if nest.stored_in[name] is not None]
+        if per_step:
+            raise self.error("outputs stored per step are not lowered by the gfx950 backend yet",
+                             nest.stores[per_step[0]].node)
         self._check_reads_before_assignment()
-        scopes, carried = self._trace(phases, segments, bound, by_node)
-        outs = []
-        for name in self.nest.outputs:
-            shape, dt, fill = outputs[name]
-            value = scopes["last"].stores[name]
-            vshape, vdt = (tuple(value.shape), value.dtype) if isinstance(value, jaxlite.Array) else ((), dt)
-            self._check_store(output_tiles[name], vshape)
-            outs.append(Output(name, shape, dt, fill, output_tiles[name], (vshape, vdt)))
-        return Plan(
-            nest=self.nest, inputs=self.inputs, tunable=self.tunable, parallel=parallel, reductions=reductions,
-            phases=phases, segments=segments, operands=operands, indices=indices, outputs=tuple(outs),
-            carried=carried, scopes=scopes, env=self.env, constants=self._constants(),
-        )
+        scopes, carried = self._trace(phases, segments, bound_vars, by_node)
+        outputs = tuple(self._output(name, allocated[name], out_tiles[name], scopes["last"].stores[name])
+                        for name in nest.outputs)
+        return Plan(nest=nest, inputs=self.inputs, tunable=self.tunable, parallel=parallel, reductions=reductions,
+                    phases=phases, segments=segments, operands=operands, indices=tuple(self.indices.values()),
+                    outputs=outputs, carried=carried, scopes=scopes, env=self.env, constants=self._constants())
 
     # ------------------------------------------------------------------ prologue and outputs
 
-    def _prologue(self) -> Dict[str, Tuple[Tuple[int, ...], DType, Any]]:
-        allocation_of = {id(stmt): name for name, stmt in self.nest.allocations.items()}
-        outputs = {}
-        with jaxlite.default_device("meta"):
-            for stmt in self.nest.prologue:
-                name = allocation_of.get(id(stmt))
-                if name is not None:
-                    outputs[name] = self._allocation(name, stmt.value)  # type: ignore[attr-defined]
-                    self.env[name] = jaxlite.zeros(*outputs[name][:2])
-                    continue
-                try:
-                    exec(compile(ast.Module([stmt], []), self.nest.filename, "exec"), self.env)
-                except KernelError:
-                    raise
-                except Exception as e:
-                    raise self.error(f"the prologue runs on the inputs' shapes and dtypes, and failed: {e!r}", stmt) from e
-        return outputs
+    def _run_prologue(self) -> Dict[str, Tuple[Tuple[int, ...], DType, Any]]:
+        """Run the prologue on meta arrays; each output's (shape, dtype, fill) from its allocation."""
+        which = {id(stmt): name for name, stmt in self.nest.allocations.items()}
+        found: Dict[str, Tuple[Tuple[int, ...], DType, Any]] = {}
+        for stmt in self.nest.prologue:
+            name = which.get(id(stmt))
+            if name is None:
+                self.envs.run(stmt)
+                continue
+            found[name] = _allocation(self.envs, name, stmt.value)  # type: ignore[attr-defined]
+            with jaxlite.default_device("meta"):
+                self.env[name] = jaxlite.zeros(found[name][0], found[name][1])
+        return found
 
-    def _allocation(self, name: str, call: ast.expr) -> Tuple[Tuple[int, ...], DType, Any]:
-        usage = f"allocate output `{name}` with jnp.zeros(shape, dtype) or jnp.full(shape, value, dtype)"
-        if isinstance(call, ast.Name) and call.id in self.nest.params:
-            raise self.error(f"outputs updated in place (`{name} = {call.id}`) are not lowered by the gfx950 backend yet", call)
-        if not isinstance(call, ast.Call):
-            raise self.error(usage, call)
-        func = self.eval(call.func)
-        if func is not jaxlite.zeros and func is not jaxlite.full:
-            raise self.error(usage, call)
-        args = [self.eval(a) for a in call.args]
-        kwargs = {k.arg: self.eval(k.value) for k in call.keywords if k.arg}
+    def _output(self, name: str, allocated: Tuple[Tuple[int, ...], DType, Any], tile: Tile, value: Any) -> Output:
+        shape, dt, fill = allocated
+        if isinstance(value, jaxlite.Array):
+            vshape, vdt = tuple(value.shape), value.dtype
+        else:
+            vshape, vdt = (), dt
         try:
-            value = func(*args, **kwargs)
-        except Exception as e:
-            raise self.error(f"{usage}: {e!r}", call) from e
-        fill = 0 if func is jaxlite.zeros else (args[1] if len(args) > 1 else kwargs.get("fill_value"))
-        if not isinstance(fill, (int, float, bool)):
-            raise self.error(f"output `{name}` is filled with a scalar constant, not {type(fill).__name__}", call)
-        return tuple(value.shape), value.dtype, fill
+            fits = np.broadcast_shapes(vshape, tile.shape) == tile.shape
+        except ValueError:
+            fits = False
+        if not fits:
+            raise self.error(f"{tile.text}: can't store a value of shape {vshape} in a {tile.shape} tile",
+                             self.nest.stores[name].node)
+        return Output(name, shape, dt, fill, tile, (vshape, vdt))
 
     # ------------------------------------------------------------------ loops
 
-    def _range(self, loop: Loop) -> Range:
-        if loop.mask is not None and element_reads(loop.mask, assigned(self.nest.tile)):
-            raise self.error("a mask can't read values the tile code computes (it is evaluated before the kernel runs)",
-                             loop.mask)
-        if any(element_reads(b, self.indices) for b in loop.bounds):
-            raise self.error("loops with runtime bounds (a cursor) are not lowered by the gfx950 backend yet", loop.node)
-        bounds = [self.eval(b) for b in loop.bounds]
-        if not all(isinstance(b, int) for b in bounds):
-            raise self.error(f"loop bounds are ints when planning, got {bounds}", loop.node)
-        if len(bounds) == 3 and bounds[2] <= 0:
-            raise self.error(f"`{loop.var}` steps by {bounds[2]}: loops count up", loop.node)
-        r = range(*bounds)
-        if not r:
-            raise self.error(f"`{loop.var}` loops over {r}, which is empty", loop.node)
-        if (r.stop - r.start) % r.step:
-            raise self.error(f"`{loop.var}` loops over {r}: the range must be a whole number of steps of {r.step}", loop.node)
-        if r.start % r.step:
-            raise self.error(f"`{loop.var}` loops over {r}: it must start at a multiple of its step", loop.node)
-        runtime = loop.mask is not None and bool(element_reads(loop.mask, self.indices))
-        if runtime and loop in self.nest.parallel:
-            raise self.error("a tile mask can't read index arrays: mask the reduction loop's steps instead", loop.mask)
-        return Range(loop.var, r.start, r.step, len(r), loop.mask, runtime)
-
     def _phases(self, reductions: Tuple[Range, ...]):
-        """The reduction loops that take steps and the code around them; a loop of one iteration and no mask
-        joins the code around it, its variable bound to its value (`bound`)."""
+        """The reduction loops that take steps, and the code at a tile's first step and after each of them. A
+        loop of one iteration with no mask takes no step: its body joins the code around it, with its
+        variable bound to its one value (returned as `bound`)."""
         nest = self.nest
         phases: List[Phase] = []
-        segments: List[List[ast.stmt]] = [list(nest.segments[0])]
-        bound: Dict[str, int] = {}
+        code: List[List[ast.stmt]] = [list(nest.segments[0])]
+        bound_vars: Dict[str, int] = {}
         for r, body, after in zip(reductions, nest.bodies, nest.segments[1:]):
             if r.count == 1 and r.mask is None:
-                bound[r.var] = r.start
-                segments[-1] += list(body) + list(after)
-                continue
-            phases.append(Phase(r, tuple(body)))
-            segments.append(list(after))
-        return tuple(phases), tuple(tuple(s) for s in segments), bound
+                bound_vars[r.var] = r.start
+                code[-1] += [*body, *after]
+            else:
+                phases.append(Phase(r, tuple(body)))
+                code.append(list(after))
+        return tuple(phases), tuple(tuple(c) for c in code), bound_vars
 
     # ------------------------------------------------------------------ index arrays
 
     def _index_arrays(self) -> Tuple[Index, ...]:
-        nest, params = self.nest, set(self.nest.params)
-        trees: List[ast.AST] = [*nest.tile, *(loop.mask for loop in nest.reductions if loop.mask is not None)]
-        trees += [bound for loop in nest.loops for bound in loop.bounds]
-        elements = [n for tree in trees for n in element_reads(tree, params)]
+        """The inputs read element by element (in tile code, reduction masks or loop bounds): int32 arrays the
+        kernel reads when it runs, each indexed in every dim and never also read as tiles."""
+        nest = self.nest
+        places: List[ast.AST] = list(nest.tile)
+        places += [loop.mask for loop in nest.reductions if loop.mask is not None]
+        places += [b for loop in nest.loops for b in loop.bounds]
         found = []
         for p, name in enumerate(nest.params):
-            mine = [n for n in elements if n.value.id == name]  # type: ignore[attr-defined]
-            if not mine:
+            elements = [n for place in places for n in element_reads(place, {name})]
+            if not elements:
                 continue
-            ids = {id(n) for n in mine}
-            tiles = [n for tree in trees for n in ast.walk(tree)
-                     if isinstance(n, ast.Subscript) and isinstance(n.value, ast.Name) and n.value.id == name
-                     and id(n) not in ids]
-            if tiles:
-                raise self.error(
-                    f"`{name}` is read element by element (an index array) and as tiles: read it one way or the other",
-                    tiles[0],
-                )
+            element_ids = {id(n) for n in elements}
+            as_tiles = next((n for place in places for n in ast.walk(place)
+                             if isinstance(n, ast.Subscript) and isinstance(n.value, ast.Name)
+                             and n.value.id == name and id(n) not in element_ids), None)
+            if as_tiles is not None:
+                raise self.error(f"`{name}` is read element by element (an index array) and as tiles: read it one way "
+                                 "or the other", as_tiles)
             spec = self.inputs[p]
             if spec.dtype != jaxlite.int32:
                 raise self.error(f"`{name}` is read element by element, an index array: it must be int32, not "
-                                 f"{spec.dtype.name}", mine[0])
-            for node in mine:
-                if len(subscript_dims(node)) != len(spec.shape):
-                    raise self.error(f"{ast.unparse(node)}: index every one of {name}'s {len(spec.shape)} dims", node)
+                                 f"{spec.dtype.name}", elements[0])
+            short = next((n for n in elements if len(index_dims(n)) != len(spec.shape)), None)
+            if short is not None:
+                raise self.error(f"{ast.unparse(short)}: index every one of {name}'s {len(spec.shape)} dims", short)
             found.append(Index(name, p, tuple(spec.shape), spec.dtype))
         return tuple(found)
 
     def _check_element_bounds(self) -> None:
-        """Index array elements are read at indices inside the arrays, for every loop value."""
-        trees: List[ast.AST] = [*self.nest.tile, *(l.mask for l in self.nest.reductions if l.mask is not None)]
-        for tree in trees:
-            for node in element_reads(tree, self.indices):
-                ix = self.indices[node.value.id]  # type: ignore[attr-defined]
-                for expr, dim in zip(subscript_dims(node), ix.shape):
-                    loops = [self.ranges[v] for v in sorted(reads(expr) & self.ranges.keys())]
-                    for values in itertools.product(*(range(r.count) for r in loops)):
-                        at = {r.var: r.value(b) for r, b in zip(loops, values)}
-                        value = self.eval(expr, at)
-                        if not 0 <= value < dim:
-                            raise self.error(f"{ast.unparse(node)}: reads element {value} of a dim of {dim}", node)
+        """Every index-array element the tile code or a reduction mask reads is inside its array, for every value
+        of the loops its index expressions read."""
+        nest = self.nest
+        places: List[ast.AST] = [*nest.tile, *(loop.mask for loop in nest.reductions if loop.mask is not None)]
+        for place in places:
+            for node in element_reads(place, self.indices):
+                shape = self.indices[node.value.id].shape  # type: ignore[attr-defined]
+                for expr, dim in zip(index_dims(node), shape):
+                    loops = [self.ranges[v] for v in sorted(used(expr) & set(self.ranges))]
+                    for blocks in itertools.product(*(range(r.count) for r in loops)):
+                        at = self.eval(expr, {r.var: r.value(b) for r, b in zip(loops, blocks)})
+                        if not 0 <= at < dim:
+                            raise self.error(f"{ast.unparse(node)}: reads element {at} of a dim of {dim}", node)
 
     # ------------------------------------------------------------------ tiles
 
-    def _window(self, index: ast.expr, dim: int, text: str) -> Window:
-        usage = (f"{text}: each index is `v:v + size` or `v` for a loop variable v, `:`, constants "
-                 "(`start:stop`, an int), or an element of an index array (`w[ids[e], :]`)")
-        loop_vars = reads(index) & self.ranges.keys()
-        if isinstance(index, ast.Subscript) and isinstance(index.value, ast.Name) and index.value.id in self.indices:
-            if any(isinstance(i, ast.Slice) for i in subscript_dims(index)):
-                raise self.error(f"{text}: windows gathered through index-array slices are not lowered yet", index)
-            return Window(None, 0, None, index, frozenset(loop_vars))
-        if isinstance(index, ast.Slice):
-            lower, upper = index.lower, index.upper
-            if index.step is not None:
-                raise self.error(usage, index)
-            if isinstance(lower, ast.Name) and lower.id in self.ranges:
-                if not (isinstance(upper, ast.BinOp) and isinstance(upper.op, ast.Add)
-                        and ast.dump(upper.left) == ast.dump(lower) and not reads(upper.right) & self.ranges.keys()):
-                    raise self.error(usage, index)
-                return self._checked(Window(lower.id, 0, self._int(upper.right, text)), dim, text, index)
-            if loop_vars:
-                raise self.error(usage, index)
-            start = 0 if lower is None else self._int(lower, text)
-            stop = dim if upper is None else self._int(upper, text)
-            return self._checked(Window(None, start, stop - start), dim, text, index)
-        if isinstance(index, ast.Name) and index.id in self.ranges:
-            return self._checked(Window(index.id, 0, None), dim, text, index)
-        if loop_vars:
-            raise self.error(usage, index)
-        return self._checked(Window(None, self._int(index, text), None), dim, text, index)
-
-    def _int(self, node: ast.expr, text: str) -> int:
-        value = self.eval(node)
-        if not isinstance(value, int):
-            raise self.error(f"{text}: tile bounds are ints when planning, not {value!r}", node)
-        return int(value)
-
-    def _checked(self, window: Window, dim: int, text: str, node: ast.AST) -> Window:
-        if window.size is not None and window.size <= 0:
-            raise self.error(f"{text}: a slice takes at least one element", node)
-        first = window.offset
-        last = window.offset + (window.size or 1)
-        if window.loop:
-            r = self.ranges[window.loop]
-            first += r.start
-            last += r.value(r.count - 1)
-        if first < 0 or last > dim:
-            raise self.error(f"{text}: reads elements {first} to {last - 1} of a dim of {dim}", node)
-        return window
-
-    def _tile(self, array: str, shape: Tuple[int, ...], dt: DType, index: Sequence[ast.expr], node: ast.AST) -> Tile:
-        text = f"{array}[{', '.join(ast.unparse(i) for i in index)}]"
-        if len(index) != len(shape):
-            raise self.error(f"{text}: index every one of {array}'s {len(shape)} dims", node)
-        windows = tuple(self._window(i, d, text) for i, d in zip(index, shape))
-        sliced = [w.size is not None for w in windows]
-        if not any(sliced):
-            raise self.error(f"{text}: a tile keeps at least one dim (slice it, `v:v + 1`)", node)
-        if not all(sliced[sliced.index(True):]):
-            raise self.error(f"{text}: integer indices go before every sliced dim", node)
-        return Tile(array, windows, dt, text)
-
-    def _operands(self, phases: Tuple[Phase, ...], segments: Tuple[Tuple[ast.stmt, ...], ...]):
+    def _operands(self, phases: Tuple[Phase, ...], windows: _Windows):
+        """Every tile read of an input, in source order: the same read text is one operand. Its kind follows
+        the loops that move it: none (ONCE), a phase's loop (STREAM), or only parallel loops (TILE; STREAM when
+        nothing takes steps)."""
+        params = {name: k for k, name in enumerate(self.nest.params)}
+        reads = sorted((n for stmt in self.nest.tile for n in ast.walk(stmt)
+                        if isinstance(n, ast.Subscript) and isinstance(n.value, ast.Name)
+                        and n.value.id in params and n.value.id not in self.indices),
+                       key=lambda n: (n.lineno, n.col_offset))
         operands: List[Operand] = []
-        by_key: Dict[str, Operand] = {}
-        by_node: Dict[int, Operand] = {}
-        params = {name: i for i, name in enumerate(self.nest.params)}
-        subscripts = [n for stmt in self.nest.tile for n in ast.walk(stmt) if isinstance(n, ast.Subscript)]
-        for node in sorted(subscripts, key=lambda n: (n.lineno, n.col_offset)):
-            if not isinstance(node.value, ast.Name) or node.value.id in self.indices:
-                continue
-            param = params.get(node.value.id)
-            if param is None:
-                continue
-            spec = self.inputs[param]
-            tile = self._tile(node.value.id, spec.shape, spec.dtype, subscript_dims(node), node)
-            moving = {v for v in tile.loops if v in self.ranges and self.ranges[v].count > 1}
-            phase = next((p for p, ph in enumerate(phases) if ph.range.var in moving), None)
+        same_text: Dict[str, Operand] = {}
+        by_node: Dict[Tuple[int, int, int, int], Operand] = {}
+        for node in reads:
             key = ast.dump(node)
-            if key in by_key:
-                by_node[_pos(node)] = by_key[key]
+            if key in same_text:
+                by_node[_pos(node)] = same_text[key]
                 continue
+            array = node.value.id  # type: ignore[attr-defined]
+            spec = self.inputs[params[array]]
+            tile = windows.tile(array, spec.shape, spec.dtype, index_dims(node), node)
+            moving = {v for v in tile.loops if v in self.ranges and self.ranges[v].count > 1}
+            phase = next((k for k, ph in enumerate(phases) if ph.range.var in moving), None)
             if not moving:
                 kind = Kind.ONCE
             elif phase is not None or not phases:
                 kind = Kind.STREAM
             else:
                 kind = Kind.TILE
-            taken = {*self.nest.params, *(op.name for op in operands)}
-            name = tile.array if tile.array not in {op.tile.array for op in operands} else _fresh(tile.array, taken)
-            operand = Operand(name, param, tile, kind, phase)
-            operands.append(operand)
-            by_key[key] = by_node[_pos(node)] = operand
+            name = array
+            if any(op.tile.array == array for op in operands):
+                name = _fresh(array, {*self.nest.params, *(op.name for op in operands)})
+            op = Operand(name, params[array], tile, kind, phase)
+            operands.append(op)
+            same_text[key] = by_node[_pos(node)] = op
         return tuple(operands), by_node
 
-    def _output_tile(self, name: str, shape: Tuple[int, ...], dt: DType, parallel: Tuple[Range, ...]) -> Tile:
+    def _output_tile(self, name: str, shape: Tuple[int, ...], dt: DType, parallel: Tuple[Range, ...],
+                     windows: _Windows) -> Tile:
+        """The window an output's store writes: every parallel loop places it along exactly one dim, covering
+        that dim one step per tile; dims no loop places are written whole."""
         store = self.nest.stores[name]
-        tile = self._tile(name, shape, dt, store.index, store.node)
+        tile = windows.tile(name, shape, dt, store.index, store.node)
         if any(w.index is not None for w in tile.windows):
             raise self.error(f"{tile.text}: stores at windows an index array chooses are not lowered yet", store.node)
-        uses = [w.loop for w in tile.windows if w.loop]
+        placing = [w.loop for w in tile.windows if w.loop]
         for r in parallel:
-            if uses.count(r.var) != 1:
-                raise self.error(
-                    f"{tile.text}: every parallel loop places each output tile, so `{r.var}` indexes exactly one dim "
-                    "of the output", store.node)
-        for window, dim in zip(tile.windows, shape):
-            r = self.ranges.get(window.loop) if window.loop else None
-            if r is None:
-                if window.offset != 0 or window.size != dim:
-                    raise self.error(f"{tile.text}: dims no loop places are stored whole, with `:`", store.node)
-            elif (window.size or 1) != r.step or r.start != 0 or r.count * r.step != dim:
+            if placing.count(r.var) != 1:
+                raise self.error(f"{tile.text}: every parallel loop places each output tile, so `{r.var}` indexes "
+                                 "exactly one dim of the output", store.node)
+        for w, dim in zip(tile.windows, shape):
+            r = self.ranges.get(w.loop) if w.loop else None
+            if r is None and (w.offset != 0 or w.size != dim):
+                raise self.error(f"{tile.text}: dims no loop places are stored whole, with `:`", store.node)
+            if r is not None and ((w.size or 1) != r.step or r.start != 0 or r.count * r.step != dim):
                 raise self.error(f"{tile.text}: loop `{r.var}` must cover the dim of {dim} exactly, one step per tile",
                                  store.node)
         return tile
 
-    def _check_store(self, tile: Tile, vshape: Tuple[int, ...]) -> None:
-        import numpy as np
-
-        node = self.nest.stores[tile.array].node
-        try:
-            ok = np.broadcast_shapes(vshape, tile.shape) == tile.shape
-        except ValueError:
-            ok = False
-        if not ok:
-            raise self.error(f"{tile.text}: can't store a value of shape {vshape} in a {tile.shape} tile", node)
-
     def _check_reads_before_assignment(self) -> None:
-        nest = self.nest
-        early = (first_reads(nest.tile) & assigned(nest.tile)) - set(nest.outputs)
-        for stmt in flatten(nest.tile):
-            names = sorted(reads(stmt) & early)
-            if names:
-                raise self.error(
-                    f"`{names[0]}` is read before the tile assigns it: nothing carries over from one tile to the next", stmt)
+        """Nothing carries from one tile to the next: a name the tile assigns can't be read before that."""
+        tile = self.nest.tile
+        too_early = (used_before_bound(tile) & bound(tile)) - set(self.nest.outputs)
+        if not too_early:
+            return
+        for stmt in in_order(tile):
+            hit = used(stmt) & too_early
+            if hit:
+                raise self.error(f"`{min(hit)}` is read before the tile assigns it: nothing carries over from one tile "
+                                 "to the next", stmt)
 
     def _constants(self) -> Dict[str, Any]:
+        """The module and closure values the tile code reads, as they are when planning."""
         nest = self.nest
-        own = assigned(nest.tile) | {r.var for r in nest.loops} | set(nest.params) | set(nest.outputs)
-        names = set().union(*(reads(stmt) for stmt in flatten(nest.tile))) - own
-        return {name: self.env[name] for name in sorted(names) if name in self.env}
+        own = bound(nest.tile) | {loop.var for loop in nest.loops} | set(nest.params) | set(nest.outputs)
+        wanted: Set[str] = set()
+        for stmt in in_order(nest.tile):
+            wanted |= used(stmt)
+        return {name: self.env[name] for name in sorted(wanted - own) if name in self.env}
 
     # ------------------------------------------------------------------ the trace
 
     def _rewrite(self, stmts: Sequence[ast.stmt], by_node: Dict[int, Operand]) -> List[ast.stmt]:
         """The tile code as the trace runs it: tile reads, index-array elements and stores as calls of the
-        tracer, and `@` as the matrix-core product."""
+        tracer (`@` keeps its text: the trace runs under jaxlite.matrix_units())."""
         indices, outputs = set(self.indices), set(self.nest.outputs)
         nest = self.nest
 
@@ -553,14 +623,14 @@ class _Planner:
                 if op is not None:
                     return ast.copy_location(ast.Call(ast.Name(READ, ast.Load()), [ast.Constant(op.name)], []), node)
                 if isinstance(node.value, ast.Name) and node.value.id in indices:
-                    dims = [self.visit(d) for d in subscript_dims(node)]
+                    dims = [self.visit(d) for d in index_dims(node)]
                     return ast.copy_location(ast.Call(ast.Name(INDEX, ast.Load()),
                                                       [ast.Constant(node.value.id), ast.Tuple(dims, ast.Load())], []), node)
                 self.generic_visit(node)
                 return node
 
             def visit_Assign(self, node: ast.Assign) -> ast.stmt:
-                store = as_store(node)
+                store = store_of(node)
                 if store is not None and store.output in outputs:
                     value = self.visit(copy.deepcopy(store.value))
                     call = ast.Call(ast.Name(STORE, ast.Load()), [ast.Constant(store.output), value], [])
@@ -571,10 +641,10 @@ class _Planner:
         out = []
         for stmt in stmts:
             new = Rewrite().visit(copy.deepcopy(stmt))
-            out.append(mxu.rewrite_matmuls(new))
+            out.append(new)
         return [ast.fix_missing_locations(s) for s in out]
 
-    def _trace(self, phases, segments, bound, by_node):
+    def _trace(self, phases, segments, bound_vars, by_node):
         """Trace the tile's scopes in the order they run; find the carried values and their types."""
         nest = self.nest
         order: List[Tuple[str, Tuple[ast.stmt, ...]]] = [("seg0", segments[0])]
@@ -583,18 +653,18 @@ class _Planner:
         made: Set[str] = set()
         carried_names: Set[str] = set()
         for _, stmts in order:
-            carried_names |= first_reads(stmts) & made
-            made |= assigned(stmts)
+            carried_names |= used_before_bound(stmts) & made
+            made |= bound(stmts)
         carried_names -= set(nest.outputs)
         types: Dict[str, Tuple[Tuple[int, ...], DType]] = {}
         scopes: Dict[str, Scope] = {}
 
         def run(name: str, stmts: Tuple[ast.stmt, ...], carried_in: Dict[str, Tuple[Tuple[int, ...], Any]]) -> Scope:
-            with jaxlite.trace() as tr:
+            with jaxlite.trace() as tr, jaxlite.matrix_units():
                 locals_: Dict[str, Any] = {}
                 for var in self.ranges:
                     locals_[var] = jaxlite.leaf("loop", (), jaxlite.int32, var=var)
-                for var, value in bound.items():
+                for var, value in bound_vars.items():
                     locals_[var] = value
                 leaves = {}
                 for cname, (shape, dt) in carried_in.items():
@@ -605,7 +675,6 @@ class _Planner:
                         locals_[cname] = dt
                 stores: Dict[str, Any] = {}
                 scope_env = dict(self.env)
-                scope_env.update(mxu.FUNCTIONS)
                 scope_env[READ] = lambda op: self._load(op)
                 scope_env[INDEX] = lambda arr, idx: self._index_load(arr, idx)
                 scope_env[STORE] = lambda out, value: stores.__setitem__(out, value)
@@ -617,7 +686,7 @@ class _Planner:
                         raise
                     except Exception as e:
                         raise self.error(f"tile code failed when traced with symbolic tiles: {e!r}", stmt) from e
-                values = {k: v for k, v in locals_.items() if k not in self.ranges and k not in bound}
+                values = {k: v for k, v in locals_.items() if k not in self.ranges and k not in bound_vars}
                 return Scope(name, list(tr.nodes), values, leaves, stores)
 
         def type_of(v: Any) -> Tuple[Tuple[int, ...], Any]:
@@ -628,7 +697,7 @@ class _Planner:
             raise self.error(f"a carried value must be an array or a number, not {type(v).__name__}")
 
         for idx, (name, stmts) in enumerate(order):
-            needed = {c: types[c] for c in (first_reads(stmts) & carried_names) if c in types}
+            needed = {c: types[c] for c in (used_before_bound(stmts) & carried_names) if c in types}
             scope = run(name, stmts, needed)
             if name.startswith("body"):
                 # Carried values keep one type: run the body again from what it leaves until they agree.

@@ -159,7 +159,7 @@ def profile(kernel: Any, args: Sequence[Any], runs: int = 5) -> KernelProfile:
     """Where `kernel`'s time goes on the GPU for these inputs (and tunable, if given)."""
     from .api import _tensor
 
-    arrays, _ = kernel._split(tuple(args))
+    arrays, _ = kernel._arguments(tuple(args))
     config = kernel.lower(*args).config
     lowered = kernel.lowered(kernel.signature(*arrays), config, trace=True)
     return measure(lowered, [_tensor(a) for a in arrays], runs)

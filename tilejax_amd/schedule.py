@@ -35,7 +35,7 @@ import numpy as np
 
 from . import gfx950
 from .plan import Plan, Range
-from .tilecode import reads
+from .syntax import used as reads
 
 __all__ = ["CODE_SHIFT", "Schedule", "make_schedule", "STEP_TILE", "STEP_CODE", "STEP_COUNT", "TILE_TABLE",
            "FILL_TABLE"]

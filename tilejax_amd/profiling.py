@@ -157,7 +157,7 @@ def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile
 
 def profile(kernel: Any, args: Sequence[Any], runs: int = 5) -> KernelProfile:
     """Where `kernel`'s time goes on the GPU for these inputs (and tunable, if given)."""
-    from .api import _tensor
+    from .api import _as_tensor as _tensor
 
     arrays, _ = kernel._arguments(tuple(args))
     config = kernel.lower(*args).config

@@ -16,11 +16,11 @@ def test_relative_imports_resolve():
             if not f.endswith(".py"):
                 continue
             text = open(os.path.join(here, f)).read()
-            for dots, mod, names in re.findall(r"from (\.+)(\w*) import ([\w, ]+)", text):
+            for dots, mod, names in re.findall(r"from (\.+)(\w*) import ([\w, ]+(?: as \w+)?)", text):
                 parts = package.split(".")
                 parts = parts[: len(parts) - (len(dots) - 1)] + ([mod] if mod else [])
                 module = importlib.import_module(".".join(parts))
-                for name in (n.strip() for n in names.split(",")):
+                for name in (n.strip().split(" as ")[0] for n in names.split(",")):
                     if name and not hasattr(module, name):
                         try:
                             importlib.import_module(f"{module.__name__}.{name}")

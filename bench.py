@@ -45,13 +45,25 @@ def _log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+WARM_S = [1.0]  # seconds of untimed calls before each leg's warm-up steps (--warm-seconds)
+
+
 def time_kernel(run, steps: int, warmup: int):
     """(mean ms per call, per-call ms list): HIP events around each call on torch's current stream, which
-    is the stream the generated kernels are launched on."""
+    is the stream the generated kernels are launched on.
+
+    Before the `warmup` untimed steps, the leg is run back to back for WARM_S seconds: after host work leaves
+    the GPU idle its clock takes 50-100 calls of an 8192^3 matmul (tens of ms) to return to its sustained
+    level, so a few warm-up steps alone would time the ramp, not the kernel."""
     import torch
 
     from tilejax_amd import runtime
 
+    start = time.perf_counter()
+    while time.perf_counter() - start < WARM_S[0]:
+        for _ in range(8):
+            run()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
@@ -94,6 +106,31 @@ def check_dense(got, x, y) -> dict:
     finally:
         torch.backends.cuda.matmul.allow_tf32 = allow
     return {"ulp_max_typical": round(worst_ulp, 3), "bound_use": round(worst_use, 4)}
+
+
+def time_cpu(call, calls: int, repeats: int = 5) -> float:
+    """Seconds per call on the CPU, as the reference's benchmarks/timing.py:12-22 times: one warm-up call,
+    then the median over `repeats` of the mean over `calls` back-to-back calls."""
+    call()
+    means = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            call()
+        means.append((time.perf_counter() - t0) / calls)
+    return statistics.median(means)
+
+
+def cpu_leg(what: str, call, work: float, unit: str, calls: int = 1) -> dict:
+    """A leg's CPU baseline: `call` runs the spec's own reference path (kernel.reference: the loop nest
+    through jaxlite on torch CPU tensors, `@` accumulating in f32) on a bounded sample of the leg's workload
+    that does `work` FLOP (or bytes); its rate in `unit` (TFLOP/s or GB/s)."""
+    import torch
+
+    t = time_cpu(call, calls)
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    return {"value": round(work / t / scale, 4), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{what}; median of 5 means of {calls} call(s), {t * 1e3:.1f} ms per call"}
 
 
 def cpu_baseline(budget_s: float = 12.0):
@@ -140,10 +177,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     # Each leg starts after host work (lowering, input set-up) that leaves the GPU idle, and the clock then
-    # takes some tens of milliseconds of load to return to its sustained level: 200 untimed calls cover
-    # that for every leg. (The first leg of a process has still measured up to 10 % slower than the same
-    # kernel later in the process, with 200 or 1000 warm-up calls alike.)
-    ap.add_argument("--warmup", type=int, default=200)
+    # takes tens of milliseconds of load to return to its sustained level: `--warm-seconds` of untimed calls
+    # (time_kernel) cover that for every leg, whatever the warm-up step count.
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--tiles", default="512,512,512", help="dense matmul spec tiles tm,tn,tk")
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -153,7 +189,10 @@ def main() -> int:
                     "default: profiles/traffic.json")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first copy a 1 GiB tensor once: the known-size kernel rocprofv3 counters are scaled by")
+    ap.add_argument("--warm-seconds", type=float, default=1.0,
+                    help="seconds of untimed back-to-back calls before each leg's warm-up steps")
     args = ap.parse_args()
+    WARM_S[0] = args.warm_seconds
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}): this build has no multi-GPU path",
               file=sys.stderr)
@@ -178,12 +217,16 @@ def main() -> int:
     legs = set(args.only.split(",")) if args.only else {"dense", "causal", "rmsnorm", "attention", "moe", "decode"}
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(N_DENSE, N_DENSE, generator=g).to(torch.bfloat16).to(dev)
+    xh = torch.randn(N_DENSE, N_DENSE, generator=g).to(torch.bfloat16)
     g = torch.Generator().manual_seed(1)
-    y = torch.randn(N_DENSE, N_DENSE, generator=g).to(torch.bfloat16).to(dev)
+    yh = torch.randn(N_DENSE, N_DENSE, generator=g).to(torch.bfloat16)
+    x, y = xh.to(dev), yh.to(dev)
     flop = 2.0 * N_DENSE**3
     tiles = MatmulTiles(*(int(v) for v in args.tiles.split(",")))
     out = {}
+    # Each leg's CPU baseline, run after the GPU legs: (leg, what, call, work, unit, calls)
+    cpu_jobs = [("dense", f"kernel.reference of the headline on x[:512] @ y (a band of 512 rows, 1/16 of it), {tiles}",
+                 lambda: matmul.reference(xh[:512], yh, tiles), 2.0 * 512 * N_DENSE * N_DENSE, "TFLOP/s", 1)]
 
     _log(f"dense matmul {N_DENSE}^3 tiles {tiles}: lowering")
     lowered = matmul.lower(x, y, tiles)
@@ -222,14 +265,22 @@ def main() -> int:
         _log(f"  {cms * 1e3:.1f} us/call = {cms / ms:.3f} x dense")
         out["causal"] = {"tiles": [ct.tm, ct.tn, ct.tk], "us": round(cms * 1e3, 2), "vs_dense": round(cms / ms, 4),
                          "tflops_dense_equiv": round(flop / (cms * 1e-3) / 1e12, 2)}
+        cpu_jobs.append(("causal", f"kernel.reference of the whole 8192^3 causal matmul, {ct} (rate on the dense "
+                         "FLOP count, as the GPU leg's tflops_dense_equiv)",
+                         lambda: causal_matmul.reference(xh, yh, ct), flop, "TFLOP/s", 1))
 
     if "rmsnorm" in legs:
         try:
             from examples.rmsnorm_matmul import NormMatmulTiles, rmsnorm_matmul
 
             g = torch.Generator().manual_seed(2)
-            gamma = (1 + 0.1 * torch.randn(1, N_DENSE, generator=g)).to(torch.bfloat16).to(dev)
-            rl = rmsnorm_matmul.lower(x, gamma, y, NormMatmulTiles(tiles.tm, tiles.tn, tiles.tk))
+            gh = (1 + 0.1 * torch.randn(1, N_DENSE, generator=g)).to(torch.bfloat16)
+            gamma = gh.to(dev)
+            nt = NormMatmulTiles(tiles.tm, tiles.tn, tiles.tk)
+            rl = rmsnorm_matmul.lower(x, gamma, y, nt)
+            cpu_jobs.append(("rmsnorm_matmul", f"kernel.reference on rows 0..511 of the 8192^3 workload, {nt}",
+                             lambda: rmsnorm_matmul.reference(xh[:512], gh, yh, nt), 2.0 * 512 * N_DENSE * N_DENSE,
+                             "TFLOP/s", 1))
             rms_, _ = time_kernel(lambda: rl.run(x, gamma, y), args.steps, args.warmup)
             _log(f"RMSNorm + matmul {N_DENSE}^3: {rms_ * 1e3:.1f} us = {rms_ / ms:.3f} x dense")
             out["rmsnorm_matmul"] = {"shape": [N_DENSE] * 3, "us": round(rms_ * 1e3, 2), "vs_dense": round(rms_ / ms, 4),
@@ -244,10 +295,14 @@ def main() -> int:
 
             for key, (B, H, S, D) in (("attention", (4, 16, 2048, 128)), ("attention_4096", (1, 16, 4096, 128))):
                 gens = [torch.Generator().manual_seed(s) for s in (0, 1, 2)]
-                q, k, v = (torch.randn(B, H, S, D, generator=gg).to(torch.bfloat16) for gg in gens)
-                q = (q.float() * D**-0.5).to(torch.bfloat16)
-                q, k, v = q.to(dev), k.to(dev), v.to(dev)
+                qh, kh, vh = (torch.randn(B, H, S, D, generator=gg).to(torch.bfloat16) for gg in gens)
+                qh = (qh.float() * D**-0.5).to(torch.bfloat16)
+                q, k, v = qh.to(dev), kh.to(dev), vh.to(dev)
                 blocks = AttentionBlocks(512, 512)
+                hs = 2  # the CPU sample: batch 0, heads 0 and 1 (each head is its own tiles of the nest)
+                cpu_jobs.append((key, f"kernel.reference on batch 0, heads 0..{hs - 1} of ({B}, {H}, {S}, {D}), {blocks}",
+                                 lambda qs=qh[:1, :hs].clone(), ks=kh[:1, :hs].clone(), vs=vh[:1, :hs].clone(), b=blocks:
+                                 causal_attention.reference(qs, ks, vs, b), 2.0 * hs * S * S * D, "TFLOP/s", 1))
                 al = causal_attention.lower(q, k, v, blocks)
                 ams, _ = time_kernel(lambda: al.run(q, k, v), args.steps, args.warmup)
                 aflop = 2.0 * B * H * S * S * D  # algorithmic causal count (QK^T and PV over the lower triangle)
@@ -266,10 +321,15 @@ def main() -> int:
 
             g = torch.Generator().manual_seed(0)
             counts = torch.multinomial(torch.full((8,), 1 / 8), 64, replacement=True, generator=g).bincount(minlength=8)
-            ge = torch.repeat_interleave(torch.arange(8), counts).to(torch.int32).to(dev)
-            xs = torch.randn(16384, 4096, generator=g).to(torch.bfloat16).to(dev)
-            w = (torch.randn(8, 4096, 14336, generator=g) * 0.02).to(torch.bfloat16).to(dev)
-            gl = grouped_matmul.lower(xs, w, ge, GroupTiles(512, 512))
+            geh = torch.repeat_interleave(torch.arange(8), counts).to(torch.int32)
+            xsh = torch.randn(16384, 4096, generator=g).to(torch.bfloat16)
+            wh = (torch.randn(8, 4096, 14336, generator=g) * 0.02).to(torch.bfloat16)
+            ge, xs, w = geh.to(dev), xsh.to(dev), wh.to(dev)
+            gt = GroupTiles(512, 512)
+            gl = grouped_matmul.lower(xs, w, ge, gt)
+            cpu_jobs.append(("moe", f"kernel.reference on groups 0 and 1 (512 rows) of config 4, all 8 experts, {gt}",
+                             lambda: grouped_matmul.reference(xsh[:512], wh, geh[:2], gt), 2.0 * 512 * 4096 * 14336,
+                             "TFLOP/s", 1))
             mms, _ = time_kernel(lambda: gl.run(xs, w, ge), args.steps, args.warmup)
             mflop = 2.0 * 16384 * 4096 * 14336
             mtf = mflop / (mms * 1e-3) / 1e12
@@ -288,11 +348,17 @@ def main() -> int:
             B, H, Hkv, D, P, pages = 64, 32, 8, 128, 16, 512
             g = torch.Generator().manual_seed(0)
             lengths = torch.randint(128, 8193, (B,), generator=g, dtype=torch.int32)
-            q = (torch.randn(B, 1, H, D, generator=g) * D**-0.5).to(torch.bfloat16).to(dev)
-            table = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32).to(dev)
-            kp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
-            vp = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
-            ln = lengths.to(dev)
+            qh = (torch.randn(B, 1, H, D, generator=g) * D**-0.5).to(torch.bfloat16)
+            tableh = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32)
+            kph = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16)
+            vph = torch.randn(B * pages, P, Hkv * D, generator=g).to(torch.bfloat16)
+            q, table, kp, vp, ln = qh.to(dev), tableh.to(dev), kph.to(dev), vph.to(dev), lengths.to(dev)
+            nb = 8  # the CPU sample: sequences 0..7 over the whole page pool
+            sample_bytes = int(lengths[:nb].sum()) * Hkv * D * 2 * 2
+            cpu_jobs.append(("decode", f"kernel.reference on sequences 0..{nb - 1} of config 5 (their valid K and V rows "
+                             f"through the page table: {sample_bytes} bytes)",
+                             lambda: paged_gqa_decode.reference(qh[:nb], kph, vph, tableh[:nb], lengths[:nb]),
+                             sample_bytes, "GB/s", 1))
             from tilejax_amd.tune import Config
 
             dsig = paged_gqa_decode.signature(q, kp, vp, table, ln)
@@ -317,9 +383,15 @@ def main() -> int:
             from examples.decode import DecodeTiles, gqa_decode
 
             S = pages * P
-            kc = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
-            vc = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).to(dev)
+            kch = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16)
+            vch = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16)
+            kc, vc = kch.to(dev), vch.to(dev)
             gl = gqa_decode.lower(q, kc, vc, ln, DecodeTiles(512))
+            cblocks = int(sum(-(-int(n) // 512) for n in lengths[:nb])) * 512 * Hkv * D * 2 * 2
+            cpu_jobs.append(("decode_contiguous", f"kernel.reference on sequences 0..{nb - 1} ({cblocks} bytes of "
+                             "whole 512-position blocks)",
+                             lambda: gqa_decode.reference(qh[:nb], kch[:nb].clone(), vch[:nb].clone(), lengths[:nb],
+                                                          DecodeTiles(512)), cblocks, "GB/s", 1))
             gc = gqa_decode.lowered(gqa_decode.signature(q, kc, vc, ln), Config(DecodeTiles(512), gl.config.pipeline, True))
             gms = min(time_kernel(lambda: gl.run(q, kc, vc, ln), args.steps, args.warmup)[0],
                       time_kernel(lambda: gc.run(q, kc, vc, ln), args.steps, args.warmup)[0])
@@ -356,9 +428,18 @@ def main() -> int:
                      "frac": round(achieved / PEAK_TFLOPS, 4), "traffic": traffic},
         "legs": out,
     }
+    result["warmup_s"] = WARM_S[0]
     if not args.no_cpu:
         _log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline()
+        for leg, what, call, work, unit, calls in cpu_jobs:
+            if leg not in out or "error" in out[leg]:
+                continue
+            try:
+                out[leg]["cpu_baseline"] = cpu_leg(what, call, work, unit, calls)
+                _log(f"  cpu {leg}: {out[leg]['cpu_baseline']['value']} {unit}")
+            except Exception as e:  # reported, not hidden
+                out[leg]["cpu_baseline"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
     print(json.dumps(result), flush=True)
     return 0
 

@@ -32,7 +32,7 @@ NOW = "__builtin_amdgcn_s_memrealtime()"
 class Arg:
     """One kernel argument: a pointer to an input, output, table or workspace buffer, or an int."""
 
-    kind: str  # "input", "output", "table", "workspace", "int"
+    kind: str  # "input", "output", "table", "state", "workspace", "int"
     key: Any  # input/output position, table/workspace name, or the int's value
     ctype: str  # the C type of the struct field
     name: str
@@ -56,6 +56,9 @@ class Program:
     inputs: List[Tuple[Tuple[int, ...], jaxlite.DType]]
     tables: Dict[str, np.ndarray] = field(default_factory=dict)
     workspace: Dict[str, int] = field(default_factory=dict)  # name -> bytes (uninitialised: launches write before reading)
+    # name -> int32 count: counters kept on the device from call to call, zero when made (once per device);
+    # a kernel that uses one leaves it zero again when it ends (the work queues' heads)
+    state: Dict[str, int] = field(default_factory=dict)
     lds_bytes: int = 0
     notes: Dict[str, Any] = field(default_factory=dict)  # what the lowering chose (hardware tiles, ...)
     _modules: Dict[int, runtime.Module] = field(default_factory=dict, repr=False)
@@ -70,8 +73,10 @@ class Program:
     def device_tables(self, device: torch.device) -> Dict[str, torch.Tensor]:
         key = device.index or 0
         if key not in self._tables:
-            self._tables[key] = {name: torch.from_numpy(np.ascontiguousarray(t)).to(device)
-                                 for name, t in self.tables.items()}
+            made = {name: torch.from_numpy(np.ascontiguousarray(t)).to(device) for name, t in self.tables.items()}
+            made.update({name: torch.zeros(max(n, 1), dtype=torch.int32, device=device)
+                         for name, n in self.state.items()})
+            self._tables[key] = made
         return self._tables[key]
 
     def check_inputs(self, arrays: Sequence[torch.Tensor]) -> None:
@@ -184,7 +189,7 @@ def pack(args: Sequence[Arg], arrays: Sequence[torch.Tensor], outputs: Sequence[
             pointers.append(arrays[a.key].data_ptr())
         elif a.kind == "output":
             pointers.append(outputs[a.key].data_ptr())
-        elif a.kind == "table":
+        elif a.kind in ("table", "state"):
             pointers.append(tables[a.key].data_ptr())
         elif a.kind == "workspace":
             pointers.append(workspace[a.key].data_ptr())

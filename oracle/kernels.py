@@ -264,3 +264,64 @@ def rmsnorm_matmul_float64(x: torch.Tensor, gamma: torch.Tensor, w: torch.Tensor
     xd, gd, wd = x.double().cpu(), gamma.double().cpu(), w.double().cpu()
     normed = xd / torch.sqrt((xd * xd).mean(dim=1, keepdim=True) + eps) * gd
     return (normed @ wd).numpy()
+
+
+def _gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    """The tanh form of GELU, as jax.nn.gelu computes it by default."""
+    return 0.5 * x * (1.0 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)))
+
+
+def attention_block(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor, w_up: torch.Tensor,
+                    w_down: torch.Tensor, bq: int = 256, bk: int = 256, bf: int = 1024,
+                    eps: float = 1e-6) -> torch.Tensor:
+    """examples/attention_block.py:47-80 of the reference: per (batch, query block) tile, the causal online
+    softmax over key blocks for every head (p rounded to the inputs' dtype before `p @ v`), the heads side
+    by side, RMSNorm rounded to the inputs' dtype, then over blocks of hidden units y += bf16(gelu(h @
+    w_up[:, f]))) @ w_down[f]; products accumulate in f32; the tile stored in the inputs' dtype."""
+    B, H, S, Dh = q.shape
+    F = w_up.shape[1]
+    bq, bk, bf = min(bq, S), min(bk, S), min(bf, F)
+    dtype = q.dtype
+    qf, kf, vf = _f32(q), _f32(k), _f32(v)
+    gf, uf, df = _f32(gamma), _f32(w_up), _f32(w_down)
+    out = torch.zeros((B, S, H * Dh), dtype=dtype)
+    for b in range(B):
+        for i in range(0, S, bq):
+            row_max = torch.full((H, bq, 1), MASK_VALUE)
+            row_sum = torch.zeros((H, bq, 1))
+            acc = torch.zeros((H, bq, Dh))
+            rows = i + torch.arange(bq).reshape(-1, 1)
+            for j in range(0, S, bk):
+                if j > i + bq - 1:
+                    continue
+                cols = j + torch.arange(bk).reshape(1, -1)
+                s = torch.stack([torch.where(cols <= rows, qf[b, h, i:i + bq] @ kf[b, h, j:j + bk].T,
+                                             torch.tensor(MASK_VALUE)) for h in range(H)])
+                max_new = torch.maximum(row_max, s.max(dim=2, keepdim=True).values)
+                p = torch.exp(s - max_new)
+                alpha = torch.exp(row_max - max_new)
+                row_sum = alpha * row_sum + p.sum(dim=2, keepdim=True)
+                pv = torch.stack([p[h].to(dtype).float() @ vf[b, h, j:j + bk] for h in range(H)])
+                acc = alpha * acc + pv
+                row_max = max_new
+            heads = acc / row_sum
+            a = torch.cat([heads[h] for h in range(H)], dim=1)
+            normed = (a * torch.rsqrt((a * a).mean(dim=1, keepdim=True) + eps) * gf[0:1]).to(dtype).float()
+            y = torch.zeros((bq, H * Dh))
+            for f in range(0, F, bf):
+                hidden = _gelu_tanh(normed @ uf[:, f:f + bf])
+                y += hidden.to(dtype).float() @ df[f:f + bf]
+            out[b, i:i + bq] = y.to(dtype)
+    return out
+
+
+def attention_block_float64(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gamma: torch.Tensor,
+                            w_up: torch.Tensor, w_down: torch.Tensor, eps: float = 1e-6) -> np.ndarray:
+    """The block in float64 with nothing rounded: causal attention per head, the heads side by side,
+    RMSNorm, tanh-GELU feed-forward (the reference's tests/test_examples.py:168-177 check)."""
+    a = torch.as_tensor(attention_float64(q, k, v))  # (B, H, S, Dh)
+    B, H, S, Dh = a.shape
+    a = a.permute(0, 2, 1, 3).reshape(B, S, H * Dh)
+    normed = a / torch.sqrt((a * a).mean(dim=-1, keepdim=True) + eps) * gamma.double().cpu()
+    up = normed @ w_up.double().cpu()
+    return (_gelu_tanh(up) @ w_down.double().cpu()).numpy()

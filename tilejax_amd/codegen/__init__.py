@@ -9,7 +9,9 @@ HIP kernel generated from the plan and schedule:
 - `flash`: the online-softmax reduction of attention over static masks (causal flash attention);
 - `decode`: the same reduction under runtime masks and runtime page windows (paged decode attention).
 
-A loop nest no family takes raises KernelError naming the kernel: the gfx950 backend doesn't lower it yet.
+Every other loop nest (and one a family recognises but can't take, say a head dim it has no layout for)
+lowers to `generic`: one persistent kernel evaluating the traced tile code pass by pass per tile, correct
+for any nest the planner accepts and tuned for none. A nest even that can't lower raises KernelError.
 """
 
 from __future__ import annotations
@@ -40,22 +42,29 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
              cursor: bool = False) -> Program:
     """The program for this plan, schedule and pipeline; with `cursor`, a kernel with runtime masks finds
     its steps itself as it runs rather than from device-built step tables (the decode family)."""
-    from . import decode, flash, gemm
+    from . import decode, flash, gemm, generic
 
     name = _symbol(plan)
-    found = gemm.match(plan)
-    if found is not None:
-        if cursor:
-            raise KernelError(f"{plan.nest.name}: the matmul family reads runtime masks from device step tables "
-                              "(no cursor)")
-        return gemm.lower(plan, schedule, pipeline, found, name, trace=trace)
-    found = flash.match(plan)
-    if found is not None:
-        return flash.lower(plan, schedule, pipeline, found, name, trace=trace)
-    found = decode.match(plan)
-    if found is not None:
-        return decode.lower(plan, schedule, pipeline, found, name, trace=trace, cursor=cursor)
-    raise KernelError(
-        f"{plan.nest.name}: the gfx950 backend has no lowering for this loop nest's tile code yet "
-        "(it lowers matmuls with pointwise epilogues and online-softmax attention)"
-    )
+    family_error = None
+    try:
+        found = gemm.match(plan)
+        if found is not None:
+            if cursor:
+                raise KernelError(f"{plan.nest.name}: the matmul family reads runtime masks from device step "
+                                  "tables (no cursor)")
+            return gemm.lower(plan, schedule, pipeline, found, name, trace=trace)
+        found = flash.match(plan)
+        if found is not None:
+            return flash.lower(plan, schedule, pipeline, found, name, trace=trace)
+        found = decode.match(plan)
+        if found is not None:
+            return decode.lower(plan, schedule, pipeline, found, name, trace=trace, cursor=cursor)
+    except KernelError as e:
+        family_error = e
+    if cursor:
+        raise family_error or KernelError(f"{plan.nest.name}: only the decode family finds its steps with a cursor")
+    try:
+        return generic.lower(plan, schedule, pipeline, name, trace=trace)
+    except KernelError as e:
+        why = f"; {family_error}" if family_error is not None else ""
+        raise KernelError(f"{plan.nest.name}: the gfx950 backend has no lowering for this loop nest: {e}{why}") from e

@@ -679,14 +679,18 @@ class _Planner:
                 scope_env[INDEX] = lambda arr, idx: self._index_load(arr, idx)
                 scope_env[STORE] = lambda out, value: stores.__setitem__(out, value)
                 code = self._rewrite(stmts, by_node)
+                # one namespace, as a function's: comprehensions and lambdas in tile code see its names
+                namespace = scope_env
+                namespace.update(locals_)
                 for stmt in code:
                     try:
-                        exec(compile(ast.Module([stmt], []), nest.filename, "exec"), scope_env, locals_)
+                        exec(compile(ast.Module([stmt], []), nest.filename, "exec"), namespace)
                     except KernelError:
                         raise
                     except Exception as e:
                         raise self.error(f"tile code failed when traced with symbolic tiles: {e!r}", stmt) from e
-                values = {k: v for k, v in locals_.items() if k not in self.ranges and k not in bound_vars}
+                names = (set(locals_) | bound(stmts)) - set(self.ranges) - set(bound_vars)
+                values = {k: namespace[k] for k in names if k in namespace}
                 return Scope(name, list(tr.nodes), values, leaves, stores)
 
         def type_of(v: Any) -> Tuple[Tuple[int, ...], Any]:

@@ -80,6 +80,13 @@ def standard() -> Iterator[Tuple[object, tuple]]:
     for t, h, kv, block in ((1, 8, 2, 128), (1, 4, 4, 256), (3, 8, 2, 128)):
         yield decode.gqa_decode, (_bf16(4, t, h, 128), _bf16(4, 512, kv * 128), _bf16(4, 512, kv * 128), _i32(4),
                                   decode.DecodeTiles(block))
+    from examples import attention_block as ab
+
+    BT = ab.BlockTiles
+    for (s_, f_, dt), tiles in ((((512, 512, _bf16)), BT(128, 128)), (((512, 512, _bf16)), BT(256, 128)),
+                                (((256, 1024, _bf16)), BT(128, 128, 256)), (((256, 256, _f32)), BT(128, 128, 256))):
+        yield ab.attention_block, (dt(1, 2, s_, 128), dt(1, 2, s_, 128), dt(1, 2, s_, 128), dt(1, 256),
+                                   dt(256, f_), dt(f_, 256), tiles)
     try:
         from examples import causal_attention as ca
 

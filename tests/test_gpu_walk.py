@@ -1,0 +1,127 @@
+"""The generic gfx950 kernel walking plans of the tile as written (tilejax_amd/walk.py), against float64
+closed forms: repeat loops, runtime loop bounds and a runtime count of tiles, ragged rows, windows gathered
+through index-array slices, outputs updated in place and scattered, outputs stored per step, and index
+arrays the tile code computes (routing inside a kernel). The cases and closed forms are tests/test_walk.py's.
+
+Tolerance: f32 results within the reference's own f32 bounds for these tests (rtol 1e-4 plus 1e-3, or 1e-5
+plus 1e-4 for sums of a few terms; tests/test_repeat_loops.py, test_runtime_ranges.py of the reference);
+integer-placed results (scatters, copies, in-place outputs) exactly where no arithmetic happens. The bf16
+ragged case within rtol 1e-2 (2 bf16 ulp) of float64.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import tilejax_amd
+from tests.helpers import make_kernel, rand
+from tests.test_walk import (FFN_STACK, GATHER, LAYERED, MASKED_IN_PLACE, MOE, NESTED, OFFSETS, ONCE_PER_TILE,
+                             RAGGED, SCAN, SCATTER, SPANS, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, counted_float64,
+                             ffn_inputs, ffn_stack_float64, gather_float64, i32, layered_float64, moe_inputs,
+                             once_per_tile_float64, ragged_float64, route, routed_float64, scan_float64,
+                             scatter_float64, spans_float64, sums_float64, two_repeats_float64)
+
+pytestmark = pytest.mark.gpu
+
+
+def run(kernel, *inputs, what):
+    print(f"walk: {what} {[tuple(t.shape) for t in inputs]}", flush=True)
+    lowered = kernel.lower(*inputs)
+    assert lowered.plan.walk and lowered.program.notes["family"] == "generic"
+    got = lowered.run(*(t.cuda() for t in inputs))
+    torch.cuda.synchronize()
+    return tuple(g.cpu() for g in got) if isinstance(got, tuple) else got.cpu()
+
+
+def close(got, want, rtol=1e-4, atol=1e-3):
+    got = np.asarray(got.double())
+    err = np.abs(got - want)
+    bad = err > atol + rtol * np.abs(want)
+    assert not bad.any(), f"{int(bad.sum())} of {bad.size} differ; max |diff| {err.max():.3g}"
+    print(f"  max |diff| {err.max():.3g}", flush=True)
+
+
+def test_repeat_loop_carries_layers():
+    inputs = ffn_inputs()
+    close(run(make_kernel(FFN_STACK), *inputs, what="ffn_stack"), ffn_stack_float64(*inputs))
+
+
+@pytest.mark.parametrize("limits", [(256, 0, 100), (0, 0, 0)])
+def test_reductions_around_and_in_a_repeat_loop_with_masks(limits):
+    x, w = rand((256, 256)), rand((3, 384, 128), 1) / 20
+    got = run(make_kernel(LAYERED), x, w, i32(*limits), what=f"layered {limits}")
+    close(got, layered_float64(x, w, limits))
+
+
+def test_two_repeat_loops():
+    x, w = rand((128, 128)), rand((2, 256, 128), 1)
+    close(run(make_kernel(TWO_REPEATS), x, w, what="two repeats"), two_repeats_float64(x, w))
+
+
+def test_runtime_ranges():
+    cache, lengths = rand((4, 512, 128)), i32(0, 1, 300, 512)
+    close(run(make_kernel(SUMS), cache, lengths, what="sums"), sums_float64(cache, lengths), 1e-5, 1e-4)
+    x, w = rand((3, 64, 128)), rand((256, 128), 1)
+    lo, hi = i32(0, 8, 16), i32(16, 8, 64)
+    close(run(make_kernel(SPANS), x, w, lo, hi, what="spans"), spans_float64(x, w, lo, hi), 1e-5, 1e-4)
+    x, n = rand((3, 4, 8, 128)), i32(2, 4, 9)
+    close(run(make_kernel(COUNTED), x, n, what="counted"), counted_float64(x, n), 1e-5, 1e-4)
+
+
+def test_ragged_rows_and_a_runtime_count_of_tiles():
+    kernel = make_kernel(RAGGED, tilejax_amd=tilejax_amd)
+    q = rand((64, 8, 128), dtype=torch.bfloat16)
+    rows = i32(0, 5, 21, 37, 40, 40, 40)
+    for n in (4, 6, 0):  # (6: two empty tiles; 0: no tiles, the input as it was)
+        got = run(kernel, q, rows, i32(n), what=f"ragged n={n}")
+        close(got, ragged_float64(q, rows, i32(n)), 1e-2, 0)
+    got = run(make_kernel(STATIC_RAGGED, tilejax_amd=tilejax_amd), rand((48, 8, 128)), i32(0, 16, 20, 36),
+              what="static ragged")
+    want = np.asarray(rand((48, 8, 128)).double())
+    want[:36] *= 3
+    close(got, want, 1e-5, 1e-5)
+
+
+def test_gathered_and_nested_windows():
+    pages, w, table = rand((10, 8, 128)), rand((10, 8, 128), 1), i32(3, 1, 4, 1, 5, 9, 2, 6)
+    close(run(make_kernel(GATHER), pages, table, w, what="gather"), gather_float64(pages, table, w), 1e-5, 1e-4)
+    pages, table, first, n = rand((6, 8, 128)), i32(5, 4, 3, 2), i32(0, 3), i32(2, 2)
+    want = np.stack([np.asarray(pages[5].double() + pages[4].double()), np.asarray(2 * pages[2].double())])
+    close(run(make_kernel(NESTED), pages, table, first, n, what="nested"), want, 1e-5, 1e-4)
+
+
+def test_scatter_into_an_input_updated_in_place():
+    x, pool, slots = rand((3, 16, 128)), rand((7, 16, 128), 1), i32(5, 0, 2)
+    out, new = run(make_kernel(SCATTER), x, pool, slots, what="scatter")
+    want_out, want_new = scatter_float64(x, pool, slots)
+    close(out, want_out, 0, 0)  # (x2: exact)
+    close(new, want_new, 1e-6, 0)
+    assert torch.equal(new[[1, 3, 4, 6]], pool[[1, 3, 4, 6]])  # the slots no tile stores, as they were
+
+
+def test_masked_tiles_of_an_input_updated_in_place_keep_its_values():
+    x = rand((256, 256))
+    out, new = run(make_kernel(MASKED_IN_PLACE), x, what="masked in place")
+    keep = np.kron(np.tril(np.ones((2, 2))), np.ones((128, 128))).astype(bool)
+    close(out, np.where(keep, np.asarray(x.double()) + 1, 0.0), 1e-6, 0)
+    close(new, np.where(keep, np.asarray(x.double()) * 3, np.asarray(x.double())), 1e-6, 0)
+
+
+def test_a_scan_stores_a_tile_per_step():
+    x, w = rand((512, 256)), rand((128, 128), 1) / 16
+    got = run(make_kernel(SCAN), x, w, what="scan")
+    for g, want in zip(got, scan_float64(x, w)):
+        close(g, want, 1e-4, 1e-4)
+
+
+def test_routing_inside_the_kernel():
+    kernel = make_kernel(MOE, route=route)
+    for seed in (0, 3):
+        x, router, w = moe_inputs(seed)
+        close(run(kernel, x, router, w, what=f"routed seed {seed}"), routed_float64(x, router, w), 2e-4, 2e-4)
+
+
+def test_indices_made_once_per_tile():
+    x = rand((5, 16, 256))
+    got = run(make_kernel(ONCE_PER_TILE, OFFSETS=OFFSETS), x, what="once per tile")
+    close(got, once_per_tile_float64(x), 1e-5, 1e-4)

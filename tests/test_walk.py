@@ -1,0 +1,647 @@
+"""Plans of the tile as written (tilejax_amd/walk.py), on the CPU: repeat loops, runtime loop bounds and a
+runtime count of tiles, ragged rows, windows gathered through index-array slices, outputs updated in place and
+scattered, outputs stored per step, and index arrays the tile code computes.
+
+The cases restate the reference's tests of these forms (tests/test_repeat_loops.py, test_runtime_ranges.py,
+test_in_place.py, test_step_outputs.py, test_computed_indices.py), each with a float64 closed form written
+from the loop nest's meaning (not from the kernel's code). Here `kernel.reference` (the nest run eagerly over
+jaxlite) is checked against those closed forms, the plans against the reference's own plan facts where they
+carry over (which values a tile keeps, step counts), and every generated kernel is compiled for gfx950 (no
+GPU needed); tests/test_gpu_walk.py runs the kernels.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import tilejax_amd
+from tests.helpers import make_kernel, rand
+from tilejax_amd import KernelError, jaxlite, runtime
+from tilejax_amd.jaxlite import jax, jnp
+
+
+def f64(a):
+    return np.asarray(torch.as_tensor(np.asarray(a)).double() if not isinstance(a, torch.Tensor) else a.double())
+
+
+def i32(*values):
+    return torch.tensor(values, dtype=torch.int32)
+
+
+def close(got, want, rtol=1e-4, atol=1e-3):
+    np.testing.assert_allclose(f64(got), want, rtol=rtol, atol=atol)
+
+
+def compiles(lowered):
+    """The generated kernel compiles for gfx950."""
+    assert lowered.program.notes.get("walk"), lowered.program.notes
+    runtime.compile_source(lowered.source, f"{lowered.program.name}.hip")
+
+
+# ------------------------------------------------------------------------------------- repeat loops
+
+FFN_STACK = """
+def ffn_stack(x, gamma, w_up, w_down):
+    M, D = x.shape
+    L, _, F = w_up.shape
+    out = jnp.zeros((M, D), jnp.float32)
+    for i in range(0, M, 128):
+        h = x[i : i + 128, :]
+        for l in range(L):  # a layer per iteration
+            n = h * gamma[l, 0:1, :]
+            y = jnp.zeros((128, D))
+            for f in range(0, F, 128):
+                y += jnp.maximum(n @ w_up[l, :, f : f + 128], 0.0) @ w_down[l, f : f + 128, :]
+            h = h + y * (l + 1)
+        out = out.at[i : i + 128, :].set(h)
+    return out
+"""
+
+
+def ffn_stack_float64(x, gamma, w_up, w_down):
+    h = f64(x)
+    for layer in range(w_up.shape[0]):
+        n = h * f64(gamma[layer])
+        h = h + (layer + 1) * np.maximum(n @ f64(w_up[layer]), 0) @ f64(w_down[layer])
+    return h
+
+
+def ffn_inputs(layers=3):
+    return (rand((256, 128)), 1 + 0.1 * rand((layers, 1, 128), 1), rand((layers, 128, 256), 2) / 12,
+            rand((layers, 256, 128), 3) / 16)
+
+
+LAYERED = """
+def layered(x, w, limits):
+    M, K = x.shape
+    L = w.shape[0]
+    out = jnp.zeros((M, 128), jnp.float32)
+    for i in range(0, M, 128):
+        a = jnp.zeros((128, 128))
+        for k in range(0, K, 128):  # a reduction loop before the repeat loop
+            a += x[i : i + 128, k : k + 128]
+        h = a * 0.5
+        for l in range(L):
+            y = jnp.zeros((128, 128))
+            for f in range(0, 384, 128):  # layer l runs l + 1 blocks: a mask reading the repeat loop
+                if f > l * 128:
+                    continue
+                y += h @ w[l, f : f + 128, :]
+            h = h + y * 0.1
+            z = h * 0
+            for g in range(0, 256, 128):  # a mask read when the kernel runs
+                if g >= limits[l]:
+                    continue
+                z += x[i : i + 128, g : g + 128] * (l + 1)
+            h = h + z
+        t = h * 2
+        for c in range(0, 256, 128):  # one after it
+            t = t + x[i : i + 128, c : c + 128]
+        out = out.at[i : i + 128, :].set(t)
+    return out
+"""
+
+
+def layered_float64(x, w, limits):
+    x, w = f64(x), f64(w)
+    out = []
+    for i in range(0, x.shape[0], 128):
+        blocks = [x[i : i + 128, k : k + 128] for k in range(0, x.shape[1], 128)]
+        h = sum(blocks) * 0.5
+        for layer in range(w.shape[0]):
+            y = sum(h @ w[layer, f : f + 128] for f in range(0, 128 * (layer + 1), 128) if f < 384)
+            h = h + y * 0.1
+            h = h + sum((layer + 1) * blocks[g // 128] for g in range(0, 256, 128) if g < limits[layer])
+        out.append(2 * h + blocks[0] + blocks[1])
+    return np.concatenate(out)
+
+
+TWO_REPEATS = """
+def two_repeats(x, w):
+    out = jnp.zeros((128, 128), jnp.float32)
+    for i in range(0, 128, 128):
+        h = x[i : i + 128, :]
+        for l in range(2):
+            for f in range(0, 256, 128):
+                if f > l * 128:
+                    continue
+                h = h + w[l, f : f + 128, :]
+        u = h * 1
+        for m in range(2):
+            v = u * 2
+            for g in range(0, 256, 128):
+                v = v + w[m, g : g + 128, :] * (m + 1)
+            u = v
+        out = out.at[i : i + 128, :].set(u)
+    return out
+"""
+
+
+def two_repeats_float64(x, w):
+    xf, wf = f64(x), f64(w)
+    h = xf + wf[0, :128] + wf[1, :128] + wf[1, 128:]
+    for m in range(2):
+        h = 2 * h + (m + 1) * (wf[m, :128] + wf[m, 128:])
+    return h
+
+
+def test_repeat_loop_carries_layers():
+    kernel = make_kernel(FFN_STACK)
+    inputs = ffn_inputs()
+    close(kernel.reference(*inputs), ffn_stack_float64(*inputs))
+    lowered = kernel.lower(*inputs)
+    plan = lowered.plan
+    assert plan.walk and set(plan.kept) == {"h", "n", "y"}
+    assert [b.kind for b in plan.tree] == ["code", "repeat", "code"]
+    assert lowered.steps == 2 * 3 * 2  # (tiles, layers, blocks of hidden units)
+    compiles(lowered)
+
+
+@pytest.mark.parametrize("limits", [(256, 0, 100), (0, 0, 0)])
+def test_reductions_around_and_in_a_repeat_loop_with_masks(limits):
+    kernel = make_kernel(LAYERED)
+    x, w = rand((256, 256)), rand((3, 384, 128), 1) / 20
+    lim = i32(*limits)
+    close(kernel.reference(x, w, lim), layered_float64(x, w, limits))
+    lowered = kernel.lower(x, w, lim)
+    assert lowered.plan.walk and [b.kind for b in lowered.plan.tree] == ["code", "loop", "code", "repeat", "code",
+                                                                         "loop", "code"]
+    compiles(lowered)
+
+
+def test_two_repeat_loops():
+    kernel = make_kernel(TWO_REPEATS)
+    x, w = rand((128, 128)), rand((2, 256, 128), 1)
+    close(kernel.reference(x, w), two_repeats_float64(x, w))
+    lowered = kernel.lower(x, w)
+    assert lowered.steps == 1 + 2 + 2 * 2  # (the masked step of the first loop's first iteration skipped)
+    compiles(lowered)
+
+
+def test_repeat_loop_errors():
+    nested = """
+    def f(x):
+        out = jnp.zeros((128, 128))
+        for i in range(0, 128, 128):
+            h = x[i : i + 128, :]
+            for l in range(2):
+                for m in range(2):
+                    for f in range(0, 128, 128):
+                        h = h + x[f : f + 128, :]
+            out = out.at[i : i + 128, :].set(h)
+        return out
+    """
+    with pytest.raises(KernelError, match="repeat loops don't nest"):
+        make_kernel(nested)
+    changes_shape = """
+    def f(x):
+        out = jnp.zeros((128, 128))
+        for i in range(0, 128, 128):
+            h = x[i : i + 128, :]
+            for l in range(2):
+                for f in range(0, 128, 128):
+                    h = jnp.concatenate([h, h], axis=0)
+            out = out.at[i : i + 128, :].set(h[0:128, :])
+        return out
+    """
+    with pytest.raises(KernelError, match="changes shape"):
+        make_kernel(changes_shape).lower(rand((128, 128)))
+
+
+# ------------------------------------------------------------------------------------- runtime ranges
+
+SUMS = """
+def sums(cache, lengths):
+    B, S, D = cache.shape
+    out = jnp.zeros((B, 8, D))
+    for b in range(B):
+        acc = jnp.zeros((8, D))
+        for j in range(0, lengths[b], 128):  # the cache's blocks up to its length
+            rows = j + jax.lax.broadcasted_iota(jnp.int32, (128, D), 0)
+            acc += jnp.sum(jnp.where(rows < lengths[b], cache[b, j : j + 128, :], 0.0).reshape(16, 8, D), axis=0)
+        out = out.at[b, :, :].set(acc)
+    return out
+"""
+
+
+def sums_float64(cache, lengths):
+    out = np.zeros((cache.shape[0], 8, cache.shape[2]))
+    for b, n in enumerate(np.asarray(lengths)):
+        rows = np.concatenate([f64(cache[b, :n]), np.zeros((-n % 8, cache.shape[2]))])
+        out[b] = rows.reshape(-1, 8, cache.shape[2]).sum(0)
+    return out
+
+
+SPANS = """
+def spans(x, w, lo, hi):
+    B, S, D = x.shape
+    out = jnp.zeros((B, 8, D))
+    for b in range(B):
+        acc = jnp.zeros((8, D))
+        for j in range(lo[b], hi[b], 8):  # from lo[b] to hi[b]
+            acc += x[b, j : j + 8, :]
+        for k in range(0, 256, 128):  # a static loop after it
+            acc += jnp.sum(w[k : k + 128, :].reshape(16, 8, D), axis=0)
+        out = out.at[b, :, :].set(acc)
+    return out
+"""
+
+
+def spans_float64(x, w, lo, hi):
+    want = np.stack([f64(x[b, int(a):int(z)]).reshape(-1, 8, x.shape[2]).sum(0) for b, (a, z) in enumerate(zip(lo, hi))])
+    return want + f64(w).reshape(-1, 8, w.shape[1]).sum(0)
+
+
+COUNTED = """
+def counted(x, n):
+    B, S, _, D = x.shape
+    out = jnp.zeros((B, 8, D))
+    for b in range(B):
+        if b == 1:
+            continue
+        acc = jnp.zeros((8, D))
+        for j in range(n[b]):
+            acc += x[b, j, :, :]
+        out = out.at[b, :, :].set(acc)
+    return out
+"""
+
+
+def counted_float64(x, n):
+    want = np.stack([f64(x[b, : min(int(c), x.shape[1])]).sum(0) for b, c in enumerate(n)])
+    want[1] = 0
+    for b, c in enumerate(n):  # steps past the dim read its last block (the index is clamped, as JAX clamps)
+        if b != 1 and int(c) > x.shape[1]:
+            want[b] += (int(c) - x.shape[1]) * f64(x[b, -1])
+    return want
+
+
+def test_runtime_range_steps_through_each_tiles_blocks():
+    kernel = make_kernel(SUMS)
+    cache, lengths = rand((4, 512, 128)), i32(0, 1, 300, 512)  # (an empty range)
+    close(kernel.reference(cache, lengths), sums_float64(cache, lengths), 1e-5, 1e-4)
+    lowered = kernel.lower(cache, lengths)
+    assert lowered.plan.walk and not lowered.plan.bounds["j"].static
+    compiles(lowered)
+
+
+def test_runtime_ranges_with_a_start_and_a_static_loop():
+    kernel = make_kernel(SPANS)
+    x, w = rand((3, 64, 128)), rand((256, 128), 1)
+    lo, hi = i32(0, 8, 16), i32(16, 8, 64)
+    close(kernel.reference(x, w, lo, hi), spans_float64(x, w, lo, hi), 1e-5, 1e-4)
+    compiles(kernel.lower(x, w, lo, hi))
+
+
+def test_runtime_range_indexes_with_its_value_under_a_tile_mask():
+    kernel = make_kernel(COUNTED)
+    x, n = rand((3, 4, 8, 128)), i32(2, 4, 9)  # (9: past the dim, clamped)
+    close(kernel.reference(x, n), counted_float64(x, n), 1e-5, 1e-4)
+    compiles(kernel.lower(x, n))
+
+
+# ------------------------------------------------------------------------------------- ragged rows, gathers
+
+RAGGED = """
+def ragged(q, rows, n):
+    T, D, dtype = q.shape[0], q.shape[2], q.dtype
+    out = q
+    for k in range(n[0]):  # the tiles, counted as the kernel runs
+        x = q[tilejax_amd.rows(rows[k], rows[k + 1], 16), :, :]
+        acc = jnp.zeros((16, 8, D))
+        for j in range(0, 2 * D, D):
+            acc += x.astype(jnp.float32) * 2
+        out = out.at[tilejax_amd.rows(rows[k], rows[k + 1], 16), :, :].set(acc.astype(dtype))
+    return out
+"""
+
+
+def ragged_float64(q, rows, n):
+    want = f64(q).copy()
+    want[: int(rows[int(n[0])])] *= 4
+    return want
+
+
+STATIC_RAGGED = """
+def static_ragged(q, rows):
+    out = q
+    for k in range(3):
+        acc = jnp.zeros((16, 8, 128))
+        for j in range(0, rows[k + 1] - rows[k], 16):
+            acc += q[tilejax_amd.rows(rows[k], rows[k + 1], 16), :, :] * 3
+        out = out.at[tilejax_amd.rows(rows[k], rows[k + 1], 16), :, :].set(acc)
+    return out
+"""
+
+GATHER = """
+def gather(pages, table, w):
+    B = table.shape[0] // 4
+    out = jnp.zeros((B, 8, 128))
+    for b in range(B):
+        acc = jnp.sum(w[table[b * 4 : b * 4 + 2], :, :], axis=0) * 0  # (a tile's own gathered window)
+        for p in range(0, 4, 2):  # two pages a step, gathered through the table
+            acc += jnp.sum(pages[table[b * 4 + p : b * 4 + p + 2], :, :], axis=0) * w[table[0 : 0 + 2], :, :][0]
+        out = out.at[b, :, :].set(acc)
+    return out
+"""
+
+
+def gather_float64(pages, table, w):
+    t = np.asarray(table).reshape(-1, 4)
+    return np.stack([f64(pages)[t[b]].sum(0) * f64(w)[int(table[0])] for b in range(t.shape[0])])
+
+
+NESTED = """
+def nested(pages, table, first, n):
+    out = jnp.zeros((2, 8, 128))
+    for b in range(2):
+        acc = jnp.zeros((8, 128))
+        for p in range(n[b]):
+            acc += pages[table[first[b] + p], :, :]
+        out = out.at[b, :, :].set(acc)
+    return out
+"""
+
+
+def test_ragged_rows_and_a_runtime_count_of_tiles():
+    kernel = make_kernel(RAGGED, tilejax_amd=tilejax_amd)
+    q = rand((64, 8, 128), dtype=torch.bfloat16)
+    rows, n = i32(0, 5, 21, 37, 40, 40, 40), i32(4)  # tiles of 5, 16, 16 and 3 rows; rows 40.. untouched
+    close(kernel.reference(q, rows, n), ragged_float64(q, rows, n), 1e-2, 0)
+    np.testing.assert_array_equal(f64(kernel.reference(q, rows, i32(0))), f64(q))  # no tiles at all
+    lowered = kernel.lower(q, rows, n)
+    assert lowered.schedule.runtime_tiles and lowered.plan.aliases == {"out": 0}
+    compiles(lowered)
+
+
+def test_ragged_stores_of_static_tiles():
+    kernel = make_kernel(STATIC_RAGGED, tilejax_amd=tilejax_amd)
+    q, rows = rand((48, 8, 128)), i32(0, 16, 20, 36)
+    want = f64(q).copy()
+    want[:36] *= 3
+    close(kernel.reference(q, rows), want, 1e-5, 1e-5)
+    compiles(kernel.lower(q, rows))
+
+
+def test_windows_gathered_through_index_array_slices():
+    kernel = make_kernel(GATHER)
+    pages, w = rand((10, 8, 128)), rand((10, 8, 128), 1)
+    table = i32(3, 1, 4, 1, 5, 9, 2, 6)
+    close(kernel.reference(pages, table, w), gather_float64(pages, table, w), 1e-5, 1e-4)
+    lowered = kernel.lower(pages, table, w)
+    assert [ix.name for ix in lowered.plan.indices] == ["table"]
+    assert lowered.plan.accesses["pages"].dims[0].gather is not None
+    compiles(lowered)
+
+
+def test_nested_elements_in_windows_are_clamped():
+    kernel = make_kernel(NESTED)
+    pages, table, first, n = rand((6, 8, 128)), i32(5, 4, 3, 2), i32(0, 3), i32(2, 2)  # 3 + 1: past the table
+    want = np.stack([f64(pages[5]) + f64(pages[4]), f64(pages[2]) + f64(pages[2])])
+    close(kernel.reference(pages, table, first, n), want, 1e-5, 1e-4)
+    compiles(kernel.lower(pages, table, first, n))
+
+
+# ------------------------------------------------------------------------------------- in place, per step
+
+SCATTER = """
+def scatter(x, pool, slots):
+    B, H, D = x.shape
+    new = pool
+    out = jnp.zeros((B, H, D))
+    for b in range(B):
+        for h in range(0, H, 8):
+            old = pool[slots[b], h : h + 8, :]
+            out = out.at[b, h : h + 8, :].set(old * 2)
+            new = new.at[slots[b], h : h + 8, :].set(old + x[b, h : h + 8, :])
+    return out, new
+"""
+
+
+def scatter_float64(x, pool, slots):
+    pool, x = f64(pool), f64(x)
+    out, new = np.zeros(x.shape), pool.copy()
+    for b, s in enumerate(np.asarray(slots)):
+        out[b], new[s] = 2 * pool[s], pool[s] + x[b]
+    return out, new
+
+
+MASKED_IN_PLACE = """
+def masked_in_place(x):
+    out = jnp.zeros((256, 256))
+    new = x
+    for i in range(0, 256, 128):
+        for j in range(0, 256, 128):
+            if j > i:
+                continue
+            out = out.at[i : i + 128, j : j + 128].set(x[i : i + 128, j : j + 128] + 1)
+            new = new.at[i : i + 128, j : j + 128].set(x[i : i + 128, j : j + 128] * 3)
+    return out, new
+"""
+
+SCAN = """
+def scan(x, w):
+    S, D = x.shape
+    out = jnp.zeros((S, D), jnp.float32)
+    last = jnp.zeros((8, D), jnp.float32)
+    for j in range(0, D, 128):
+        state = jnp.zeros((128, 128), jnp.float32)
+        for i in range(0, S, 128):  # a chunk per step: its outputs stored by the step
+            state = state * 0.5 + x[i : i + 128, j : j + 128] @ w[:, :]
+            out = out.at[i : i + 128, j : j + 128].set(state)
+        last = last.at[:, j : j + 128].set(state[0:8, :])
+    return out, last
+"""
+
+
+def scan_float64(x, w):
+    x, w = f64(x), f64(w)
+    out = np.zeros_like(x)
+    for j in range(0, x.shape[1], 128):
+        state = np.zeros((128, 128))
+        for i in range(0, x.shape[0], 128):
+            state = state * 0.5 + x[i : i + 128, j : j + 128] @ w
+            out[i : i + 128, j : j + 128] = state
+    last = np.concatenate([out[-128:-120, j : j + 128] for j in range(0, x.shape[1], 128)], 1)
+    return out, last
+
+
+def test_scatter_into_an_input_updated_in_place():
+    kernel = make_kernel(SCATTER)
+    x, pool, slots = rand((3, 16, 128)), rand((7, 16, 128), 1), i32(5, 0, 2)
+    got_out, got_new = kernel.reference(x, pool, slots)
+    want_out, want_new = scatter_float64(x, pool, slots)
+    close(got_out, want_out, 1e-6, 0)
+    close(got_new, want_new, 1e-6, 0)  # slots 1, 3, 4, 6 as they were
+    assert torch.equal(pool, rand((7, 16, 128), 1))  # the input itself is unchanged
+    lowered = kernel.lower(x, pool, slots)
+    assert lowered.plan.aliases == {"new": 1} and lowered.plan.outputs[1].fill is None
+    compiles(lowered)
+
+
+def test_masked_tiles_of_an_input_updated_in_place_keep_its_values():
+    kernel = make_kernel(MASKED_IN_PLACE)
+    x = rand((256, 256))
+    out, new = kernel.reference(x)
+    keep = np.kron(np.tril(np.ones((2, 2))), np.ones((128, 128))).astype(bool)
+    close(out, np.where(keep, f64(x) + 1, 0.0), 1e-6, 0)
+    close(new, np.where(keep, f64(x) * 3, f64(x)), 1e-6, 0)
+    compiles(kernel.lower(x))
+
+
+def test_a_scan_stores_a_tile_per_step():
+    kernel = make_kernel(SCAN)
+    x, w = rand((512, 256)), rand((128, 128), 1) / 16
+    got = kernel.reference(x, w)
+    for g, want in zip(got, scan_float64(x, w)):
+        close(g, want, 1e-4, 1e-4)
+    lowered = kernel.lower(x, w)
+    assert lowered.plan.walk and lowered.steps == 2 * 4
+    compiles(lowered)
+
+
+@pytest.mark.parametrize(("code", "message"), [
+    ("out = jnp.zeros((7, 8, 128))\n    for b in range(3):\n        out = out.at[slots[b], :, :].set(x[b, :, :])",
+     "an index array places this tile, so no tile might store the rest of `out`: allocate it as an input updated in "
+     "place"),
+    ("out = slots\n    for b in range(3):\n        out = out.at[b].set(slots[b])",
+     "output `out` updates `slots` in place, but `slots` is an index array"),
+    ("out = wrong\n    for b in range(3):\n        out = out.at[b, :, :].set(x[b, :, :])",
+     r"allocate output `out` with jnp.zeros\(shape, dtype\) or jnp.full\(shape, value, dtype\), or as an input "
+     r"updated in place \(`out = x`\)"),
+])
+def test_in_place_errors(code, message):
+    kernel = make_kernel(f"def f(x, slots):\n    {code}\n    return out\n", wrong=3)
+    with pytest.raises(KernelError, match=message):
+        kernel.lower(rand((3, 8, 128)), i32(0, 1, 2))
+
+
+def test_an_input_updated_in_place_whole():
+    kernel = make_kernel("def f(x, slots):\n    out = x\n    for b in range(3):\n"
+                         "        out = out.at[b, :, :].set(x[b, :, :])\n    return out\n")
+    x = rand((3, 8, 128))
+    close(kernel.reference(x, i32(0, 1, 2)), f64(x), 0, 0)
+    compiles(kernel.lower(x, i32(0, 1, 2)))
+
+
+# ------------------------------------------------------------------------------------- computed index arrays
+
+E, K = 8, 2
+
+
+def route(logits):
+    """The K experts with the highest summed logits over the tokens, how many to use (the second only if its
+    score is positive), and each token's weight for each, (K, T, 1)."""
+    lanes = jax.lax.broadcasted_iota(jnp.int32, (1, logits.shape[1]), 1)
+    score = jnp.where(lanes < E, jnp.sum(logits, axis=0, keepdims=True), -jnp.inf)
+    chosen, weights, scores = [], [], []
+    for _ in range(K):
+        best = jnp.max(score, axis=1, keepdims=True)
+        pick = jnp.min(jnp.where(score == best, lanes, logits.shape[1]), axis=1, keepdims=True)
+        chosen.append(pick)
+        scores.append(best)
+        weights.append(jax.nn.sigmoid(jnp.sum(jnp.where(lanes == pick, logits, 0.0), axis=1, keepdims=True)))
+        score = jnp.where(lanes == pick, -jnp.inf, score)
+    ids = jnp.concatenate(chosen, axis=1).reshape(K).astype(jnp.int32)
+    n = (1 + (scores[1] > 0).astype(jnp.int32)).reshape(1)
+    return ids, n, jnp.stack(weights)
+
+
+MOE = """
+def routed(x, router, w):
+    T, D = x.shape
+    L = w.shape[0]
+    out = jnp.zeros((T, D))
+    for i in range(0, T, T):
+        h = x[i : i + T, :]
+        for layer in range(L):
+            blocks = jnp.stack([h[:, 0:128], h[:, 128:256]])
+            logits = jnp.zeros((T, 128))
+            for d in range(0, D, 128):  # the router, a block of rows a step
+                logits += blocks[d // 128] @ router[layer, d : d + 128, :]
+            chosen, n, weights = route(logits)
+            acc = jnp.zeros((T, D))
+            for c in range(0, n[0] * D, D):  # the chosen experts: as many as the routing says
+                acc += weights[c // D] * (h @ w[layer, chosen[c // D], :, :])
+            h = h + acc
+        out = out.at[i : i + T, :].set(h)
+    return out
+"""
+
+
+def routed_float64(x, router, w):
+    """The routing decided in f32 as the kernel decides it (from float64 logits rounded to f32), the rest in
+    float64."""
+    h = f64(x)
+    for layer in range(w.shape[0]):
+        logits = h @ f64(router[layer])
+        ids, n, weights = (np.asarray(a) for a in route(jaxlite.Array(torch.tensor(logits, dtype=torch.float32))))
+        h = h + sum(f64(weights[k]) * (h @ f64(w[layer, ids[k]])) for k in range(int(n[0])))
+    return h
+
+
+def moe_inputs(seed=0):
+    return rand((8, 256), seed), rand((3, 256, 128), seed + 1) * 0.1, rand((3, E, 256, 256), seed + 2) * 0.05
+
+
+def test_routing_inside_the_kernel_places_and_counts_later_steps():
+    kernel = make_kernel(MOE, route=route)
+    x, router, w = moe_inputs()
+    np.testing.assert_allclose(f64(kernel.reference(x, router, w)), routed_float64(x, router, w), rtol=2e-4,
+                               atol=2e-4)
+    lowered = kernel.lower(x, router, w)
+    kept = lowered.plan.kept
+    assert kept["chosen"].shape == (K,) and kept["n"].shape == (1,) and kept["chosen"].dtype == jaxlite.int32
+    compiles(lowered)
+
+
+OFFSETS = (0, 2)
+
+ONCE_PER_TILE = """
+def once_per_tile(x):
+    out = jnp.zeros((16, 128))
+    for i in range(0, 16, 8):
+        acc = jnp.zeros((8, 128))
+        for d in range(0, 256, 128):
+            acc += x[0, i : i + 8, d : d + 128]
+        n = (jnp.sum(acc > 0) % 3).astype(jnp.int32).reshape(1)  # made once per tile
+        for c in range(1, n[0] + OFFSETS[1] + 1):
+            acc += x[c, i : i + 8, 0:128]
+        out = out.at[i : i + 8, :].set(acc)
+    return out
+"""
+
+
+def once_per_tile_float64(x):
+    x = f64(x)
+    out = []
+    for i in range(0, 16, 8):
+        acc = x[0, i : i + 8, :128] + x[0, i : i + 8, 128:]
+        n = int((acc > 0).sum()) % 3
+        for c in range(1, n + OFFSETS[1] + 1):
+            acc = acc + x[min(c, x.shape[0] - 1), i : i + 8, :128]
+        out.append(acc)
+    return np.concatenate(out)
+
+
+def test_indices_made_once_per_tile_and_constants_in_bounds():
+    kernel = make_kernel(ONCE_PER_TILE, OFFSETS=OFFSETS)
+    x = rand((5, 16, 256))
+    close(kernel.reference(x), once_per_tile_float64(x), 1e-5, 1e-4)
+    compiles(kernel.lower(x))
+
+
+def test_the_step_planner_still_takes_the_phases_of_steps_form():
+    """A nest of the phases-of-steps form keeps its step plan (the kernel families read it)."""
+    kernel = make_kernel("""
+    def mm(x, y):
+        out = jnp.zeros((256, 256), jnp.float32)
+        for i in range(0, 256, 128):
+            for j in range(0, 256, 128):
+                acc = jnp.zeros((128, 128), jnp.float32)
+                for k in range(0, 256, 128):
+                    acc += x[i : i + 128, k : k + 128] @ y[k : k + 128, j : j + 128]
+                out = out.at[i : i + 128, j : j + 128].set(acc)
+        return out
+    """)
+    assert not kernel.lower(rand((256, 256)), rand((256, 256))).plan.walk

@@ -20,6 +20,7 @@ from typing import Any
 from .api import Kernel, Lowered, compare, kernel
 from .errors import KernelError
 from .pipeline import Pipeline
+from .ragged import rows
 from .tunable import choice, tunable
 
 __all__ = [
@@ -36,6 +37,7 @@ __all__ = [
     "enable_profiling",
     "kernel",
     "profile",
+    "rows",
     "tunable",
 ]
 

@@ -45,6 +45,11 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
     from . import decode, flash, gemm, generic
 
     name = _symbol(plan)
+    if plan.walk:
+        if cursor:
+            raise KernelError(f"{plan.nest.name}: a plan of the tile as written finds its steps as it runs already "
+                              "(no cursor mode)")
+        return generic.lower_walk(plan, schedule, pipeline, name, trace=trace)
     family_error = None
     try:
         found = gemm.match(plan)

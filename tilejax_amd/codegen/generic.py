@@ -25,9 +25,11 @@ update of the scope is computed, so updates that read other carried values see t
 
 from __future__ import annotations
 
+import ast
+import copy
 import inspect
 import math
-from typing import Any, Callable, Dict, List, Optional, Sequence, Set, Tuple
+from typing import Any, Callable, Dict, List, Optional, Sequence, Set, Tuple, Union
 
 import numpy as np
 
@@ -37,12 +39,13 @@ from ..jaxlite import DType, Node
 from ..pipeline import Pipeline
 from ..plan import Plan
 from ..schedule import CODE_SHIFT, STEP_CODE, Schedule
+from ..syntax import bound, used
 from .common import Index, decode_fill, decode_tile, static_tile_steps, strides, work_lists
 from .device import PRELUDE
-from .expr import ElementEmitter, _broadcast_index, _rounded, ctype, literal
+from .expr import ElementEmitter, _broadcast_index, _rounded, ctype, int_expr, literal
 from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 
-__all__ = ["lower"]
+__all__ = ["lower", "lower_walk"]
 
 THREADS = 256
 MEM_BUDGET = 2 << 30  # bytes of tile memory over the whole grid
@@ -179,6 +182,23 @@ class _Elements(ElementEmitter):
                 inside.append(f"(({idx[k]}) >= {lo} && ({idx[k]}) < {lo + d})")
             cond = " && ".join(inside) or "true"
             return f"(({cond}) ? ({ct})({self._at(src, tuple(inner))}) : ({ct})0)"
+        if op == "getitem" and any(isinstance(k, Node) for k in (a[1] if isinstance(a[1], tuple) else (a[1],))):
+            # an element chosen by a traced integer (`weights[c // D]`): clamped into its dim, as JAX clamps
+            src, key = a[0], (a[1] if isinstance(a[1], tuple) else (a[1],))
+            inner, k_out = [], 0
+            for k, d in enumerate(src.shape):
+                sel = key[k] if k < len(key) else slice(None)
+                if isinstance(sel, Node):
+                    inner.append(f"ak_clamp((int)({self._at(sel, ())}), 0, {d - 1})")
+                elif isinstance(sel, slice):
+                    start, _, step = sel.indices(d)
+                    inner.append(f"({start} + ({idx[k_out]}) * {step})")
+                    k_out += 1
+                elif isinstance(sel, int):
+                    inner.append(str(sel % d))
+                else:
+                    raise KernelError("tile values are indexed per element by integers, slices and traced integers")
+            return self._at(src, tuple(inner))
         if op == "repeat":
             b = _bound_args(n)
             src, reps, axis = b["x"], b["repeats"], b["axis"]
@@ -222,6 +242,7 @@ class _Generic:
         phase_vars = {ph.range.var for ph in plan.phases}
         # reduction loops of one iteration and no mask run inline: their variable is their one value
         self.inline = {r.var: r.start for r in plan.reductions if r.var not in phase_vars}
+        self.types: Dict[str, Any] = plan.carried  # the values a tile keeps in its memory between scopes
         for c, car in plan.carried.items():
             self.buf.add(f"c_{c}", math.prod(car.shape), _stype(car.dtype))
 
@@ -267,10 +288,11 @@ class _Generic:
                 return f"{self.buf.ref(name)}[{_flat(n.shape, idx)}]"
             if n.op == "loop":
                 return f"lv_{n.kwargs['var']}"
-            if n.op == "index":
+            if n.op == "index":  # an index-array element, clamped into the array as JAX clamps
                 ix = plan.index(n.kwargs["array"])
                 parts = [em.at(i, ()) if isinstance(i, Node) else literal(i) for i in n.args]
-                flat = " + ".join(f"({p}) * {s}" for p, s in zip(parts, strides(ix.shape))) or "0"
+                flat = " + ".join(f"ak_clamp((int)({p}), 0, {d - 1}) * {s}"
+                                  for p, s, d in zip(parts, strides(ix.shape), ix.shape)) or "0"
                 return f"args.{ix.name}[{flat}]"
             if n.op in _WHOLE:
                 raise KernelError(f"`{n.op}` read before it is computed")
@@ -434,23 +456,27 @@ class _Generic:
         scope, the output stores)."""
         plan = self.plan
         scope = plan.scopes[key]
-        updates = []
-        for c in plan.carried:
-            if c not in scope.values:
-                continue
+        updates = self._updates(scope, [c for c in plan.carried if c in scope.values])
+        stores = [(o, scope.stores[o.name]) for o in plan.outputs] if store else []
+        return self._emit(updates, stores, ind)
+
+    @staticmethod
+    def _updates(scope: Any, names: Sequence[str]) -> List[Tuple[str, Any]]:
+        """The kept values a scope assigns anew (not those it leaves as they came in)."""
+        out = []
+        for c in names:
             v = scope.values[c]
             leaf = scope.carried_in.get(c)
             if isinstance(v, jaxlite.Sym) and leaf is not None and v.node is leaf:
                 continue  # unchanged
-            updates.append((c, v))
+            out.append((c, v))
+        return out
+
+    def _emit(self, updates: List[Tuple[str, Any]], stores: List[Tuple[Any, Any]], ind: str) -> List[str]:
+        """Passes computing what the updates and stores read, the updates (staged), the stores, then the
+        staged values copied over the kept ones."""
         roots = [v.node for _, v in updates if isinstance(v, jaxlite.Sym)]
-        stores = []
-        if store:
-            for out in plan.outputs:
-                val = scope.stores[out.name]
-                stores.append((out, val))
-                if isinstance(val, jaxlite.Sym):
-                    roots.append(val.node)
+        roots += [val.node for _, val in stores if isinstance(val, jaxlite.Sym)]
         out: List[str] = []
         materialized: Dict[int, str] = {}
         order = self._needed(roots)
@@ -468,7 +494,7 @@ class _Generic:
         em = self._elements(materialized)
         staged = []
         for c, v in updates:
-            car = plan.carried[c]
+            car = self.types[c]
             stage = self.buf.add(f"u_{c}", math.prod(car.shape), _stype(car.dtype))
             staged.append((c, stage))
             if isinstance(v, jaxlite.Sym):
@@ -485,7 +511,7 @@ class _Generic:
         if staged:
             lines = []
             for c, stage in staged:
-                car = plan.carried[c]
+                car = self.types[c]
                 size = math.prod(car.shape)
                 lines.append(f"{ind}for (int e_ = tid; e_ < {size}; e_ += {THREADS}) "
                              f"{self.buf.ref('c_' + c)}[e_] = {self.buf.ref(stage)}[e_];")
@@ -680,6 +706,280 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
 """
 
 
+class _Walk(_Generic):
+    """The generic kernel for a plan of the tile as written (tilejax_amd/walk.py): each tile walks the
+    plan's tree of blocks, straight-line code as passes, reduction and repeat loops as loops whose bounds and
+    masks it evaluates as it runs (from loop variables, constants, index-array elements and elements of
+    index arrays the tile code computed), reading windows whose starts it evaluates the same way (clamped
+    into their dims, as JAX clamps) and storing outputs where the stores' windows say. Before it, a launch
+    fills every output: with its allocation's value, or, for an input updated in place, with that input.
+    A runtime count of tiles is counted on the device; the kernel is persistent over tiles either way."""
+
+    def __init__(self, plan: Plan, sch: Schedule, name: str, trace: bool) -> None:
+        self.plan, self.sch, self.name, self.trace = plan, sch, name, trace
+        self.buf = _Buffers()
+        self.index = Index(plan, lambda v: f"lv_{v}")
+        self.tables = {}
+        self.lines = []
+        self.inline = {}
+        self.types = plan.kept
+        for c, car in plan.kept.items():
+            self.buf.add(f"c_{c}", math.prod(car.shape), _stype(car.dtype))
+        nest = plan.nest
+        self.loop_vars = {loop.var for loop in nest.loops}
+        self.runtime = self.loop_vars | {ix.name for ix in plan.indices} | bound(nest.tile)
+
+    # ------------------------------------------------------------------------------------------ integers
+
+    def _fold(self, node: ast.expr) -> ast.expr:
+        """`node` with every subexpression that reads nothing the kernel learns as it runs evaluated now."""
+        plan, runtime = self.plan, self.runtime
+
+        class Fold(ast.NodeTransformer):
+            def visit(self, n: ast.AST) -> ast.AST:
+                if isinstance(n, ast.expr) and not isinstance(n, ast.Constant) and not used(n) & runtime:
+                    value = plan.eval(n)
+                    if isinstance(value, (bool, np.bool_)):
+                        return ast.copy_location(ast.Constant(bool(value)), n)
+                    if isinstance(value, (int, np.integer)):
+                        return ast.copy_location(ast.Constant(int(value)), n)
+                return self.generic_visit(n)
+
+        return Fold().visit(copy.deepcopy(node))  # type: ignore[return-value]
+
+    def _name(self, v: str) -> Optional[str]:
+        if v in self.loop_vars:
+            return f"lv_{v}"
+        value = self.plan.env.get(v)
+        if isinstance(value, (bool, np.bool_)):
+            return "true" if value else "false"
+        if isinstance(value, (int, np.integer)):
+            return str(int(value))
+        return None
+
+    def _element(self, sub: ast.Subscript) -> str:
+        """An element of an index array (an input) or of an int32 array the tile keeps, clamped into it."""
+        if not isinstance(sub.value, ast.Name):
+            raise KernelError(f"`{ast.unparse(sub)}` isn't an element of an index array")
+        name = sub.value.id
+        if name in {ix.name for ix in self.plan.indices}:
+            shape, ref = self.plan.index(name).shape, f"args.{name}"
+        elif name in self.plan.kept and self.plan.kept[name].dtype.kind in "iu":
+            shape, ref = self.plan.kept[name].shape, self.buf.ref(f"c_{name}")
+        else:
+            raise KernelError(f"`{ast.unparse(sub)}`: the kernel reads elements of index arrays and of int32 arrays "
+                              "the tile code computed, not of this")
+        dims = list(sub.slice.elts) if isinstance(sub.slice, ast.Tuple) else [sub.slice]
+        if len(dims) != len(shape) or any(isinstance(d, ast.Slice) for d in dims):
+            raise KernelError(f"`{ast.unparse(sub)}`: index every dim of `{name}` with an integer")
+        flat = " + ".join(f"ak_clamp({self._int(d)}, 0, {n - 1}) * {st}"
+                          for d, n, st in zip(dims, shape, strides(shape))) or "0"
+        return f"{ref}[{flat}]"
+
+    def _int(self, node: Union[int, ast.expr]) -> str:
+        if isinstance(node, int):
+            return str(node)
+        return f"(int)({int_expr(self._fold(node), self._name, self._element)})"
+
+    # ------------------------------------------------------------------------------------------ windows
+
+    def _gather(self, sub: ast.Subscript, e: str, dim: int) -> str:
+        """Element e of `ids[..., a : a + n]`, an index into a dim of `dim` (clamped into both)."""
+        name = sub.value.id  # type: ignore[attr-defined]
+        dims = list(sub.slice.elts) if isinstance(sub.slice, ast.Tuple) else [sub.slice]
+        if name in {ix.name for ix in self.plan.indices}:
+            shape, ref = self.plan.index(name).shape, f"args.{name}"
+        else:
+            shape, ref = self.plan.kept[name].shape, self.buf.ref(f"c_{name}")
+        terms = []
+        for d, n, st in zip(dims, shape, strides(shape)):
+            at = f"({self._int(d.lower)} + ({e}))" if isinstance(d, ast.Slice) else self._int(d)  # type: ignore[arg-type]
+            terms.append(f"ak_clamp({at}, 0, {n - 1}) * {st}")
+        return f"{ref}[{' + '.join(terms)}]"
+
+    def _coords(self, acc: Any, shape: Sequence[int], idx: Tuple[str, ...], store: bool
+                ) -> Tuple[str, List[str]]:
+        """The flat element address of `acc` at tile index `idx`, and the conditions a store writes under
+        (rows before `stop`; gathered elements inside the dim: JAX drops updates out of the array)."""
+        terms, conds, k = [], [], 0
+        for d, dim, stride in zip(acc.dims, shape, strides(shape)):
+            if d.gather is not None:
+                g = self._gather(d.gather, idx[k], dim)
+                k += 1
+                if store:
+                    conds.append(f"(unsigned)({g}) < {dim}u")
+                    coord = g
+                else:
+                    coord = f"ak_clamp({g}, 0, {dim - 1})"
+            elif d.size is None:
+                coord = self._int(d.start) if isinstance(d.start, int) else f"ak_clamp({self._int(d.start)}, 0, {dim - 1})"
+            elif d.stop is not None:
+                at = f"({self._int(d.start)} + ({idx[k]}))"
+                k += 1
+                if store:
+                    conds.append(f"{at} < {self._int(d.stop)} && (unsigned){at} < {dim}u")
+                    coord = at
+                else:
+                    coord = f"ak_clamp({at}, 0, {dim - 1})"
+            else:
+                base = (self._int(d.start) if isinstance(d.start, int)
+                        else f"ak_clamp({self._int(d.start)}, 0, {dim - d.size})")
+                coord = f"({base} + ({idx[k]}))"
+                k += 1
+            terms.append(f"(long long)({coord}) * {stride}")
+        return " + ".join(terms) or "0", conds
+
+    def _load(self, n: Node, idx: Tuple[str, ...]) -> str:
+        acc = self.plan.accesses[n.kwargs["operand"]]
+        addr, _ = self._coords(acc, self.plan.inputs[acc.param].shape, idx, store=False)
+        src = f"args.{acc.array}[{addr}]"
+        dt = acc.dtype
+        if dt.name == "bfloat16":
+            return f"ak_bf16_to_f32({src})"
+        if dt.name == "float16":
+            return f"(float)__builtin_bit_cast(_Float16, {src})"
+        return f"({ctype(dt)})({src})"
+
+    def _output_store(self, o: Any, val: Any, em: _Elements, ind: str) -> List[str]:
+        acc = self.plan.placed[o.name]
+        kept = acc.shape
+
+        def body(idx: Tuple[str, ...]) -> List[str]:
+            addr, conds = self._coords(acc, o.shape, idx, store=True)
+            if isinstance(val, jaxlite.Sym):
+                v = em.at(val.node, _broadcast_index(val.node.shape, kept, idx))
+            else:
+                v = literal(val, o.dtype)
+            line = _write(f"args.{o.name}_out", addr, o.dtype, v)
+            return [f"if ({' && '.join(conds)}) {line}"] if conds else [line]
+
+        return self._pass(kept, body, ind)
+
+    # ------------------------------------------------------------------------------------------ the tree
+
+    def _block(self, b: Any, ind: str) -> List[str]:
+        scope = b.scope
+        updates = self._updates(scope, [c for c in b.binds if c in self.plan.kept and c in scope.values])
+        outputs = {o.name: o for o in self.plan.outputs}
+        stores = [(outputs[name], value) for name, value in scope.stores.items()]
+        return self._emit(updates, stores, ind)
+
+    def _tree(self, blocks: Sequence[Any], ind: str) -> List[str]:
+        out: List[str] = []
+        for b in blocks:
+            if b.kind == "code":
+                out += self._block(b, ind)
+                continue
+            bd = self.plan.bounds[b.loop]
+            v = bd.var
+            out.append(f"{ind}{{ const int b0_{v} = {self._int(bd.start)}, b1_{v} = {self._int(bd.stop)};")
+            out.append(f"{ind}for (int lv_{v} = b0_{v}; lv_{v} < b1_{v}; lv_{v} += {bd.step}) {{")
+            if bd.mask is not None:
+                out.append(f"{ind}  if ({self._int(bd.mask)}) continue;")
+            out += self._block(b, ind + "  ") if b.kind == "loop" else self._tree(b.children, ind + "  ")
+            out.append(f"{ind}}} }}")
+        return out
+
+    def _tiles(self) -> Tuple[List[str], str]:
+        """Setting each parallel loop's value from the tile index t (the outermost slowest), and the count
+        of tiles (an expression the kernel evaluates when the outermost loop's bounds are read as it runs)."""
+        plan = self.plan
+        parallel = [plan.bounds[loop.var] for loop in plan.nest.parallel]
+        inner = parallel[1:]
+        inner_count = math.prod(b.count for b in inner)
+        first = parallel[0]
+        if first.static:
+            total = str(first.count * inner_count)
+            setup = ""
+        else:
+            setup = (f"const int p0_ = {self._int(first.start)}, p1_ = {self._int(first.stop)}; "
+                     f"const long long total_ = p1_ > p0_ ? (long long)((p1_ - p0_ + {first.step - 1}) / {first.step}) * "
+                     f"{inner_count} : 0;")
+            total = "total_"
+        lines = ["long long r_ = t;"]
+        for b in reversed(inner):
+            lines.append(f"const int lv_{b.var} = {b.start} + (int)(r_ % {b.count}) * {b.step}; r_ /= {b.count};")
+        start0 = str(first.start) if first.static else "p0_"
+        lines.append(f"const int lv_{first.var} = {start0} + (int)r_ * {first.step};")
+        masks = [self._int(b.mask) for b in parallel if b.mask is not None]
+        if masks:
+            lines.append(f"if ({' || '.join(masks)}) continue;")
+        return [setup] + lines, total
+
+    def _init(self) -> str:
+        """The launch before the kernel: every output filled, with its allocation's value or its input."""
+        lines = []
+        for o in self.plan.outputs:
+            n = math.prod(o.shape)
+            if o.name in self.plan.aliases:
+                src = self.plan.nest.params[self.plan.aliases[o.name]]
+                body = f"args.{o.name}_out[e] = args.{src}[e];"
+            else:
+                body = _write(f"args.{o.name}_out", "e", o.dtype, literal(o.fill if o.fill is not None else 0, o.dtype))
+            lines.append(f"  for (long long e = (long long)blockIdx.x * {THREADS} + threadIdx.x; e < {n}LL; "
+                         f"e += (long long)gridDim.x * {THREADS}) {body}")
+        return "\n".join(lines)
+
+    def program(self) -> Program:
+        plan, sch = self.plan, self.sch
+        decode, total = self._tiles()
+        tile_code = self._tree(plan.tree, "    ")
+        per_wg = max(self.buf.size, ALIGN)
+        if per_wg > MEM_BUDGET:
+            raise KernelError(f"{plan.nest.name}: a tile needs {per_wg} bytes of tile memory, more than the generic "
+                              f"lowering's {MEM_BUDGET}")
+        most = MAX_GRID if sch.runtime_tiles else max(1, min(sch.tiles, MAX_GRID))
+        grid = max(1, min(most, MEM_BUDGET // per_wg))
+        args = self._args()
+        src = self._walk_source(args, decode, total, tile_code)
+        elements = max(math.prod(o.shape) for o in plan.outputs)
+        init_grid = max(1, min(-(-elements // THREADS), 2048))
+        workspace = {"gx_mem": per_wg * grid}
+        if self.trace:
+            workspace[TRACE] = grid * TRACE_FIELDS * 8
+        launches = [Launch(f"{self.name}_init", args, (init_grid, 1, 1), (THREADS, 1, 1), 0),
+                    Launch(self.name, args, (grid, 1, 1), (THREADS, 1, 1), 0)]
+        return Program(
+            name=self.name, source=src, launches=launches,
+            outputs=[(o.shape, o.dtype) for o in plan.outputs], inputs=[(s.shape, s.dtype) for s in plan.inputs],
+            tables={}, workspace=workspace, lds_bytes=0,
+            notes={"family": "generic", "walk": True, "grid": grid, "items": sch.tiles, "tile_memory": per_wg,
+                   "trace_workgroups": grid if self.trace else 0, "trace_slots": grid, "slices_per_step": 1})
+
+    def _walk_source(self, args: List[Arg], decode: List[str], total: str, tile_code: List[str]) -> str:
+        plan = self.plan
+        t0 = f"const unsigned long long tr_0 = {NOW};" if self.trace else ""
+        t1 = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; tr[0] = 0; "
+              f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = tiles_; }}" if self.trace else "")
+        body = "\n    ".join(decode[1:])
+        return f"""// Generated by tilejax_amd for `{plan.nest.name}`: the generic gfx950 lowering of the tile as written
+// (blocks walked per tile in each workgroup's tile memory of {self.buf.size} bytes).
+{PRELUDE}
+AK_INLINE float ak_gelu_exact(float x) {{ return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }}
+AK_INLINE int ak_ipow(int b, int e) {{ int r = 1; for (int k = 0; k < e; ++k) r *= b; return e < 0 ? 0 : r; }}
+AK_INLINE float ak_fmod_floor(float a, float b) {{ const float r = fmodf(a, b); return (r != 0.0f && ((r < 0.0f) != (b < 0.0f))) ? r + b : r; }}
+{c_struct(f"{self.name}_args", args)}
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_init(const {self.name}_args args) {{
+{self._init()}
+}}
+extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
+  const int tid = threadIdx.x;
+  char* ak_mem = args.gx_mem + (long long)blockIdx.x * {max(self.buf.size, ALIGN)};
+  (void)ak_mem;
+  {t0}
+  long long tiles_ = 0; (void)tiles_;
+  {decode[0]}
+  for (long long t = blockIdx.x; t < {total}; t += gridDim.x) {{
+    {body}
+    ++tiles_;
+{chr(10).join(tile_code)}
+    __syncthreads();
+  }}
+  {t1}
+}}
+"""
+
+
 def _ctype_in(dt: DType) -> str:
     return {"bfloat16": "ak_u16", "float16": "ak_u16", "float32": "float", "float64": "double", "int32": "int",
             "int64": "long long", "int16": "short", "int8": "signed char", "uint8": "unsigned char",
@@ -706,3 +1006,7 @@ def _write(ptr: str, addr: str, dt: DType, value: str) -> str:
 
 def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, name: str, trace: bool = False) -> Program:
     return _Generic(plan, sch, name, trace).program()
+
+
+def lower_walk(plan: Plan, sch: Schedule, pipeline: Pipeline, name: str, trace: bool = False) -> Program:
+    return _Walk(plan, sch, name, trace).program()

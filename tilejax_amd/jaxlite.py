@@ -526,13 +526,16 @@ def _index(index: Any) -> Any:
         return slice(_index(index.start), _index(index.stop), _index(index.step))
     if isinstance(index, Array):
         if index.ndim == 0:
+            if index.t.device.type == "meta":
+                return 0  # a traced scalar index: the result's type doesn't depend on its value
             return int(index)
         return index.t.long()
     return index
 
 
 def _clamped(index: Any, shape: Tuple[int, ...]) -> Any:
-    """Integer indices clamped into their dims, as JAX clamps them."""
+    """Integer indices (and integer index arrays) clamped into their dims, as JAX clamps reads: negative
+    ones count from the end first."""
     idx = index if isinstance(index, tuple) else (index,)
     out, dim = [], 0
     for i in idx:
@@ -547,9 +550,35 @@ def _clamped(index: Any, shape: Tuple[int, ...]) -> Any:
             n = shape[dim]
             i = n + i if i < 0 else i
             i = 0 if i < 0 else (n - 1 if i >= n else i)
+        elif isinstance(i, torch.Tensor) and i.dtype != torch.bool and dim < len(shape) and i.device.type != "meta":
+            n = shape[dim]
+            i = torch.where(i < 0, i + n, i).clamp(0, n - 1)
         out.append(i)
         dim += 1
     return tuple(out)
+
+
+def _set(target: torch.Tensor, index: Any, value: Any) -> None:
+    """`target[index] = value` as JAX updates: out-of-range integer indices are clamped, except the entries
+    of one integer index array (a gathered or ragged window), whose updates out of the array are dropped."""
+    idx = index if isinstance(index, tuple) else (index,)
+    v = value.to(target.dtype) if isinstance(value, torch.Tensor) else value
+    arrays = [k for k, i in enumerate(idx) if isinstance(i, torch.Tensor) and i.dtype != torch.bool]
+    plain = all(i is not None and i is not Ellipsis for i in idx)
+    if len(arrays) == 1 and plain and idx[arrays[0]].ndim == 1 and target.device.type != "meta":
+        k = arrays[0]
+        n = target.shape[k]
+        i = torch.where(idx[k] < 0, idx[k] + n, idx[k])
+        keep = (i >= 0) & (i < n)
+        if not bool(keep.all()):
+            # the dropped entries write a spare row past the end, which is then cut off
+            spare = torch.cat([target, target.narrow(k, 0, 1)], k)
+            moved = list(_clamped(idx, tuple(spare.shape)))
+            moved[k] = torch.where(keep, i, n)
+            spare[tuple(moved)] = v
+            target.copy_(spare.narrow(k, 0, n))
+            return
+    target[_clamped(idx, tuple(target.shape))] = v
 
 
 @_op("getitem")
@@ -560,8 +589,7 @@ def getitem(x: Array, index: Any) -> Array:
 @_op("scatter_set")
 def scatter_set(x: Array, index: Any, value: Any) -> Array:
     out = x.t.clone()
-    v = _t(value)
-    out[_clamped(_index(index), x.shape)] = v.to(out.dtype) if isinstance(v, torch.Tensor) else v
+    _set(out, _index(index), _t(value))
     return Array(out)
 
 
@@ -575,8 +603,7 @@ def scatter_add(x: Array, index: Any, value: Any) -> Array:
 def store_(x: Array, index: Any, value: Any) -> Array:
     """`x.at[index].set(value)` writing into `x`'s own buffer: what `kernel.reference` does for output
     stores (an output is never read by tile code, so no one sees the buffer change)."""
-    v = _t(value)
-    x.t[_clamped(_index(index), x.shape)] = v.to(x.t.dtype) if isinstance(v, torch.Tensor) else v
+    _set(x.t, _index(index), _t(value))
     return x
 
 

@@ -30,10 +30,16 @@ from .jaxlite import DType, Node, Sym
 from .parse import Loop, Nest
 from .syntax import bound, element_reads, in_order, index_dims, store_of, used, used_before_bound
 
-__all__ = ["Carried", "Index", "Kind", "Operand", "Output", "Phase", "Plan", "Range", "Scope", "Spec", "Tile",
-           "Window", "make_plan"]
+__all__ = ["Carried", "Index", "Kind", "NeedsWalk", "Operand", "Output", "Phase", "Plan", "Range", "Scope", "Spec",
+           "Tile", "Window", "make_plan"]
 
 READ, INDEX, STORE = "__tilejax_read__", "__tilejax_index__", "__tilejax_store__"
+
+
+class NeedsWalk(KernelError):
+    """A nest the step planner doesn't take but the walk planner (walk.py) may: repeat loops, runtime loop
+    bounds, outputs updated in place or stored per step or where index arrays say, gathered and ragged
+    windows, windows and bounds the tile code computes. Its message is the step planner's reason."""
 
 
 @dataclass(frozen=True)
@@ -172,6 +178,15 @@ class Plan:
     env: Dict[str, Any]
     constants: Dict[str, Any]
     repeats: Tuple[Any, ...] = ()
+    # A plan of the tile as written (walk.py), for nests without the phases-of-steps form: its blocks, the
+    # values kept between them, every loop's bounds, the tile reads and output stores, in-place outputs.
+    walk: bool = False
+    tree: Tuple[Any, ...] = ()
+    kept: Dict[str, Carried] = field(default_factory=dict)
+    bounds: Dict[str, Any] = field(default_factory=dict)
+    accesses: Dict[str, Any] = field(default_factory=dict)
+    placed: Dict[str, Any] = field(default_factory=dict)
+    aliases: Dict[str, int] = field(default_factory=dict)  # output -> the input it updates in place
 
     @property
     def single_step(self) -> bool:
@@ -220,8 +235,14 @@ def evaluate(nest: Nest, env: Dict[str, Any], node: ast.expr, values: Optional[M
 
 
 def make_plan(nest: Nest, fn: Callable, inputs: Sequence[Spec], tunable: Any = None) -> Plan:
-    """Resolve `nest` (parsed from `fn`) for inputs of these shapes and dtypes and the tunable's values."""
-    return _Planner(nest, fn, tuple(inputs), tunable).plan()
+    """Resolve `nest` (parsed from `fn`) for inputs of these shapes and dtypes and the tunable's values: a
+    plan of phases and steps when the nest has that form, else a plan of the tile as written (walk.py)."""
+    try:
+        return _Planner(nest, fn, tuple(inputs), tunable).plan()
+    except NeedsWalk:
+        from .walk import plan_walk
+
+        return plan_walk(nest, fn, tuple(inputs), tunable)
 
 
 class _Env:
@@ -261,9 +282,10 @@ class _Env:
 def _allocation(env: _Env, name: str, call: ast.expr) -> Tuple[Tuple[int, ...], DType, Any]:
     """An output's (shape, dtype, fill) from its allocation, `jnp.zeros(shape, dtype)` or `jnp.full(...)`."""
     nest = env.nest
-    usage = f"allocate output `{name}` with jnp.zeros(shape, dtype) or jnp.full(shape, value, dtype)"
+    usage = (f"allocate output `{name}` with jnp.zeros(shape, dtype) or jnp.full(shape, value, dtype), or as an "
+             f"input updated in place (`{name} = x`)")
     if isinstance(call, ast.Name) and call.id in nest.params:
-        raise nest.error(f"outputs updated in place (`{name} = {call.id}`) are not lowered by the gfx950 backend yet", call)
+        raise NeedsWalk(f"output `{name}` updates `{call.id}` in place", filename=nest.filename, node=call)
     maker = env.eval(call.func) if isinstance(call, ast.Call) else None
     if maker is not jaxlite.zeros and maker is not jaxlite.full:
         raise nest.error(usage, call)
@@ -291,8 +313,8 @@ def _loop_range(env: _Env, loop: Loop, parallel: bool, indices: Mapping[str, Any
     if loop.mask is not None and element_reads(loop.mask, computed):
         raise nest.error("a mask can't read values the tile code computes (it is evaluated before the kernel runs)",
                          loop.mask)
-    if any(element_reads(b, indices) for b in loop.bounds):
-        raise nest.error("loops with runtime bounds (a cursor) are not lowered by the gfx950 backend yet", loop.node)
+    if any(element_reads(b, indices) or used(b) & computed for b in loop.bounds):
+        raise NeedsWalk(f"`{loop.var}`'s bounds are read when the kernel runs", filename=nest.filename, node=loop.node)
     values = [env.eval(b) for b in loop.bounds]
     if any(not isinstance(v, int) for v in values):
         raise nest.error(f"loop bounds are ints when planning, got {values}", loop.node)
@@ -314,6 +336,18 @@ def _loop_range(env: _Env, loop: Loop, parallel: bool, indices: Mapping[str, Any
     return Range(loop.var, start, step, len(span), loop.mask, runtime)
 
 
+def _is_rows_call(env: "_Env", index: ast.expr) -> bool:
+    """Is `index` a call of `tilejax_amd.rows` (a ragged window of rows)?"""
+    if not (isinstance(index, ast.Call) and isinstance(index.func, (ast.Name, ast.Attribute))):
+        return False
+    from .ragged import rows
+
+    try:
+        return env.eval(index.func) is rows
+    except KernelError:
+        return False
+
+
 class _Windows:
     """Reads the index expressions of tile reads and stores into Windows. A dim's index is one of:
     `v : v + n` (a loop variable v, n an int: moves with v), `v` (an integer index moving with v), constants
@@ -333,10 +367,12 @@ class _Windows:
 
     def window(self, index: ast.expr, dim: int, text: str) -> Window:
         movers = used(index) & set(self.ranges)
+        nest = self.env.nest
+        gathered = (isinstance(index, ast.Subscript) and isinstance(index.value, ast.Name)
+                    and index.value.id in nest.params and any(isinstance(d, ast.Slice) for d in index_dims(index)))
+        if gathered or _is_rows_call(self.env, index) or used(index) & bound(nest.tile):
+            raise NeedsWalk(f"{text}: a window the kernel finds as it runs", filename=nest.filename, node=index)
         if isinstance(index, ast.Subscript) and isinstance(index.value, ast.Name) and index.value.id in self.indices:
-            if any(isinstance(d, ast.Slice) for d in index_dims(index)):
-                raise self.env.nest.error(f"{text}: windows gathered through index-array slices are not lowered yet",
-                                          index)
             return Window(None, 0, None, index, frozenset(movers))
         if isinstance(index, ast.Slice):
             return self._slice(index, dim, text, movers)
@@ -406,8 +442,8 @@ class _Planner:
     def plan(self) -> Plan:
         nest = self.nest
         if nest.repeats:
-            raise self.error("repeat loops (a loop around reduction loops) are not lowered by the gfx950 backend yet",
-                             nest.repeats[0].loop.node)
+            raise NeedsWalk("repeat loops run as the tile is written", filename=nest.filename,
+                            node=nest.repeats[0].loop.node)
         allocated = self._run_prologue()
         self.indices = {ix.name: ix for ix in self._index_arrays()}
         parallel = tuple(_loop_range(self.envs, loop, True, self.indices) for loop in nest.parallel)
@@ -422,8 +458,7 @@ class _Planner:
         out_tiles = {name: self._output_tile(name, *allocated[name][:2], parallel, windows) for name in nest.outputs}
         per_step = [name for name in nest.outputs if nest.stored_in[name] is not None]
         if per_step:
-            raise self.error("outputs stored per step are not lowered by the gfx950 backend yet",
-                             nest.stores[per_step[0]].node)
+            raise NeedsWalk("outputs stored per step", filename=nest.filename, node=nest.stores[per_step[0]].node)
         self._check_reads_before_assignment()
         scopes, carried = self._trace(phases, segments, bound_vars, by_node)
         outputs = tuple(self._output(name, allocated[name], out_tiles[name], scopes["last"].stores[name])
@@ -573,7 +608,8 @@ class _Planner:
         store = self.nest.stores[name]
         tile = windows.tile(name, shape, dt, store.index, store.node)
         if any(w.index is not None for w in tile.windows):
-            raise self.error(f"{tile.text}: stores at windows an index array chooses are not lowered yet", store.node)
+            raise NeedsWalk(f"{tile.text}: a store at a window an index array chooses", filename=self.nest.filename,
+                            node=store.node)
         placing = [w.loop for w in tile.windows if w.loop]
         for r in parallel:
             if placing.count(r.var) != 1:
@@ -660,38 +696,7 @@ class _Planner:
         scopes: Dict[str, Scope] = {}
 
         def run(name: str, stmts: Tuple[ast.stmt, ...], carried_in: Dict[str, Tuple[Tuple[int, ...], Any]]) -> Scope:
-            with jaxlite.trace() as tr, jaxlite.matrix_units():
-                locals_: Dict[str, Any] = {}
-                for var in self.ranges:
-                    locals_[var] = jaxlite.leaf("loop", (), jaxlite.int32, var=var)
-                for var, value in bound_vars.items():
-                    locals_[var] = value
-                leaves = {}
-                for cname, (shape, dt) in carried_in.items():
-                    if isinstance(dt, DType):
-                        sym = jaxlite.leaf("carried", shape, dt, name=cname)
-                        locals_[cname], leaves[cname] = sym, sym.node
-                    else:  # a Python number carried as itself
-                        locals_[cname] = dt
-                stores: Dict[str, Any] = {}
-                scope_env = dict(self.env)
-                scope_env[READ] = lambda op: self._load(op)
-                scope_env[INDEX] = lambda arr, idx: self._index_load(arr, idx)
-                scope_env[STORE] = lambda out, value: stores.__setitem__(out, value)
-                code = self._rewrite(stmts, by_node)
-                # one namespace, as a function's: comprehensions and lambdas in tile code see its names
-                namespace = scope_env
-                namespace.update(locals_)
-                for stmt in code:
-                    try:
-                        exec(compile(ast.Module([stmt], []), nest.filename, "exec"), namespace)
-                    except KernelError:
-                        raise
-                    except Exception as e:
-                        raise self.error(f"tile code failed when traced with symbolic tiles: {e!r}", stmt) from e
-                names = (set(locals_) | bound(stmts)) - set(self.ranges) - set(bound_vars)
-                values = {k: namespace[k] for k in names if k in namespace}
-                return Scope(name, list(tr.nodes), values, leaves, stores)
+            return self._run_scope(name, stmts, carried_in, set(self.ranges), bound_vars, by_node)
 
         def type_of(v: Any) -> Tuple[Tuple[int, ...], Any]:
             if isinstance(v, jaxlite.Array):
@@ -730,6 +735,43 @@ class _Planner:
                 if isinstance(dt, DType):
                     carried[c] = Carried(c, shape, dt)
         return scopes, carried
+
+    def _run_scope(self, name: str, stmts: Sequence[ast.stmt], carried_in: Dict[str, Tuple[Tuple[int, ...], Any]],
+                   loop_vars: Set[str], bound_vars: Mapping[str, Any], by_node: Mapping[Any, Any]) -> Scope:
+        """Trace `stmts` with symbolic loop variables and carried values of the given types (a Python number
+        carried as itself): the Nodes they make, the names they leave bound, their output stores."""
+        with jaxlite.trace() as tr, jaxlite.matrix_units():
+            locals_: Dict[str, Any] = {}
+            for var in loop_vars:
+                locals_[var] = jaxlite.leaf("loop", (), jaxlite.int32, var=var)
+            for var, value in bound_vars.items():
+                locals_[var] = value
+            leaves = {}
+            for cname, (shape, dt) in carried_in.items():
+                if isinstance(dt, DType):
+                    sym = jaxlite.leaf("carried", shape, dt, name=cname)
+                    locals_[cname], leaves[cname] = sym, sym.node
+                else:  # a Python number carried as itself
+                    locals_[cname] = dt
+            stores: Dict[str, Any] = {}
+            scope_env = dict(self.env)
+            scope_env[READ] = lambda op: self._load(op)
+            scope_env[INDEX] = lambda arr, idx: self._index_load(arr, idx)
+            scope_env[STORE] = lambda out, value: stores.__setitem__(out, value)
+            code = self._rewrite(stmts, by_node)
+            # one namespace, as a function's: comprehensions and lambdas in tile code see its names
+            namespace = scope_env
+            namespace.update(locals_)
+            for stmt in code:
+                try:
+                    exec(compile(ast.Module([stmt], []), self.nest.filename, "exec"), namespace)
+                except KernelError:
+                    raise
+                except Exception as e:
+                    raise self.error(f"tile code failed when traced with symbolic tiles: {e!r}", stmt) from e
+            names = (set(locals_) | bound(stmts)) - set(loop_vars) - set(bound_vars)
+            values = {k: namespace[k] for k in names if k in namespace}
+            return Scope(name, list(tr.nodes), values, leaves, stores)
 
     def _load(self, name: str) -> Sym:
         op = next(o for o in self.operands if o.name == name)

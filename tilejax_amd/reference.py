@@ -8,8 +8,9 @@ all under `jaxlite.matrix_units()`, so `@` accumulates in f32 and `a @ b.T` cont
 
 One thing differs from running the function, for speed and not meaning: an output store
 `out = out.at[index].set(value)` writes into the output's own buffer. An output is allocated fresh in the
-prologue and tile code never reads it (parse.py checks), so no one can see the difference; a functional
-copy per tile would copy a whole 8192^2 output once per tile.
+prologue (an input updated in place, `new = pool`, is copied first) and tile code never reads it (parse.py
+checks), so no one can see the difference; a functional copy per tile would copy a whole 8192^2 output once
+per tile.
 
 Module and closure values are read as they are when the reference is made (when the kernel is built for a
 signature), as the kernel's constants are.
@@ -164,6 +165,10 @@ class _Interpreter:
             env[nest.tunable] = args[len(nest.params)] if len(args) > len(nest.params) else None
         with jaxlite.matrix_units():
             self.prologue(env)
+            inputs = {id(a) for a in args}
+            for name in nest.outputs:  # an input updated in place: its own copy (the input stays as it was)
+                if id(env[name]) in inputs:
+                    env[name] = jaxlite.Array(env[name].t.clone())
             self._tiles(0, env)
         outs = tuple(env[name] for name in nest.outputs)
         return outs if len(outs) > 1 else outs[0]

@@ -118,6 +118,8 @@ class Schedule:
 def make_schedule(plan: Plan) -> Schedule:
     """The steps `plan`'s kernel runs; KernelError if a mask leaves nothing to run or tables don't fit."""
     nest = plan.nest
+    if plan.walk:
+        return _walked(plan)
     phases = [phase.range for phase in plan.phases]
     counts = tuple(r.count for r in phases)
     tile_masks = [r.mask for r in plan.parallel if r.mask is not None]
@@ -245,6 +247,23 @@ def _check_tables(plan: Plan, tables: Dict[str, np.ndarray], more: int = 0) -> N
 def _check_tiles(plan: Plan, tiles: int, fills: int) -> None:
     if tiles * max(fills, 1) >= 2**31:
         raise plan.nest.error("too many output tiles for the kernel's int32 step arithmetic", plan.nest.parallel[0].node)
+
+
+def _walked(plan: Plan) -> Schedule:
+    """A plan of the tile as written: the kernel walks every tile of the parallel loops (evaluating tile masks
+    and a runtime count of tiles itself), no tables. `steps` counts reduction-loop iterations when bounds
+    and masks are static (else 0); `runtime_tiles` when the count of tiles is known only as the kernel runs."""
+    from .walk import static_steps
+
+    parallel = [plan.bounds[loop.var] for loop in plan.nest.parallel]
+    runtime_tiles = not all(b.static for b in parallel)
+    tiles = 0 if runtime_tiles else math.prod(b.count for b in parallel)
+    steps = static_steps(plan) or 0
+    return Schedule(
+        tiles=tiles, total_tiles=tiles, steps=steps, phase_counts=(), phase_steps=(), step_tables=False,
+        outer=plan.parallel, inner=(), pattern_tiles=tiles, pattern_steps=steps, pattern_fills=0, tile_tables=False,
+        runtime_tiles=runtime_tiles,
+    )
 
 
 def _arithmetic(plan: Plan, counts: Tuple[int, ...]) -> Schedule:

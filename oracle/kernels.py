@@ -126,6 +126,52 @@ def grouped_matmul(xs: torch.Tensor, w: torch.Tensor, group_expert: torch.Tensor
     return out
 
 
+def expert_ffn(xs: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+               tile_expert: torch.Tensor, bf: int = 256) -> torch.Tensor:
+    """examples/moe.py:167-187 of the reference: per tile of G rows and per block of bf hidden units, the gate
+    and up products in f32, silu(g) * u rounded to the input dtype, its product with the down block added in
+    f32; tiles whose expert is negative keep the zeros; the expert index is clamped into [0, E)."""
+    M, D = xs.shape
+    E, _, F = w_gate.shape
+    G = M // tile_expert.shape[0]
+    bf = min(bf, F)
+    xf, wg, wu, wd = _f32(xs), _f32(w_gate), _f32(w_up), _f32(w_down)
+    te = tile_expert.cpu().numpy()
+    out = torch.zeros((M, D), dtype=xs.dtype)
+    for i in range(0, M, G):
+        e = int(te[i // G])
+        if e < 0:
+            continue
+        e = min(e, E - 1)
+        acc = torch.zeros((G, D))
+        for f in range(0, F, bf):
+            g = xf[i:i + G] @ wg[e, :, f:f + bf]
+            u = xf[i:i + G] @ wu[e, :, f:f + bf]
+            hidden = (g * torch.sigmoid(g) * u).to(xs.dtype).float()
+            acc += hidden @ wd[e, f:f + bf, :]
+        out[i:i + G] = acc.to(xs.dtype)
+    return out
+
+
+def expert_ffn_float64(xs: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                       tile_expert: torch.Tensor) -> np.ndarray:
+    """The SwiGLU layer in float64 with nothing rounded: silu(x @ w_gate[e]) * (x @ w_up[e]) @ w_down[e] per
+    tile of G rows, zeros for a negative expert."""
+    M, D = xs.shape
+    E = w_gate.shape[0]
+    G = M // tile_expert.shape[0]
+    x, wg, wu, wd = (t.detach().cpu().double() for t in (xs, w_gate, w_up, w_down))
+    out = torch.zeros((M, D), dtype=torch.float64)
+    for t, e in enumerate(tile_expert.cpu().tolist()):
+        if e < 0:
+            continue
+        e = min(e, E - 1)
+        rows = x[t * G:(t + 1) * G]
+        g = rows @ wg[e]
+        out[t * G:(t + 1) * G] = (g * torch.sigmoid(g) * (rows @ wu[e])) @ wd[e]
+    return out.numpy()
+
+
 def paged_gqa_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor, block_tables: torch.Tensor,
                      lengths: torch.Tensor) -> torch.Tensor:
     """examples/decode.py:199-223: query head h of new token t attends its kv head h // (H / Hkv) over the

@@ -110,3 +110,45 @@ def test_baseline_config_against_torch():
                             matmul_floor(xs[rows], w[e]))
         worst = max(worst, report["bound_use"])
     print(f"MoE config 4: largest bound use over all 64 groups {worst:.3f}", flush=True)
+
+
+@pytest.mark.parametrize("experts,block_f", [([0, 2, -1, 9], 128), ([1, 1, 0, -1], 512)])
+def test_expert_ffn_matches_oracle(experts, block_f):
+    """The reference's SwiGLU layer with runtime expert windows (examples/moe.py:167-187), lowered to the generic
+    kernel. Floor: the gate and up products' f32 summation floors carried through silu(g) * u (|silu'| <= 1.1),
+    the rounding of the hidden activations to bf16 moving each by up to 2^-8 of itself (the kernel and the
+    oracle can round to either side), both through |w_down|, plus the down product's own f32 floor."""
+    from examples.moe import ExpertTiles, expert_ffn
+    from tests.tolerance import P_ROUND
+
+    g = torch.Generator().manual_seed(11)
+    M, D, F, E = 512, 256, 512, 4
+    xs = torch.randn(M, D, generator=g).to(torch.bfloat16)
+    wg, wu = ((torch.randn(E, D, F, generator=g) / 16).to(torch.bfloat16) for _ in range(2))
+    wd = (torch.randn(E, F, D, generator=g) / 16).to(torch.bfloat16)
+    te = torch.tensor(experts, dtype=torch.int32)
+    tiles = ExpertTiles(block_f=block_f)
+    lowered = expert_ffn.lower(xs, wg, wu, wd, te, tiles)
+    assert lowered.program.notes["family"] == "generic"
+    print(f"expert_ffn experts={experts} {tiles}", flush=True)
+    got = lowered.run(xs.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), te.cuda())
+    torch.cuda.synchronize()
+    want = kernels.expert_ffn(xs, wg, wu, wd, te, block_f)
+    floor = torch.zeros(M, D)
+    G = M // len(experts)
+    for t, e in enumerate(experts):
+        if e < 0:
+            continue
+        e = min(e, E - 1)
+        rows = xs[t * G:(t + 1) * G].float()
+        gate, up = rows @ wg[e].float(), rows @ wu[e].float()
+        hidden = (gate * torch.sigmoid(gate) * up).abs()
+        moved = 1.1 * matmul_floor(rows, wg[e]) * up.abs() + gate.abs() * matmul_floor(rows, wu[e])
+        floor[t * G:(t + 1) * G] = ((moved + 2 * P_ROUND * hidden) @ wd[e].float().abs()
+                                    + matmul_floor(hidden.to(torch.bfloat16), wd[e]))
+    check_bf16(f"expert_ffn experts={experts}", got.cpu(), want, floor)
+    exact = torch.as_tensor(kernels.expert_ffn_float64(xs, wg, wu, wd, te))
+    assert (got.cpu().double() - exact).abs().max().item() < 3e-2 * exact.abs().max().item()
+    for t, e in enumerate(experts):
+        if e < 0:
+            assert not got[t * G:(t + 1) * G].float().any()

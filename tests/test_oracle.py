@@ -188,3 +188,31 @@ def test_grouped_matmul_routes_groups_to_their_experts():
             assert not got[rows].any()
         else:
             _close(got[rows], xs[rows].double() @ w[e].double())
+
+
+def _expert_inputs(G=64, E=3, D=128, F=256):
+    xs = rand((4 * G, D), 0, BF)
+    return xs, rand((E, D, F), 1, BF) / 8, rand((E, D, F), 2, BF) / 8, rand((E, F, D), 3, BF) / 8
+
+
+def test_expert_ffn_is_swiglu_per_tile():
+    xs, wg, wu, wd = _expert_inputs()
+    te = torch.tensor([0, 2, -1, 9], dtype=torch.int32)  # -1: zeros; 9: clamped to expert E - 1
+    got = kernels.expert_ffn(xs, wg, wu, wd, te, bf=64).double()
+    want = kernels.expert_ffn_float64(xs, wg, wu, wd, te)
+    _close(got, want)
+    assert not got[128:192].any()
+    with pytest.raises(AssertionError):  # gate and up swapped: silu(u) * g
+        _close(kernels.expert_ffn(xs, wu, wg, wd, te, bf=64).double(), want)
+
+
+def test_expert_ffn_float64_is_silu_of_the_gate_when_up_is_one():
+    """x = 1/D everywhere and w_up = 1 give up = 1; w_down = I leaves silu(gate) = g / (1 + e^-g)."""
+    G, D = 64, 128
+    xs = torch.full((G, D), 1.0 / D)
+    wg = rand((1, D, D), 4) * 4
+    wu, wd = torch.ones((1, D, D)), torch.eye(D)[None]
+    g = (xs.double() @ wg[0].double()).numpy()
+    want = g / (1 + np.exp(-g))
+    np.testing.assert_allclose(kernels.expert_ffn_float64(xs, wg, wu, wd, torch.tensor([0], dtype=torch.int32)),
+                               want, rtol=1e-12, atol=1e-12)

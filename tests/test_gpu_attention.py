@@ -121,3 +121,26 @@ def test_split_tiles_call_after_call():
     _close("attention (1, 2, 1024, 128) split", outs[0], kernels.causal_attention(qc, kc, vc, 256, 256),
            _floor(qc, kc, vc))
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("hardware,buffers", [
+    ((("bkv", 64), ("waves", 8)), 2),
+    ((("bkv", 32), ("waves", 4)), 2),
+    ((("bkv", 32), ("waves", 8)), 2),
+    ((), 3),  # K and V two blocks ahead through three LDS stages
+    ((), 4),
+])
+def test_kernel_shapes_the_tuner_tries(hardware, buffers):
+    """Each gfx950 kernel shape the tuner may pick (waves per workgroup, keys per block, ring depth) against
+    the oracle, at a shape where every block class (full, partial, skipped) occurs."""
+    from tilejax_amd import Pipeline
+    from tilejax_amd.tune import Config
+
+    shape, blocks = (2, 4, 1024, 128), AttentionBlocks(256, 256)
+    q, k, v = _inputs(*shape, seed=3)
+    sig = causal_attention.signature(q, k, v)
+    lowered = causal_attention.lowered(sig, Config(blocks, Pipeline(buffers, 2), False, hardware))
+    print(f"attention {shape} {blocks} hardware={hardware} buffers={buffers}", flush=True)
+    got = lowered.run(q.cuda(), k.cuda(), v.cuda())
+    torch.cuda.synchronize()
+    _close(f"attention {hardware} {buffers}", got, kernels.causal_attention(q, k, v, 256, 256), _floor(q, k, v))

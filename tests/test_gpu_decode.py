@@ -199,3 +199,19 @@ def test_paged_decode_with_new_tokens(cursor):
     got = lowered.run(*(t.cuda() for t in ins))
     _close(f"decode two tokens cursor={cursor}", got, kernels.paged_gqa_decode(*ins), ins)
     _close(f"decode two tokens cursor={cursor} vs float64", got, kernels.gqa_float64(*ins), ins)
+
+
+@pytest.mark.parametrize("buffers,cursor", [(2, False), (4, False), (2, True), (4, True)])
+def test_depths_the_tuner_tries(buffers, cursor):
+    """Decode with 2 and 4 steps fetched ahead (the pipeline's input buffers; the default is 3), from tables
+    and with a cursor, against the oracle."""
+    from tilejax_amd import Pipeline
+    from tilejax_amd.tune import Config
+
+    lengths = (0, 5, 1600, 1023, 1025)
+    ins = _inputs(5, 32, 8, 128, 16, 100, lengths, seed=9)
+    lowered = paged_gqa_decode.lowered(paged_gqa_decode.signature(*ins), Config(None, Pipeline(buffers, 2), cursor))
+    print(f"paged decode depth {buffers} cursor={cursor}", flush=True)
+    got = lowered.run(*(t.cuda() for t in ins))
+    torch.cuda.synchronize()
+    _close(f"paged decode depth {buffers} cursor={cursor}", got, kernels.paged_gqa_decode(*ins), ins)

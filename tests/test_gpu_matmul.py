@@ -220,3 +220,25 @@ def test_causal_matmul_f32_operands():
     torch.cuda.synchronize()
     _close_f32(got, torch.tril(x.double() @ y.double()))
     assert not got.cpu().triu(1).any()
+
+
+@pytest.mark.parametrize("hardware,buffers", [
+    ((("bm", 256), ("bn", 128)), 2),
+    ((("bm", 128), ("bn", 256)), 2),
+    ((("bm", 128), ("bn", 128)), 3),
+    ((), 4),
+])
+def test_workgroup_tiles_the_tuner_tries(hardware, buffers):
+    """Each gfx950 workgroup tile and LDS ring depth the tuner may pick, dense and causal, against the oracle."""
+    from tilejax_amd import Pipeline
+    from tilejax_amd.tune import Config
+
+    tiles = MatmulTiles(512, 512, 512)
+    x, y = _inputs(1024, 1024, 1024, seed=7)
+    for kernel, oracle in ((matmul, kernels.matmul), (causal_matmul, kernels.causal_matmul)):
+        lowered = kernel.lowered(kernel.signature(x, y), Config(tiles, Pipeline(buffers, 2), False, hardware))
+        print(f"{kernel.nest.name} 1024^3 {tiles} hardware={hardware} buffers={buffers} "
+              f"-> {lowered.program.notes['hw_tile']} x{lowered.program.notes['stages']}", flush=True)
+        got = lowered.run(x.cuda(), y.cuda())
+        torch.cuda.synchronize()
+        _close(got, oracle(x, y, 512, 512, 512), x, y, f"{kernel.nest.name} {hardware}")

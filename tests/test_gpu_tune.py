@@ -135,3 +135,20 @@ def test_tuning_decode_tries_both_ways_of_finding_steps():
     tuning = paged_gqa_decode.tuning(q, kp, vp, table, lengths)
     print(tuning, flush=True)
     assert {t.config.cursor for t in tuning.trials if t.profile is not None} == {False, True}
+
+
+def test_tuning_at_the_dense_baseline_tries_workgroup_tiles():
+    """BASELINE config 2 (dense 8192^3 bf16 at 512^3 tiles): tuning tries the matmul family's other workgroup
+    tiles, each a different kernel that is checked against the reference, and picks one at least as fast
+    as the default."""
+    from tilejax_amd.tune import tune
+
+    x, y = _inputs(8192, seed=2)
+    print("tuning matmul 8192^3 from its default tiles", flush=True)
+    tuning = tune(matmul, matmul.signature(x, y), [x, y], budget=6)
+    print(tuning, flush=True)
+    shapes = {t.config.hardware for t in tuning.trials if t.profile is not None}
+    assert len(shapes) >= 3, shapes  # the default 256 x 256 and at least two others ran
+    first = tuning.trials[0]
+    assert first.config == matmul.default_config(matmul.signature(x, y)) and first.profile is not None
+    assert tuning.best.seconds <= first.seconds

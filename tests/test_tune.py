@@ -96,9 +96,9 @@ def test_proposals_follow_the_bottleneck():
     dma = Trial(start, profile(start, seconds=10.0, wait=5.0))
     assert proposals(k, sig, dma)[0] == Config(Tiles(), Pipeline(3, 2))
     assert [c.tunable for c in proposals(k, sig, dma)[1:]] == [Tiles(tm=256), Tiles(tk=256)]
-    # Exposed output waits: one more output buffer.
+    # Exposed output waits: no more output buffers (gfx950 kernels store from registers: nothing to queue).
     outs = Trial(start, profile(start, seconds=10.0, out_wait=5.0))
-    assert proposals(k, sig, outs)[0] == Config(Tiles(), Pipeline(2, 3))
+    assert all(c.pipeline.output_buffers == 2 for c in proposals(k, sig, outs))
     # Compute-bound: every neighbour, fewest steps first; without regions the same plus one more stage.
     compute = Trial(start, profile(start, seconds=10.0))
     assert [c.tunable for c in proposals(k, sig, compute)] == [Tiles(tm=256), Tiles(tk=256), Tiles(tm=64)]
@@ -148,3 +148,34 @@ def test_a_kernel_without_a_tunable_tunes_its_buffering():
     dma = Trial(start, profile(start, seconds=10.0, wait=5.0))
     bigger = Pipeline(start.pipeline.input_buffers + 1, start.pipeline.output_buffers)
     assert proposals(k, sig, dma)[0] == Config(None, bigger)
+
+
+# --------------------------------------------------------------------------------- the gfx950 vocabulary
+
+
+def test_hardware_choices_are_distinct_kernels():
+    """The tuner's gfx950 vocabulary: the matmul's workgroup tiles and attention's waves and key blocks
+    each build a different kernel, and each compiles."""
+    from examples.causal_attention import AttentionBlocks, causal_attention
+    from examples.matmul import MatmulTiles, matmul
+    from tilejax_amd import runtime
+    from tilejax_amd.codegen import hardware_choices
+
+    bf = jaxlite.bfloat16
+    cases = [(matmul, (spec(1024, 1024, dtype=bf), spec(1024, 1024, dtype=bf)), MatmulTiles(512, 512, 512), 4),
+             (causal_attention, tuple(spec(2, 4, 512, 128, dtype=bf) for _ in range(3)), AttentionBlocks(256, 256), 4)]
+    for kernel, args, tiles, count in cases:
+        sig = kernel.signature(*args)
+        plan, schedule = kernel.build(sig, tiles)
+        shapes = hardware_choices(plan, schedule)
+        assert len(shapes) == count and shapes[0] == ()
+        sources = set()
+        for hw in shapes:
+            lowered = kernel.lowered(sig, Config(tiles, Pipeline(2, 2), False, hw))
+            runtime.compile_source(lowered.source, f"{kernel.nest.name}.hip")
+            sources.add(lowered.source)
+        assert len(sources) == count
+    plan, schedule = matmul.build(matmul.signature(spec(1024, 1024, dtype=bf), spec(1024, 1024, dtype=bf)),
+                                  MatmulTiles(512, 512, 512))
+    assert [dict(h) for h in hardware_choices(plan, schedule)][1:] == [{"bm": 256, "bn": 128}, {"bm": 128, "bn": 256},
+                                                                      {"bm": 128, "bn": 128}]

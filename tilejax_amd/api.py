@@ -237,7 +237,8 @@ class Kernel:
             plan, schedule = self.build(signature, config.tunable)
             if config.cursor and not plan.either:
                 raise KernelError(f"{self.nest.name}: only a kernel with runtime masks finds its steps with a cursor")
-            program = codegen.generate(plan, schedule, config.pipeline, trace=trace, cursor=config.cursor)
+            program = codegen.generate(plan, schedule, config.pipeline, trace=trace, cursor=config.cursor,
+                                       hardware=dict(getattr(config, "hardware", ())))
             entry.lowered[key] = Lowered(plan, schedule, config, program.source, trace, program)
         return entry.lowered[key]
 

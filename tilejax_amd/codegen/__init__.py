@@ -17,7 +17,7 @@ for any nest the planner accepts and tuned for none. A nest even that can't lowe
 from __future__ import annotations
 
 import re
-from typing import Any
+from typing import Any, Dict, List, Optional, Tuple
 
 from ..errors import KernelError
 from ..pipeline import Pipeline
@@ -25,23 +25,58 @@ from ..plan import Plan
 from ..schedule import Schedule
 from .program import Program
 
-__all__ = ["Program", "default_pipeline", "generate"]
+__all__ = ["Program", "default_pipeline", "generate", "hardware_choices"]
 
 
 def _symbol(plan: Plan) -> str:
     return "tj_" + re.sub(r"[^A-Za-z0-9_]", "_", plan.nest.name)
 
 
+def _family(plan: Plan) -> Tuple[str, Any]:
+    """The kernel family that takes `plan` and its match, or ("generic", error or None): the first family
+    whose matcher recognises the nest; a family that recognises it but can't take it leaves its KernelError."""
+    from . import decode, flash, gemm
+
+    if plan.walk:
+        return "generic", None
+    try:
+        for name, module in (("gemm", gemm), ("flash", flash), ("decode", decode)):
+            found = module.match(plan)
+            if found is not None:
+                return name, found
+    except KernelError as e:
+        return "generic", e
+    return "generic", None
+
+
 def default_pipeline(plan: Plan, schedule: Schedule) -> Pipeline:
-    """Two LDS slots per streamed operand (a 256x256x64 bf16 matmul tile fills 128 KiB with two), two
-    output buffers: the starting point tuning moves from."""
-    return Pipeline(2, 2)
+    """The buffering each family measured best at the BASELINE configs: two LDS stages for the matmul (a
+    256x256x64 bf16 tile fills 128 KiB with two) and for attention (two 4-wave workgroups per CU), three
+    steps ahead for decode. Output buffers: the reference's default two, which change nothing here (the gfx950
+    kernels store from registers, see pipeline.py)."""
+    family, _ = _family(plan)
+    return Pipeline(3 if family == "decode" else 2, 2)
+
+
+def hardware_choices(plan: Plan, schedule: Schedule) -> List[Tuple[Tuple[str, int], ...]]:
+    """The kernel shapes tuning may try for `plan` beside its buffering, as sorted (knob, value) tuples, the
+    default first: the matmul's workgroup tile, attention's waves per workgroup and keys per block."""
+    from . import flash, gemm
+
+    family, found = _family(plan)
+    choices: List[Dict[str, int]] = [{}]
+    if family == "gemm":
+        choices = gemm.hardware_choices(found)
+    elif family == "flash":
+        choices = flash.hardware_choices(found)
+    return [()] + [tuple(sorted(c.items())) for c in choices[1:]]  # () is the default shape
 
 
 def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool = False,
-             cursor: bool = False) -> Program:
-    """The program for this plan, schedule and pipeline; with `cursor`, a kernel with runtime masks finds
-    its steps itself as it runs rather than from device-built step tables (the decode family)."""
+             cursor: bool = False, hardware: Optional[Dict[str, int]] = None) -> Program:
+    """The program for this plan, schedule and pipeline (and `hardware` knobs of the family's kernel shape,
+    from `hardware_choices`); with `cursor`, a kernel with runtime masks finds its steps itself as it runs
+    rather than from device-built step tables (the decode family)."""
     from . import decode, flash, gemm, generic
 
     name = _symbol(plan)
@@ -57,10 +92,10 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
             if cursor:
                 raise KernelError(f"{plan.nest.name}: the matmul family reads runtime masks from device step "
                                   "tables (no cursor)")
-            return gemm.lower(plan, schedule, pipeline, found, name, trace=trace)
+            return gemm.lower(plan, schedule, pipeline, found, name, trace=trace, hardware=hardware)
         found = flash.match(plan)
         if found is not None:
-            return flash.lower(plan, schedule, pipeline, found, name, trace=trace)
+            return flash.lower(plan, schedule, pipeline, found, name, trace=trace, hardware=hardware)
         found = decode.match(plan)
         if found is not None:
             return decode.lower(plan, schedule, pipeline, found, name, trace=trace, cursor=cursor)

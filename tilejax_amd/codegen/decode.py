@@ -54,7 +54,8 @@ THREADS = 256
 WAVES = 4
 RP = 32  # query rows the kernels work on: a spec's R <= 32 rows, the rest zero
 SUB = 16  # key positions per kernel step: a spec step of P positions (a page, a cache block) is P / SUB of them
-DEPTH = 3  # K register sets and V LDS stages: pages fetched ahead of the step being computed
+DEPTH = 3  # K register sets and V LDS stages (steps fetched ahead of the one computed): the default
+MAX_DEPTH = 4
 
 
 @dataclass
@@ -115,9 +116,9 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
 
 class _Decode:
     def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False,
-                 cursor: bool = False) -> None:
+                 cursor: bool = False, depth: int = DEPTH) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
-        self.trace, self.cursor = trace, cursor
+        self.trace, self.cursor, self.depth = trace, cursor, depth
         if m.rows > RP or m.page % SUB or m.width % (32 * WAVES):
             raise KernelError(f"the gfx950 decode lowering takes up to {RP} query rows, pages (or cache blocks) of a multiple "
                               f"of {SUB} positions and widths that are multiples of {32 * WAVES} "
@@ -128,7 +129,7 @@ class _Decode:
         self.grid = gfx950.CUS
         self.slots = self.grid + sch.pattern_tiles
         self.max_per = -(-sch.pattern_steps * self.sub // self.grid)  # most kernel steps one workgroup takes
-        self.lds = DEPTH * SUB * m.width * 2 + WAVES * SUB * RP * 4 + 20 * self.max_per
+        self.lds = self.depth * SUB * m.width * 2 + WAVES * SUB * RP * 4 + 20 * self.max_per
         # with a cursor the attention kernel evaluates the mask itself: a 64-block word per tile and word
         self.words = sch.pattern_tiles * -(-plan.phases[0].range.count // 64)
         if cursor:
@@ -260,7 +261,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
         slabs = WQ // 32  # K = 32 slabs of S^T = K Q^T per wave
         dtiles = WQ // 32  # 32-wide tiles of acc^T per wave
         loads = P * W // 8 // THREADS  # 16-byte V loads per thread per step
-        D = DEPTH
+        D = self.depth
         phase, index = self.phase, self.index
         radix = sch.phase_radix * sch.iterations
         jvar = phase.var
@@ -686,6 +687,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
 
 def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: str, trace: bool = False,
           cursor: bool = False) -> Program:
+    """The decode program; its depth (K register sets and V LDS stages: steps fetched ahead) is the
+    pipeline's input buffers, 2 to MAX_DEPTH."""
     if m.out.dtype.name != "bfloat16":
         raise KernelError("the gfx950 decode lowering stores bf16 outputs")
-    return _Decode(plan, sch, m, name, trace, cursor).program()
+    depth = max(2, min(pipeline.input_buffers, MAX_DEPTH))
+    return _Decode(plan, sch, m, name, trace, cursor, depth).program()

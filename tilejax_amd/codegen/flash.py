@@ -57,9 +57,10 @@ MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 on
 # they keep no step with each other, one's MFMA work runs beside the other's softmax. Measured against one
 # workgroup of 8 waves (256 rows) and four stages: equal at (4, 16, 2048, 128), 5 % faster at
 # (1, 16, 4096, 128).
-AHEAD = 1  # K and V blocks are loaded this many blocks ahead of use; one barrier per block
-STAGES = AHEAD + 1  # LDS stages of K and V (at least AHEAD + 1)
-RING = AHEAD + 2  # block-table entries kept in scalars: blocks b .. b + AHEAD + 1, at b modulo RING
+# K and V blocks are loaded `ahead` blocks ahead of use (the pipeline's input buffers less one, at most
+# MAX_AHEAD) through ahead + 1 LDS stages, one barrier per block; block-table entries of blocks b .. b + ahead
+# + 1 are kept in a ring of ahead + 2 scalars, at b modulo the ring.
+MAX_AHEAD = 3
 WAVES = 4  # waves per workgroup (None: 8 for tiles of a multiple of 256 query rows, else 4)
 BKV = 64  # keys per block (a multiple of 32)
 K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
@@ -270,17 +271,22 @@ def _loop_window(op: Operand, var: str) -> Tuple[int, Any]:
 
 class _Flash:
     def __init__(self, plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str,
-                 trace: bool = False) -> None:
+                 trace: bool = False, hardware: Optional[Dict[str, int]] = None) -> None:
         self.plan, self.sch, self.pipeline, self.m, self.name = plan, sch, pipeline, m, name
         self.trace = trace
+        hardware = hardware or {}
+        # K and V blocks loaded `ahead` blocks ahead through ahead + 1 LDS stages: the pipeline's input buffers
+        self.ahead = max(1, min(pipeline.input_buffers - 1, MAX_AHEAD))
+        self.stages, self.ring = self.ahead + 1, self.ahead + 2
         if m.d % 32 or m.dv % 32 or m.d > 128 or m.dv > 128:
             raise KernelError(f"the gfx950 attention lowering takes head dims that are multiples of 32 up to 128 "
                               f"(got {m.d} and {m.dv})")
-        self.nw = WAVES or (8 if m.rows % 256 == 0 else 4 if m.rows % 128 == 0 else 0)
-        if not self.nw:
-            raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of 128 rows (got {m.rows})")
+        self.nw = hardware.get("waves", WAVES) or (8 if m.rows % 256 == 0 else 4 if m.rows % 128 == 0 else 0)
+        if not self.nw or m.rows % (32 * self.nw):
+            raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of {32 * (self.nw or 4)} "
+                              f"rows (got {m.rows})")
         self.bq = 32 * self.nw
-        self.bkv = BKV
+        self.bkv = hardware.get("bkv", BKV)
         if m.bk % self.bkv:
             raise KernelError(f"the gfx950 attention lowering needs key blocks of a multiple of {self.bkv} (got {m.bk})")
         if plan.runtime or sch.runtime:
@@ -454,7 +460,7 @@ class _Flash:
             per_item = self.bq * m.dv // 4 // 256
             launches.append(Launch(f"{self.name}_merge", args, (len(merges) * per_item, 1, 1), (256, 1, 1), 0))
         flop = 2.0 * sum(w for w in weights) * 32 * self.bkv * (m.d + m.dv)
-        lds = STAGES * self.bkv * (m.d + m.dv) * 2
+        lds = self.stages * self.bkv * (m.d + m.dv) * 2
         return Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
             inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
@@ -569,7 +575,7 @@ class _Flash:
 // spec tile {m.rows} x {m.bk} (head dims {D}, {DV}); workgroup {bq} query rows in {nw} waves, key blocks of {bkv}.
 {PRELUDE}
 {struct}""")
-        for s in range(STAGES):
+        for s in range(self.stages):
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
         w(f"""
@@ -762,39 +768,39 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
             a(f"{ind}}}")
             return o
 
-        # K and V blocks stream through STAGES LDS stages, loaded AHEAD blocks ahead. At the barrier that opens
-        # block b every wave has finished reading the stage block b + AHEAD goes into (that of block
-        # b + AHEAD - STAGES), so that load is issued right after it.
+        # K and V blocks stream through `stages` LDS stages, loaded `ahead` blocks ahead. At the barrier that opens
+        # block b every wave has finished reading the stage block b + ahead goes into (that of block
+        # b + ahead - stages, stages = ahead + 1), so that load is issued right after it.
         per_block = ldk_n + ldv_n
 
-        unroll = STAGES * RING // math.gcd(STAGES, RING)  # loop positions: stage p % STAGES, ring slot p % RING
-        w(f"  int bj[{RING}], bc[{RING}];  // table entries of blocks b .. b + {RING - 1}, at b mod {RING}")
-        for x in range(AHEAD + 1):
+        unroll = self.stages * self.ring // math.gcd(self.stages, self.ring)  # positions: stage p % stages, slot p % ring
+        w(f"  int bj[{self.ring}], bc[{self.ring}];  // table entries of blocks b .. b + {self.ring - 1}, at b mod {self.ring}")
+        for x in range(self.ahead + 1):
             w(entry_load(str(x), x, "  "))
-        for s in range(AHEAD):
+        for s in range(self.ahead):
             w(f"  if ({s} < nblk) {{")
             L.extend(issue(s, s, "    "))
             w("  }")
         w("  ak_bf16x8 pf[" + str(ks) + "];  // P^T of the block (srcB of O^T = V^T P^T)")
         w(f"  for (int b = 0; b < nblk; b += {unroll}) {{")
         for p_ in range(unroll):
-            s, r_ = p_ % STAGES, p_ % RING
+            s, r_ = p_ % self.stages, p_ % self.ring
             w(f"    {{ const int b_ = b + {p_};")
             w("      if (b_ < nblk) {")
             if tr:
                 w(f"        const unsigned long long tr_w0 = {NOW};")
-            # Block b_ has landed; the (at most AHEAD - 1) later blocks issued may still be in flight.
-            for ahead in range(AHEAD - 1, 0, -1):
-                w(f"        {'if' if ahead == AHEAD - 1 else 'else if'} (b_ + {ahead} < nblk) {{ AK_WAIT_VM({ahead * per_block}); }}")
-            w("        " + ("else " if AHEAD > 1 else "") + "{ AK_WAIT_VM(0); }")
+            # Block b_ has landed; the (at most self.ahead - 1) later blocks issued may still be in flight.
+            for ahead in range(self.ahead - 1, 0, -1):
+                w(f"        {'if' if ahead == self.ahead - 1 else 'else if'} (b_ + {ahead} < nblk) {{ AK_WAIT_VM({ahead * per_block}); }}")
+            w("        " + ("else " if self.ahead > 1 else "") + "{ AK_WAIT_VM(0); }")
             w("        AK_WAIT_LGKM0();")
             w('        asm volatile("s_barrier" ::: "memory");')
             if tr:
                 w(f"        {{ const unsigned long long tr_w1 = {NOW}; if (b_ == 0) tr_fill = tr_w1 - tr_i0; else tr_wait += tr_w1 - tr_w0; }}")
-            w(f"        if (b_ + {AHEAD} < nblk) {{")
-            L.extend(issue((r_ + AHEAD) % RING, (s + AHEAD) % STAGES, "          "))
+            w(f"        if (b_ + {self.ahead} < nblk) {{")
+            L.extend(issue((r_ + self.ahead) % self.ring, (s + self.ahead) % self.stages, "          "))
             w("        }")
-            w(entry_load(f"b_ + {AHEAD + 1}", (r_ + AHEAD + 1) % RING, "        "))
+            w(entry_load(f"b_ + {self.ahead + 1}", (r_ + self.ahead + 1) % self.ring, "        "))
             L.extend(compute(s, "        ", r_))
             w("      }")
             w("    }")
@@ -1074,11 +1080,25 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
 """
 
 
-def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str, trace: bool = False) -> Program:
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: str, trace: bool = False,
+          hardware: Optional[Dict[str, int]] = None) -> Program:
     if m.q.tile.dtype.name == "float32":
         if m.out.dtype.name not in ("float32", "bfloat16"):
             raise KernelError("the gfx950 attention lowering stores f32 or bf16 outputs")
         return _FlashF32(plan, sch, pipeline, m, name, trace).program()
     if m.out.dtype.name != "bfloat16":
         raise KernelError("the gfx950 attention lowering stores bf16 outputs")
-    return _Flash(plan, sch, pipeline, m, name, trace).program()
+    return _Flash(plan, sch, pipeline, m, name, trace, hardware).program()
+
+
+def hardware_choices(m: FlashMatch) -> List[Dict[str, int]]:
+    """The kernel shapes tuning may try for this match: waves per workgroup (32 query rows each) and keys
+    per block. The first is the default."""
+    if m.q.tile.dtype.name == "float32":
+        return [{}]
+    found = []
+    for waves in (WAVES, 8 if WAVES == 4 else 4):
+        for bkv in (BKV, 32 if BKV == 64 else 64):
+            if m.rows % (32 * waves) == 0 and m.bk % bkv == 0:
+                found.append({"waves": waves, "bkv": bkv})
+    return found or [{}]

@@ -359,11 +359,13 @@ class HwTile:
         return self.stages * (self.bm + self.bn) * self.bk * 2
 
 
-def hardware_tile(m: GemmMatch, pipeline: Pipeline) -> HwTile:
+def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str, int]] = None) -> HwTile:
     """The workgroup tile for a spec tile (tm, tn, tk): at most 256 x 256 outputs (four waves of 128 x 128 at
-    most), K slices of 64 (32 if tk is an odd multiple of 64, 16 for tk = 32) so every tile's slice count is even, and the
-    LDS stages the pipeline asks for where they divide a step's slices and fit in LDS."""
-    bm, bn = min(m.tm, 256), min(m.tn, 256)
+    most; `hardware` may cap each side, "bm" and "bn"), K slices of 64 (32 if tk is an odd multiple of 64, 16
+    for tk = 32) so every tile's slice count is even, and the LDS stages the pipeline asks for where they
+    divide a step's slices and fit in LDS."""
+    hardware = hardware or {}
+    bm, bn = min(m.tm, hardware.get("bm", 256)), min(m.tn, hardware.get("bn", 256))
     if m.tm % bm or m.tn % bn or bm % 64 or bn % 64:
         raise KernelError(f"the gfx950 matmul lowering needs tiles that are multiples of 64 (got {m.tm} x {m.tn})")
     if m.tk % 64 and m.tk != 32:
@@ -391,9 +393,23 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline) -> HwTile:
 QUEUE_TAIL = [False]
 
 
-def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, name: str, trace: bool = False) -> Program:
-    hw = hardware_tile(m, pipeline)
+def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, name: str, trace: bool = False,
+          hardware: Optional[Dict[str, int]] = None) -> Program:
+    hw = hardware_tile(m, pipeline, hardware)
     return _Gemm(plan, sch, pipeline, m, hw, name, trace).program()
+
+
+def hardware_choices(m: GemmMatch) -> List[Dict[str, int]]:
+    """The workgroup tiles tuning may try for this match, as caps on each side (256 x 256 first, the
+    default; then 256 x 128, 128 x 256 and 128 x 128 where the spec tile divides into them)."""
+    found, seen = [], set()
+    for bm, bn in ((256, 256), (256, 128), (128, 256), (128, 128)):
+        got = (min(m.tm, bm), min(m.tn, bn))
+        if got in seen or m.tm % got[0] or m.tn % got[1]:
+            continue
+        seen.add(got)
+        found.append({"bm": bm, "bn": bn})
+    return found
 
 
 class _Gemm:
@@ -467,7 +483,7 @@ class _Gemm:
 
     def _check_parts(self) -> None:
         """f32 operands: every reduction block the kernel reads starts on a BK-slice boundary of the array, so
-        slice j of the operand is slices 3j..3j+2 of its parts."""
+        slice j of the operand is slices 6j..6j+5 of its parts (F32_PARTS: six bf16 slices per f32 slice)."""
         plan, m, bk = self.plan, self.m, self.hw.bk
         for role, op in (("a", m.a), ("b", m.b)):
             shape = plan.inputs[op.param].shape
@@ -477,7 +493,7 @@ class _Gemm:
                 raise KernelError(f"the gfx950 matmul lowering takes f32 operands whose reduction dim and windows "
                                   f"are multiples of {bk} and whose rows are multiples of 8 elements")
         if plan.phases:
-            r = plan.phases[0].range
+            r = plan.phases[m.mphase].range  # the matmul's own loop (a row-sum loop may run before it)
             if r.start % bk or r.step % bk:
                 raise KernelError(f"the gfx950 matmul lowering takes f32 operands with reduction blocks on "
                                   f"multiples of {bk}")
@@ -1240,14 +1256,20 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             pk[h2][1] = ak_pack_bf16x2(res[2], res[3]);
           }}
           const bool up = lane_e >= 32;
-          const unsigned r0 = __shfl_xor(up ? pk[0][0] : pk[1][0], 32), r1 = __shfl_xor(up ? pk[0][1] : pk[1][1], 32);
-          const ak_u32x4 v = up ? ak_u32x4{{r0, r1, pk[1][0], pk[1][1]}} : ak_u32x4{{pk[0][0], pk[0][1], r0, r1}};
+          // lane and lane ^ 32 swap halves: the low lanes keep pk[0] and take their partner's pk[0], the high
+          // lanes take their partner's pk[1] and keep pk[1] (v_permlane32_swap, no LDS crossbar)
+          const auto s0 = __builtin_amdgcn_permlane32_swap(pk[0][0], pk[1][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(pk[0][1], pk[1][1], false, false);
+          const ak_u32x4 v = ak_u32x4{{s0[0], s1[0], s0[1], s1[1]}};
           const int ec8 = sn * {bn} + wn * {wtn} + j_ * 32 + 16 * p2 + (up ? 8 : 0);
           *(ak_u32x4*)((ak_u16*){O} + obase + (long long)er * {ldo} + ec8) = v;
         }}
       }}
     }}"""
-        EPILOGUE_LOOP = paired_loop if out_bf16 and ldo % 8 == 0 else old_loop  # (16-byte aligned rows)
+        if out_bf16 and ldo % 8:
+            raise KernelError("the gfx950 matmul lowering stores bf16 outputs 16 bytes at a time: rows of a multiple "
+                              f"of 8 elements, not {ldo}")
+        EPILOGUE_LOOP = paired_loop if out_bf16 else old_loop
         w(f"""    // Epilogue: the accumulator holds C transposed (lane: one row, four consecutive columns per group).
     // The lane index goes through an empty asm so the stores' addresses are computed here, not hoisted
     // above the K loop where they would take registers the loop needs.

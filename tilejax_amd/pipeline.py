@@ -1,16 +1,19 @@
 """How deeply a kernel buffers its copies: the part of a schedule that is the kernel's, not the user's.
 
-The reference's Pipeline (src/autokernel/pipeline.py:42-147) counts VMEM slots per copy. On gfx950 the
-same two numbers mean:
+The reference's Pipeline (src/autokernel/pipeline.py:42-147) counts VMEM slots per copy. On gfx950,
+`input_buffers` is the depth of the ring each family streams its operands through (1-4):
 
-- `input_buffers`: LDS slots in the ring each streamed operand rotates through (1-4). A step's tiles are
-  fetched `input_buffers - 1` steps ahead (across tile boundaries: the kernel is persistent), so more
-  slots hide more HBM latency at the cost of LDS, which also bounds occupancy.
-- `output_buffers`: with 2 or more, a tile's last step starts the next tile's first fetches before its
-  output stores (the stores drain while the next tile computes); with 1, stores go first.
+- matmul: LDS stages of the A and B slices (at least 2, where they divide a step's slices and fit in LDS);
+- attention: K and V blocks loaded `input_buffers - 1` blocks ahead through that many + 1 LDS stages;
+- decode: K register sets and V LDS stages, steps fetched ahead (2-4).
 
-`default_pipeline` picks the deepest ring (3, as the reference measured best, else 2) that fits the LDS
-the lowering needs per workgroup.
+`output_buffers` is accepted (1-3) for the reference's API and changes nothing here: the gfx950 kernels
+store output tiles straight from registers, with no output copy to queue, so the tuner doesn't propose it.
+`codegen.default_pipeline` gives each family the buffering it measured best (two stages for the matmul and
+attention, three steps ahead for decode).
+
+Bursts (the reference's one-step kernels grouping their DMA copies against HBM read/write turnaround) have
+no counterpart in these kernels, which load through LDS rings and store from registers: a `burst` raises.
 """
 
 from __future__ import annotations

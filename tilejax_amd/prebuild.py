@@ -106,9 +106,51 @@ def standard() -> Iterator[Tuple[object, tuple]]:
         pass
 
 
+def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
+    """(kernel, signature arguments, Config, trace) of the kernel shapes the GPU tests pin and the tuning test
+    at the dense BASELINE config tries (the tuner builds with trace regions)."""
+    if ROOT not in sys.path:
+        sys.path.insert(0, ROOT)
+    from examples import causal_attention as ca
+    from examples import causal_matmul as cm
+    from examples import decode
+    from examples import matmul as mm
+
+    from .codegen import hardware_choices
+    from .pipeline import Pipeline
+    from .tune import Config
+
+    tiles = mm.MatmulTiles(512, 512, 512)
+    for kernel in (mm.matmul, cm.causal_matmul):
+        for hw, n in (((("bm", 256), ("bn", 128)), 2), ((("bm", 128), ("bn", 256)), 2), ((("bm", 128), ("bn", 128)), 3),
+                      ((), 4)):
+            yield kernel, (_bf16(1024, 1024), _bf16(1024, 1024)), Config(tiles, Pipeline(n, 2), False, hw), False
+    args = (_bf16(8192, 8192), _bf16(8192, 8192))
+    plan, schedule = mm.matmul.build(mm.matmul.signature(*args), mm.matmul.default_tunable)
+    for hw in hardware_choices(plan, schedule):
+        for n in (2, 3):
+            yield mm.matmul, args, Config(mm.matmul.default_tunable, Pipeline(n, 2), False, hw), True
+    blocks = ca.AttentionBlocks(256, 256)
+    for hw, n in (((("bkv", 64), ("waves", 8)), 2), ((("bkv", 32), ("waves", 4)), 2),
+                  ((("bkv", 32), ("waves", 8)), 2), ((), 3), ((), 4)):
+        yield ca.causal_attention, tuple(_bf16(2, 4, 1024, 128) for _ in range(3)), Config(blocks, Pipeline(n, 2), False, hw), False
+    ins = (_bf16(5, 1, 32, 128), _bf16(500, 16, 1024), _bf16(500, 16, 1024), _i32(5, 100), _i32(5))
+    for n in (2, 4):
+        for cursor in (False, True):
+            yield decode.paged_gqa_decode, ins, Config(None, Pipeline(n, 2), cursor), False
+
+
 def compile_all(verbose: bool = True) -> List[str]:
-    """Lower and compile every standard kernel; the names of those the backend can't lower yet."""
+    """Lower and compile every standard kernel and tested kernel shape; the names of those the backend can't
+    lower yet."""
+    from . import runtime
+
     skipped = []
+    for kernel, args, config, trace in shapes():
+        lowered = kernel.lowered(kernel.signature(*args), config, trace=trace)
+        runtime.compile_source(lowered.source, f"{kernel.nest.name}.hip")
+        if verbose:
+            print(f"compiled {kernel.nest.name} {[a[0] for a in args]} {config}{' traced' if trace else ''}", flush=True)
     for kernel, args in standard():
         try:
             lowered = kernel.lower(*args)

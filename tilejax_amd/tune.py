@@ -2,12 +2,14 @@
 and let its profile pick the next schedules.
 
 The reference's tuner (src/autokernel/tune.py:57-368), on the MI355X: a schedule is a `Config` (the
-kernel's tunable and its `Pipeline`); `search` hill-climbs from the defaults, moving to the first proposal
-at least 1 % faster, for at most `BUDGET` candidates; a candidate that fails to build, compile or run, or
-whose result differs from the reference, is a `Trial` with an error (infinitely slow). `proposals` orders
-the next schedules by the bottleneck: exposed input waits -> one more LDS slot, then the neighbouring
-tunables moving fewer bytes; overhead -> neighbours with fewer, bigger steps; otherwise every neighbour,
-fewest steps first. Neighbours that build the same loops are skipped.
+kernel's tunable, its `Pipeline`, and here also the family's kernel shape on gfx950: the matmul's
+workgroup tile, attention's waves per workgroup and keys per block); `search` hill-climbs from the
+defaults, moving to the first proposal at least 1 % faster, for at most `BUDGET` candidates; a candidate
+that fails to build, compile or run, or whose result differs from the reference, is a `Trial` with an
+error (infinitely slow). `proposals` orders the next schedules by the bottleneck: exposed input waits ->
+one more LDS slot, then the family's other kernel shapes, then the neighbouring tunables moving fewer
+bytes; overhead -> neighbours with fewer, bigger steps; otherwise every neighbour, fewest steps first.
+Neighbours that build the same loops are skipped.
 
 Tuning needs a GPU; without one the defaults are used (and `kernel(...)` raises anyway: no CPU fallback).
 """
@@ -24,11 +26,17 @@ import torch
 
 from . import profiling
 from .errors import KernelError
-from .pipeline import MAX_INPUT_BUFFERS, MAX_OUTPUT_BUFFERS, Pipeline
+from .pipeline import MAX_INPUT_BUFFERS, Pipeline
 from .plan import Kind, Operand, Plan
 from .profiling import KernelProfile
 from .schedule import Schedule
 from .tunable import choices, neighbours
+
+
+def codegen_hardware_choices(plan: Plan, schedule: Schedule) -> List[Tuple[Tuple[str, int], ...]]:
+    from .codegen import hardware_choices
+
+    return hardware_choices(plan, schedule)
 
 __all__ = ["BUDGET", "Config", "Trial", "Tuning", "proposals", "random_inputs", "search", "tune"]
 
@@ -40,15 +48,20 @@ MIN_GAIN = 0.01
 
 @dataclass(frozen=True)
 class Config:
-    """A schedule: the kernel's tunable (None if it has none), its buffering, and whether a kernel with
-    runtime masks finds its steps with a cursor as it runs (src/autokernel/tune.py:57-72)."""
+    """A schedule: the kernel's tunable (None if it has none), its buffering, whether a kernel with runtime
+    masks finds its steps with a cursor as it runs (src/autokernel/tune.py:57-72), and the family's kernel
+    shape on gfx950 (`hardware`: sorted (knob, value) pairs from codegen.hardware_choices, () for the
+    default: the matmul's workgroup tile, attention's waves per workgroup and keys per block)."""
 
     tunable: Any
     pipeline: Pipeline
     cursor: bool = False
+    hardware: Tuple[Tuple[str, int], ...] = ()
 
     def __str__(self) -> str:
         rest = f"{self.pipeline}, steps found as it runs" if self.cursor else str(self.pipeline)
+        if self.hardware:
+            rest += ", " + " ".join(f"{k}={v}" for k, v in self.hardware)
         if self.tunable is None:
             return rest
         fields = ", ".join(f"{k}={getattr(self.tunable, k)!r}" for k in choices(self.tunable))
@@ -146,11 +159,13 @@ def proposals(kernel: Any, signature: Any, trial: Trial) -> List[Config]:
     buffering = []
     if prof.regions and prof.exposed_wait_s > exposed and pipe.input_buffers < MAX_INPUT_BUFFERS:
         buffering.append(dataclasses.replace(pipe, input_buffers=pipe.input_buffers + 1))
-    if prof.regions and prof.out_wait_s > exposed and pipe.output_buffers < MAX_OUTPUT_BUFFERS:
-        buffering.append(dataclasses.replace(pipe, output_buffers=pipe.output_buffers + 1))
     if not prof.regions and pipe.input_buffers < MAX_INPUT_BUFFERS:
         buffering.append(dataclasses.replace(pipe, input_buffers=pipe.input_buffers + 1))
-    moves = [Config(config.tunable, p, config.cursor) for p in buffering]
+    moves = [Config(config.tunable, p, config.cursor, config.hardware) for p in buffering]
+    # the family's other kernel shapes (workgroup tiles, waves, key blocks) at this tunable and buffering
+    for hw in codegen_hardware_choices(plan, schedule):
+        if hw != config.hardware and (hw or config.hardware):
+            moves.append(Config(config.tunable, pipe, config.cursor, hw))
     if plan.either:  # the other way of finding the steps (src/autokernel/tune.py:186-187), where it lowers
         other = dataclasses.replace(config, cursor=not config.cursor)
         try:
@@ -166,7 +181,7 @@ def proposals(kernel: Any, signature: Any, trial: Trial) -> List[Config]:
             continue
         if _loop_steps(plan) == loops:
             continue
-        near.append((_stats(plan, schedule), Config(tunable, pipe, config.cursor)))
+        near.append((_stats(plan, schedule), Config(tunable, pipe, config.cursor, config.hardware)))
     if prof.bottleneck == "dma":
         near = sorted((n for n in near if (n[0].bytes, n[0].steps) < (here.bytes, here.steps)),
                       key=lambda n: (n[0].bytes, n[0].steps))
@@ -195,10 +210,11 @@ def _other_kernels(kernel: Any, signature: Any, start: Config) -> List[Config]:
     generated kernels differ from its own."""
     here = kernel.lowered(signature, start).source
     found = []
-    plan, _ = kernel.build(signature, start.tunable)
+    plan, schedule = kernel.build(signature, start.tunable)
     cursors = (False, True) if plan.either else (start.cursor,)
-    for n, m, cursor in itertools.product(range(1, MAX_INPUT_BUFFERS + 1), range(1, MAX_OUTPUT_BUFFERS + 1), cursors):
-        config = Config(start.tunable, Pipeline(n, m), cursor)
+    shapes = codegen_hardware_choices(plan, schedule)
+    for n, cursor, hw in itertools.product(range(1, MAX_INPUT_BUFFERS + 1), cursors, shapes):
+        config = Config(start.tunable, Pipeline(n, start.pipeline.output_buffers), cursor, hw)
         if config == start:
             continue
         try:

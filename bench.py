@@ -17,8 +17,9 @@ It also carries:
 
 - `roofline`: the dense kernel's achieved TFLOP/s (algorithmic 2*8192^3 FLOP per launch over its mean
   launch time, from HIP events recorded on the stream the kernel runs on) against the 2.5 PFLOP/s bf16
-  dense MFMA peak; `traffic` is HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE, passed in with
-  `--traffic` (null otherwise);
+  dense MFMA peak; `traffic` is HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE runs
+  (profiles/traffic.json, used only when its recorded source hash is this run's dense kernel's; null
+  otherwise), or `--traffic`;
 - `cpu_baseline`: the CPU oracle's restatement of `kernel.fn` (oracle/kernels.py: the same loop nest,
   bf16 products accumulated in f32) timed on this host's cores on a bounded band of the same workload.
 
@@ -159,9 +160,16 @@ def cpu_baseline(budget_s: float = 12.0):
                       f"512^3 tiles, median of {len(times)} calls ({t * 1e3:.1f} ms each)"}
 
 
-def _measured_traffic(tiles):
+def source_hash(source: str) -> str:
+    import hashlib
+
+    return hashlib.sha256(source.encode()).hexdigest()[:16]
+
+
+def _measured_traffic(tiles, source: str):
     """HBM bytes per launch of the dense kernel at these tiles, from the committed rocprofv3 FETCH_SIZE and
-    WRITE_SIZE runs (profiles/traffic.json, scaled by a known-size copy), or None."""
+    WRITE_SIZE runs (profiles/traffic.json, scaled by a known-size copy), or None: also when the kernel
+    measured there (its source's hash) is not the kernel this run generated."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
@@ -169,7 +177,10 @@ def _measured_traffic(tiles):
     except (OSError, ValueError):
         return None
     entry = data.get("dense_8192_" + "x".join(str(t) for t in tiles))
-    return float(entry["bytes_per_launch"]) if entry else None
+    if not entry or entry.get("source_sha256") != source_hash(source):
+        _log("roofline.traffic: profiles/traffic.json measured another dense kernel; null until it is re-measured")
+        return None
+    return float(entry["bytes_per_launch"])
 
 
 def main() -> int:
@@ -407,7 +418,7 @@ def main() -> int:
             out["decode"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
 
     achieved = flop / (launch_ms * 1e-3) / 1e12
-    traffic = float(args.traffic) if args.traffic else _measured_traffic(out["dense"]["tiles"])
+    traffic = float(args.traffic) if args.traffic else _measured_traffic(out["dense"]["tiles"], lowered.source)
     result = {
         "metric": "bf16 TFLOP/s + % MFMA peak: 8192^3 matmul; causal MHA B4 H16 S2048 D128",
         "value": round(tflops, 2),

@@ -1,0 +1,117 @@
+"""The LDS ring protocol of the generated kernels, checked on the CPU (tilejax_amd/codegen/protocol.py).
+
+Each kernel family records, as it emits the kernel's text, the waits, barriers, loads and reads of its loop;
+the checker replays them for many block counts (matmul items back to back, as the persistent kernel runs
+them) and requires every read to follow a wait and barrier that landed its block, and every load into a
+stage to follow a wait and barrier after the reads of the block it replaces. This stands in for the
+reference's interpreter race detector (tests/helpers.py:26-35 of the reference), which has no gfx950
+counterpart. A planted mistake in each family's events (a barrier dropped, a wait loosened) must fail.
+"""
+
+import pytest
+
+from examples.causal_attention import AttentionBlocks, causal_attention
+from examples.causal_matmul import causal_matmul
+from examples.decode import paged_gqa_decode
+from examples.matmul import MatmulTiles, matmul
+from examples.moe import GroupTiles, grouped_matmul
+from tests.helpers import spec
+from tilejax_amd import Pipeline, jaxlite
+from tilejax_amd.codegen.protocol import ProtocolError, check, loads_reads
+from tilejax_amd.tune import Config
+
+BF, F32, I32 = jaxlite.bfloat16, jaxlite.float32, jaxlite.int32
+
+
+def _lowered(kernel, args, tunable, buffers=2, hardware=(), cursor=False):
+    return kernel.lowered(kernel.signature(*args), Config(tunable, Pipeline(buffers, 2), cursor, hardware))
+
+
+def _matmul_cases():
+    sq = (spec(1024, 1024, dtype=BF), spec(1024, 1024, dtype=BF))
+    for buffers in (2, 3, 4):
+        for hw in ((), (("bm", 256), ("bn", 128)), (("bm", 128), ("bn", 128))):
+            yield f"matmul b{buffers} {hw}", _lowered(matmul, sq, MatmulTiles(512, 512, 512), buffers, hw)
+    yield "causal", _lowered(causal_matmul, sq, MatmulTiles(512, 512, 512))
+    yield "matmul tk 32", _lowered(matmul, sq, MatmulTiles(256, 256, 32))
+    yield "matmul f32", _lowered(matmul, (spec(256, 384, dtype=F32), spec(384, 256, dtype=F32)), MatmulTiles(128, 128, 128))
+    yield "grouped", _lowered(grouped_matmul, (spec(1024, 512, dtype=BF), spec(4, 512, 1024, dtype=BF), spec(4, dtype=I32)),
+                              GroupTiles(512, 256))
+
+
+@pytest.mark.parametrize("name,lowered", list(_matmul_cases()), ids=lambda x: x if isinstance(x, str) else "")
+def test_matmul_ring(name, lowered):
+    prog = lowered.program
+    rec, stages = prog.protocol, prog.notes["stages"]
+    covered = set()
+    for rounds in (1, 2, 3, 5):
+        T = rounds * stages  # slices per item: the kernel's loop takes whole rounds of its stages
+        events = rec.replay(T) + rec.replay(T) + rec.replay(2 * T)  # items back to back
+        check(events, name)
+        covered |= loads_reads(events)
+    assert covered == {(k, s) for k in ("load", "read") for s in range(stages)}
+
+
+def _flash_cases():
+    args = tuple(spec(2, 4, 1024, 128, dtype=BF) for _ in range(3))
+    for buffers in (2, 3, 4):
+        for hw in ((), (("bkv", 32), ("waves", 8))):
+            yield f"attention b{buffers} {hw}", _lowered(causal_attention, args, AttentionBlocks(256, 256), buffers, hw)
+
+
+@pytest.mark.parametrize("name,lowered", list(_flash_cases()), ids=lambda x: x if isinstance(x, str) else "")
+def test_attention_ring(name, lowered):
+    rec = lowered.program.protocol
+    for nblk in range(0, 14):
+        check(rec.replay(nblk), f"{name}, {nblk} blocks")
+
+
+@pytest.mark.parametrize("buffers,cursor", [(2, False), (3, False), (4, False), (3, True)])
+def test_decode_rings(buffers, cursor):
+    args = (spec(5, 1, 32, 128, dtype=BF), spec(500, 16, 1024, dtype=BF), spec(500, 16, 1024, dtype=BF),
+            spec(5, 100, dtype=I32), spec(5, dtype=I32))
+    rec = _lowered(paged_gqa_decode, args, None, buffers, cursor=cursor).program.protocol
+    for steps in range(1, 14):
+        check(rec.replay(steps), f"decode depth {buffers}, {steps} steps")
+
+
+def _drop(events, kind, which=1):
+    """The events with the `which`-th event of `kind` removed."""
+    seen = 0
+    for i, ev in enumerate(events):
+        if ev[0] == kind:
+            seen += 1
+            if seen == which:
+                return events[:i] + events[i + 1:]
+    raise AssertionError(f"no {which}th {kind}")
+
+
+def _loosen(events, which=2):
+    """The `which`-th wait for loads allowed one more instruction in flight."""
+    seen = 0
+    out = list(events)
+    for i, ev in enumerate(out):
+        if ev[0] == "wait_vm":
+            seen += 1
+            if seen == which:
+                out[i] = ("wait_vm", ev[1] + 1)
+                return out
+    raise AssertionError("no such wait")
+
+
+def test_planted_mistakes_fail():
+    sq = (spec(1024, 1024, dtype=BF), spec(1024, 1024, dtype=BF))
+    mm = _lowered(matmul, sq, MatmulTiles(512, 512, 512)).program.protocol.replay(8)
+    fa = _lowered(causal_attention, tuple(spec(2, 4, 1024, 128, dtype=BF) for _ in range(3)),
+                  AttentionBlocks(256, 256)).program.protocol.replay(6)
+    args = (spec(5, 1, 32, 128, dtype=BF), spec(500, 16, 1024, dtype=BF), spec(500, 16, 1024, dtype=BF),
+            spec(5, 100, dtype=I32), spec(5, dtype=I32))
+    dc = _lowered(paged_gqa_decode, args, None, 3).program.protocol.replay(8)
+    for name, events in (("matmul", mm), ("attention", fa), ("decode", dc)):
+        check(events, name)
+        with pytest.raises(ProtocolError):  # (the first block's barriers can be redundant)
+            check(_drop(events, "barrier", 3), f"{name} without its third barrier")
+        with pytest.raises(ProtocolError):
+            check(_loosen(events, 2), f"{name} with a loose wait")
+    with pytest.raises(ProtocolError, match="still read"):  # the matmul's wait for its LDS reads dropped
+        check(_drop(mm, "wait_lgkm", 1), "matmul without a read wait")

@@ -45,6 +45,7 @@ from .common import Index, strides, tile_base
 from .device import PRELUDE
 from .expr import ElementEmitter, literal
 from .flash import Softmax, _is, _strip, softmax_structure
+from .protocol import Recorder
 from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 from .steps import attach_step_builder
 
@@ -221,7 +222,7 @@ class _Decode:
                       Launch(self.name, args, (self.grid, 1, 1), (THREADS, 1, 1), 0),
                       Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (THREADS, 1, 1), 0)],
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
-            tables=tables, workspace=workspace, lds_bytes=self.lds,
+            tables=tables, workspace=workspace, lds_bytes=self.lds, protocol=self.protocol,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
                    "cursor": self.cursor,
                    # trace regions cover the attention kernel; a slice is one kernel step, SUB positions
@@ -400,10 +401,13 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
                 f"{ind}}}",
             ]
 
+        rec = self.protocol = Recorder()  # V pages through LDS stages, K fragments through register sets
+
         def step(j: str, u: int, ind: str) -> List[str]:
             """Step j (= u modulo D): its K fragments in kb{u}, its V page in dc_sv{u}."""
             o: List[str] = []
             a = o.append
+            record = not rec.body.get(u)  # each position's events once (the loop and the tail emit the same)
             a(f"{ind}{{ const int j_ = {j};")
             a(f"{ind}  const int t = __builtin_amdgcn_readfirstlane(dc_st[j_][0]), code = __builtin_amdgcn_readfirstlane(dc_st[j_][1]);")
             if self.trace:
@@ -412,11 +416,17 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}  AK_WAIT_VM({wait_n});")
             # every wave is past step j - 1, so its V stage is free; every thread's part of V(j) has landed
             a(f'{ind}  asm volatile("s_barrier" ::: "memory");')
+            if record:
+                rec.at(u, lambda b, n: ("wait_vm", wait_n))
+                rec.at(u, lambda b, n: ("barrier",))
             if self.trace:
                 # the first step's wait is the pipeline fill; a flush inside the wait is output time
                 a(f"{ind}  {{ const unsigned long long d_ = {NOW} - tr_w0 - (tr_out - tr_o0);"
                   f" if (j_ == 0) tr_fill = d_; else tr_wait += d_; }}")
             o.extend(issue_v(f"j_ + {D - 1}", (u + D - 1) % D, ind + "  "))
+            if record:
+                rec.at(u, lambda b, n, st=(u + D - 1) % D: ("load", st, b + D - 1, loads))
+                rec.at(u, lambda b, n, ku=u: ("read_own", ("k", ku), b))  # the S product reads kb{u}
             a(f"{ind}  const bool run = !(code & 4);")
             # partial S^T over this wave's columns
             a(f"{ind}  if (run) {{")
@@ -434,6 +444,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}  }}")
             # kb{u} has been read: refill it D steps ahead
             o.extend(issue_k(f"j_ + {D}", u, ind + "  "))
+            if record:
+                rec.at(u, lambda b, n, ku=u: ("load", ("k", ku), b + D, slabs))
             a(f"{ind}  if (run) {{")
             a(f"{ind}    {self._decode_tile('t')}")
             a(f"{ind}    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step}; (void)lv_{jvar};")
@@ -442,6 +454,12 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             # an LDS-only barrier: the pages in flight stay in flight
             a(f"{ind}    AK_WAIT_LGKM0();")
             a(f'{ind}    asm volatile("s_barrier" ::: "memory");')
+            if record:
+                rec.at(u, lambda b, n: ("wait_lgkm",))
+                rec.at(u, lambda b, n: ("barrier",))
+                rec.at(u, lambda b, n, st=u: ("read", st, b))
+                # the transposed reads feed this step's MFMAs: their results are waited for before those run
+                rec.at(u, lambda b, n: ("wait_lgkm",))
             # softmax: lane = query row er, positions 8 (lane / 32) + e
             # the lane's row; the mask sees rows past R (zero queries, never stored) as row R - 1
             a(f"{ind}    const int lr = lane & 31, er = {'lr' if m.rows == RP else f'ak_imin(lr, {m.rows - 1})'};")
@@ -482,9 +500,13 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
 
         # prologue: what steps -D .. -1 would have issued: K(0), then V(x) and K(x + 1) for x < D - 1
         L.extend(issue_k("0", 0, "  "))
+        rec.add(("load", ("k", 0), 0, slabs))
         for x in range(D - 1):
             L.extend(issue_v(str(x), x, "  "))
             L.extend(issue_k(str(x + 1), x + 1, "  "))
+            rec.add(("load", x, x, loads))
+            rec.add(("load", ("k", x + 1), x + 1, slabs))
+        rec.loop(D)
         # whole rounds of D steps with no condition between them (the compiler's wait counts stay exact),
         # then the last steps; no wait drains the queue except at a tile change
         w("  int j = 0;")

@@ -47,6 +47,7 @@ from .common import Index, decode_tile, static_tile_steps, strides, tile_base
 from .device import PRELUDE
 from .expr import Emitter, Interval, intervals, literal, nodes_between
 from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
+from .protocol import Recorder
 
 __all__ = ["FlashMatch", "match", "lower"]
 
@@ -464,7 +465,7 @@ class _Flash:
         return Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
             inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
-            lds_bytes=lds,
+            lds_bytes=lds, protocol=getattr(self, "protocol", None),
             notes={"family": "flash", "block_q": self.bq, "block_kv": self.bkv, "waves": nw, "items": len(items),
                    "executed_flop": flop, "split_items": len(merges), "chunks": self.slots,
                    # the reference's step is (query tile, key block) of the spec; a workgroup's slice here is
@@ -774,13 +775,16 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
         per_block = ldk_n + ldv_n
 
         unroll = self.stages * self.ring // math.gcd(self.stages, self.ring)  # positions: stage p % stages, slot p % ring
+        rec = self.protocol = Recorder()  # the loop's LDS events (a stage holds a block's K and V), as emitted
         w(f"  int bj[{self.ring}], bc[{self.ring}];  // table entries of blocks b .. b + {self.ring - 1}, at b mod {self.ring}")
         for x in range(self.ahead + 1):
             w(entry_load(str(x), x, "  "))
         for s in range(self.ahead):
             w(f"  if ({s} < nblk) {{")
             L.extend(issue(s, s, "    "))
+            rec.add(("load", s, s, per_block), lambda n, s=s: s < n)
             w("  }")
+        rec.loop(unroll)
         w("  ak_bf16x8 pf[" + str(ks) + "];  // P^T of the block (srcB of O^T = V^T P^T)")
         w(f"  for (int b = 0; b < nblk; b += {unroll}) {{")
         for p_ in range(unroll):
@@ -793,15 +797,22 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
             for ahead in range(self.ahead - 1, 0, -1):
                 w(f"        {'if' if ahead == self.ahead - 1 else 'else if'} (b_ + {ahead} < nblk) {{ AK_WAIT_VM({ahead * per_block}); }}")
             w("        " + ("else " if self.ahead > 1 else "") + "{ AK_WAIT_VM(0); }")
+            rec.at(p_, lambda b, n, A=self.ahead: ("wait_vm", next((a * per_block for a in range(A - 1, 0, -1)
+                                                                     if b + a < n), 0)))
             w("        AK_WAIT_LGKM0();")
             w('        asm volatile("s_barrier" ::: "memory");')
+            rec.at(p_, lambda b, n: ("wait_lgkm",))
+            rec.at(p_, lambda b, n: ("barrier",))
             if tr:
                 w(f"        {{ const unsigned long long tr_w1 = {NOW}; if (b_ == 0) tr_fill = tr_w1 - tr_i0; else tr_wait += tr_w1 - tr_w0; }}")
             w(f"        if (b_ + {self.ahead} < nblk) {{")
             L.extend(issue((r_ + self.ahead) % self.ring, (s + self.ahead) % self.stages, "          "))
+            rec.at(p_, lambda b, n, st=(s + self.ahead) % self.stages, A=self.ahead: ("load", st, b + A, per_block),
+                   lambda b, n, A=self.ahead: b + A < n)
             w("        }")
             w(entry_load(f"b_ + {self.ahead + 1}", (r_ + self.ahead + 1) % self.ring, "        "))
             L.extend(compute(s, "        ", r_))
+            rec.at(p_, lambda b, n, st=s: ("read", st, b))
             w("      }")
             w("    }")
         w("  }")

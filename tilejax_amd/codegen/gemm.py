@@ -39,6 +39,7 @@ from .common import Index, decode_fill, decode_tile, static_tile_steps, strides,
 from .device import PRELUDE
 from .expr import ElementEmitter, Emitter, Interval, ctype, intervals, literal, nodes_between
 from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
+from .protocol import Recorder
 
 __all__ = ["GemmMatch", "match", "lower"]
 
@@ -733,6 +734,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
         prog = Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)], inputs=inputs,
             tables=dict(self.tables), workspace=workspace, state=dict(self.state), lds_bytes=hw.lds,
+            protocol=self.protocol,
             notes={"family": "gemm", "hw_tile": (hw.bm, hw.bn, hw.bk), "stages": hw.stages, "grid": grid,
                    "items": len(items), "constant_items": sum(1 for _, s, _ in items if (s >> 16) == 2),
                    "queued_items": self.n_small,
@@ -1153,15 +1155,22 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             return out
 
         ind = "    "
+        # the LDS events of one item's slices, as emitted (`protocol.check` replays items back to back)
+        rec = self.protocol = Recorder()
         if self.trace:
             w(f"{ind}const unsigned long long tr_i0 = {now}; tr_slices += T;")
         for s in range(S):
             L.extend(issue(str(s), s, ind))
+            rec.add(("load", s, s, per_slice))
         w(f"{ind}AK_WAIT_VM({per_slice * (S - 1)});")
         w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+        rec.add(("wait_vm", per_slice * (S - 1)))
+        rec.add(("barrier",))
         if self.trace:
             w(f"{ind}const unsigned long long tr_c0 = {now}; tr_fill += tr_c0 - tr_i0;")
         L.extend(reads(0, 0, 0, ind))
+        rec.add(("read", 0, 0))
+        rec.loop(S)
         w(f"{ind}for (int g = 0; g < T; g += {S}) {{")
         ind2 = ind + "  "
         for s in range(S):
@@ -1170,6 +1179,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                 w(f"{ind2}{{")
                 if k16 < k16s - 1:
                     L.extend(reads(s, k16 + 1, cur ^ 1, ind2 + "  "))
+                    rec.at(s, lambda b, n, st=s: ("read", st, b))
                     L.extend(mfmas(cur, ind2 + "  "))
                     L.extend(hints(ind2 + "  ", False))
                 else:
@@ -1181,16 +1191,26 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                     w(f"{ind2}  AK_WAIT_LGKM0();")
                     w(f"{ind2}  AK_WAIT_VM({per_slice * (S - 2)});")
                     w(f'{ind2}  asm volatile("s_barrier" ::: "memory");')
+                    rec.at(s, lambda b, n: ("wait_lgkm",))
+                    rec.at(s, lambda b, n: ("wait_vm", per_slice * (S - 2)))
+                    rec.at(s, lambda b, n: ("barrier",))
                     if self.trace:
                         w(f"{ind2}  tr_wait += {now} - tr_w0;")
                     L.extend(issue(f"g + {s + S}", s, ind2 + "  "))
+                    rec.at(s, lambda b, n, st=s: ("load", st, b + S, per_slice))
                     L.extend(reads((s + 1) % S, 0, cur ^ 1, ind2 + "  "))
+                    rec.at(s, lambda b, n, st=(s + 1) % S: ("read", st, b + 1))
                     L.extend(mfmas(cur, ind2 + "  "))
                     L.extend(hints(ind2 + "  ", True))
                 w(f"{ind2}}}")
         w(f"{ind}}}")
-        w(f"{ind}AK_WAIT_VM(0);")
+        # every load and LDS read of the item done, in every wave, before the next item's loads reuse the stages
+        w(f"{ind}AK_WAIT_VM(0); AK_WAIT_LGKM0();")
         w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+        rec.end_loop()
+        rec.add(("wait_vm", 0))
+        rec.add(("wait_lgkm",))
+        rec.add(("barrier",))
         if self.trace:
             w(f"{ind}const unsigned long long tr_o0 = {now}; tr_comp += tr_o0 - tr_c0;")
         if self.split:

@@ -61,6 +61,7 @@ class Program:
     state: Dict[str, int] = field(default_factory=dict)
     lds_bytes: int = 0
     notes: Dict[str, Any] = field(default_factory=dict)  # what the lowering chose (hardware tiles, ...)
+    protocol: Any = field(default=None, repr=False, compare=False)  # the LDS ring's events (protocol.Recorder)
     _modules: Dict[int, runtime.Module] = field(default_factory=dict, repr=False)
     _tables: Dict[int, Dict[str, torch.Tensor]] = field(default_factory=dict, repr=False)
 

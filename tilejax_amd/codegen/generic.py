@@ -51,6 +51,7 @@ THREADS = 256
 MEM_BUDGET = 2 << 30  # bytes of tile memory over the whole grid
 MAX_GRID = 1024
 ALIGN = 256
+MFMA_PRODUCTS = [True]  # bf16 products of 32-multiple shapes on the matrix cores (else scalar f32 FMAs)
 
 # Ops a pass must compute whole before anything reads an element of them.
 _WHOLE = {"reduce_max", "reduce_min", "reduce_sum", "reduce_mean", "reduce_any", "argmax", "dot", "dot_nt"}
@@ -338,6 +339,9 @@ class _Generic:
         N = y.shape[0] if n.op == "dot_nt" else y.shape[1]
         em = self._elements(materialized)
         dt = n.dtype
+        if (MFMA_PRODUCTS[0] and x.dtype.name == y.dtype.name == "bfloat16" and dt.name in ("float32", "bfloat16")
+                and M % 32 == 0 and N % 32 == 0 and K % 16 == 0):
+            return self._dot_mfma(n, name, x, y, M, N, K, em, ind)
         integer = dt.kind in "iub"
         acc_t = "long long" if integer else ("double" if dt.itemsize == 8 else "float")
 
@@ -356,6 +360,51 @@ class _Generic:
                     self._store_into(name, dt, res)]
 
         return self._pass((M, N), body, ind)
+
+    def _dot_mfma(self, n: Node, name: str, x: Node, y: Node, M: int, N: int, K: int, em: "_Elements",
+                  ind: str) -> List[str]:
+        """A product of bf16 matrices on the matrix cores: each wave takes 32 x 32 blocks of the output in
+        turn and accumulates them in f32 over K in steps of 16 (v_mfma_f32_32x32x16_bf16); a lane computes
+        the 8 operand elements its fragments hold (whatever fuses into the operands) and packs them. C's
+        element (i, j) of a block is lane j % 32's register 8 (r / 4) + 4 (lane / 32) + r % 4 == i."""
+        nt = n.op == "dot_nt"
+        blocks_n = N // 32
+        xa = em.at(x, ("(ib_ + (lane_ & 31))", "(k0_ + 8 * (lane_ >> 5) + e_)"))
+        yb = (em.at(y, ("(jb_ + (lane_ & 31))", "(k0_ + 8 * (lane_ >> 5) + e_)")) if nt
+              else em.at(y, ("(k0_ + 8 * (lane_ >> 5) + e_)", "(jb_ + (lane_ & 31))")))
+        out = self.buf.ref(name)
+        res = "acc_[r_]" if n.dtype.name == "float32" else _rounded("acc_[r_]", n.dtype)
+        return [
+            f"{ind}{{ const int lane_ = tid & 63, wave_ = tid >> 6;",
+            f"{ind}  for (int blk_ = wave_; blk_ < {(M // 32) * blocks_n}; blk_ += {THREADS // 64}) {{",
+            f"{ind}    const int ib_ = (blk_ / {blocks_n}) * 32, jb_ = (blk_ % {blocks_n}) * 32;",
+            f"{ind}    ak_f32x16 acc_ = {{}};",
+            f"{ind}    for (int k0_ = 0; k0_ < {K}; k0_ += 16) {{",
+            f"{ind}      unsigned pa_[4], pb_[4];",
+            f"{ind}      #pragma unroll",
+            f"{ind}      for (int e2_ = 0; e2_ < 4; ++e2_) {{",
+            f"{ind}        float va_[2], vb_[2];",
+            f"{ind}        #pragma unroll",
+            f"{ind}        for (int h_ = 0; h_ < 2; ++h_) {{",
+            f"{ind}          const int e_ = 2 * e2_ + h_;",
+            f"{ind}          va_[h_] = (float)({xa});",
+            f"{ind}          vb_[h_] = (float)({yb});",
+            f"{ind}        }}",
+            f"{ind}        pa_[e2_] = ak_pack_bf16x2(va_[0], va_[1]);",
+            f"{ind}        pb_[e2_] = ak_pack_bf16x2(vb_[0], vb_[1]);",
+            f"{ind}      }}",
+            f"{ind}      acc_ = __builtin_amdgcn_mfma_f32_32x32x16_bf16(",
+            f"{ind}          __builtin_bit_cast(ak_bf16x8, ak_u32x4{{pa_[0], pa_[1], pa_[2], pa_[3]}}),",
+            f"{ind}          __builtin_bit_cast(ak_bf16x8, ak_u32x4{{pb_[0], pb_[1], pb_[2], pb_[3]}}), acc_, 0, 0, 0);",
+            f"{ind}    }}",
+            f"{ind}    #pragma unroll",
+            f"{ind}    for (int r_ = 0; r_ < 16; ++r_)",
+            f"{ind}      {out}[(ib_ + 8 * (r_ >> 2) + 4 * (lane_ >> 5) + (r_ & 3)) * {N} + jb_ + (lane_ & 31)] = "
+            f"({self.buf.types[name]})({res});",
+            f"{ind}  }}",
+            f"{ind}}}",
+            f"{ind}__syncthreads();",
+        ]
 
     def _reduce(self, n: Node, name: str, materialized: Dict[int, str], ind: str) -> List[str]:
         b = _bound_args(n)

@@ -125,3 +125,35 @@ def test_indices_made_once_per_tile():
     x = rand((5, 16, 256))
     got = run(make_kernel(ONCE_PER_TILE, OFFSETS=OFFSETS), x, what="once per tile")
     close(got, once_per_tile_float64(x), 1e-5, 1e-4)
+
+
+def test_pairs_and_word_stores():
+    from tests.test_walk import PAIRS, WRITE, pairs_float64, write_expected, write_inputs
+
+    kv, table = rand((5, 16, 4, 2, 128), dtype=torch.bfloat16), i32(4, 0, 2, 3)
+    print("generic: pairs", flush=True)
+    got = make_kernel(PAIRS, tilejax_amd=tilejax_amd).lower(kv, table).run(kv.cuda(), table.cuda())
+    torch.cuda.synchronize()
+    close(got.cpu(), pairs_float64(kv, table), 1e-5, 1e-4)
+    ins = write_inputs()
+    for n in (3, 0):  # (0: no runs, the cache as it was)
+        got = run(make_kernel(WRITE, tilejax_amd=tilejax_amd), *ins, i32(n), what=f"word stores n={n}")
+        assert torch.equal(got, write_expected(*ins[:3], n))  # bits moved, nothing computed: exact
+
+
+def test_ragged_paged_attention_write_and_decode():
+    """The reference's RPA cache write and decode kernels (examples/ragged_paged_attention.py): the write
+    exact, the decode within 2e-2 of float64 (bf16 p and outputs; the reference's attention tolerance)."""
+    from examples.ragged_paged_attention import make_decode, rpa_write
+    from tests.test_walk import rpa_decode_float64, rpa_inputs, write_expected, write_inputs
+
+    cache, keys, values, table, page, first, stop, src = write_inputs()
+    got = run(rpa_write, cache, keys, values, table, page, src, first, stop, i32(3), what="rpa_write")
+    assert torch.equal(got, write_expected(cache, keys, values, 3))
+    decode = make_decode(0.5)
+    for lens, decodes in (((20, 64, 5, 0), 2), ((33, 1, 64, 17), 4)):
+        ins = rpa_inputs(lens, decodes)
+        got = run(decode, *ins, what=f"rpa_decode kv_lens={lens} decodes={decodes}")
+        close(got, rpa_decode_float64(*ins, 0.5), 2e-2, 2e-2)
+        rows = torch.arange(len(lens)) >= decodes
+        assert torch.equal(got[rows], ins[0][rows])  # the other rows keep their queries

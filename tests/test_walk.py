@@ -33,8 +33,8 @@ def close(got, want, rtol=1e-4, atol=1e-3):
 
 
 def compiles(lowered):
-    """The generated kernel compiles for gfx950."""
-    assert lowered.program.notes.get("walk"), lowered.program.notes
+    """The generated kernel (the generic one) compiles for gfx950."""
+    assert lowered.program.notes["family"] == "generic", lowered.program.notes
     runtime.compile_source(lowered.source, f"{lowered.program.name}.hip")
 
 
@@ -645,3 +645,150 @@ def test_the_step_planner_still_takes_the_phases_of_steps_form():
         return out
     """)
     assert not kernel.lower(rand((256, 256)), rand((256, 256))).plan.walk
+
+
+# ------------------------------------------------------------------------------------- row pairs as words
+
+PAIRS = """
+def pairs_kernel(kv, table):
+    out = jnp.zeros((2, 16, 128), jnp.float32)
+    for b in range(2):
+        acc = jnp.zeros((16, 128), jnp.float32)
+        for p in range(2):
+            words = tilejax_amd.pairs(kv[table[b * 2 + p], :, :, :, :])  # (16, 4, 128)
+            lows = jnp.stack([words[:, g, :] for g in range(4)])
+            whole = tilejax_amd.pairs(kv[table[b * 2 + p], :, :, :, :])[0]
+            k = jax.lax.bitcast_convert_type(lows << 16, jnp.float32)
+            high = tilejax_amd.pairs(kv[table[b * 2 + p], :, :, :, :])[:, 1, :] & jnp.uint32(0xFFFF0000)
+            v = jax.lax.bitcast_convert_type(high, jnp.float32)
+            acc += jnp.sum(k, axis=0) + v + jnp.sum(jax.lax.bitcast_convert_type(whole << 16, jnp.float32)) * 0
+        out = out.at[b, :, :].set(acc)
+    return out
+"""
+
+
+def pairs_float64(kv, table):
+    """Row 0 of each pair summed over the 4 heads, plus head 1's row 1, over each batch's 2 pages."""
+    x = kv.double()
+    t = table.reshape(2, 2).tolist()
+    return np.stack([sum((x[t[b][p], :, :, 0, :].sum(1) + x[t[b][p], :, 1, 1, :]).numpy() for p in range(2))
+                     for b in range(2)])
+
+
+WRITE = """
+def write(cache, keys, values, table, page, first, stop, src, n):
+    ps, dtype = cache.shape[1], cache.dtype
+    out = cache
+    for w in range(n[0]):  # a step per run of rows, counted as the kernel runs
+        k = keys[tilejax_amd.rows(src[w], src[w] + stop[w] - first[w], ps), :, :]
+        v = values[tilejax_amd.rows(src[w], src[w] + stop[w] - first[w], ps), :, :]
+        bits = jax.lax.bitcast_convert_type(k.astype(jnp.float32), jnp.uint32) >> 16
+        words = bits | (jax.lax.bitcast_convert_type(v.astype(jnp.float32), jnp.uint32) & jnp.uint32(0xFFFF0000))
+        out = out.at[table[page[w]], tilejax_amd.rows(first[w], stop[w], ps), :, :, :].set(
+            tilejax_amd.unpairs(words, dtype)
+        )
+    return out
+"""
+
+
+def write_inputs():
+    cache = rand((6, 16, 4, 2, 128), dtype=torch.bfloat16)
+    keys, values = rand((32, 4, 128), 1, torch.bfloat16), rand((32, 4, 128), 2, torch.bfloat16)
+    return (cache, keys, values, i32(5, 2, 0, 4), i32(1, 3, 0, 0), i32(3, 0, 10, 0), i32(16, 7, 11, 0),
+            i32(0, 13, 20, 0))
+
+
+def write_expected(cache, keys, values, n):
+    """Runs (page, first, stop, source row): tokens src.. go to page table[page] positions first..stop."""
+    want = cache.clone()
+    for page, a, b, r in [(2, 3, 16, 0), (4, 0, 7, 13), (5, 10, 11, 20)][:n]:
+        want[page, a:b, :, 0, :], want[page, a:b, :, 1, :] = keys[r:r + b - a], values[r:r + b - a]
+    return want
+
+
+def test_pairs_read_a_tiles_row_pairs_as_words():
+    kernel = make_kernel(PAIRS, tilejax_amd=tilejax_amd)
+    kv, table = rand((5, 16, 4, 2, 128), dtype=torch.bfloat16), i32(4, 0, 2, 3)
+    close(kernel.reference(kv, table), pairs_float64(kv, table), 1e-5, 1e-4)
+    compiles(kernel.lower(kv, table))
+
+
+@pytest.mark.parametrize("n", [3, 0])
+def test_runs_counted_as_the_kernel_runs_store_words(n):
+    kernel = make_kernel(WRITE, tilejax_amd=tilejax_amd)
+    ins = write_inputs()
+    got = kernel.reference(*ins, i32(n))
+    assert torch.equal(got, write_expected(*ins[:3], n))
+    compiles(kernel.lower(*ins, i32(n)))
+
+
+@pytest.mark.parametrize(("code", "message"), [
+    ("a = tilejax_amd.pairs(x[i : i + 16, :])", r"takes a 16-bit tile of pairs of rows \(\.\.\., 2, d\), not float32"),
+])
+def test_pairs_errors(code, message):
+    kernel = make_kernel(f"""
+    def f(x):
+        out = jnp.zeros((32, 128))
+        for i in range(0, 32, 16):
+            {code}
+            out = out.at[i : i + 16, :].set(x[i : i + 16, :])
+        return out
+    """, tilejax_amd=tilejax_amd)
+    with pytest.raises(KernelError, match=message):
+        kernel.lower(rand((32, 128)))
+
+
+# ------------------------------------------------------------------------------------- ragged paged attention
+
+def rpa_inputs(kv_lens=(20, 64, 5, 0), decodes=2, H=32, Hkv=8, D=128, ps=16, pps=4, seed=0):
+    """A paged cache (pages, ps, Hkv, 2, D) bf16 with each sequence's pages distinct random pages of the
+    pool, q (T, H, D) with one row per sequence, and the distribution (sequences below `decodes` decode)."""
+    g = torch.Generator().manual_seed(seed)
+    S = len(kv_lens)
+    pages = S * pps + 1
+    cache = torch.randn(pages, ps, Hkv, 2, D, generator=g).to(torch.bfloat16)
+    table = torch.randperm(pages - 1, generator=g)[:S * pps].to(torch.int32) + 1
+    q = (torch.randn(S, H, D, generator=g) * D**-0.5).to(torch.bfloat16)
+    return q, cache, torch.tensor(kv_lens, dtype=torch.int32), table, torch.tensor([decodes, S, S], dtype=torch.int32)
+
+
+def rpa_decode_float64(q, cache, kv_lens, table, distribution, sm_scale):
+    """Each decode sequence's heads attending their kv head (h // (H / Hkv)) over positions below kv_len,
+    in float64; the other rows are their queries."""
+    S, H, D = q.shape
+    ps, Hkv = cache.shape[1], cache.shape[2]
+    pps = table.shape[0] // S
+    out = q.double().clone()
+    for s in range(S):
+        n = int(kv_lens[s])
+        if s >= int(distribution[0]) or n == 0:
+            if s >= int(distribution[0]):
+                continue
+            out[s] = 0.0  # no positions: acc 0 over a clamped sum
+            continue
+        pos = torch.arange(n)
+        pages = table[s * pps + pos // ps].long()
+        k = cache[pages, pos % ps, :, 0, :].double()  # (n, Hkv, D)
+        v = cache[pages, pos % ps, :, 1, :].double()
+        for h in range(H):
+            g = h // (H // Hkv)
+            w = torch.softmax(sm_scale * (k[:, g, :] @ q[s, h].double()), 0)
+            out[s, h] = w @ v[:, g, :]
+    return out.numpy()
+
+
+def test_rpa_write_and_decode():
+    from examples.ragged_paged_attention import make_decode, rpa_write
+
+    ins = write_inputs()
+    cache, keys, values, table, page, first, stop, src = ins
+    got = rpa_write.reference(cache, keys, values, table, page, src, first, stop, i32(3))
+    assert torch.equal(got, write_expected(cache, keys, values, 3))
+    compiles(rpa_write.lower(cache, keys, values, table, page, src, first, stop, i32(3)))
+    decode = make_decode(0.5)
+    q, cache, kv_lens, table, dist = rpa_inputs()
+    want = rpa_decode_float64(q, cache, kv_lens, table, dist, 0.5)
+    close(decode.reference(q, cache, kv_lens, table, dist), want, 2e-2, 2e-2)
+    lowered = decode.lower(q, cache, kv_lens, table, dist)
+    assert lowered.plan.walk and lowered.plan.aliases == {"out": 0}
+    compiles(lowered)

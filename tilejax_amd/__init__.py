@@ -19,6 +19,7 @@ from typing import Any
 
 from .api import Kernel, Lowered, compare, kernel
 from .errors import KernelError
+from .packing import pairs, unpairs
 from .pipeline import Pipeline
 from .ragged import rows
 from .tunable import choice, tunable
@@ -36,9 +37,11 @@ __all__ = [
     "compare",
     "enable_profiling",
     "kernel",
+    "pairs",
     "profile",
     "rows",
     "tunable",
+    "unpairs",
 ]
 
 __version__ = "0.1.0"

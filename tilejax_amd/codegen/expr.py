@@ -16,6 +16,7 @@ import struct
 from typing import Any, Callable, Dict, List, Optional, Sequence, Set, Tuple
 
 from ..errors import KernelError
+from .. import jaxlite
 from ..jaxlite import DType, Node
 
 __all__ = ["CExpr", "Emitter", "int_expr", "literal", "nodes_between", "depends_on"]
@@ -25,6 +26,8 @@ def literal(value: Any, dt: Optional[DType] = None) -> str:
     """A C literal for a Python number (as a float, int or bool constant)."""
     if isinstance(value, bool):
         return "true" if value else "false"
+    if dt is not None and dt.kind == "u":
+        return f"{int(value)}u"
     if dt is not None and dt.kind in "iu":
         return f"{int(value)}"
     if isinstance(value, int) and (dt is None or dt.kind in "iub"):
@@ -375,6 +378,8 @@ class ElementEmitter:
             return self._at(arg, _broadcast_index(arg.shape, shape, idx))
         if isinstance(arg, (bool, int, float)):
             return literal(arg, dt)
+        if isinstance(arg, jaxlite.Array) and arg.ndim == 0 and arg.t.device.type != "meta":
+            return literal(arg.t.item(), arg.dtype)  # a concrete scalar made in tile code (`jnp.uint32(...)`)
         raise KernelError(f"the gfx950 lowering can't compute {arg!r} per element")
 
     def _at(self, n: Node, idx: Tuple[str, ...]) -> str:

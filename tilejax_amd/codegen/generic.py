@@ -79,6 +79,8 @@ def _stype(dt: DType) -> str:
         return "double" if dt.itemsize == 8 else "float"
     if dt.kind == "b":
         return "int"
+    if dt.kind == "u":
+        return "unsigned long long" if dt.itemsize == 8 else "unsigned"
     return "long long" if dt.itemsize == 8 else "int"
 
 
@@ -183,6 +185,23 @@ class _Elements(ElementEmitter):
                 inside.append(f"(({idx[k]}) >= {lo} && ({idx[k]}) < {lo + d})")
             cond = " && ".join(inside) or "true"
             return f"(({cond}) ? ({ct})({self._at(src, tuple(inner))}) : ({ct})0)"
+        if op == "bitcast_convert_type":  # the same width: f32 <-> 32-bit integers, 16-bit <-> 16-bit
+            src = a[0]
+            v = self._at(src, idx)
+            sdt = src.dtype
+            if sdt.itemsize == 4 and dt.itemsize == 4:
+                return f"__builtin_bit_cast({ct}, ({ctype(sdt)})({v}))" if sdt.kind != dt.kind else f"({ct})({v})"
+            if sdt.itemsize == 2 and dt.itemsize == 2:
+                return _from_bits16(_bits16(v, sdt), dt)
+            raise KernelError(f"bitcast_convert_type from {sdt.name} to {dt.name} is not lowered")
+        if op == "pairs":  # (..., 2, d) 16-bit -> (..., d) words: row 0 in the low half
+            src = a[0]
+            lo = _bits16(self._at(src, (*idx[:-1], "0", idx[-1])), src.dtype)
+            hi = _bits16(self._at(src, (*idx[:-1], "1", idx[-1])), src.dtype)
+            return f"((unsigned)({lo}) | ((unsigned)({hi}) << 16))"
+        if op == "unpairs":  # (..., d) words -> (..., 2, d) 16-bit: row r from the word's half r
+            w = self._at(a[0], (*idx[:-2], idx[-1]))
+            return _from_bits16(f"((((unsigned)({w})) >> (16 * ({idx[-2]}))) & 0xFFFFu)", dt)
         if op == "getitem" and any(isinstance(k, Node) for k in (a[1] if isinstance(a[1], tuple) else (a[1],))):
             # an element chosen by a traced integer (`weights[c // D]`): clamped into its dim, as JAX clamps
             src, key = a[0], (a[1] if isinstance(a[1], tuple) else (a[1],))
@@ -221,7 +240,7 @@ class _Buffers:
 
     def add(self, name: str, count: int, stype: str) -> str:
         if name not in self.offsets:
-            width = 8 if stype in ("double", "long long") else 4
+            width = 8 if stype in ("double", "long long", "unsigned long long") else 4
             self.offsets[name] = self.size
             self.types[name] = stype
             self.size += -(-max(count, 1) * width // ALIGN) * ALIGN
@@ -1027,6 +1046,26 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
   {t1}
 }}
 """
+
+
+def _bits16(value: str, dt: DType) -> str:
+    """The 16 bits of a 16-bit float value (carried as a float, exactly) or integer."""
+    if dt.name == "bfloat16":
+        return f"(ak_bf16_bits((float)({value})) & 0xFFFFu)"
+    if dt.name == "float16":
+        return f"(unsigned)__builtin_bit_cast(unsigned short, (_Float16)(float)({value}))"
+    return f"((unsigned)({value}) & 0xFFFFu)"
+
+
+def _from_bits16(bits: str, dt: DType) -> str:
+    """A 16-bit value of `dt` from its bits, as the emitter carries it (16-bit floats as float)."""
+    if dt.name == "bfloat16":
+        return f"__builtin_bit_cast(float, (unsigned)({bits}) << 16)"
+    if dt.name == "float16":
+        return f"(float)__builtin_bit_cast(_Float16, (unsigned short)({bits}))"
+    if dt.kind == "i":
+        return f"(int)(short)(unsigned short)({bits})"
+    return f"(unsigned)({bits})"
 
 
 def _ctype_in(dt: DType) -> str:

@@ -691,6 +691,10 @@ def _binary(name: str, fn: Callable[[torch.Tensor, torch.Tensor], torch.Tensor])
     @_op(name)
     def op(a: Any, b: Any) -> Array:
         ta, tb = _pair(a, b)
+        if torch.uint32 in (ta.dtype, tb.dtype):
+            # torch computes few ops on uint32: in int64, then wrapped back to 32 bits (comparisons stay bool)
+            wide = fn(ta.to(torch.int64), tb.to(torch.int64))
+            return Array(wide if wide.dtype == torch.bool else (wide & 0xFFFFFFFF).to(torch.uint32))
         return Array(fn(ta, tb))
 
     op.__name__ = name
@@ -765,6 +769,37 @@ sign = _unary("sign", torch.sign)
 invert = _unary("invert", torch.bitwise_not)
 logical_not = _unary("logical_not", torch.logical_not)
 reciprocal = _unary("reciprocal", torch.reciprocal, True)
+
+
+@_op("bitcast_convert_type")
+def bitcast_convert_type(x: Any, new_dtype: Any) -> Array:
+    """x's bits as `new_dtype` of the same width (jax.lax.bitcast_convert_type; widths that differ are the
+    packing helpers' business, tilejax_amd.pairs / unpairs)."""
+    t, dt = _t(x), dtype(new_dtype)
+    if t.element_size() != dt.itemsize:
+        raise TypeError(f"bitcast_convert_type between widths {t.element_size()} and {dt.itemsize} is not supported")
+    return Array(t.contiguous().view(dt.torch))
+
+
+@_op("pairs")
+def pairs(x: Any) -> Array:
+    """A 16-bit tile (..., 2, d) as uint32 words (..., d): x[..., 0, i] in each word's low half, x[..., 1, i]
+    in its high half."""
+    t = _t(x)
+    if t.element_size() != 2:
+        raise TypeError(f"pairs takes a 16-bit tile of pairs of rows (..., 2, d), not {_BY_TORCH[t.dtype].name}")
+    if t.dim() < 2 or t.shape[-2] != 2:
+        raise TypeError(f"pairs takes a 16-bit tile of pairs of rows (..., 2, d), not shape {tuple(t.shape)}")
+    return Array(t.transpose(-1, -2).contiguous().view(torch.uint32).squeeze(-1))
+
+
+@_op("unpairs")
+def unpairs(words: Any, new_dtype: Any) -> Array:
+    """`pairs` undone: uint32 words (..., d) as a tile (..., 2, d) of the 16-bit `new_dtype`."""
+    t, dt = _t(words), dtype(new_dtype)
+    if t.dtype != torch.uint32 or dt.itemsize != 2:
+        raise TypeError(f"unpairs takes uint32 words and a 16-bit dtype, not {t.dtype} and {dt.name}")
+    return Array(t.contiguous().view(dt.torch).reshape(*t.shape, 2).transpose(-1, -2))
 
 
 @_op("astype")
@@ -1079,7 +1114,7 @@ jnp = _namespace(
 )
 lax = _namespace(
     "jax.lax", broadcasted_iota=broadcasted_iota, rsqrt=rsqrt, dot_general=dot_general,
-    Precision=Precision, exp=exp, max=maximum, min=minimum, select=select,
+    Precision=Precision, exp=exp, max=maximum, min=minimum, select=select, bitcast_convert_type=bitcast_convert_type,
     div=lambda a, b: floor_divide(a, b), rem=remainder, tanh=tanh,
 )
 nn = _namespace("jax.nn", silu=silu, sigmoid=sigmoid, relu=relu, gelu=gelu, softmax=softmax)

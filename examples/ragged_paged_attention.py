@@ -102,3 +102,86 @@ def make_decode(sm_scale: float) -> tilejax_amd.Kernel:
         return out
 
     return rpa_decode
+
+
+# --------------------------------------------------------------------------- prefill and mixed: a block of queries
+
+BLOCK_Q = 256  # query tokens per tile
+
+
+@tilejax_amd.tunable
+class PrefillTiles:
+    pages: int = tilejax_amd.choice(1, 2, 4, 8, default=4)  # cache pages per step
+
+
+def head_rows(qb, kv_heads):
+    """A block of queries (BQ, H, D) as each kv head's rows (Hkv, BQ * G, D), row t * G + i being token t's
+    query head g * G + i (G = H / Hkv, as GQA groups heads)."""
+    bq, h, d = qb.shape
+    g = h // kv_heads
+    return jnp.stack([qb[:, i * g : (i + 1) * g, :].reshape(bq * g, d) for i in range(kv_heads)])
+
+
+def token_heads(rows, heads):
+    """`head_rows` undone: (Hkv, BQ * G, D) -> (BQ, H, D)."""
+    kv_heads, n, d = rows.shape
+    g = heads // kv_heads
+    return jnp.concatenate([rows[i].reshape(n // g, g, d) for i in range(kv_heads)], axis=1)
+
+
+def visible(heads, rows, cols, first_row, first_col, stop):
+    """Which (row, column) pairs attend: row t * G + i (a query at position first_row + t) sees position
+    first_col + c if it is no later than its own and before `stop`."""
+    shape = (1, rows, cols)
+    pos = first_row + jax.lax.broadcasted_iota(jnp.int32, shape, 1) // heads
+    col = first_col + jax.lax.broadcasted_iota(jnp.int32, shape, 2)
+    return (col <= pos) & (col < stop)
+
+
+def online_softmax_heads(s, v, row_max, row_sum, acc):
+    """`online_softmax` for every kv head at once: s (Hkv, R, n), v (Hkv, n, D), stats (Hkv, R, 128)."""
+    n, d = s.shape[-1], v.shape[-1]
+    max_new = jnp.maximum(row_max, jnp.max(s, axis=-1, keepdims=True))
+    p = jnp.exp(s - jnp.tile(max_new, (1, 1, n // LANES)))
+    alpha = jnp.exp(row_max - max_new)
+    row_sum = alpha * row_sum + jnp.sum(p, axis=-1, keepdims=True)
+    pv = jax.lax.dot_general(p.astype(v.dtype), v, (((2,), (1,)), ((0,), (0,))), preferred_element_type=jnp.float32)
+    return max_new, row_sum, jnp.tile(alpha, (1, 1, d // LANES)) * acc + pv
+
+
+def make_prefill(sm_scale: float, block_q: int = BLOCK_Q) -> tilejax_amd.Kernel:
+    """The attention of the sequences with several new tokens (RPA's prefill and mixed cases), a tile per
+    block of a sequence's queries: tile k < n_tiles[0] is queries tile_rows[k] .. tile_rows[k + 1] of a
+    sequence whose pages start at page_indices[tile_page[k]], its first query at position tile_pos[k],
+    attending positions before tile_stop[k]. The output is q updated in place."""
+
+    @tilejax_amd.kernel
+    def rpa_prefill(q, kv_cache, page_indices, tile_page, tile_rows, tile_pos, tile_stop, n_tiles,
+                    tiles=PrefillTiles()):
+        _, H, D = q.shape
+        ps, Hkv = kv_cache.shape[1], kv_cache.shape[2]
+        G, NP, BQ = H // Hkv, tiles.pages, block_q
+        dtype = q.dtype
+        out = q
+        for k in range(n_tiles[0]):  # the tiles, counted as the kernel runs
+            qh = head_rows(q[tilejax_amd.rows(tile_rows[k], tile_rows[k + 1], BQ), :, :], Hkv)
+            row_max = jnp.full((Hkv, BQ * G, LANES), MASK_VALUE, jnp.float32)
+            row_sum = jnp.zeros((Hkv, BQ * G, LANES), jnp.float32)
+            acc = jnp.zeros((Hkv, BQ * G, D), jnp.float32)
+            for j in range(0, tile_stop[k], NP * ps):  # NP pages a step, up to the tile's last query
+                words = tilejax_amd.pairs(
+                    kv_cache[page_indices[tile_page[k] + j // ps : tile_page[k] + j // ps + NP], :, :, :, :]
+                )  # the step's pages as words (NP, ps, Hkv, D)
+                kv = [keys_values(words[:, :, g, :]) for g in range(Hkv)]
+                k_heads = jnp.stack([k_ for k_, _ in kv])  # (Hkv, NP * ps, D)
+                v_heads = jnp.stack([v_ for _, v_ in kv])
+                s = jax.lax.dot_general(qh, k_heads, (((2,), (2,)), ((0,), (0,))), preferred_element_type=jnp.float32)
+                ok = visible(G, BQ * G, NP * ps, tile_pos[k], j, tile_stop[k])
+                row_max, row_sum, acc = online_softmax_heads(
+                    jnp.where(ok, s * sm_scale, MASK_VALUE), v_heads, row_max, row_sum, acc
+                )
+            o = acc * jnp.tile(1.0 / jnp.maximum(row_sum, 1e-30), (1, 1, D // LANES))
+            out = out.at[tilejax_amd.rows(tile_rows[k], tile_rows[k + 1], BQ), :, :].set(token_heads(o, H).astype(dtype))
+        return out
+
+    return rpa_prefill

@@ -792,3 +792,59 @@ def test_rpa_write_and_decode():
     lowered = decode.lower(q, cache, kv_lens, table, dist)
     assert lowered.plan.walk and lowered.plan.aliases == {"out": 0}
     compiles(lowered)
+
+
+def prefill_inputs(q_lens=(40, 25), kv_lens=(70, 25), H=8, Hkv=2, D=128, ps=64, pps=2, block_q=32, seed=1):
+    """Prefill sequences' new queries (T, H, D), a paged cache holding them, and the prefill tiles: a tile per
+    block of block_q queries of a sequence (first query at position kv_len - q_len)."""
+    g = torch.Generator().manual_seed(seed)
+    S, T = len(q_lens), sum(q_lens)
+    pages = S * pps + 1
+    cache = torch.randn(pages, ps, Hkv, 2, D, generator=g).to(torch.bfloat16)
+    table = (torch.randperm(pages - 1, generator=g)[:S * pps] + 1).to(torch.int32)
+    q = (torch.randn(T, H, D, generator=g) * D**-0.5).to(torch.bfloat16)
+    tile_page, rows, pos, stop = [], [0], [], []
+    start = 0
+    for s, (ql, kl) in enumerate(zip(q_lens, kv_lens)):
+        for b in range(0, ql, block_q):
+            n = min(block_q, ql - b)
+            tile_page.append(s * pps)
+            rows.append(start + b + n)
+            pos.append(kl - ql + b)
+            stop.append(kl - ql + b + n)
+        start += ql
+    t = lambda v: torch.tensor(v, dtype=torch.int32)  # noqa: E731
+    return q, cache, table, t(tile_page), t(rows), t(pos), t(stop), t([len(pos)])
+
+
+def rpa_prefill_float64(q, cache, table, tile_page, tile_rows, tile_pos, tile_stop, n_tiles, sm_scale):
+    """Each tile's queries attending causally (positions up to their own, below the stop) over their
+    sequence's pages, head h to kv head h // (H / Hkv), in float64; rows of no tile keep their queries."""
+    T, H, D = q.shape
+    ps, Hkv = cache.shape[1], cache.shape[2]
+    out = q.double().clone()
+    for k in range(int(n_tiles[0])):
+        for r in range(int(tile_rows[k]), int(tile_rows[k + 1])):
+            own = int(tile_pos[k]) + r - int(tile_rows[k])
+            n = min(own + 1, int(tile_stop[k]))
+            pos = torch.arange(n)
+            pages = table[int(tile_page[k]) + pos // ps].long()
+            keys = cache[pages, pos % ps, :, 0, :].double()
+            vals = cache[pages, pos % ps, :, 1, :].double()
+            for h in range(H):
+                gk = h // (H // Hkv)
+                w = torch.softmax(sm_scale * (keys[:, gk, :] @ q[r, h].double()), 0)
+                out[r, h] = w @ vals[:, gk, :]
+    return out.numpy()
+
+
+def test_rpa_prefill():
+    from examples.ragged_paged_attention import PrefillTiles, make_prefill
+
+    prefill = make_prefill(0.5, block_q=32)
+    ins = prefill_inputs()
+    want = rpa_prefill_float64(*ins, 0.5)
+    close(prefill.reference(*ins, PrefillTiles(2)), want, 2e-2, 2e-2)
+    lowered = prefill.lower(*ins, PrefillTiles(2))
+    assert lowered.plan.walk and lowered.schedule.runtime_tiles
+    compiles(lowered)

@@ -987,8 +987,12 @@ def matmul_nt(a: Any, b: Any, preferred_element_type: Any = None) -> Array:
 
 def dot_general(x: Any, y: Any, dimension_numbers: Any, preferred_element_type: Any = None, precision: Any = None) -> Array:
     (lc, rc), (lb, rb) = dimension_numbers
+    if tuple(lb) == (0,) and tuple(rb) == (0,) and len(x.shape) == 3 and len(y.shape) == 3:
+        # one leading batch dim: the batch's products, stacked
+        inner = ((tuple(c - 1 for c in lc), tuple(c - 1 for c in rc)), ((), ()))
+        return stack([dot_general(x[b], y[b], inner, preferred_element_type) for b in range(x.shape[0])])
     if tuple(lb) or tuple(rb) or len(x.shape) != 2 or len(y.shape) != 2:
-        raise NotImplementedError("dot_general: two matrices without batch dims")
+        raise NotImplementedError("dot_general: two matrices, or a leading batch dim of two stacks of them")
     lc, rc = tuple(lc), tuple(rc)
     xx = x if lc == (1,) else transpose(x)
     if rc == (1,):

@@ -227,6 +227,9 @@ def test_causal_matmul_f32_operands():
     ((("bm", 128), ("bn", 256)), 2),
     ((("bm", 128), ("bn", 128)), 3),
     ((), 4),
+    ((("bm", 256), ("bn", 256), ("waves", 8)), 2),
+    ((("bm", 256), ("bn", 128), ("waves", 8)), 3),
+    ((("bm", 128), ("bn", 128), ("waves", 8)), 2),
 ])
 def test_workgroup_tiles_the_tuner_tries(hardware, buffers):
     """Each gfx950 workgroup tile and LDS ring depth the tuner may pick, dense and causal, against the oracle."""
@@ -238,7 +241,8 @@ def test_workgroup_tiles_the_tuner_tries(hardware, buffers):
     for kernel, oracle in ((matmul, kernels.matmul), (causal_matmul, kernels.causal_matmul)):
         lowered = kernel.lowered(kernel.signature(x, y), Config(tiles, Pipeline(buffers, 2), False, hardware))
         print(f"{kernel.nest.name} 1024^3 {tiles} hardware={hardware} buffers={buffers} "
-              f"-> {lowered.program.notes['hw_tile']} x{lowered.program.notes['stages']}", flush=True)
+              f"-> {lowered.program.notes['hw_tile']} x{lowered.program.notes['stages']} in {lowered.program.notes['waves']} waves",
+              flush=True)
         got = lowered.run(x.cuda(), y.cuda())
         torch.cuda.synchronize()
         _close(got, oracle(x, y, 512, 512, 512), x, y, f"{kernel.nest.name} {hardware}")

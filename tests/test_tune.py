@@ -89,19 +89,25 @@ def test_proposals_follow_the_bottleneck():
     bf = jaxlite.bfloat16
     sig = k.signature(spec(256, 256, dtype=bf), spec(256, 128, dtype=bf))
     start = Config(Tiles(), Pipeline(2, 2))
+
+    def tiles(found):  # the tunable moves (the family's other kernel shapes keep the tunable)
+        return [c.tunable for c in found if not c.hardware]
+
     # Per-step overhead: bigger tiles only, fewest steps first (tm=512 doesn't divide the 256 rows).
     overhead = Trial(start, profile(start, seconds=10.0, compute=1.0))
-    assert [c.tunable for c in proposals(k, sig, overhead)] == [Tiles(tm=256), Tiles(tk=256)]
+    assert tiles(proposals(k, sig, overhead)) == [Tiles(tm=256), Tiles(tk=256)]
+    # ... after the other kernel shapes at these tiles: the 128 x 128 workgroup tile in eight waves
+    assert [c.hardware for c in proposals(k, sig, overhead) if c.hardware] == [(("bm", 256), ("bn", 256), ("waves", 8))]
     # Exposed input waits: one more LDS stage first, then the schedules that move fewer bytes.
     dma = Trial(start, profile(start, seconds=10.0, wait=5.0))
     assert proposals(k, sig, dma)[0] == Config(Tiles(), Pipeline(3, 2))
-    assert [c.tunable for c in proposals(k, sig, dma)[1:]] == [Tiles(tm=256), Tiles(tk=256)]
+    assert tiles(proposals(k, sig, dma)[1:]) == [Tiles(tm=256), Tiles(tk=256)]
     # Exposed output waits: no more output buffers (gfx950 kernels store from registers: nothing to queue).
     outs = Trial(start, profile(start, seconds=10.0, out_wait=5.0))
     assert all(c.pipeline.output_buffers == 2 for c in proposals(k, sig, outs))
     # Compute-bound: every neighbour, fewest steps first; without regions the same plus one more stage.
     compute = Trial(start, profile(start, seconds=10.0))
-    assert [c.tunable for c in proposals(k, sig, compute)] == [Tiles(tm=256), Tiles(tk=256), Tiles(tm=64)]
+    assert tiles(proposals(k, sig, compute)) == [Tiles(tm=256), Tiles(tk=256), Tiles(tm=64)]
     blind = Trial(start, profile(start, seconds=10.0, wait=5.0, regions=False))
     assert proposals(k, sig, blind)[1:] == proposals(k, sig, compute)
     # After a failure: two buffers, then the neighbours that build.
@@ -154,15 +160,15 @@ def test_a_kernel_without_a_tunable_tunes_its_buffering():
 
 
 def test_hardware_choices_are_distinct_kernels():
-    """The tuner's gfx950 vocabulary: the matmul's workgroup tiles and attention's waves and key blocks
-    each build a different kernel, and each compiles."""
+    """The tuner's gfx950 vocabulary: the matmul's workgroup tiles (in four or eight waves) and attention's
+    waves and key blocks each build a different kernel, and each compiles."""
     from examples.causal_attention import AttentionBlocks, causal_attention
     from examples.matmul import MatmulTiles, matmul
     from tilejax_amd import runtime
     from tilejax_amd.codegen import hardware_choices
 
     bf = jaxlite.bfloat16
-    cases = [(matmul, (spec(1024, 1024, dtype=bf), spec(1024, 1024, dtype=bf)), MatmulTiles(512, 512, 512), 4),
+    cases = [(matmul, (spec(1024, 1024, dtype=bf), spec(1024, 1024, dtype=bf)), MatmulTiles(512, 512, 512), 8),
              (causal_attention, tuple(spec(2, 4, 512, 128, dtype=bf) for _ in range(3)), AttentionBlocks(256, 256), 4)]
     for kernel, args, tiles, count in cases:
         sig = kernel.signature(*args)
@@ -177,5 +183,6 @@ def test_hardware_choices_are_distinct_kernels():
         assert len(sources) == count
     plan, schedule = matmul.build(matmul.signature(spec(1024, 1024, dtype=bf), spec(1024, 1024, dtype=bf)),
                                   MatmulTiles(512, 512, 512))
-    assert [dict(h) for h in hardware_choices(plan, schedule)][1:] == [{"bm": 256, "bn": 128}, {"bm": 128, "bn": 256},
-                                                                      {"bm": 128, "bn": 128}]
+    tiles = [{"bm": 256, "bn": 128}, {"bm": 128, "bn": 256}, {"bm": 128, "bn": 128}]
+    assert [dict(h) for h in hardware_choices(plan, schedule)][1:] == (
+        tiles + [{"bm": 256, "bn": 256, "waves": 8}] + [{**t, "waves": 8} for t in tiles])

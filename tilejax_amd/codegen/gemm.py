@@ -44,7 +44,7 @@ from .protocol import Recorder
 __all__ = ["GemmMatch", "match", "lower"]
 
 THREADS = 256  # the fixup kernel's workgroup
-WAVE_GRID = (2, 2)  # waves of the matmul workgroup along M and N
+WAVE_GRIDS = {4: (2, 2), 8: (2, 4)}  # waves of the matmul workgroup along M and N, by waves per workgroup
 MFMA = 32  # 32x32x16 bf16 MFMA tiles
 
 
@@ -354,6 +354,11 @@ class HwTile:
     bn: int
     bk: int
     stages: int
+    waves: int = 4  # per workgroup: 4 (one per SIMD, 128 x 128 each of a 256 x 256 tile) or 8 (two per SIMD)
+
+    @property
+    def grid(self) -> Tuple[int, int]:
+        return WAVE_GRIDS[self.waves]
 
     @property
     def lds(self) -> int:
@@ -361,11 +366,15 @@ class HwTile:
 
 
 def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str, int]] = None) -> HwTile:
-    """The workgroup tile for a spec tile (tm, tn, tk): at most 256 x 256 outputs (four waves of 128 x 128 at
-    most; `hardware` may cap each side, "bm" and "bn"), K slices of 64 (32 if tk is an odd multiple of 64, 16
-    for tk = 32) so every tile's slice count is even, and the LDS stages the pipeline asks for where they
-    divide a step's slices and fit in LDS."""
+    """The workgroup tile for a spec tile (tm, tn, tk): at most 256 x 256 outputs (`hardware` may cap each
+    side, "bm" and "bn"), computed by four waves (128 x 128 each at most) or, with "waves": 8, by eight (two
+    per SIMD, 128 x 64 each); K slices of 64 (32 if tk is an odd multiple of 64, 16 for tk = 32) so every
+    tile's slice count is even, and the LDS stages the pipeline asks for where they divide a step's slices
+    and fit in LDS."""
     hardware = hardware or {}
+    waves = hardware.get("waves", 4)
+    if waves not in WAVE_GRIDS:
+        raise KernelError(f"the gfx950 matmul lowering runs workgroups of 4 or 8 waves, not {waves}")
     bm, bn = min(m.tm, hardware.get("bm", 256)), min(m.tn, hardware.get("bn", 256))
     if m.tm % bm or m.tn % bn or bm % 64 or bn % 64:
         raise KernelError(f"the gfx950 matmul lowering needs tiles that are multiples of 64 (got {m.tm} x {m.tn})")
@@ -384,7 +393,10 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
     # More buffers than 64-deep slices can have in LDS: slices half as deep, so loads run further ahead.
     if pipeline.input_buffers > stages and bk == 64 and deepest(32) > stages:
         bk, stages = 32, deepest(32)
-    return HwTile(bm, bn, bk, stages)
+    wm, wn = WAVE_GRIDS[waves]
+    if bm % (32 * wm) or bn % (32 * wn):
+        raise KernelError(f"a {bm} x {bn} workgroup tile does not split into {waves} waves of whole 32 x 32 blocks")
+    return HwTile(bm, bn, bk, stages, waves)
 
 
 # Small items (K-split chunks, filled and constant tiles) pulled from a shared queue once a workgroup's own
@@ -402,7 +414,8 @@ def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, name: str
 
 def hardware_choices(m: GemmMatch) -> List[Dict[str, int]]:
     """The workgroup tiles tuning may try for this match, as caps on each side (256 x 256 first, the
-    default; then 256 x 128, 128 x 256 and 128 x 128 where the spec tile divides into them)."""
+    default; then 256 x 128, 128 x 256 and 128 x 128 where the spec tile divides into them), each also with
+    eight waves per workgroup instead of four."""
     found, seen = [], set()
     for bm, bn in ((256, 256), (256, 128), (128, 256), (128, 128)):
         got = (min(m.tm, bm), min(m.tn, bn))
@@ -410,6 +423,8 @@ def hardware_choices(m: GemmMatch) -> List[Dict[str, int]]:
             continue
         seen.add(got)
         found.append({"bm": bm, "bn": bn})
+    # eight waves (two per SIMD) where the tile splits into them
+    found += [{**h, "waves": 8} for h in list(found) if min(m.tn, h["bn"]) % 128 == 0 and min(m.tm, h["bm"]) % 64 == 0]
     return found
 
 
@@ -708,7 +723,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             self.tables["tile_steps"] = static_tile_steps(sch)
         args = self._args()
         source = self._source(args)
-        launches = [Launch(self.name, args, (grid, 1, 1), (64 * WAVE_GRID[0] * WAVE_GRID[1], 1, 1), 0)]
+        launches = [Launch(self.name, args, (grid, 1, 1), (64 * hw.waves, 1, 1), 0)]
         workspace = {}
         if self.x3:
             for role in ("b",) if self.prologue else ("a", "b"):
@@ -735,7 +750,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)], inputs=inputs,
             tables=dict(self.tables), workspace=workspace, state=dict(self.state), lds_bytes=hw.lds,
             protocol=self.protocol,
-            notes={"family": "gemm", "hw_tile": (hw.bm, hw.bn, hw.bk), "stages": hw.stages, "grid": grid,
+            notes={"family": "gemm", "hw_tile": (hw.bm, hw.bn, hw.bk), "stages": hw.stages, "waves": hw.waves, "grid": grid,
                    "items": len(items), "constant_items": sum(1 for _, s, _ in items if (s >> 16) == 2),
                    "queued_items": self.n_small,
                    "split": self.split, "trace_workgroups": grid if self.trace else 0,
@@ -874,7 +889,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
     def _source(self, args: List[Arg]) -> str:
         plan, sch, m, hw = self.plan, self.sch, self.m, self.hw
         bm, bn, bk, S = hw.bm, hw.bn, hw.bk, hw.stages
-        WM, WN = WAVE_GRID
+        WM, WN = hw.grid
         T = 64 * WM * WN  # threads of the workgroup
         wtm, wtn = bm // WM, bn // WN
         mi, ni = wtm // MFMA, wtn // MFMA

@@ -631,6 +631,33 @@ def test_indices_made_once_per_tile_and_constants_in_bounds():
     compiles(kernel.lower(x))
 
 
+PICKED = """
+def picked(x, ids):
+    out = jnp.zeros((512, 128))
+    for i in range(0, 512, 128):
+        b = jnp.minimum(ids[i // 128], 3)
+        out = out.at[i : i + 128, :].set(x[i : i + 128, :] * ids[b])
+    return out
+"""
+
+
+def picked_float64(x, ids):
+    ids = np.asarray(ids)
+    scale = np.repeat([ids[min(int(ids[t]), 3)] for t in range(4)], 128)[:, None]
+    return np.asarray(x.double()) * scale
+
+
+def test_an_element_index_the_tile_code_computes():
+    """`ids[b]` with `b` computed by the tile: the reference's planner rejects naming an element first
+    (tests/test_index_arrays.py:299-311); here the walk planner reads the element as the tile runs."""
+    kernel = make_kernel(PICKED)
+    x, ids = rand((512, 128)), i32(2, 0, 7, 1)
+    lowered = kernel.lower(x, ids)
+    assert lowered.plan.walk
+    close(kernel.reference(x, ids), picked_float64(x, ids), 1e-6, 0)
+    compiles(lowered)
+
+
 def test_the_step_planner_still_takes_the_phases_of_steps_form():
     """A nest of the phases-of-steps form keeps its step plan (the kernel families read it)."""
     kernel = make_kernel("""

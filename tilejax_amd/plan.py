@@ -234,6 +234,44 @@ def evaluate(nest: Nest, env: Dict[str, Any], node: ast.expr, values: Optional[M
         raise nest.error(f"can't evaluate `{ast.unparse(node)}` when planning: {e!r}", node) from e
 
 
+SHAPE_ATTRIBUTES = frozenset({"shape", "dtype", "ndim", "size"})
+
+
+def _data_read(stmt: ast.stmt, params: Sequence[str]) -> Optional[ast.Name]:
+    """The first use of an input array in `stmt` that needs its data (anything but its shape, dtype, ndim,
+    size or len), or None."""
+    parent: Dict[ast.AST, ast.AST] = {}
+    for node in ast.walk(stmt):
+        for child in ast.iter_child_nodes(node):
+            parent[child] = node
+    for node in ast.walk(stmt):
+        if not (isinstance(node, ast.Name) and node.id in params and isinstance(node.ctx, ast.Load)):
+            continue
+        up = parent.get(node)
+        if isinstance(up, ast.Attribute) and up.attr in SHAPE_ATTRIBUTES:
+            continue
+        if isinstance(up, ast.Call) and isinstance(up.func, ast.Name) and up.func.id == "len" and node in up.args:
+            continue
+        return node
+    return None
+
+
+def _check_named_scopes(nest: Nest, envs: "_Env") -> None:
+    """Every `with` in the tile opens `jax.named_scope(name)` with one string."""
+    for node in ast.walk(nest.function):
+        if not isinstance(node, ast.With):
+            continue
+        for item in node.items:
+            call = item.context_expr
+            ok = isinstance(call, ast.Call) and len(call.args) == 1 and not call.keywords
+            try:
+                ok = ok and envs.eval(call.func) is jaxlite.named_scope and isinstance(envs.eval(call.args[0]), str)
+            except KernelError:
+                ok = False
+            if not ok:
+                raise nest.error("tile code opens only `with jax.named_scope(name):` blocks, `name` a string", node)
+
+
 def make_plan(nest: Nest, fn: Callable, inputs: Sequence[Spec], tunable: Any = None) -> Plan:
     """Resolve `nest` (parsed from `fn`) for inputs of these shapes and dtypes and the tunable's values: a
     plan of phases and steps when the nest has that form, else a plan of the tile as written (walk.py)."""
@@ -264,6 +302,10 @@ class _Env:
         return evaluate(self.nest, self.scope, node, values)
 
     def run(self, stmt: ast.stmt) -> None:
+        data = _data_read(stmt, self.nest.params)
+        if data is not None:
+            raise self.nest.error(f"the prologue runs on the inputs' shapes and dtypes: it can't read `{data.id}`'s data "
+                                  "(only its .shape, .dtype, .ndim, .size or len)", stmt)
         try:
             with jaxlite.default_device("meta"):
                 exec(compile(ast.Module([stmt], []), self.nest.filename, "exec"), self.scope)
@@ -430,6 +472,7 @@ class _Planner:
         self.nest, self.fn, self.inputs, self.tunable = nest, fn, inputs, tunable
         self.envs = _Env(nest, fn, inputs, tunable)
         self.env = self.envs.scope
+        _check_named_scopes(nest, self.envs)
         self.ranges: Dict[str, Range] = {}
         self.indices: Dict[str, Index] = {}
 
@@ -487,8 +530,11 @@ class _Planner:
         shape, dt, fill = allocated
         if isinstance(value, jaxlite.Array):
             vshape, vdt = tuple(value.shape), value.dtype
-        else:
+        elif isinstance(value, (bool, int, float)):
             vshape, vdt = (), dt
+        else:
+            raise self.error(f"{tile.text}: a stored value must be an array or a number, not {type(value).__name__}",
+                             self.nest.stores[name].node)
         try:
             fits = np.broadcast_shapes(vshape, tile.shape) == tile.shape
         except ValueError:
@@ -552,11 +598,15 @@ class _Planner:
         """Every index-array element the tile code or a reduction mask reads is inside its array, for every value
         of the loops its index expressions read."""
         nest = self.nest
+        computed = bound(nest.tile) - set(self.ranges)
         places: List[ast.AST] = [*nest.tile, *(loop.mask for loop in nest.reductions if loop.mask is not None)]
         for place in places:
             for node in element_reads(place, self.indices):
                 shape = self.indices[node.value.id].shape  # type: ignore[attr-defined]
                 for expr, dim in zip(index_dims(node), shape):
+                    if used(expr) & computed:  # an element the tile code picks: read as the tile runs
+                        raise NeedsWalk(f"{ast.unparse(node)}: an element index the tile code computes",
+                                        filename=nest.filename, node=node)
                     loops = [self.ranges[v] for v in sorted(used(expr) & set(self.ranges))]
                     for blocks in itertools.product(*(range(r.count) for r in loops)):
                         at = self.eval(expr, {r.var: r.value(b) for r, b in zip(loops, blocks)})
@@ -698,12 +748,13 @@ class _Planner:
         def run(name: str, stmts: Tuple[ast.stmt, ...], carried_in: Dict[str, Tuple[Tuple[int, ...], Any]]) -> Scope:
             return self._run_scope(name, stmts, carried_in, set(self.ranges), bound_vars, by_node)
 
-        def type_of(v: Any) -> Tuple[Tuple[int, ...], Any]:
+        def type_of(v: Any, c: str = "", stmts: Sequence[ast.stmt] = ()) -> Tuple[Tuple[int, ...], Any]:
             if isinstance(v, jaxlite.Array):
                 return tuple(v.shape), v.dtype
             if isinstance(v, (int, float, bool)):
                 return (), v  # a Python number: carried as the number until an array replaces it
-            raise self.error(f"a carried value must be an array or a number, not {type(v).__name__}")
+            raise self.error(f"a carried value must be an array or a number: this code makes `{c}` not an array "
+                             f"({type(v).__name__})", stmts[0] if stmts else None)
 
         for idx, (name, stmts) in enumerate(order):
             needed = {c: types[c] for c in (used_before_bound(stmts) & carried_names) if c in types}
@@ -711,22 +762,30 @@ class _Planner:
             if name.startswith("body"):
                 # Carried values keep one type: run the body again from what it leaves until they agree.
                 for _ in range(3):
-                    after = {c: type_of(scope.values[c]) for c in needed if c in scope.values}
+                    after = {c: type_of(scope.values[c], c, stmts) for c in needed if c in scope.values}
                     changed = {c: t for c, t in after.items() if _type_key(t) != _type_key(needed[c])}
                     if not changed:
                         break
                     for c, t in changed.items():
-                        if isinstance(needed[c][1], DType) and isinstance(t[1], DType) and needed[c][0] != t[0]:
-                            raise self.error(f"carried value `{c}` changes shape between steps: {needed[c][0]} -> {t[0]}",
-                                             phases[int(name[4:])].body[0])
-                        needed[c] = t
+                        if isinstance(needed[c][1], DType) and isinstance(t[1], DType):
+                            if needed[c][0] != t[0]:
+                                raise self.error(f"carried value `{c}` changes shape between steps: {needed[c][0]} -> "
+                                                 f"{t[0]}", phases[int(name[4:])].body[0])
+                            raise self.error(f"carried value `{c}` keeps one type: a step starts with it as "
+                                             f"{needed[c][1].name}{list(needed[c][0])} and leaves {t[1].name}"
+                                             f"{list(t[0])}", phases[int(name[4:])].body[0])
+                        needed[c] = t  # (a Python number becomes the array it meets)
                     scope = run(name, stmts, needed)
                 else:
                     raise self.error("a carried value's type doesn't settle", phases[int(name[4:])].body[0])
+                still = sorted(c for c, t in needed.items() if not isinstance(t[1], DType))
+                if still:
+                    raise self.error(f"carried value `{still[0]}` stays a Python number through the loop's steps, so it "
+                                     "must be an array (start it with jnp.zeros or jnp.full)", phases[int(name[4:])].body[0])
             scopes[name] = scope
             for k, v in scope.values.items():
                 if k in carried_names:
-                    types[k] = type_of(v)
+                    types[k] = type_of(v, k, stmts)
         scopes["last"] = scopes[order[-1][0]]
         carried = {}
         for c in sorted(carried_names):

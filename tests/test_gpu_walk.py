@@ -16,9 +16,9 @@ import torch
 import tilejax_amd
 from tests.helpers import make_kernel, rand
 from tests.test_walk import (FFN_STACK, GATHER, LAYERED, MASKED_IN_PLACE, MOE, NESTED, OFFSETS, ONCE_PER_TILE,
-                             RAGGED, SCAN, SCATTER, SPANS, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, PICKED, counted_float64,
+                             RAGGED, SCAN, SCATTER, SPANS, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, PICKED, EARLY, counted_float64,
                              ffn_inputs, ffn_stack_float64, gather_float64, i32, layered_float64, moe_inputs,
-                             picked_float64,
+                             picked_float64, early_float64,
                              once_per_tile_float64, ragged_float64, route, routed_float64, scan_float64,
                              scatter_float64, spans_float64, sums_float64, two_repeats_float64)
 
@@ -126,6 +126,11 @@ def test_an_element_index_the_tile_code_computes():
     x = rand((512, 128))
     for ids in (i32(2, 0, 7, 1), i32(3, 3, 0, 9)):
         close(run(make_kernel(PICKED), x, ids, what=f"picked {ids.tolist()}"), picked_float64(x, ids), 1e-6, 0)
+
+
+def test_windows_placed_by_an_array_made_before_the_loop():
+    x = rand((2, 8, 128))
+    close(run(make_kernel(EARLY), x, what="early"), early_float64(x), 1e-6, 1e-6)
 
 
 def test_indices_made_once_per_tile():

@@ -658,6 +658,43 @@ def test_an_element_index_the_tile_code_computes():
     compiles(lowered)
 
 
+EARLY = """
+def early(x):
+    out = jnp.zeros((8, 128))
+    for i in range(0, 8, 8):
+        ids = 1 - jnp.arange(2, dtype=jnp.int32)  # made before the first loop, then again
+        ids = ids + 0
+        acc = jnp.zeros((8, 128))
+        for c in range(2):
+            acc += x[ids[c], i : i + 8, :] * (c + 1)
+        out = out.at[i : i + 8, :].set(acc)
+    return out
+"""
+
+
+def early_float64(x):
+    x = f64(x)
+    return x[1, 0:8] + 2 * x[0, 0:8]
+
+
+def test_windows_placed_by_an_array_made_before_the_loop():
+    """The reference's planner rejects an index array made before the first reduction loop, or assigned
+    twice (tests/test_computed_indices.py:205-232); the walk planner keeps it and places the windows."""
+    kernel = make_kernel(EARLY)
+    x = rand((2, 8, 128))
+    assert kernel.lower(x).plan.walk
+    close(kernel.reference(x), early_float64(x), 1e-6, 1e-6)
+    compiles(kernel.lower(x))
+
+
+def test_a_window_placed_by_what_the_same_part_computes_is_an_error():
+    source = EARLY.replace("        for c in range(2):\n            acc += x[ids[c], i : i + 8, :] * (c + 1)\n",
+                           "        acc += x[ids[0], i : i + 8, :]\n")
+    assert source != EARLY
+    with pytest.raises(KernelError, match="a window is placed by `ids`, which the same part of the tile computes"):
+        make_kernel(source).lower(rand((2, 8, 128)))
+
+
 def test_the_step_planner_still_takes_the_phases_of_steps_form():
     """A nest of the phases-of-steps form keeps its step plan (the kernel families read it)."""
     kernel = make_kernel("""

@@ -835,8 +835,9 @@ class _Walk(_Generic):
         elif name in self.plan.kept and self.plan.kept[name].dtype.kind in "iu":
             shape, ref = self.plan.kept[name].shape, self.buf.ref(f"c_{name}")
         else:
-            raise KernelError(f"`{ast.unparse(sub)}`: the kernel reads elements of index arrays and of int32 arrays "
-                              "the tile code computed, not of this")
+            what = (f"{self.plan.kept[name].dtype.name} values" if name in self.plan.kept else "a value no later part keeps")
+            raise KernelError(f"`{ast.unparse(sub)}`: an element placing a window comes from an index array or an int32 "
+                              f"array the tile code computed and keeps; `{name}` is {what}")
         dims = list(sub.slice.elts) if isinstance(sub.slice, ast.Tuple) else [sub.slice]
         if len(dims) != len(shape) or any(isinstance(d, ast.Slice) for d in dims):
             raise KernelError(f"`{ast.unparse(sub)}`: index every dim of `{name}` with an integer")

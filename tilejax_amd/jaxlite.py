@@ -669,6 +669,10 @@ def arange(start: int, stop: Optional[int] = None, step: int = 1, dtype: Any = N
     if stop is None:
         start, stop = 0, start
     dt = int32 if dtype is None else globals()["dtype"](dtype)
+    if _TRACE is not None and all(isinstance(v, int) for v in (start, stop, step)):
+        # traced tile code: an iota node (the kernels compute each element's value), not a constant array
+        n = len(range(start, stop, step))
+        return leaf("iota", (n,), dt, dimension=0) * step + start
     return Array(torch.arange(start, stop, step, dtype=dt.torch, device=_DEVICE[-1]))
 
 
@@ -798,7 +802,8 @@ def unpairs(words: Any, new_dtype: Any) -> Array:
     """`pairs` undone: uint32 words (..., d) as a tile (..., 2, d) of the 16-bit `new_dtype`."""
     t, dt = _t(words), dtype(new_dtype)
     if t.dtype != torch.uint32 or dt.itemsize != 2:
-        raise TypeError(f"unpairs takes uint32 words and a 16-bit dtype, not {t.dtype} and {dt.name}")
+        have = _BY_TORCH[t.dtype].name if t.dtype in _BY_TORCH else str(t.dtype)
+        raise TypeError(f"unpairs takes uint32 words and a 16-bit dtype, not {have} and {dt.name}")
     return Array(t.contiguous().view(dt.torch).reshape(*t.shape, 2).transpose(-1, -2))
 
 

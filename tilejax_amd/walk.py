@@ -321,6 +321,17 @@ class _WalkPlanner(_Planner):
         if len(index) != len(shape):
             raise self.error(f"{text}: index every one of {array}'s {len(shape)} dims", node)
         dims = tuple(self._dim(i, n, text) for i, n in zip(index, shape))
+        # Index arrays (ragged rows, gathers) follow NumPy's rules in JAX: with integer indices they broadcast
+        # as one block, whose dims go first unless the block is contiguous. The kernel reads each index along
+        # its own dim, which agrees only for one array index next to every integer index.
+        arrays = [k for k, d in enumerate(dims) if d.stop is not None or d.gather is not None]
+        if len(arrays) > 1:
+            raise self.error(f"{text}: a window is placed through one `rows` or index-array slice", node)
+        if arrays:
+            block = sorted(arrays + [k for k, d in enumerate(dims) if d.size is None])
+            if block[-1] - block[0] + 1 != len(block):
+                raise self.error(f"{text}: `rows` (or an index-array slice) goes right after the integer indices, with "
+                                 "no slice between them (NumPy and JAX would put its rows first)", node)
         kept = [d.size is not None for d in dims]
         if True not in kept:
             raise self.error(f"{text}: a tile keeps at least one dim (slice it, `v:v + 1`)", node)
@@ -444,6 +455,24 @@ class _WalkPlanner(_Planner):
             read_early |= set().union(*(used(b) for b in loop.bounds))
         made = set().union(*(bound(b) for b in leaves)) if leaves else set()
         kept_names = (read_early & made) - set(nest.outputs) - loop_vars
+        # A window placed by an element of an array the tile computes reads the array as the kernel keeps it:
+        # computed in an earlier part of the tile (before the loop that reads the window), not the same one.
+        for leaf in leaves:
+            here = bound(leaf)
+            for stmt in leaf:
+                for node in ast.walk(stmt):
+                    acc = by_node.get(_pos(node)) if isinstance(node, ast.Subscript) else None
+                    if acc is None:
+                        continue
+                    for d in acc.dims:
+                        exprs = [e for e in (d.stop, d.gather) if e is not None]
+                        if not isinstance(d.start, int):
+                            exprs.append(d.start)
+                        late = sorted(set().union(*(used(e) for e in exprs)) & here) if exprs else []
+                        if late:
+                            raise self.error(f"{acc.text}: a window is placed by `{late[0]}`, which the same part of "
+                                             f"the tile computes: compute it before the loop that reads the window",
+                                             node)
         types: Dict[str, Tuple[Tuple[int, ...], Any]] = {}
         stores: Dict[str, Any] = {}
         counter = itertools.count()

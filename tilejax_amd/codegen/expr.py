@@ -475,6 +475,32 @@ class ElementEmitter:
                 else:
                     raise KernelError("only static slices and integers index tile values per element")
             return self._at(src, tuple(inner))
+        if op == "scatter_set":
+            # x.at[key].set(v): inside the region the key selects, v (broadcast to the region), else x. Integer
+            # keys the kernel computes select their one element; one out of the dim selects nothing (JAX drops
+            # updates out of the array).
+            src, key, val = a[0], a[1], a[2]
+            key = key if isinstance(key, tuple) else (key,)
+            conds, vidx, vshape = [], [], []
+            for k, d in enumerate(src.shape):
+                sel = key[k] if k < len(key) else slice(None)
+                i = idx[k]
+                if isinstance(sel, slice):
+                    start, stop, step = sel.indices(d)
+                    if (start, stop, step) != (0, d, 1):
+                        c = f"({i}) >= {start} && ({i}) < {stop}"
+                        conds.append(f"({c} && ((({i}) - {start}) % {step}) == 0)" if step != 1 else f"({c})")
+                    vidx.append(f"((({i}) - {start}) / {step})" if (start or step != 1) else i)
+                    vshape.append(len(range(start, stop, step)))
+                elif isinstance(sel, int):
+                    conds.append(f"(({i}) == {sel % d})")
+                elif isinstance(sel, Node) and sel.shape == () and sel.dtype.kind in "iu":
+                    conds.append(f"(({i}) == (int)({self._at(sel, ())}))")
+                else:
+                    raise KernelError("x.at[...].set per element takes static slices, integers and scalar integers")
+            inside = " && ".join(conds) or "true"
+            v = self._val(val, tuple(vidx), tuple(vshape), dt)
+            return f"(({inside}) ? ({ct})({v}) : ({ct})({self._at(src, idx)}))"
         if op == "transpose":
             perm = n.kwargs.get("axes") or tuple(reversed(range(len(shape))))
             inner = [None] * len(perm)

@@ -101,3 +101,104 @@ def test_fn_multiplies_bf16_with_f32_accumulation():
     want = (x.double() @ y.double()).bfloat16()
     assert got.dtype == torch.bfloat16
     assert (got.float() - want.float()).abs().max().item() <= 2e-2 * want.float().abs().max().item()
+
+
+def test_compare_checks_a_big_output_a_chunk_at_a_time(monkeypatch):
+    """The reference's tests/test_api.py:103-108: the bf16 floor is 2e-2 of the largest value anywhere, even
+    when it sits in a later chunk."""
+    from tilejax_amd import api
+
+    monkeypatch.setattr(api, "COMPARE_CHUNK", 2)
+    want = torch.tensor([[1.0, 2.0, 3.0], [4.0, 5.0, 100.0]], dtype=torch.bfloat16)
+    one = want.clone()
+    one[0, 0] += 1.0
+    assert compare("bf16", one, want) == 1.0
+    two = want.clone()
+    two[0, 0] += 4.0
+    two[1, 1] -= 4.0
+    with pytest.raises(AssertionError, match="2 of 6 elements"):
+        compare("bf16", two, want)
+
+
+SCALED = """
+def scaled(x):
+    out = jnp.zeros(x.shape)
+    for i in range(0, x.shape[0], 8):
+        out = out.at[i : i + 8, :].set(x[i : i + 8, :] * SCALE)
+    return out
+"""
+
+
+def test_constants_are_read_when_a_signature_is_first_built():
+    """As jax.jit reads globals when it traces: a signature built before a global changes keeps the value it
+    read; a new signature reads the new one (the reference's tests/test_api.py:55-62)."""
+    from tests.helpers import make_kernel, rand
+
+    kernel = make_kernel(SCALED, SCALE=2.0)
+    x = rand((8, 128))
+    first = kernel.reference(x)
+    kernel.fn.__globals__["SCALE"] = 3.0
+    assert torch.equal(kernel.reference(x), first)
+    wide = rand((16, 128))
+    assert torch.allclose(kernel.reference(wide), 3 * wide)
+
+
+def test_closures_are_read_too():
+    from tests.helpers import rand
+    from tilejax_amd.jaxlite import jnp
+
+    def make(scale):
+        @autokernel.kernel
+        def scaled(x):
+            out = jnp.zeros(x.shape)
+            for i in range(0, x.shape[0], 8):
+                out = out.at[i : i + 8, :].set(x[i : i + 8, :] * scale)
+            return out
+
+        return scaled
+
+    x = rand((16, 128))
+    assert torch.allclose(make(4.0).reference(x), 4 * x) and torch.allclose(make(0.5).reference(x), x / 2)
+
+
+def test_errors_quote_the_line_when_they_can():
+    import ast
+
+    node = ast.Pass(lineno=1)
+    assert str(KernelError("boom", filename=__file__, node=node)).startswith(f"{__file__}:1: boom\n    ")
+    assert str(KernelError("boom", filename="<nowhere>", node=node)) == "<nowhere>:1: boom"
+    assert str(KernelError("boom")) == "boom"
+
+
+def test_matmul_assignment():
+    """`acc @= w[k]` on a carried value (the reference's tests/test_api.py:164-180)."""
+    from tests.helpers import make_kernel, rand
+
+    kernel = make_kernel("""
+    def f(x, w):
+        out = jnp.zeros((128, 128))
+        for i in range(0, 128, 128):
+            acc = x[i : i + 128, :]
+            for k in range(0, 2):
+                acc @= w[k, :, :]
+            out = out.at[i : i + 128, :].set(acc)
+        return out
+    """)
+    x, w = rand((128, 128)), rand((2, 128, 128), 1) / 8
+    want = x.double() @ w[0].double() @ w[1].double()
+    assert (kernel.reference(x, w).double() - want).abs().max() < 1e-4
+    assert kernel.lower(x, w).program.notes["family"] == "generic"
+
+
+def test_prologue_comprehensions_see_globals():
+    from tests.helpers import make_kernel, spec
+
+    kernel = make_kernel("""
+    def f(x):
+        R = min(d // T for d in x.shape)
+        out = jnp.zeros((R * T, 128))
+        for i in range(0, R * T, T):
+            out = out.at[i : i + T, :].set(x[i : i + T, :])
+        return out
+    """, T=8)
+    assert kernel.lower(spec(16, 128)).tiles == 2

@@ -271,6 +271,14 @@ class _AsWritten:
         self.__wrapped__ = fn
         functools.update_wrapper(self, fn)
 
+    @property
+    def __globals__(self) -> Dict[str, Any]:  # the function's own globals, as on the plain function
+        return self.__wrapped__.__globals__
+
+    @property
+    def __code__(self) -> Any:
+        return self.__wrapped__.__code__
+
     def __call__(self, *args: Any) -> Any:
         device = next((a.device for a in args if isinstance(a, torch.Tensor)), "cpu")
         with jaxlite.default_device(device):

@@ -277,8 +277,53 @@ def no_stream(x):
     return out
 """, lambda: (rand((2, 128, 128)),), lambda x: (np.concatenate([4 * f64(x)[1] + 2] * 2),), rtol=1e-6, atol=1e-6)
 
+EMPTY_SOURCE = """
+def empty_steps(x):
+    out = jnp.zeros((256, 128))
+    for i in range(0, 256, 128):
+        acc = jnp.full((128, 128), 2.0)
+        for k in range(0, 256, 128):
+            if SKIP:
+                continue
+            acc += x[i : i + 128, k : k + 128]
+        out = out.at[i : i + 128, :].set(acc + 1)
+    return out
+"""
+
+
+def _empty_case(skip: str) -> Case:
+    def want(x):
+        out = np.full((256, 128), 3.0)
+        for i in (0, 128):
+            for k in (0, 128):
+                if not eval(skip, {"i": i, "k": k}):
+                    out[i:i + 128] += f64(x)[i:i + 128, k:k + 128]
+        return (out,)
+
+    return Case(f"a mask that skips steps ({skip}): a tile of none takes one empty step",
+                EMPTY_SOURCE.replace("SKIP", skip), lambda: (rand((256, 256)),), want)
+
+
+EMPTY_ALL, EMPTY_TILE, EMPTY_STEP = (_empty_case(s) for s in ("True", "i == 0", "i == 128 and k == 0"))
+
+MASKED_CARRIED = Case("values a masked loop makes for the code after it", """
+def masked_carried(x):
+    out = jnp.zeros((256, 128))
+    for i in range(0, 256, 128):
+        acc = jnp.zeros((128, 128))
+        for k in range(0, 256, 128):
+            if k > i:
+                continue
+            acc += x[i : i + 128, k : k + 128]
+            twice = acc * 2
+        out = out.at[i : i + 128, :].set(twice)
+    return out
+""", lambda: (rand((256, 256)),),
+    lambda x: (2 * np.concatenate([f64(x)[:128, :128], f64(x)[128:, :128] + f64(x)[128:, 128:]]),))
+
 CASES = [MASKS, STEP_MASK, TILE_MASK, SINGLE_STEP, PER_TILE_CASTS, BROADCAST_STORE, OFFSET_WINDOWS, INT_START,
-         BACK_TO_BACK, UNPACKING, PARTIAL_UPDATES, SHARED_WINDOWS, NO_STREAM]
+         BACK_TO_BACK, UNPACKING, PARTIAL_UPDATES, SHARED_WINDOWS, NO_STREAM, EMPTY_ALL, EMPTY_TILE, EMPTY_STEP,
+         MASKED_CARRIED]
 
 
 def check(case: Case, got: Any, wants: Tuple[np.ndarray, ...]) -> None:

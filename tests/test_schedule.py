@@ -177,3 +177,50 @@ def test_runtime_mask_tables_count_the_steps_that_run():
     assert count == 1 + 1 + 3 + 4
     assert step_code[0] & 4 and step_code[0] & 3 == 3  # the empty sequence's one step: empty, first, last
     assert list(step_tile[:count]) == [0, 1, 2, 2, 2, 3, 3, 3, 3]
+
+
+@pytest.mark.parametrize("skip,empty", [("True", True), ("i == 0", True), ("i == 128 and k == 0", False)])
+def test_a_tile_whose_mask_skips_every_step_takes_one_empty_step(skip, empty):
+    """The reference's tests/test_schedule.py:100-130: a tile all of whose blocks the mask skips still takes
+    one step, marked empty (its body doesn't run); the others take exactly their blocks."""
+    from tests.codegen_cases import EMPTY_SOURCE
+
+    kernel = make_kernel(EMPTY_SOURCE.replace("SKIP", skip))
+    sch = schedule_of(kernel, spec(256, 256))
+    assert sch.empty == empty
+    steps = [(sch.step_at(s), sch.empty_at(s)) for s in range(sch.steps)]
+    runs = {(i, k) for i in (0, 128) for k in (0, 128) if not eval(skip, {"i": i, "k": k})}
+    for i in (0, 128):
+        mine = [k for (tile, _, k), is_empty in steps if tile == i // 128 and not is_empty]
+        assert mine == [k // 128 for ii, k in sorted(runs) if ii == i]
+        assert any(tile == i // 128 for (tile, _, _), _e in steps)  # every tile takes a step
+
+
+def test_values_a_masked_loop_makes_for_the_code_after_it_are_carried():
+    from tests.codegen_cases import MASKED_CARRIED
+
+    kernel = make_kernel(MASKED_CARRIED.source)
+    assert set(kernel.lower(spec(256, 256)).plan.carried) == {"acc", "twice"}
+
+
+def test_step_arithmetic_stays_in_int32():
+    kernel = make_kernel("""
+    def f(x):
+        out = jnp.zeros((2**20, 256, 128))
+        for b in range(2**20):
+            for i in range(0, 256, 128):
+                if i:
+                    continue
+                out = out.at[b, i : i + 128, :].set(1.0)
+        return out
+    """)
+    with pytest.raises(KernelError, match="int32 step arithmetic"):
+        schedule_of(kernel, spec(8, 128))
+
+
+def test_a_causal_matmul_of_one_tile_needs_no_tables():
+    from examples.causal_matmul import causal_matmul
+    from examples.matmul import MatmulTiles
+
+    lowered = causal_matmul.lower(spec(256, 256), spec(256, 256), MatmulTiles(256, 256, 128))
+    assert lowered.schedule.tables == {}

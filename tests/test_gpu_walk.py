@@ -16,7 +16,9 @@ import torch
 import tilejax_amd
 from tests.helpers import make_kernel, rand
 from tests.test_walk import (FFN_STACK, GATHER, LAYERED, MASKED_IN_PLACE, MOE, NESTED, OFFSETS, ONCE_PER_TILE,
-                             RAGGED, SCAN, SCATTER, SPANS, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, PICKED, EARLY, counted_float64,
+                             RAGGED, SCAN, SCATTER, SPANS, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, PICKED, EARLY, CHOSEN,
+                             MIXED_MASKS, ONE_LAYER_STEPS, RUNTIME_IN_REPEAT, chosen_float64, chosen_inputs,
+                             counted_float64, mixed_masks_float64, runtime_in_repeat_float64,
                              ffn_inputs, ffn_stack_float64, gather_float64, i32, layered_float64, moe_inputs,
                              picked_float64, early_float64,
                              once_per_tile_float64, ragged_float64, route, routed_float64, scan_float64,
@@ -131,6 +133,23 @@ def test_an_element_index_the_tile_code_computes():
 def test_windows_placed_by_an_array_made_before_the_loop():
     x = rand((2, 8, 128))
     close(run(make_kernel(EARLY), x, what="early"), early_float64(x), 1e-6, 1e-6)
+
+
+def test_padding_iterations_and_layers_of_one_step():
+    ins = chosen_inputs()
+    close(run(make_kernel(CHOSEN), *ins, what="chosen"), chosen_float64(*ins), 1e-4, 1e-3)
+    for source, layers in ((ONE_LAYER_STEPS, 3), (FFN_STACK, 1)):
+        ins = ffn_inputs(layers)
+        close(run(make_kernel(source), *ins, what=f"ffn layers={layers}"), ffn_stack_float64(*ins))
+
+
+def test_runtime_ranges_in_repeat_loops_and_mixed_masks():
+    x, n = rand((8, 384)), i32(2, 384, 0, 256)
+    close(run(make_kernel(RUNTIME_IN_REPEAT), x, n, what="runtime in repeat"), runtime_in_repeat_float64(x, n),
+          1e-5, 1e-5)
+    x, n, lengths = rand((24, 512)), i32(256), i32(512, 0, 200)
+    close(run(make_kernel(MIXED_MASKS), x, n, lengths, what="mixed masks"), mixed_masks_float64(x, n, lengths),
+          1e-5, 1e-5)
 
 
 def test_indices_made_once_per_tile():

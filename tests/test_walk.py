@@ -695,6 +695,122 @@ def test_a_window_placed_by_what_the_same_part_computes_is_an_error():
         make_kernel(source).lower(rand((2, 8, 128)))
 
 
+CHOSEN = """
+def chosen(x, w, ids, n):
+    M, K = x.shape
+    C = ids.shape[0]
+    out = jnp.zeros((M, K), jnp.float32)
+    for i in range(0, M, 128):
+        h = x[i : i + 128, :]
+        acc = jnp.zeros((128, K))
+        for c in range(C):  # the chosen experts, then padding
+            for f in range(0, K, K):
+                if c >= n[0]:  # padding: an empty step, its expert's weights never read
+                    continue
+                acc += h @ w[ids[c], :, :] * (c + 1)
+        out = out.at[i : i + 128, :].set(acc)
+    return out
+"""
+
+
+def chosen_inputs():
+    return rand((256, 128)), rand((6, 128, 128), 1) / 10, i32(4, 1, 0, 0), i32(2)
+
+
+def chosen_float64(x, w, ids, n):
+    x, w = f64(x), f64(w)
+    return sum(x @ w[int(ids[c])] * (c + 1) for c in range(int(n[0])))
+
+
+def test_an_empty_iteration_skips_what_only_its_steps_read():
+    """The reference's tests/test_repeat_loops.py:214-227: padding iterations take no work."""
+    kernel = make_kernel(CHOSEN)
+    ins = chosen_inputs()
+    close(kernel.reference(*ins), chosen_float64(*ins), 1e-4, 1e-3)
+    compiles(kernel.lower(*ins))
+
+
+ONE_LAYER_STEPS = FFN_STACK.replace("range(0, F, 128)", "range(0, F, F)").replace("f + 128", "f + F")
+
+
+def test_repeat_loops_of_one_iteration_and_of_whole_layer_steps():
+    """The reference's tests/test_repeat_loops.py:230-247: a repeat loop whose reduction is one step a
+    layer, and a repeat loop of one iteration."""
+    for source, layers in ((ONE_LAYER_STEPS, 3), (FFN_STACK, 1)):
+        kernel = make_kernel(source)
+        ins = ffn_inputs(layers)
+        close(kernel.reference(*ins), ffn_stack_float64(*ins))
+        compiles(kernel.lower(*ins))
+
+
+RUNTIME_IN_REPEAT = """
+def runtime_in_repeat(x, n):
+    out = jnp.zeros((8, 128))
+    for i in range(0, 8, 8):
+        acc = jnp.zeros((8, 128))
+        for j in range(n[0]):
+            acc += x[i : i + 8, 0:128]
+        for l in range(3):
+            for k in range(0, n[1 + l], 128):
+                acc += x[i : i + 8, k : k + 128] * (l + 1)
+        out = out.at[i : i + 8, :].set(acc)
+    return out
+"""
+
+
+def runtime_in_repeat_float64(x, n):
+    x = f64(x)
+    want = int(n[0]) * x[:, :128]
+    for layer in range(3):
+        for k in range(0, int(n[1 + layer]), 128):
+            want = want + x[:, k:k + 128] * (layer + 1)
+    return want
+
+
+MIXED_MASKS = """
+def mixed_masks(x, n, lengths):
+    out = jnp.zeros((24, 128))
+    for i in range(0, 24, 8):
+        acc = jnp.zeros((8, 128))
+        for j in range(0, n[0], 128):  # a runtime range
+            acc += x[i : i + 8, j : j + 128]
+        for j2 in range(0, 512, 128):
+            if j2 >= lengths[i // 8] or j2 == 128:  # a runtime mask
+                continue
+            acc += x[i : i + 8, j2 : j2 + 128] * 2
+        for j3 in range(0, 256, 128):
+            if j3 > 0:  # a static mask
+                continue
+            acc += x[i : i + 8, j3 : j3 + 128] * 3
+        out = out.at[i : i + 8, :].set(acc)
+    return out
+"""
+
+
+def mixed_masks_float64(x, n, lengths):
+    x = f64(x)
+    out = np.zeros((24, 128))
+    for t, length in enumerate(lengths.tolist()):
+        rows = x[8 * t:8 * t + 8]
+        want = sum(rows[:, j:j + 128] for j in range(0, int(n[0]), 128)) + 3 * rows[:, :128]
+        want = want + 2 * sum(rows[:, j:j + 128] for j in range(0, 512, 128) if j < length and j != 128)
+        out[8 * t:8 * t + 8] = want
+    return out
+
+
+def test_runtime_ranges_in_repeat_loops_and_mixed_masks():
+    """The reference's tests/test_computed_indices.py:140-193: a runtime range inside a repeat loop, and a
+    runtime range, a runtime mask and a static mask in one tile."""
+    kernel = make_kernel(RUNTIME_IN_REPEAT)
+    x, n = rand((8, 384)), i32(2, 384, 0, 256)
+    close(kernel.reference(x, n), runtime_in_repeat_float64(x, n), 1e-5, 1e-5)
+    compiles(kernel.lower(x, n))
+    kernel = make_kernel(MIXED_MASKS)
+    x, n, lengths = rand((24, 512)), i32(256), i32(512, 0, 200)
+    close(kernel.reference(x, n, lengths), mixed_masks_float64(x, n, lengths), 1e-5, 1e-5)
+    compiles(kernel.lower(x, n, lengths))
+
+
 def test_the_step_planner_still_takes_the_phases_of_steps_form():
     """A nest of the phases-of-steps form keeps its step plan (the kernel families read it)."""
     kernel = make_kernel("""

@@ -18,6 +18,8 @@ from tests.helpers import make_kernel, rand
 from tests.test_walk import (FFN_STACK, GATHER, LAYERED, MASKED_IN_PLACE, MOE, NESTED, OFFSETS, ONCE_PER_TILE,
                              RAGGED, SCAN, SCATTER, SPANS, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, PICKED, EARLY, CHOSEN,
                              MIXED_MASKS, ONE_LAYER_STEPS, RUNTIME_IN_REPEAT, chosen_float64, chosen_inputs,
+                             ONLY_IN_PLACE, RAGGED_BOTH, PAIRS_PER_ITERATION, only_in_place_float64,
+                             ragged_both_float64, pairs_per_iteration_float64,
                              counted_float64, mixed_masks_float64, runtime_in_repeat_float64,
                              ffn_inputs, ffn_stack_float64, gather_float64, i32, layered_float64, moe_inputs,
                              picked_float64, early_float64,
@@ -150,6 +152,17 @@ def test_runtime_ranges_in_repeat_loops_and_mixed_masks():
     x, n, lengths = rand((24, 512)), i32(256), i32(512, 0, 200)
     close(run(make_kernel(MIXED_MASKS), x, n, lengths, what="mixed masks"), mixed_masks_float64(x, n, lengths),
           1e-5, 1e-5)
+
+
+def test_in_place_ragged_and_pairs_forms():
+    x = rand((256, 128))
+    close(run(make_kernel(ONLY_IN_PLACE), x, what="only in place"), only_in_place_float64(x), 1e-6, 0)
+    x, y, n = rand((20, 256)), rand((8, 512)), i32(4, 9, 128, 300)
+    got = run(make_kernel(RAGGED_BOTH, tilejax_amd=tilejax_amd), x, y, n, what="ragged both dims")
+    close(got, ragged_both_float64(x, y, n), 1e-6, 0)
+    kv, x = rand((2, 16, 2, 128), dtype=torch.bfloat16), rand((2, 32, 128))
+    got = run(make_kernel(PAIRS_PER_ITERATION, tilejax_amd=tilejax_amd), kv, x, what="pairs per iteration")
+    close(got, pairs_per_iteration_float64(kv, x), 1e-5, 1e-5)
 
 
 def test_indices_made_once_per_tile():

@@ -811,6 +811,78 @@ def test_runtime_ranges_in_repeat_loops_and_mixed_masks():
     compiles(kernel.lower(x, n, lengths))
 
 
+ONLY_IN_PLACE = """
+def only_in_place(x):
+    new = x
+    for i in range(0, 256, 128):
+        if i > 0:
+            continue
+        new = new.at[i : i + 128, :].set(x[i : i + 128, :] * 3)
+    return new
+"""
+
+
+def only_in_place_float64(x):
+    x = f64(x)
+    return np.concatenate([3 * x[:128], x[128:]])
+
+
+RAGGED_BOTH = """
+def ragged_both(x, y, n):
+    out = jnp.zeros((8, 256))
+    for i in range(0, 8, 8):
+        a = x[tilejax_amd.rows(n[0], n[1], 8), :]
+        b = y[0:8, tilejax_amd.rows(n[2], n[3], 256)]
+        rows = jax.lax.broadcasted_iota(jnp.int32, (8, 256), 0)
+        cols = jax.lax.broadcasted_iota(jnp.int32, (8, 256), 1)
+        ok = (rows < n[1] - n[0]) & (cols < n[3] - n[2])  # (past the stops: unspecified)
+        out = out.at[i : i + 8, :].set(jnp.where(ok, a + b, 0.0))
+    return out
+"""
+
+
+def ragged_both_float64(x, y, n):
+    want = np.zeros((8, 256))
+    want[:5, :172] = f64(x)[4:9, :172] + f64(y)[:5, 128:300]
+    return want
+
+
+PAIRS_PER_ITERATION = """
+def pairs_per_iteration(kv, x):
+    out = jnp.zeros((16, 128))
+    for i in range(0, 16, 16):
+        acc = jnp.zeros((16, 128))
+        for l in range(2):
+            for k in range(0, 32, 16):
+                keys = jax.lax.bitcast_convert_type(tilejax_amd.pairs(kv[l, :, :, :]) << 16, jnp.float32)
+                acc += keys + x[l, k : k + 16, :]
+        out = out.at[i : i + 16, :].set(acc)
+    return out
+"""
+
+
+def pairs_per_iteration_float64(kv, x):
+    return sum(2 * f64(kv)[n, :, 0, :] + f64(x)[n, :16] + f64(x)[n, 16:] for n in range(2))
+
+
+def test_in_place_ragged_and_pairs_forms():
+    """The reference's tests/test_in_place.py:98-113 (an output updated in place fills nothing),
+    tests/test_runtime_ranges.py:170-204 (ragged reads along both dims of a tile) and :278-298 (pairs of a
+    window read once per repeat iteration)."""
+    x = rand((256, 128))
+    kernel = make_kernel(ONLY_IN_PLACE)
+    close(kernel.reference(x), only_in_place_float64(x), 1e-6, 0)
+    compiles(kernel.lower(x))
+    kernel = make_kernel(RAGGED_BOTH, tilejax_amd=tilejax_amd)
+    x, y, n = rand((20, 256)), rand((8, 512)), i32(4, 9, 128, 300)
+    close(kernel.reference(x, y, n), ragged_both_float64(x, y, n), 1e-6, 0)
+    compiles(kernel.lower(x, y, n))
+    kernel = make_kernel(PAIRS_PER_ITERATION, tilejax_amd=tilejax_amd)
+    kv, x = rand((2, 16, 2, 128), dtype=torch.bfloat16), rand((2, 32, 128))
+    close(kernel.reference(kv, x), pairs_per_iteration_float64(kv, x), 1e-5, 1e-5)
+    compiles(kernel.lower(kv, x))
+
+
 def test_the_step_planner_still_takes_the_phases_of_steps_form():
     """A nest of the phases-of-steps form keeps its step plan (the kernel families read it)."""
     kernel = make_kernel("""

@@ -183,10 +183,15 @@ def parse(fn: Callable) -> Nest:
         filename = inspect.getsourcefile(fn) or fn.__code__.co_filename
     except (OSError, TypeError) as e:
         raise KernelError(f"{name}: can't read its source; kernels are compiled from a function's Python source") from e
-    module = ast.parse(textwrap.dedent("".join(source)))
+    reader = _Reader(name, filename)
+    if name == "<lambda>":
+        raise KernelError(f"{name}: a kernel is a function defined with `def`")
+    try:
+        module = ast.parse(textwrap.dedent("".join(source)))
+    except SyntaxError as e:  # the source lines of something that isn't a whole `def`
+        raise KernelError(f"{name}: a kernel is a function defined with `def`") from e
     ast.increment_lineno(module, first - 1)
     fdef = module.body[0]
-    reader = _Reader(name, filename)
     if not isinstance(fdef, ast.FunctionDef):
         raise reader.fail("a kernel is a function defined with `def`", fdef)
     return reader.read(fdef)
@@ -336,7 +341,7 @@ class _Reader:
     def check_tile_statements(self, stmts: Iterable[ast.stmt]) -> None:
         for stmt in stmts:
             if isinstance(stmt, ast.For):
-                raise self.fail("loops nest only as parallel loops around reduction loops", stmt)
+                raise self.fail("loops nest only as parallel loops around reduction (and repeat) loops", stmt)
             if isinstance(stmt, ast.Assign):
                 if len(stmt.targets) != 1 or not _only_names(stmt.targets[0]):
                     raise self.fail("tile code assigns names: `a = ...` or `a, b = ...`", stmt)

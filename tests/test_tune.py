@@ -186,3 +186,85 @@ def test_hardware_choices_are_distinct_kernels():
     tiles = [{"bm": 256, "bn": 128}, {"bm": 128, "bn": 256}, {"bm": 128, "bn": 128}]
     assert [dict(h) for h in hardware_choices(plan, schedule)][1:] == (
         tiles + [{"bm": 256, "bn": 256, "waves": 8}] + [{**t, "waves": 8} for t in tiles])
+
+
+# ------------------------------------------------------------------------------------- tuning a kernel
+
+
+def test_off_the_gpu_tuning_uses_the_defaults():
+    """The reference's tests/test_tune.py:190-197: without a device to time on, the defaults, once per
+    signature."""
+    k = make_kernel(SOURCE, Tiles=Tiles)
+    x, y = spec(256, 256), spec(256, 128)
+    tuning = k.tuning(x, y)
+    assert tuning.config == k.default_config(k.signature(x, y)) and tuning.trials == []
+    assert k.tuning(x, y) is tuning
+
+
+def test_tuning_climbs_to_bigger_tiles_when_steps_are_overhead(monkeypatch):
+    """The reference's tests/test_tune.py:200-215, with the measurement simulated (device time in proportion
+    to the steps, most of it overhead): the search follows the proposals to the one-step tiles."""
+    from tilejax_amd import tune
+
+    def measure(kernel, signature, config, inputs, want):
+        steps = kernel.lowered(signature, config).steps
+        return Trial(config, profile(config, seconds=steps * 10e-6, steps=steps, compute=steps * 1e-6))
+
+    monkeypatch.setattr(tune, "_can_time", lambda: True)
+    monkeypatch.setattr(tune, "_measure", measure)
+    monkeypatch.setattr(tune, "random_inputs", lambda signature, bounds=None, seed=0, distinct=(): [
+        torch.zeros(s, dtype=dt.torch) for s, dt in signature])
+    k = make_kernel(SOURCE, Tiles=Tiles)
+    x, y = spec(256, 256), spec(256, 128)
+    tuning = k.tuning(x, y)
+    assert tuning.config.tunable == Tiles(tm=256, tk=256)  # one step a tile, one tile: the least overhead
+    tiles = [t.config.tunable for t in tuning.trials if not t.config.hardware]  # (beside the other kernel shapes)
+    assert tiles[:3] == [Tiles(), Tiles(tm=256), Tiles(tm=256, tk=256)]
+    assert "Tiles(tm=256, tk=256)" in str(tuning)
+
+
+def test_neighbours_that_build_the_same_kernel_arent_proposed():
+    """The reference's tests/test_tune.py:254-262: at tiles as large as the arrays, only smaller ones change
+    the kernel."""
+    from examples.matmul import MatmulTiles, matmul
+
+    sig = matmul.signature(spec(512, 512, dtype=jaxlite.bfloat16), spec(512, 512, dtype=jaxlite.bfloat16))
+    start = matmul.default_config(sig)
+    proposed = proposals(matmul, sig, Trial(start, profile(start, seconds=10.0)))
+    assert [c.tunable for c in proposed if not c.hardware] == [MatmulTiles(tm=256), MatmulTiles(tn=256),
+                                                               MatmulTiles(tk=256)]
+
+
+def test_the_default_schedule_is_the_nearest_that_builds():
+    @autokernel.tunable
+    class Rows:
+        tm: int = autokernel.choice(128, 256, 512, 1024, default=1024)
+
+    k = make_kernel("""
+    def f(x, t=Rows()):
+        out = jnp.zeros((512, 128))
+        for i in range(0, 512, t.tm):
+            out = out.at[i : i + t.tm, :].set(x[i : i + t.tm, :])
+        return out
+    """, Rows=Rows)
+    assert k.default_config(k.signature(spec(512, 128))).tunable == Rows(tm=512)  # 1024 doesn't divide 512
+
+
+def test_a_kernel_and_its_tunable_can_be_local():
+    from helpers import rand
+    from tilejax_amd.jaxlite import jnp
+
+    @autokernel.tunable
+    class Local:
+        tm: int = autokernel.choice(8, 16)
+
+    @autokernel.kernel
+    def double(x, tiles=Local()):
+        out = jnp.zeros(x.shape)
+        for i in range(0, x.shape[0], tiles.tm):
+            out = out.at[i : i + tiles.tm, :].set(x[i : i + tiles.tm, :] * 2)
+        return out
+
+    x = rand((32, 128))
+    assert torch.equal(double.reference(x), 2 * x) and torch.equal(double.reference(x, Local(tm=16)), 2 * x)
+    assert double.lower(x).schedule.tiles == 4 and double.lower(x, Local(tm=16)).schedule.tiles == 2

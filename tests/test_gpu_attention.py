@@ -129,10 +129,12 @@ def test_split_tiles_call_after_call():
     ((("bkv", 32), ("waves", 8)), 2),
     ((), 3),  # K and V two blocks ahead through three LDS stages
     ((), 4),
+    ((("bkv", 64), ("split", 0), ("waves", 4)), 2),  # no split-KV
+    ((("bkv", 64), ("split", 10), ("waves", 4)), 2),  # split above one share
 ])
 def test_kernel_shapes_the_tuner_tries(hardware, buffers):
-    """Each gfx950 kernel shape the tuner may pick (waves per workgroup, keys per block, ring depth) against
-    the oracle, at a shape where every block class (full, partial, skipped) occurs."""
+    """Each gfx950 kernel shape the tuner may pick (waves per workgroup, keys per block, ring depth, split-KV
+    share) against the oracle, at a shape where every block class (full, partial, skipped) occurs."""
     from tilejax_amd import Pipeline
     from tilejax_amd.tune import Config
 

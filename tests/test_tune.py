@@ -161,26 +161,28 @@ def test_a_kernel_without_a_tunable_tunes_its_buffering():
 
 def test_hardware_choices_are_distinct_kernels():
     """The tuner's gfx950 vocabulary: the matmul's workgroup tiles (in four or eight waves) and attention's
-    waves and key blocks each build a different kernel, and each compiles."""
+    waves, key blocks and split-KV share each build a different kernel (or, for the share, different work
+    items), and each compiles."""
     from examples.causal_attention import AttentionBlocks, causal_attention
     from examples.matmul import MatmulTiles, matmul
     from tilejax_amd import runtime
     from tilejax_amd.codegen import hardware_choices
+    from tilejax_amd.tune import _built
 
     bf = jaxlite.bfloat16
     cases = [(matmul, (spec(1024, 1024, dtype=bf), spec(1024, 1024, dtype=bf)), MatmulTiles(512, 512, 512), 8),
-             (causal_attention, tuple(spec(2, 4, 512, 128, dtype=bf) for _ in range(3)), AttentionBlocks(256, 256), 4)]
+             (causal_attention, tuple(spec(2, 4, 512, 128, dtype=bf) for _ in range(3)), AttentionBlocks(256, 256), 6)]
     for kernel, args, tiles, count in cases:
         sig = kernel.signature(*args)
         plan, schedule = kernel.build(sig, tiles)
         shapes = hardware_choices(plan, schedule)
         assert len(shapes) == count and shapes[0] == ()
-        sources = set()
+        built = set()
         for hw in shapes:
             lowered = kernel.lowered(sig, Config(tiles, Pipeline(2, 2), False, hw))
             runtime.compile_source(lowered.source, f"{kernel.nest.name}.hip")
-            sources.add(lowered.source)
-        assert len(sources) == count
+            built.add(_built(lowered))
+        assert len(built) == count
     plan, schedule = matmul.build(matmul.signature(spec(1024, 1024, dtype=bf), spec(1024, 1024, dtype=bf)),
                                   MatmulTiles(512, 512, 512))
     tiles = [{"bm": 256, "bn": 128}, {"bm": 128, "bn": 256}, {"bm": 128, "bn": 128}]

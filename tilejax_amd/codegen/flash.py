@@ -66,6 +66,17 @@ WAVES = 4  # waves per workgroup (None: 8 for tiles of a multiple of 256 query r
 BKV = 64  # keys per block (a multiple of 32)
 K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
 V_AHEAD = 4  # V fragments in flight ahead of the O MFMAs
+# Split-KV: a work item's cost is its key blocks plus ITEM_COST (its Q load, pipeline fill and stores); a
+# workgroup's share is the total over the resident workgroups (two per CU). Items above SPLIT_ABOVE shares
+# are cut into chunks of about a share, and of at least MIN_CHUNK blocks (a chunk's partial (m, l, acc) and
+# its merge cost about that much). Measured at 512 x 512 spec blocks: (1, 16, 4096, 128) 90.5 -> 87.5 us,
+# (1, 8, 8192, 128) 170 -> 155 us, (2, 4, 1024, 128) 25.3 -> 22.0 us; 1.25 shares split too much, and
+# (4, 16, 2048, 128) has no item above 1.5. Static per-workgroup work lists balanced by the same cost (LPT)
+# measured no faster than the dispatcher's own order: of two workgroups on a CU the older one issues more,
+# so equal work does not finish together.
+ITEM_COST = 2
+SPLIT_ABOVE = 1.5
+MIN_CHUNK = 3
 
 
 @dataclass
@@ -288,6 +299,10 @@ class _Flash:
                               f"rows (got {m.rows})")
         self.bq = 32 * self.nw
         self.bkv = hardware.get("bkv", BKV)
+        # split-KV above this many shares, in tenths (0: never split)
+        self.split_tenths = hardware.get("split", round(10 * SPLIT_ABOVE))
+        if self.split_tenths < 0:
+            raise KernelError(f"the split share is a number of tenths of a share, 0 or more (got {self.split_tenths})")
         if m.bk % self.bkv:
             raise KernelError(f"the gfx950 attention lowering needs key blocks of a multiple of {self.bkv} (got {m.bk})")
         if plan.runtime or sch.runtime:
@@ -400,19 +415,19 @@ class _Flash:
 
     # ------------------------------------------------------------------------------------------ program
 
-    def _split(self, items, weights):
-        """Split-KV for balance: items with more key blocks than a CU's share of all blocks (one workgroup
-        per CU at a time) are cut into chunks of consecutive blocks. A chunk runs the same online softmax
-        over its blocks and writes its (m, l, acc) to a workspace slot; the merge kernel combines a tile's
-        chunks. Returns the items (t, sub, block offset, blocks, per-wave counts, slot or -1), their weights
-        and the merge table rows (t, sub, first slot, chunks)."""
-        total = sum(it[3] for it in items)
-        share = max(1, -(-total // gfx950.CUS))
+    def _split(self, items, weights, lanes: int):
+        """Split-KV for balance: items with more than `split_tenths` / 10 times one workgroup's share of all
+        the work (`lanes` workgroups at a time) are cut into chunks of consecutive blocks. A chunk runs the same
+        online softmax over its blocks and writes its (m, l, acc) to a workspace slot; the merge kernel
+        combines a tile's chunks. Returns the items (t, sub, block offset, blocks, per-wave counts, slot or
+        -1), their weights and the merge table rows (t, sub, first slot, chunks)."""
+        total = sum(it[3] + ITEM_COST for it in items)
+        share = max(MIN_CHUNK, -(-total // lanes))
         out, w_out, merges = [], [], []
         slot = 0
         for it, wt in zip(items, weights):
             t, sub, off, cnt, waves = it
-            parts = -(-cnt // share) if cnt > share * 1.1 and len(items) < 2 * gfx950.CUS else 1
+            parts = -(-cnt // share) if self.split_tenths and 10 * cnt > share * self.split_tenths else 1
             if parts == 1:
                 out.append((t, sub, off, cnt, waves, -1))
                 w_out.append(wt)
@@ -430,9 +445,12 @@ class _Flash:
     def program(self) -> Program:
         plan, sch, m = self.plan, self.sch, self.m
         items, weights, blocks = self._items()
-        items, weights, merges = self._split(items, weights)
+        lds = self.stages * self.bkv * (m.d + m.dv) * 2
+        lanes = gfx950.CUS * max(1, min(2, gfx950.LDS_BYTES // lds))
+        items, weights, merges = self._split(items, weights, lanes)
         self.slots = sum(c for _, _, _, c in merges)
         order = sorted(range(len(items)), key=lambda i: (-weights[i], i))
+        grid = max(len(items), 1)
         nw = self.nw
         stride = 5 + 2 * nw
         table = np.zeros((max(len(items), 1), stride), np.int32)
@@ -452,7 +470,7 @@ class _Flash:
         self.tables = tables
         args = self._args()
         source = self._source(args, stride)
-        launches = [Launch(self.name, args, (max(len(items), 1), 1, 1), (64 * nw, 1, 1), 0)]
+        launches = [Launch(self.name, args, (grid, 1, 1), (64 * nw, 1, 1), 0)]
         workspace = {}
         if self.trace:
             workspace[TRACE] = max(len(items), 1) * TRACE_FIELDS * 8
@@ -461,7 +479,6 @@ class _Flash:
             per_item = self.bq * m.dv // 4 // 256
             launches.append(Launch(f"{self.name}_merge", args, (len(merges) * per_item, 1, 1), (256, 1, 1), 0))
         flop = 2.0 * sum(w for w in weights) * 32 * self.bkv * (m.d + m.dv)
-        lds = self.stages * self.bkv * (m.d + m.dv) * 2
         return Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
             inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
@@ -470,8 +487,8 @@ class _Flash:
                    "executed_flop": flop, "split_items": len(merges), "chunks": self.slots,
                    # the reference's step is (query tile, key block) of the spec; a workgroup's slice here is
                    # one block of bkv keys for its bq rows
-                   "trace_workgroups": max(len(items), 1) if self.trace else 0,
-                   "trace_slots": min(max(len(items), 1), gfx950.CUS * max(1, gfx950.LDS_BYTES // lds)),
+                   "trace_workgroups": grid if self.trace else 0,
+                   "trace_slots": min(grid, lanes),
                    "slices_per_step": (m.rows // self.bq) * (m.bk // self.bkv)},
         )
 
@@ -1103,8 +1120,9 @@ def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: FlashMatch, name: st
 
 
 def hardware_choices(m: FlashMatch) -> List[Dict[str, int]]:
-    """The kernel shapes tuning may try for this match: waves per workgroup (32 query rows each) and keys
-    per block. The first is the default."""
+    """The kernel shapes tuning may try for this match: waves per workgroup (32 query rows each), keys per
+    block, and, for the first of those, where split-KV starts (never, or above one share instead of 1.5).
+    The first is the default."""
     if m.q.tile.dtype.name == "float32":
         return [{}]
     found = []
@@ -1112,4 +1130,6 @@ def hardware_choices(m: FlashMatch) -> List[Dict[str, int]]:
         for bkv in (BKV, 32 if BKV == 64 else 64):
             if m.rows % (32 * waves) == 0 and m.bk % bkv == 0:
                 found.append({"waves": waves, "bkv": bkv})
+    if found:
+        found += [{**found[0], "split": 0}, {**found[0], "split": 10}]
     return found or [{}]

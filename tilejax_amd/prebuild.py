@@ -133,7 +133,8 @@ def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
             yield mm.matmul, args, Config(mm.matmul.default_tunable, Pipeline(n, 2), False, hw), True
     blocks = ca.AttentionBlocks(256, 256)
     for hw, n in (((("bkv", 64), ("waves", 8)), 2), ((("bkv", 32), ("waves", 4)), 2),
-                  ((("bkv", 32), ("waves", 8)), 2), ((), 3), ((), 4)):
+                  ((("bkv", 32), ("waves", 8)), 2), ((), 3), ((), 4),
+                  ((("bkv", 64), ("split", 0), ("waves", 4)), 2)):
         yield ca.causal_attention, tuple(_bf16(2, 4, 1024, 128) for _ in range(3)), Config(blocks, Pipeline(n, 2), False, hw), False
     ins = (_bf16(5, 1, 32, 128), _bf16(500, 16, 1024), _bf16(500, 16, 1024), _i32(5, 100), _i32(5))
     for n in (2, 4):

@@ -22,6 +22,7 @@ import math
 from dataclasses import dataclass, field
 from typing import TYPE_CHECKING, Any, Callable, Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from . import profiling
@@ -205,10 +206,17 @@ def _smaller(kernel: Any, signature: Any, config: Config) -> List[Config]:
     return found
 
 
+def _built(lowered: Any) -> Tuple[str, Tuple[Tuple[str, bytes], ...]]:
+    """What a lowering runs: its source and the contents of its tables (kernel shapes such as attention's
+    split-KV share change only the work-item table)."""
+    tables = lowered.program.tables
+    return lowered.source, tuple((name, np.ascontiguousarray(tables[name]).tobytes()) for name in sorted(tables))
+
+
 def _other_kernels(kernel: Any, signature: Any, start: Config) -> List[Config]:
     """The bufferings of `start` (and the other way of finding steps, where a kernel may take either) whose
-    generated kernels differ from its own."""
-    here = kernel.lowered(signature, start).source
+    generated kernels or tables differ from its own."""
+    here = _built(kernel.lowered(signature, start))
     found = []
     plan, schedule = kernel.build(signature, start.tunable)
     cursors = (False, True) if plan.either else (start.cursor,)
@@ -218,7 +226,7 @@ def _other_kernels(kernel: Any, signature: Any, start: Config) -> List[Config]:
         if config == start:
             continue
         try:
-            if kernel.lowered(signature, config).source != here:
+            if _built(kernel.lowered(signature, config)) != here:
                 found.append(config)
         except KernelError:
             continue

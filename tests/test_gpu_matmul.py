@@ -65,11 +65,12 @@ def test_matmul_verify_against_reference():
 
 def test_causal_matmul_full_size_balanced_split():
     """The 8192^3 causal matmul at 512^3 tiles: 528 computed 256x256 tiles on 256 workgroups, so 16 of them are
-    cut along K into 16 chunks whose partials a fixup kernel adds. Checked against the oracle everywhere."""
+    cut along K into 8 chunks of 16 slices whose partials a fixup kernel adds. Checked against the oracle
+    everywhere."""
     n, tiles = 8192, MatmulTiles(512, 512, 512)
     x, y = _inputs(n, n, n, seed=7)
     lowered = causal_matmul.lower(x, y, tiles)
-    assert lowered.program.notes["split"] == (16, 16, 8)
+    assert lowered.program.notes["split"] == (16, 8, 16)
     print(f"causal {n} {tiles} split {lowered.program.notes['split']}", flush=True)
     got = lowered.run(x.cuda(), y.cuda())
     torch.cuda.synchronize()

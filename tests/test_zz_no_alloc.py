@@ -43,7 +43,7 @@ def test_decode_without_allocating(cursor):
 
 
 def test_causal_split_without_allocating():
-    """The 8192^3 causal matmul's split tiles keep their f32 partials (64 MiB, the whole scratch array) in the
+    """The 8192^3 causal matmul's split tiles keep their f32 partials (32 MiB, half the scratch array) in the
     workspace; then a 2048^3 call at 256^3 tiles reuses the front of it."""
     for n, tiles in ((8192, MatmulTiles(512, 512, 512)), (2048, MatmulTiles(256, 256, 256))):
         g = torch.Generator().manual_seed(n)

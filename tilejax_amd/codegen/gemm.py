@@ -404,6 +404,12 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
 # causal 8192^3 at 512^3 tiles: 484.8-487.7 us with the queue, 479.1-483.7 us without (the queue narrows the
 # workgroups' spread, but its pulls and the later stores cost more than that gains).
 QUEUE_TAIL = [False]
+# The last round's K-split: at most MAX_SPLIT chunks per tile. Its chunks run at the kernel's end, when their
+# reads, f32 partials and the filled tiles' stores share HBM, and the fixup reads the partials again: causal
+# 8192^3 at 512^3 tiles measured 484 us at 16 chunks of 8 slices, 475-478 at 8 of 16, 477-480 at 4 of 32.
+# Running a workgroup's small items (fills, constants, its chunk) before its whole tiles, all of them or the
+# fills alone, or after its first or second whole tile by workgroup, measured 5-25 us slower.
+MAX_SPLIT = 8
 
 
 def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, name: str, trace: bool = False,
@@ -618,8 +624,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
     def _split_remainder(self, items, weights, groups):
         """Balance the last round. With n equal compute items on G workgroups, n = q G + r and r <= G / 2,
         the last round would leave most workgroups idle: r of the items are cut along the reduction into
-        `split` chunks each (r * split <= G). A chunk writes its f32 partial sums to a workspace slot, and a
-        fixup kernel adds a tile's partials in chunk order and applies the epilogue."""
+        `split` chunks each (r * split <= G, split <= MAX_SPLIT). A chunk writes its f32 partial sums to a
+        workspace slot, and a fixup kernel adds a tile's partials in chunk order and applies the epilogue."""
         hw, G = self.hw, gfx950.CUS
         compute = [k for k, (_, c, _) in enumerate(items) if (c >> 16) == 0]
         if not compute or len({weights[k] for k in compute}) != 1:
@@ -629,7 +635,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
         if r == 0 or 2 * r > G:
             return items, weights, groups
         split = 1
-        while (2 * split * r <= G and T % (2 * split) == 0 and (T // (2 * split)) % hw.stages == 0
+        while (2 * split * r <= G and 2 * split <= MAX_SPLIT and T % (2 * split) == 0 and (T // (2 * split)) % hw.stages == 0
                and T // (2 * split) >= max(4, 2 * hw.stages)):
             split *= 2
         if split == 1:
@@ -649,7 +655,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             for ch in range(split):
                 out.append((t, (c & 0xFFFF) | (3 << 16), p * split + ch))
                 w_out.append(T / split + 1)
-                g_out.append(groups[k])
+                # chunks are ordered by K range, so each XCD takes every remainder tile's chunks over the same
+                # two (of 16) K ranges: the tiles' A and B panels over those ranges are read into its L2 once
+                g_out.append(ch * gfx950.XCDS // split)
         return out, w_out, g_out
 
     def _constant_of(self, t: int, s: int) -> Optional[float]:

@@ -16,13 +16,14 @@ one, `k_pages[block_tables[b, p], :, :]`, or `k_cache[b, j : j + bk, :]`), runs 
    of them, in order) and splits the compacted list of them evenly over one workgroup per CU (a sequence's
    pages may span several workgroups, a workgroup several short sequences). It decodes its range's steps
    (tile, code, page offsets) into LDS first, then streams pages with three in flight under each step's
-   compute: K fragments HBM -> registers (`buffer_load_dwordx4`, four register sets), V rows HBM -> LDS
-   (`buffer_load_dwordx4 ... lds`, four stages); only a tile change drains the queue. Its four waves each
-   take a quarter of the query rows' width, so S = Q K^T is four partial products
-   (`v_mfma_f32_16x16x32_bf16`) summed through LDS behind an LDS-only barrier; every wave then runs the
-   softmax on the full scores and accumulates its quarter of `p @ V` (`v_mfma_f32_32x32x16_bf16`, V read
-   transposed with `ds_read_b64_tr_b16`). When a workgroup leaves a sequence it writes its partial (row
-   max, row sum, accumulator) to a workspace slot;
+   compute: K fragments HBM -> registers (`buffer_load_dwordx4`, three register sets), V rows HBM -> LDS
+   (`buffer_load_dwordx4 ... lds`, three stages); only a tile change drains the queue. Its eight waves each
+   take an eighth of the query rows' width, so S = Q K^T is eight partial products
+   (`v_mfma_f32_16x16x32_bf16`, in four chains) summed through LDS behind an LDS-only barrier; every wave
+   then runs the softmax on the full scores (rescaling only when a row's max grows by more than e^8) and
+   accumulates its eighth of `p @ V` (`v_mfma_f32_32x32x16_bf16`, V read transposed with
+   `ds_read_b64_tr_b16` as soon as the page has landed). When a workgroup leaves a sequence it writes its
+   partial (row max, row sum, accumulator) to a workspace slot;
 4. a merge kernel per sequence rescales and sums its partials (the online softmax's own merge rule:
    exact reassociation of the same sums) and evaluates the epilogue per output element.
 """
@@ -44,17 +45,18 @@ from ..schedule import CODE_SHIFT, Schedule
 from .common import Index, strides, tile_base
 from .device import PRELUDE
 from .expr import ElementEmitter, literal
-from .flash import Softmax, _is, _strip, softmax_structure
+from .flash import RESCALE_SLACK, Softmax, _is, _strip, softmax_structure
 from .protocol import Recorder
 from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 from .steps import attach_step_builder
 
 __all__ = ["DecodeMatch", "match", "lower"]
 
-THREADS = 256
-WAVES = 4
+WAVES = 8
+THREADS = 64 * WAVES
 RP = 32  # query rows the kernels work on: a spec's R <= 32 rows, the rest zero
 SUB = 16  # key positions per kernel step: a spec step of P positions (a page, a cache block) is P / SUB of them
+SP = SUB + 4  # floats per row of a wave's partial S in LDS (padded: rows 80 bytes apart)
 DEPTH = 3  # K register sets and V LDS stages (steps fetched ahead of the one computed): the default
 MAX_DEPTH = 4
 
@@ -130,7 +132,7 @@ class _Decode:
         self.grid = gfx950.CUS
         self.slots = self.grid + sch.pattern_tiles
         self.max_per = -(-sch.pattern_steps * self.sub // self.grid)  # most kernel steps one workgroup takes
-        self.lds = self.depth * SUB * m.width * 2 + WAVES * SUB * RP * 4 + 20 * self.max_per
+        self.lds = self.depth * SUB * m.width * 2 + WAVES * RP * SP * 4 + 20 * self.max_per
         # with a cursor the attention kernel evaluates the mask itself: a 64-block word per tile and word
         self.words = sch.pattern_tiles * -(-plan.phases[0].range.count // 64)
         if cursor:
@@ -289,7 +291,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
         w = L.append
         for s in range(D):  # one array per stage: the compiler then keeps the other stages' loads in flight
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sv{s}[{P * W}];")
-        w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{P}][{RP}];")
+        # each wave's partial S, row-major: a row's positions are contiguous (one 16-byte write per MFMA result
+        # and two 16-byte reads per lane), rows padded to SP floats so 16 lanes' rows fall in distinct banks
+        w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{RP}][{SP}];")
         w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][5];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
@@ -426,21 +430,32 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             o.extend(issue_v(f"j_ + {D - 1}", (u + D - 1) % D, ind + "  "))
             if record:
                 rec.at(u, lambda b, n, st=(u + D - 1) % D: ("load", st, b + D - 1, loads))
+                # V(j) is visible (its wait, then the barrier): its V^T fragments are read now, so the P V
+                # MFMAs after the softmax don't wait for LDS
+                rec.at(u, lambda b, n, st=u: ("read", st, b))
                 rec.at(u, lambda b, n, ku=u: ("read_own", ("k", ku), b))  # the S product reads kb{u}
             a(f"{ind}  const bool run = !(code & 4);")
-            # partial S^T over this wave's columns
+            a(f"{ind}  ak_bf16x8 vf[{dtiles}];")
+            # partial S^T over this wave's columns, in four MFMA chains (even and odd slabs apart)
             a(f"{ind}  if (run) {{")
-            a(f"{ind}    ak_f32x4 st[2] = {{ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}}};")
+            a(f"{ind}    const char* vs = (const char*)dc_sv{u};")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int dt = 0; dt < {dtiles}; ++dt) {{")
+            a(f"{ind}      const ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt]));")
+            a(f"{ind}      const ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt] + {4 * W * 2}));")
+            a(f"{ind}      vf[dt] = __builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));")
+            a(f"{ind}    }}")
+            a(f"{ind}    ak_f32x4 st[4] = {{ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}}};")
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int q = 0; q < {slabs}; ++q) {{")
-            a(f"{ind}      st[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb{u}[q], qf[0][q], st[0], 0, 0, 0);")
-            a(f"{ind}      st[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb{u}[q], qf[1][q], st[1], 0, 0, 0);")
+            a(f"{ind}      st[2 * (q & 1)] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb{u}[q], qf[0][q], st[2 * (q & 1)], 0, 0, 0);")
+            a(f"{ind}      st[2 * (q & 1) + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb{u}[q], qf[1][q], st[2 * (q & 1) + 1], 0, 0, 0);")
             a(f"{ind}    }}")
-            a(f"{ind}    #pragma unroll")
-            a(f"{ind}    for (int r = 0; r < 4; ++r) {{")
-            a(f"{ind}      dc_sp[wave][4 * (lane >> 4) + r][lane & 15] = st[0][r];")
-            a(f"{ind}      dc_sp[wave][4 * (lane >> 4) + r][16 + (lane & 15)] = st[1][r];")
-            a(f"{ind}    }}")
+            a(f"{ind}    st[0] += st[2];")
+            a(f"{ind}    st[1] += st[3];")
+            # st[h][r] is S^T at position 4 (lane / 16) + r, query row 16 h + lane % 16
+            a(f"{ind}    *(ak_f32x4*)&dc_sp[wave][lane & 15][4 * (lane >> 4)] = st[0];")
+            a(f"{ind}    *(ak_f32x4*)&dc_sp[wave][16 + (lane & 15)][4 * (lane >> 4)] = st[1];")
             a(f"{ind}  }}")
             # kb{u} has been read: refill it D steps ahead
             o.extend(issue_k(f"j_ + {D}", u, ind + "  "))
@@ -450,50 +465,56 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}    {self._decode_tile('t')}")
             a(f"{ind}    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step}; (void)lv_{jvar};")
             a(f"{ind}    const int su = __builtin_amdgcn_readfirstlane(dc_st[j_][4]); (void)su;")
-            a(f"{ind}    const char* vs = (const char*)dc_sv{u};")
             # an LDS-only barrier: the pages in flight stay in flight
             a(f"{ind}    AK_WAIT_LGKM0();")
             a(f'{ind}    asm volatile("s_barrier" ::: "memory");')
             if record:
                 rec.at(u, lambda b, n: ("wait_lgkm",))
                 rec.at(u, lambda b, n: ("barrier",))
-                rec.at(u, lambda b, n, st=u: ("read", st, b))
-                # the transposed reads feed this step's MFMAs: their results are waited for before those run
-                rec.at(u, lambda b, n: ("wait_lgkm",))
             # softmax: lane = query row er, positions 8 (lane / 32) + e
             # the lane's row; the mask sees rows past R (zero queries, never stored) as row R - 1
             a(f"{ind}    const int lr = lane & 31, er = {'lr' if m.rows == RP else f'ak_imin(lr, {m.rows - 1})'};")
             a(f"{ind}    float sc[8];")
+            a(f"{ind}    ak_f32x4 s_lo = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5)], s_hi = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5) + 4];")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int w_ = 1; w_ < {WAVES}; ++w_) {{")
+            a(f"{ind}      s_lo += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5)];")
+            a(f"{ind}      s_hi += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5) + 4];")
+            a(f"{ind}    }}")
             a(f"{ind}    float mx = -__builtin_inff();")
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int e = 0; e < 8; ++e) {{")
             a(f"{ind}      const int el = 8 * (lane >> 5) + e;  // the position in this kernel step")
             a(f"{ind}      const int ep = {P} * su + el;  // the position in the table step's block")
-            a(f"{ind}      const float sv = dc_sp[0][el][lr] + dc_sp[1][el][lr] + dc_sp[2][el][lr] + dc_sp[3][el][lr];")
+            a(f"{ind}      const float sv = e < 4 ? s_lo[e] : s_hi[e - 4];")
             a(f"{ind}      sc[e] = (float)({score});")
             a(f"{ind}      mx = fmaxf(mx, sc[e]);")
             a(f"{ind}    }}")
             a(f"{ind}    mx = fmaxf(mx, __shfl_xor(mx, 32));")
             a(f"{ind}    const float m_new = ak_maximum(m_run, mx);")
-            a(f"{ind}    const float alpha = ak_exp(m_run - m_new);")
+            # Lazy rescaling: the running max moves (and acc, l are rescaled) only when some row's new max
+            # exceeds it by more than RESCALE_SLACK; otherwise p = exp(s - m_run) stays below e^slack and
+            # acc, l keep one common scale, so acc / l is unchanged.
+            a(f"{ind}    if (__ballot(!(m_new <= m_run + {RESCALE_SLACK}f))) {{")
+            a(f"{ind}      const float alpha = ak_exp(m_run - m_new);")
+            a(f"{ind}      l_run *= alpha;")
+            a(f"{ind}      m_run = m_new;")
+            a(f"{ind}      #pragma unroll")
+            a(f"{ind}      for (int dt = 0; dt < {dtiles}; ++dt) acc[dt] *= alpha;")
+            a(f"{ind}    }}")
             a(f"{ind}    float ps = 0.f;")
             a(f"{ind}    unsigned pk[4];")
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int e = 0; e < 8; e += 2) {{")
-            a(f"{ind}      const float p0 = ak_exp(sc[e] - m_new), p1 = ak_exp(sc[e + 1] - m_new);")
+            a(f"{ind}      const float p0 = ak_exp(sc[e] - m_run), p1 = ak_exp(sc[e + 1] - m_run);")
             a(f"{ind}      ps += p0 + p1; pk[e >> 1] = ak_pack_bf16x2(p0, p1);")
             a(f"{ind}    }}")
             a(f"{ind}    ps += __shfl_xor(ps, 32);")
-            a(f"{ind}    l_run = alpha * l_run + ps;")
-            a(f"{ind}    m_run = m_new;")
+            a(f"{ind}    l_run += ps;")
             a(f"{ind}    const ak_bf16x8 pf = __builtin_bit_cast(ak_bf16x8, ak_u32x4{{pk[0], pk[1], pk[2], pk[3]}});")
             a(f"{ind}    #pragma unroll")
-            a(f"{ind}    for (int dt = 0; dt < {dtiles}; ++dt) {{")
-            a(f"{ind}      acc[dt] *= alpha;")
-            a(f"{ind}      ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt]));")
-            a(f"{ind}      ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt] + {4 * W * 2}));")
-            a(f"{ind}      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7)), pf, acc[dt], 0, 0, 0);")
-            a(f"{ind}    }}")
+            a(f"{ind}    for (int dt = 0; dt < {dtiles}; ++dt)")
+            a(f"{ind}      acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[dt], pf, acc[dt], 0, 0, 0);")
             a(f"{ind}  }}")
             a(f"{ind}}}")
             return o

@@ -60,6 +60,12 @@ def time_kernel(run, steps: int, warmup: int):
 
     from tilejax_amd import runtime
 
+    stream = runtime.current_stream()
+    events = [runtime.Event() for _ in range(steps + 1)]
+    # The spin kernel's module is loaded (on its first use in the process) before the warm-up: loaded between
+    # the warm-up and the timed calls, it left the GPU idle long enough for the clock to drop, and the first
+    # leg of a run measured about 10 % slower than the same kernel later (920 against 830-845 us).
+    runtime.spin(0.0, stream)
     start = time.perf_counter()
     while time.perf_counter() - start < WARM_S[0]:
         for _ in range(8):
@@ -68,8 +74,6 @@ def time_kernel(run, steps: int, warmup: int):
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
-    stream = runtime.current_stream()
-    events = [runtime.Event() for _ in range(steps + 1)]
     # A short spin kernel ahead of the start event: the host queues the first calls while it runs, so the
     # first timed call doesn't wait for its own launch (the timed region is still exactly the K calls).
     runtime.spin(2e-3, stream)

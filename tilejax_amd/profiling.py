@@ -115,6 +115,9 @@ def measure(lowered: Any, inputs: Sequence[Any], runs: int = 5) -> KernelProfile
 
     runtime.require_gpu()
     stream = runtime.current_stream()
+    # load the spin kernel (on its first use in the process) now: loaded between the warm-up and the timed
+    # calls, it leaves the GPU idle long enough for its clock to drop, and the first kernel timed runs slow
+    runtime.spin(0.0, stream)
     program = lowered.program
     workgroups = program.notes.get("trace_workgroups", 0) if lowered.trace else 0
     lowered.run(*inputs)

@@ -127,3 +127,44 @@ def test_the_f32_part_pairs_give_products_to_f32_accuracy():
     exact = a.double() * b.double()
     rel = ((got - exact).abs() / exact.abs()).max().item()
     assert rel < 8 * 2.0**-24, rel
+
+
+def test_attention_splits_only_the_longest_items():
+    """Split-KV: an item (128 query rows) is cut along the keys only above 1.5 shares of the work over the
+    512 resident workgroups. At (1, 16, 4096, 128) the 96 items of 54..64 key blocks are split in two (a
+    share is 35 blocks: 16896 blocks plus 2 per item, over 512); at (4, 16, 2048, 128) no item (at most 32
+    blocks) reaches 1.5 shares of 38. The tuner's knob moves the threshold: never, or above one share."""
+    from tilejax_amd.tune import Config
+    from tilejax_amd import Pipeline
+
+    blocks = AttentionBlocks(512, 512)
+    for shape, split, chunks in (((1, 16, 4096, 128), 96, 192), ((4, 16, 2048, 128), 0, 0)):
+        notes = causal_attention.lower(*(((shape), BF16) for _ in range(3)), blocks).program.notes
+        assert (notes["split_items"], notes["chunks"]) == (split, chunks), shape
+    sig = causal_attention.signature(*(((1, 16, 4096, 128), BF16) for _ in range(3)))
+    never = causal_attention.lowered(sig, Config(blocks, Pipeline(2, 2), False, (("split", 0),))).program
+    assert never.notes["split_items"] == 0 and "fa_merge" not in never.tables
+    one = causal_attention.lowered(sig, Config(blocks, Pipeline(2, 2), False, (("split", 10),))).program
+    # above one share: every item of 36 blocks or more, each cut into chunks of at most 35
+    assert one.notes["split_items"] == 16 * 15
+    items = one.tables["fa_items"].reshape(-1, 5 + 2 * one.notes["waves"])
+    assert items[:, 3].max() <= 35
+
+
+def test_causal_remainder_chunks_go_to_xcds_by_k_range():
+    """Causal 8192^3 at 512^3 tiles: 528 computed 256^2 tiles on 256 workgroups, so the last 16 are cut into
+    8 chunks of 16 K-slices. The chunks are handed out by K range, an XCD's 32 workgroups at a time
+    (workgroup w runs on XCD w % 8): XCD x takes chunks 2x and 2x + 1 of all 16 tiles, so it reads those
+    tiles' panels over two K ranges into its L2 once."""
+    from examples.causal_matmul import causal_matmul
+
+    prog = causal_matmul.lower(((8192, 8192), BF16), ((8192, 8192), BF16), MatmulTiles(512, 512, 512)).program
+    assert prog.notes["split"] == (16, 8, 16)
+    offsets, items = prog.tables["wg_items"], prog.tables["items"].reshape(-1, 3)
+    seen = {}
+    for w in range(len(offsets) - 1):
+        for t, code, slot in items[offsets[w]:offsets[w + 1]]:
+            if code >> 16 == 3:
+                seen.setdefault(w % 8, set()).add(int(slot) % 8)
+    assert seen == {x: {2 * x, 2 * x + 1} for x in range(4)}
+    assert sum(1 for _, code, _ in items if code >> 16 == 3) == 128

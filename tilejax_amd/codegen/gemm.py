@@ -655,8 +655,9 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             for ch in range(split):
                 out.append((t, (c & 0xFFFF) | (3 << 16), p * split + ch))
                 w_out.append(T / split + 1)
-                # chunks are ordered by K range, so each XCD takes every remainder tile's chunks over the same
-                # two (of 16) K ranges: the tiles' A and B panels over those ranges are read into its L2 once
+                # chunks are ordered by K range and equally loaded workgroups are taken an XCD at a time, so an
+                # XCD takes every remainder tile's chunks over the same K ranges (two of eight at 16 tiles): the
+                # tiles' A and B panels over those ranges are read into its L2 once
                 g_out.append(ch * gfx950.XCDS // split)
         return out, w_out, g_out
 

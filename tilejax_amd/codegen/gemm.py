@@ -367,15 +367,15 @@ class HwTile:
 
 def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str, int]] = None) -> HwTile:
     """The workgroup tile for a spec tile (tm, tn, tk): at most 256 x 256 outputs (`hardware` may cap each
-    side, "bm" and "bn"), computed by four waves (128 x 128 each at most) or, with "waves": 8, by eight (two
-    per SIMD, 128 x 64 each); K slices of 64 (32 if tk is an odd multiple of 64, 16 for tk = 32) so every
-    tile's slice count is even, and the LDS stages the pipeline asks for where they divide a step's slices
-    and fit in LDS."""
+    side, "bm" and "bn"), computed by eight waves (two per SIMD, 128 x 64 each) for a 256 x 256 tile and by
+    four (128 x 128 each at most) for a smaller one, unless "waves" says otherwise; K slices of 64 (32 if tk
+    is an odd multiple of 64, 16 for tk = 32) so every tile's slice count is even, and the LDS stages the
+    pipeline asks for where they divide a step's slices and fit in LDS."""
     hardware = hardware or {}
-    waves = hardware.get("waves", 4)
+    bm, bn = min(m.tm, hardware.get("bm", 256)), min(m.tn, hardware.get("bn", 256))
+    waves = hardware.get("waves", default_waves(bm, bn))
     if waves not in WAVE_GRIDS:
         raise KernelError(f"the gfx950 matmul lowering runs workgroups of 4 or 8 waves, not {waves}")
-    bm, bn = min(m.tm, hardware.get("bm", 256)), min(m.tn, hardware.get("bn", 256))
     if m.tm % bm or m.tn % bn or bm % 64 or bn % 64:
         raise KernelError(f"the gfx950 matmul lowering needs tiles that are multiples of 64 (got {m.tm} x {m.tn})")
     if m.tk % 64 and m.tk != 32:
@@ -418,10 +418,18 @@ def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: GemmMatch, name: str
     return _Gemm(plan, sch, pipeline, m, hw, name, trace).program()
 
 
+def default_waves(bm: int, bn: int) -> int:
+    """Waves per workgroup when the tuner doesn't say: eight for a 256 x 256 tile, four for a smaller one.
+    Measured at 8192^3 (bf16, 512^3 spec tiles), five runs each in alternating order on one box: dense 805-824
+    us with eight waves against 819-842 with four, causal 459-468 against 469-479; the grouped MoE GEMM of
+    16384 x 4096 x 14336 equal (1772 against 1766 us)."""
+    return 8 if (bm, bn) == (256, 256) else 4
+
+
 def hardware_choices(m: GemmMatch) -> List[Dict[str, int]]:
     """The workgroup tiles tuning may try for this match, as caps on each side (256 x 256 first, the
     default; then 256 x 128, 128 x 256 and 128 x 128 where the spec tile divides into them), each also with
-    eight waves per workgroup instead of four."""
+    the other number of waves per workgroup (four or eight) where the tile splits into them."""
     found, seen = [], set()
     for bm, bn in ((256, 256), (256, 128), (128, 256), (128, 128)):
         got = (min(m.tm, bm), min(m.tn, bn))
@@ -429,9 +437,14 @@ def hardware_choices(m: GemmMatch) -> List[Dict[str, int]]:
             continue
         seen.add(got)
         found.append({"bm": bm, "bn": bn})
-    # eight waves (two per SIMD) where the tile splits into them
-    found += [{**h, "waves": 8} for h in list(found) if min(m.tn, h["bn"]) % 128 == 0 and min(m.tm, h["bm"]) % 64 == 0]
-    return found
+    other = []
+    for h in found:
+        tile = (min(m.tm, h["bm"]), min(m.tn, h["bn"]))
+        waves = 12 - default_waves(*tile)  # the other of 4 and 8
+        wm, wn = WAVE_GRIDS[waves]
+        if tile[0] % (32 * wm) == 0 and tile[1] % (32 * wn) == 0:
+            other.append({**h, "waves": waves})
+    return found + other
 
 
 class _Gemm:

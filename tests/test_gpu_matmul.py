@@ -228,12 +228,15 @@ def test_causal_matmul_f32_operands():
     ((("bm", 128), ("bn", 256)), 2),
     ((("bm", 128), ("bn", 128)), 3),
     ((), 4),
-    ((("bm", 256), ("bn", 256), ("waves", 8)), 2),
+    ((("bm", 256), ("bn", 256), ("waves", 8)), 2),  # the default, spelled out
+    ((("bm", 256), ("bn", 256), ("waves", 4)), 2),
+    ((("bm", 256), ("bn", 256), ("waves", 4)), 4),
     ((("bm", 256), ("bn", 128), ("waves", 8)), 3),
     ((("bm", 128), ("bn", 128), ("waves", 8)), 2),
 ])
 def test_workgroup_tiles_the_tuner_tries(hardware, buffers):
-    """Each gfx950 workgroup tile and LDS ring depth the tuner may pick, dense and causal, against the oracle."""
+    """Each gfx950 workgroup tile, wave count and LDS ring depth the tuner may pick, dense and causal, against
+    the oracle."""
     from tilejax_amd import Pipeline
     from tilejax_amd.tune import Config
 

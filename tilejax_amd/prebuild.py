@@ -123,7 +123,8 @@ def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
     tiles = mm.MatmulTiles(512, 512, 512)
     for kernel in (mm.matmul, cm.causal_matmul):
         for hw, n in (((("bm", 256), ("bn", 128)), 2), ((("bm", 128), ("bn", 256)), 2), ((("bm", 128), ("bn", 128)), 3),
-                      ((), 4), ((("bm", 256), ("bn", 256), ("waves", 4)), 2), ((("bm", 256), ("bn", 128), ("waves", 8)), 3),
+                      ((), 4), ((("bm", 256), ("bn", 256), ("waves", 4)), 2), ((("bm", 256), ("bn", 256), ("waves", 4)), 4),
+                      ((("bm", 256), ("bn", 256), ("waves", 8)), 2), ((("bm", 256), ("bn", 128), ("waves", 8)), 3),
                       ((("bm", 128), ("bn", 128), ("waves", 8)), 2)):
             yield kernel, (_bf16(1024, 1024), _bf16(1024, 1024)), Config(tiles, Pipeline(n, 2), False, hw), False
     args = (_bf16(8192, 8192), _bf16(8192, 8192))

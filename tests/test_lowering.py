@@ -168,3 +168,15 @@ def test_causal_remainder_chunks_go_to_xcds_by_k_range():
                 seen.setdefault(w % 8, set()).add(int(slot) % 8)
     assert seen == {x: {2 * x, 2 * x + 1} for x in range(4)}
     assert sum(1 for _, code, _ in items if code >> 16 == 3) == 128
+
+
+def test_attention_stages_past_lds_are_refused_before_compiling():
+    """Three LDS stages of 128-key blocks at head dim 128 would take 192 KiB (gfx950 has 160 KiB per CU):
+    a KernelError on the host, so the tuner skips the shape, rather than a compiler error."""
+    from tilejax_amd import Pipeline
+    from tilejax_amd.tune import Config
+
+    sig = causal_attention.signature(*(((1, 2, 1024, 128), BF16) for _ in range(3)))
+    with pytest.raises(KernelError, match="LDS stages of 128 keys"):
+        causal_attention.lowered(sig, Config(AttentionBlocks(512, 512), Pipeline(3, 2), False,
+                                             (("bkv", 128), ("waves", 8)))).program

@@ -101,6 +101,8 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
             return decode.lower(plan, schedule, pipeline, found, name, trace=trace, cursor=cursor)
     except KernelError as e:
         family_error = e
+        if hardware:  # knobs of the family's kernel shape: that shape doesn't build, whatever else would
+            raise
     if cursor:
         raise family_error or KernelError(f"{plan.nest.name}: only the decode family finds its steps with a cursor")
     try:

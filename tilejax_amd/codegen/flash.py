@@ -305,6 +305,10 @@ class _Flash:
             raise KernelError(f"the split share is a number of tenths of a share, 0 or more (got {self.split_tenths})")
         if m.bk % self.bkv:
             raise KernelError(f"the gfx950 attention lowering needs key blocks of a multiple of {self.bkv} (got {m.bk})")
+        lds = self.stages * self.bkv * (m.d + m.dv) * 2
+        if lds > gfx950.LDS_BUDGET:
+            raise KernelError(f"{self.stages} LDS stages of {self.bkv} keys (head dims {m.d}, {m.dv}) take {lds} bytes of "
+                              f"LDS per workgroup; gfx950 has {gfx950.LDS_BUDGET}")
         if plan.runtime or sch.runtime:
             raise KernelError("attention with runtime masks is lowered by the decode path, not this one")
         self.jr = plan.phases[0].range

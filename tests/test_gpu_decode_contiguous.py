@@ -112,17 +112,20 @@ def test_contiguous_cursor_equals_step_tables():
     assert torch.equal(plain.run(*dev), cursor.run(*dev))
 
 
-@pytest.mark.parametrize("t, heads, kv_heads, block_kv", [(1, 8, 2, 128), (1, 4, 4, 256), (3, 8, 2, 128)])
+@pytest.mark.parametrize("t, heads, kv_heads, block_kv", [(1, 8, 2, 128), (1, 4, 4, 256), (3, 8, 2, 128),
+                                                          (1, 4, 1, 128), (1, 12, 3, 256)])
 def test_few_query_rows(t, heads, kv_heads, block_kv):
     """The reference's own cases (tests/test_decode.py:176-191): fewer than 32 query rows (t * heads), the
     kernels' rows past them zero; an empty sequence, one with just the new tokens, a partial block, a full
-    cache."""
+    cache. One and three KV heads (widths 128 and 384) take the decode kernel in four waves, the others in
+    eight."""
     g = torch.Generator().manual_seed(4)
     q = (torch.randn(4, t, heads, 128, generator=g) * 128**-0.5).to(torch.bfloat16)
     k = torch.randn(4, 512, kv_heads * 128, generator=g).to(torch.bfloat16)
     v = torch.randn(4, 512, kv_heads * 128, generator=g).to(torch.bfloat16)
     lengths = torch.tensor([0, t, 300, 512], dtype=torch.int32)
     print(f"contiguous decode t={t} heads={heads}/{kv_heads} block_kv={block_kv}", flush=True)
+    assert gqa_decode.lower(q, k, v, lengths, DecodeTiles(block_kv)).program.notes["family"] == "decode"
     got = gqa_decode(q.cuda(), k.cuda(), v.cuda(), lengths.cuda(), DecodeTiles(block_kv))
     torch.cuda.synchronize()
     what = f"contiguous decode t={t} heads={heads}/{kv_heads} block_kv={block_kv}"

@@ -122,9 +122,12 @@ class _Decode:
                  cursor: bool = False, depth: int = DEPTH) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
         self.trace, self.cursor, self.depth = trace, cursor, depth
-        if m.rows > RP or m.page % SUB or m.width % (32 * WAVES):
+        # eight waves where the width splits into them (an eighth each, a multiple of 32), else four
+        self.waves = WAVES if m.width % (32 * WAVES) == 0 else 4
+        self.threads = 64 * self.waves
+        if m.rows > RP or m.page % SUB or m.width % (32 * self.waves):
             raise KernelError(f"the gfx950 decode lowering takes up to {RP} query rows, pages (or cache blocks) of a multiple "
-                              f"of {SUB} positions and widths that are multiples of {32 * WAVES} "
+                              f"of {SUB} positions and widths that are multiples of {32 * self.waves} "
                               f"(got {m.rows}, {m.page}, {m.width})")
         self.sub = m.page // SUB  # kernel steps per spec step
         if sch.repeats != 1:
@@ -132,11 +135,11 @@ class _Decode:
         self.grid = gfx950.CUS
         self.slots = self.grid + sch.pattern_tiles
         self.max_per = -(-sch.pattern_steps * self.sub // self.grid)  # most kernel steps one workgroup takes
-        self.lds = self.depth * SUB * m.width * 2 + WAVES * RP * SP * 4 + 20 * self.max_per
+        self.lds = self.depth * SUB * m.width * 2 + self.waves * RP * SP * 4 + 20 * self.max_per
         # with a cursor the attention kernel evaluates the mask itself: a 64-block word per tile and word
         self.words = sch.pattern_tiles * -(-plan.phases[0].range.count // 64)
         if cursor:
-            self.lds += 8 * self.words + 4 * (sch.pattern_tiles + 1) + 4 * THREADS
+            self.lds += 8 * self.words + 4 * (sch.pattern_tiles + 1) + 4 * self.threads
         if self.lds > gfx950.LDS_BYTES:
             raise KernelError(f"decode over {sch.pattern_steps} pattern steps of {m.page} x {m.width} needs "
                               f"{self.lds} bytes of LDS per workgroup (gfx950 has {gfx950.LDS_BYTES})")
@@ -148,8 +151,8 @@ class _Decode:
         # The setup and merge kernels split each tile's elements over `chunks` workgroups (grid y), enough for
         # about four workgroups per CU over all tiles, each thread keeping at least one element.
         want = -(-4 * gfx950.CUS // sch.pattern_tiles)
-        self.setup_chunks = max(1, min(RP * m.width // THREADS, want))
-        self.merge_chunks = max(1, min(math.prod(m.out.tile.shape) // THREADS, want))
+        self.setup_chunks = max(1, min(RP * m.width // self.threads, want))
+        self.merge_chunks = max(1, min(math.prod(m.out.tile.shape) // self.threads, want))
 
     # -------------------------------------------------------------------------------- element emitters
 
@@ -220,9 +223,9 @@ class _Decode:
                             PRELUDE, struct, self._setup_source(), self._attention_source(), self._merge_source()])
         prog = Program(
             name=self.name, source=source,
-            launches=[Launch(f"{self.name}_setup", args, (sch.pattern_tiles, self.setup_chunks, 1), (THREADS, 1, 1), 0),
-                      Launch(self.name, args, (self.grid, 1, 1), (THREADS, 1, 1), 0),
-                      Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (THREADS, 1, 1), 0)],
+            launches=[Launch(f"{self.name}_setup", args, (sch.pattern_tiles, self.setup_chunks, 1), (self.threads, 1, 1), 0),
+                      Launch(self.name, args, (self.grid, 1, 1), (self.threads, 1, 1), 0),
+                      Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (self.threads, 1, 1), 0)],
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
             tables=tables, workspace=workspace, lds_bytes=self.lds, protocol=self.protocol,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
@@ -244,12 +247,12 @@ class _Decode:
         expr = em.at(m.q_node, ("qr", "qc"))
         return f"""
 // The tile's query rows, materialised once per tile (the setup code's value, per element); workgroup (t, y)\n// writes chunk y of tile t's elements.
-extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const {self.name}_args args) {{
+extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(const {self.name}_args args) {{
   const int t = blockIdx.x;
   {self._decode_tile("t")}
   ak_u16* dst = args.dc_q + (long long)t * {RP * W};
   const int e1 = ak_imin((int)(blockIdx.y + 1) * {-(-RP * W // self.setup_chunks)}, {RP * W});
-  for (int e = blockIdx.y * {-(-RP * W // self.setup_chunks)} + threadIdx.x; e < e1; e += {THREADS}) {{
+  for (int e = blockIdx.y * {-(-RP * W // self.setup_chunks)} + threadIdx.x; e < e1; e += {self.threads}) {{
     const int qr = e / {W}, qc = e % {W};
     dst[e] = qr < {R} ? (ak_u16)ak_bf16_bits((float)({expr})) : (ak_u16)0;  // rows past R are zero
   }}
@@ -260,10 +263,10 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
         plan, sch, m = self.plan, self.sch, self.m
         R, P, W = m.rows, SUB, m.width
         U = self.sub
-        WQ = W // WAVES  # a wave's share of the width
+        WQ = W // self.waves  # a wave's share of the width
         slabs = WQ // 32  # K = 32 slabs of S^T = K Q^T per wave
         dtiles = WQ // 32  # 32-wide tiles of acc^T per wave
-        loads = P * W // 8 // THREADS  # 16-byte V loads per thread per step
+        loads = P * W // 8 // self.threads  # 16-byte V loads per thread per step
         D = self.depth
         phase, index = self.phase, self.index
         radix = sch.phase_radix * sch.iterations
@@ -286,17 +289,16 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_setup(const 
 
         score = self._emitter(sleaf).at(m.sm.score, ("er", "ep"))
         chunks = W // 8
-        rows_per_load = THREADS // chunks
         L: List[str] = []
         w = L.append
         for s in range(D):  # one array per stage: the compiler then keeps the other stages' loads in flight
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 dc_sv{s}[{P * W}];")
         # each wave's partial S, row-major: a row's positions are contiguous (one 16-byte write per MFMA result
         # and two 16-byte reads per lane), rows padded to SP floats so 16 lanes' rows fall in distinct banks
-        w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{WAVES}][{RP}][{SP}];")
+        w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{self.waves}][{RP}][{SP}];")
         w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][5];")
         w(f"""
-extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.name}_args args) {{
+extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   {self._trace_start()}
@@ -307,7 +309,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
   if (n <= 0) {{ {self._trace_write("0")} return; }}
   // The range's steps, decoded once into LDS: tile, code, K and V page byte offsets. The loop then reads
   // them from LDS, so no global load other than the pages themselves sits in the vector memory queue.
-  for (int j = tid; j < n; j += {THREADS}) {{
+  for (int j = tid; j < n; j += {self.threads}) {{
     const int x = g0 + j, js = x / {U}, su = x - js * {U};  // the table's step, and the part of its block
     {self._cursor_step() if self.cursor else "const int t = args.rt_step_tile[js], code = args.rt_step_code[js];"}
     {self._decode_tile("t")}
@@ -324,12 +326,12 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
       (int)({math.prod(k_shape)}LL * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)args.{m.v.tile.array}, (short)0,
       (int)({math.prod(v_shape)}LL * 2), 0x00020000);
-  // V loads: LDS chunk position p = c * {THREADS} + tid: row p / {chunks}, chunk p % {chunks}, rows swizzled
+  // V loads: LDS chunk position p = c * {self.threads} + tid: row p / {chunks}, chunk p % {chunks}, rows swizzled
   // for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2).
   unsigned v_voff[{loads}];
 #pragma unroll
   for (int c = 0; c < {loads}; ++c) {{
-    const int row = c * {rows_per_load} + tid / {chunks}, ch = tid % {chunks};
+    const int p = c * {self.threads} + tid, row = p / {chunks}, ch = p % {chunks};
     v_voff[c] = (unsigned)(row * {ldv * 2} + ((ch ^ ((row & 3) << 2)) * 16));
   }}
   // K fragments (srcA of S^T, 16x16x32) straight from HBM into registers: position lane % 16, columns
@@ -400,7 +402,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             return [
                 f"{ind}{{ const int x_ = {x}; const unsigned ob_ = x_ < n ? 0u : 0x80000000u;",
                 f"{ind}  const int vo_ = __builtin_amdgcn_readfirstlane(dc_st[ak_imin(x_, n - 1)][3]);",
-                *(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, AK_LDS(&dc_sv{vs}[({c * THREADS} + wave * 64) * 8]), 16, "
+                *(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, AK_LDS(&dc_sv{vs}[({c * self.threads} + wave * 64) * 8]), 16, "
                   f"v_voff[{c}] + ob_, vo_, 0, 0);" for c in range(loads)),
                 f"{ind}}}",
             ]
@@ -477,7 +479,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
             a(f"{ind}    float sc[8];")
             a(f"{ind}    ak_f32x4 s_lo = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5)], s_hi = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5) + 4];")
             a(f"{ind}    #pragma unroll")
-            a(f"{ind}    for (int w_ = 1; w_ < {WAVES}; ++w_) {{")
+            a(f"{ind}    for (int w_ = 1; w_ < {self.waves}; ++w_) {{")
             a(f"{ind}      s_lo += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5)];")
             a(f"{ind}      s_hi += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5) + 4];")
             a(f"{ind}    }}")
@@ -551,19 +553,19 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
 
     def _cursor_scan(self) -> str:
         """With a cursor: the runtime mask of every (tile, block), a ballot per 64 blocks into LDS words (each
-        wave takes every WAVES-th tile, decoding its loop values once); each tile's kept count (a tile with
+        wave takes every `waves`-th tile, decoding its loop values once); each tile's kept count (a tile with
         no block running keeps one empty step, as the step tables do) and their exclusive scan, cs_start.
         Workgroup 0 writes the count and the tiles' first steps for the merge kernel."""
         plan, sch = self.plan, self.sch
         phase = plan.phases[0].range
         pt, count, nb = sch.pattern_tiles, phase.count, -(-phase.count // 64)
         mask = Index(plan, lambda v: f"lv_{v}").expr(phase.mask)
-        per_t = -(-pt // THREADS)
+        per_t = -(-pt // self.threads)
         return f"""__shared__ unsigned long long cs_run[{self.words}];
-  __shared__ int cs_start[{pt + 1}], cs_part[{THREADS}];
+  __shared__ int cs_start[{pt + 1}], cs_part[{self.threads}];
   // (unrolled so that several tiles' loop values and index reads are in flight at once)
 #pragma unroll 8
-  for (int t = wave; t < {pt}; t += {WAVES}) {{
+  for (int t = wave; t < {pt}; t += {self.waves}) {{
     {self._decode_tile("t")}
     for (int wi = 0; wi < {nb}; ++wi) {{
       const int kb = wi * 64 + lane;
@@ -588,7 +590,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     }}
     cs_part[tid] = mine;
     __syncthreads();
-    for (int d = 1; d < {THREADS}; d <<= 1) {{
+    for (int d = 1; d < {self.threads}; d <<= 1) {{
       const int add = tid >= d ? cs_part[tid - d] : 0;
       __syncthreads();
       cs_part[tid] += add;
@@ -596,10 +598,10 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
     }}
     int at = cs_part[tid] - mine;
     for (int t = t0; t < t1; ++t) {{ const int k = cs_start[t]; cs_start[t] = at; at += k; }}
-    if (tid == {THREADS - 1}) cs_start[{pt}] = cs_part[{THREADS - 1}];
+    if (tid == {self.threads - 1}) cs_start[{pt}] = cs_part[{self.threads - 1}];
     __syncthreads();
     if (blockIdx.x == 0) {{
-      for (int t = tid; t <= {pt}; t += {THREADS}) args.rt_tile_steps[t] = cs_start[t];
+      for (int t = tid; t <= {pt}; t += {self.threads}) args.rt_tile_steps[t] = cs_start[t];
       if (tid == 0) args.rt_count[0] = cs_start[{pt}];
     }}
   }}"""
@@ -672,7 +674,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}(const {self.
         chunk = -(-total // self.merge_chunks)
         return f"""
 // Merge a tile's partials (row max m, row sum l, accumulator) and write its output, per element; workgroup\n// (t, y) writes chunk y of tile t's elements, each computing the tile's partial weights.
-extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const {self.name}_args args) {{
+extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_merge(const {self.name}_args args) {{
   __shared__ float dc_w[{maxs}][{R}];
   __shared__ float dc_lsum[{R}];
   const int t = blockIdx.x;
@@ -683,7 +685,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
   const int w0 = ts / per, w1 = (te - 1) / per;
   const int n = w1 - w0 + 1;
   // The partials' loads go out four at a time (they are independent); the sums run in partial order.
-  for (int r = threadIdx.x; r < {R}; r += {THREADS}) {{
+  for (int r = threadIdx.x; r < {R}; r += {self.threads}) {{
     const float* mp = args.dc_m + (t + w0) * {RP} + r;
     const float* lp = args.dc_l + (t + w0) * {RP} + r;
     float mm = -__builtin_inff();
@@ -720,7 +722,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_merge(const 
   }};
   ak_u16* op = args.{m.out.name}_out + ({o_base});
   const int e1 = ak_imin((int)(blockIdx.y + 1) * {chunk}, {total});
-  for (int e = blockIdx.y * {chunk} + threadIdx.x; e < e1; e += {THREADS}) {{
+  for (int e = blockIdx.y * {chunk} + threadIdx.x; e < e1; e += {self.threads}) {{
     {" ".join(unravel)}
     op[{flat_out}] = (ak_u16)ak_bf16_bits((float)({expr}));
   }}

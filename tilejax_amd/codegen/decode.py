@@ -6,13 +6,13 @@ contiguous cache (:175-196): per output tile (one sequence) some setup code comp
 runtime mask (`p * P >= lengths[b]`, `j >= lengths[b]`) and reading each through a window (a runtime
 one, `k_pages[block_tables[b, p], :, :]`, or `k_cache[b, j : j + bk, :]`), runs the online softmax that
 `flash.softmax_structure` recognises, and the output is some epilogue of the accumulator and the row sum
-(`finish(own_blocks(acc))`). It computes exactly that, as four launches on one stream:
+(`finish(own_blocks(acc))`). It computes exactly that, as three launches on one stream:
 
 1. the device step-table builder (codegen/steps.py) evaluates the runtime mask: every sequence's pages in
-   order, compacted;
-2. a setup kernel materialises each tile's query rows (the setup code's value, per element) in a
-   workspace, so the attention kernel reads them as plain loads;
-3. the attention kernel works in kernel steps of SUB = 16 positions (a table step of P positions is P / 16
+   order, compacted; more workgroups of the same launch materialise each tile's query rows (the setup
+   code's value, per element) in a workspace, so the attention kernel reads them as plain loads (with a
+   cursor instead of tables, a setup launch of its own does);
+2. the attention kernel works in kernel steps of SUB = 16 positions (a table step of P positions is P / 16
    of them, in order) and splits the compacted list of them evenly over one workgroup per CU (a sequence's
    pages may span several workgroups, a workgroup several short sequences). It decodes its range's steps
    (tile, code, page offsets) into LDS first, then streams pages with three in flight under each step's
@@ -24,7 +24,7 @@ one, `k_pages[block_tables[b, p], :, :]`, or `k_cache[b, j : j + bk, :]`), runs 
    accumulates its eighth of `p @ V` (`v_mfma_f32_32x32x16_bf16`, V read transposed with
    `ds_read_b64_tr_b16` as soon as the page has landed). When a workgroup leaves a sequence it writes its
    partial (row max, row sum, accumulator) to a workspace slot;
-4. a merge kernel per sequence rescales and sums its partials (the online softmax's own merge rule:
+3. a merge kernel per sequence rescales and sums its partials (the online softmax's own merge rule:
    exact reassociation of the same sums) and evaluates the epilogue per output element.
 """
 
@@ -219,13 +219,19 @@ class _Decode:
             workspace[TRACE] = self.grid * TRACE_FIELDS * 8
             args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
         struct = c_struct(f"{self.name}_args", args)
+        # With step tables the query rows are set up by extra workgroups of the table builder's launch (they
+        # need no table); with a cursor, by a launch of their own.
         source = "\n".join([f"// Generated by tilejax_amd for `{plan.nest.name}`: gfx950 split-KV decode attention.",
-                            PRELUDE, struct, self._setup_source(), self._attention_source(), self._merge_source()])
+                            PRELUDE, struct, self._setup_source() if self.cursor else "", self._attention_source(),
+                            self._merge_source()])
+        launches = [Launch(self.name, args, (self.grid, 1, 1), (self.threads, 1, 1), 0),
+                    Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (self.threads, 1, 1), 0)]
+        if self.cursor:
+            launches.insert(0, Launch(f"{self.name}_setup", args, (sch.pattern_tiles, self.setup_chunks, 1),
+                                      (self.threads, 1, 1), 0))
         prog = Program(
             name=self.name, source=source,
-            launches=[Launch(f"{self.name}_setup", args, (sch.pattern_tiles, self.setup_chunks, 1), (self.threads, 1, 1), 0),
-                      Launch(self.name, args, (self.grid, 1, 1), (self.threads, 1, 1), 0),
-                      Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (self.threads, 1, 1), 0)],
+            launches=launches,
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
             tables=tables, workspace=workspace, lds_bytes=self.lds, protocol=self.protocol,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
@@ -234,28 +240,38 @@ class _Decode:
                    "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": self.sub},
         )
         if not self.cursor:
-            attach_step_builder(prog, plan, sch, self.name)
+            setup_args = [a for a in args if a.kind in ("input", "table") or a.key == "dc_q"]
+            attach_step_builder(prog, plan, sch, self.name,
+                                extra=self._setup_body(f"xb_ / {self.setup_chunks}", f"xb_ % {self.setup_chunks}"),
+                                extra_args=setup_args, extra_groups=sch.pattern_tiles * self.setup_chunks)
         return prog
 
     def _decode_tile(self, t: str) -> str:
         return " ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, {t});" for r in self.sch.inner)
 
-    def _setup_source(self) -> str:
+    def _setup_body(self, t: str, y: str) -> str:
+        """Chunk `y` of tile `t`'s query rows (the setup code's value, per element), by the workgroup's
+        threads."""
         m = self.m
         R, W = m.rows, m.width
         em = self._emitter(lambda n, idx: None)
         expr = em.at(m.q_node, ("qr", "qc"))
+        per = -(-RP * W // self.setup_chunks)
+        return f"""  {{ const int t = {t}, y_ = {y};
+    {self._decode_tile("t")}
+    ak_u16* dst = args.dc_q + (long long)t * {RP * W};
+    const int e1 = ak_imin((y_ + 1) * {per}, {RP * W});
+    for (int e = y_ * {per} + (int)threadIdx.x; e < e1; e += (int)blockDim.x) {{
+      const int qr = e / {W}, qc = e % {W};
+      dst[e] = qr < {R} ? (ak_u16)ak_bf16_bits((float)({expr})) : (ak_u16)0;  // rows past R are zero
+    }}
+  }}"""
+
+    def _setup_source(self) -> str:
         return f"""
-// The tile's query rows, materialised once per tile (the setup code's value, per element); workgroup (t, y)\n// writes chunk y of tile t's elements.
+// The tile's query rows, materialised once per tile; workgroup (t, y) writes chunk y of tile t's elements.
 extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(const {self.name}_args args) {{
-  const int t = blockIdx.x;
-  {self._decode_tile("t")}
-  ak_u16* dst = args.dc_q + (long long)t * {RP * W};
-  const int e1 = ak_imin((int)(blockIdx.y + 1) * {-(-RP * W // self.setup_chunks)}, {RP * W});
-  for (int e = blockIdx.y * {-(-RP * W // self.setup_chunks)} + threadIdx.x; e < e1; e += {self.threads}) {{
-    const int qr = e / {W}, qc = e % {W};
-    dst[e] = qr < {R} ? (ak_u16)ak_bf16_bits((float)({expr})) : (ak_u16)0;  // rows past R are zero
-  }}
+{self._setup_body("(int)blockIdx.x", "(int)blockIdx.y")}
 }}
 """
 

@@ -17,7 +17,7 @@ without a search.
 
 from __future__ import annotations
 
-from typing import List
+from typing import List, Sequence
 
 import numpy as np
 
@@ -33,7 +33,9 @@ MAX_TILES = 4096
 MAX_WORDS = 4096  # 64-block mask words kept in LDS (32 KiB)
 
 
-def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg]) -> str:
+def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg], extra: str = "") -> str:
+    """The builder kernel; `extra` is the owner kernel's code for the workgroups past the builder's own
+    (`xb_` numbers them from 0), which run beside it in the same launch."""
     if len(plan.phases) != 1:
         raise KernelError("runtime masks over more than one reduction loop are not lowered by the gfx950 backend yet")
     phase = plan.phases[0].range
@@ -64,7 +66,7 @@ def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg]) -> str
 // made once), two rounds' loads in flight together. Then per-tile kept counts, a block-wide scan of them,
 // and pass 2: each wave writes one word's entries at ballot-prefix positions, from the words alone.
 extern "C" __global__ void __launch_bounds__({THREADS}) {name}(const {name}_args args) {{
-  __shared__ unsigned long long run_w[{words}];
+{extra_blocks(extra, groups)}  __shared__ unsigned long long run_w[{words}];
   __shared__ int before_w[{words}], keep_n[{pt}], first_t[{pt}], last_t[{pt}], scan_k[{THREADS}];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -153,13 +155,23 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {name}(const {name}_args
 """
 
 
+def extra_blocks(extra: str, groups: int) -> str:
+    if not extra:
+        return ""
+    return (f"  if (blockIdx.x >= {groups}) {{  // the owner kernel's workgroups, beside the builder's\n"
+            f"    const int xb_ = blockIdx.x - {groups};\n{extra}\n    return;\n  }}\n")
+
+
 def builder_groups(words: int) -> int:
     """Workgroups of the builder: about 32 mask words (2048 table entries) each, at most 64."""
     return max(1, min(64, -(-words // 32)))
 
 
-def attach_step_builder(prog: Program, plan: Plan, sch: Schedule, kernel_name: str) -> None:
-    """Add the builder's launch (first, on the same stream), its tables and its workspace to `prog`."""
+def attach_step_builder(prog: Program, plan: Plan, sch: Schedule, kernel_name: str,
+                        extra: str = "", extra_args: Sequence[Arg] = (), extra_groups: int = 0) -> None:
+    """Add the builder's launch (first, on the same stream), its tables and its workspace to `prog`; with
+    `extra`, `extra_groups` more workgroups of the launch run that code (the owner kernel's own work that
+    needs no step table, so it needs no launch of its own), reading `extra_args` too."""
     name = f"{kernel_name}_steps"
     args: List[Arg] = []
     for ix in plan.indices:
@@ -172,7 +184,10 @@ def attach_step_builder(prog: Program, plan: Plan, sch: Schedule, kernel_name: s
     for ws, n in (("step_tile", capacity), ("step_code", capacity), ("count", 1), ("tile_steps", sch.pattern_tiles + 1)):
         prog.workspace[ws] = 4 * n
         args.append(Arg("workspace", ws, "int* __restrict__", f"rt_{ws}"))
-    prog.source += builder_source(plan, sch, name, args)
+    names = {a.name for a in args}
+    args += [a for a in extra_args if a.name not in names]
+    prog.source += builder_source(plan, sch, name, args, extra)
     words = sch.pattern_tiles * -(-plan.phases[0].range.count // 64)
-    prog.launches.insert(0, Launch(name, args, (builder_groups(words), 1, 1), (THREADS, 1, 1), 0))
+    groups = builder_groups(words) + (extra_groups if extra else 0)
+    prog.launches.insert(0, Launch(name, args, (groups, 1, 1), (THREADS, 1, 1), 0))
     prog.notes["step_builder"] = name

@@ -180,3 +180,27 @@ def test_attention_stages_past_lds_are_refused_before_compiling():
     with pytest.raises(KernelError, match="LDS stages of 128 keys"):
         causal_attention.lowered(sig, Config(AttentionBlocks(512, 512), Pipeline(3, 2), False,
                                              (("bkv", 128), ("waves", 8)))).program
+
+
+def test_decode_sets_up_query_rows_in_the_builders_launch():
+    """Decode with step tables takes three launches: the step-table builder, whose launch carries the
+    workgroups that set up each sequence's query rows, the attention kernel and the merge; with a cursor,
+    a setup launch takes the builder's place."""
+    from examples.decode import paged_gqa_decode
+    from tilejax_amd import Pipeline
+    from tilejax_amd.codegen.steps import builder_groups
+    from tilejax_amd.tune import Config
+
+    I32 = jaxlite.int32
+    sig = paged_gqa_decode.signature(((4, 1, 32, 128), BF16), ((256, 16, 1024), BF16), ((256, 16, 1024), BF16),
+                                     ((4, 64), I32), ((4,), I32))
+    tables = paged_gqa_decode.lowered(sig, paged_gqa_decode.default_config(sig)).program
+    symbols = [ln.symbol for ln in tables.launches]
+    assert symbols == ["tj_paged_gqa_decode_steps", "tj_paged_gqa_decode", "tj_paged_gqa_decode_merge"]
+    words = 4 * 1  # 4 sequences x one 64-block word of their 64 pages
+    assert tables.launches[0].grid[0] > builder_groups(words)  # the setup workgroups come after the builder's
+    assert "xb_" in tables.source and "_setup(" not in tables.source
+    base = paged_gqa_decode.default_config(sig)
+    cursor = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, True)).program
+    assert [ln.symbol for ln in cursor.launches] == ["tj_paged_gqa_decode_setup", "tj_paged_gqa_decode",
+                                                      "tj_paged_gqa_decode_merge"]

@@ -61,33 +61,32 @@ def causal_matmul(x: torch.Tensor, y: torch.Tensor, tm: int = 512, tn: int = 512
 
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, bq: int = 512, bk: int = 512) -> torch.Tensor:
     """examples/causal_attention.py:37-63: online softmax over key blocks not wholly in the future; scores
-    s = q @ k.T in f32, masked with -1e30 above the diagonal; p cast to bf16 before `p @ v` (f32 acc)."""
+    s = q @ k.T in f32, masked with -1e30 above the diagonal; p cast to bf16 before `p @ v` (f32 acc). The
+    (b, h) loops of the spec run as batch dims of each tile's products: every (b, h) is independent."""
     B, H, S, D = q.shape
     bq, bk = min(bq, S), min(bk, S)
     dtype = q.dtype
-    qf, kf, vf = _f32(q), _f32(k), _f32(v)
-    out = torch.zeros((B, H, S, D), dtype=dtype)
-    for b in range(B):
-        for h in range(H):
-            for i in range(0, S, bq):
-                row_max = torch.full((bq, 1), MASK_VALUE)
-                row_sum = torch.zeros((bq, 1))
-                acc = torch.zeros((bq, D))
-                for j in range(0, S, bk):
-                    if j > i + bq - 1:
-                        continue
-                    s = qf[b, h, i:i + bq] @ kf[b, h, j:j + bk].T
-                    rows = i + torch.arange(bq).reshape(-1, 1)
-                    cols = j + torch.arange(bk).reshape(1, -1)
-                    s = torch.where(cols <= rows, s, torch.tensor(MASK_VALUE))
-                    max_new = torch.maximum(row_max, s.max(dim=1, keepdim=True).values)
-                    p = torch.exp(s - max_new)
-                    alpha = torch.exp(row_max - max_new)
-                    row_sum = alpha * row_sum + p.sum(dim=1, keepdim=True)
-                    acc = alpha * acc + p.to(dtype).float() @ vf[b, h, j:j + bk]
-                    row_max = max_new
-                out[b, h, i:i + bq] = (acc / row_sum).to(dtype)
-    return out
+    qf, kf, vf = (_f32(t).reshape(B * H, S, D) for t in (q, k, v))
+    out = torch.zeros((B * H, S, D), dtype=dtype)
+    for i in range(0, S, bq):
+        row_max = torch.full((B * H, bq, 1), MASK_VALUE)
+        row_sum = torch.zeros((B * H, bq, 1))
+        acc = torch.zeros((B * H, bq, D))
+        rows = i + torch.arange(bq).reshape(-1, 1)
+        for j in range(0, S, bk):
+            if j > i + bq - 1:
+                continue
+            s = qf[:, i:i + bq] @ kf[:, j:j + bk].transpose(1, 2).contiguous()
+            cols = j + torch.arange(bk).reshape(1, -1)
+            s = torch.where(cols <= rows, s, torch.tensor(MASK_VALUE))
+            max_new = torch.maximum(row_max, s.max(dim=2, keepdim=True).values)
+            p = torch.exp(s - max_new)
+            alpha = torch.exp(row_max - max_new)
+            row_sum = alpha * row_sum + p.sum(dim=2, keepdim=True)
+            acc = alpha * acc + p.to(dtype).float() @ vf[:, j:j + bk]
+            row_max = max_new
+        out[:, i:i + bq] = (acc / row_sum).to(dtype)
+    return out.reshape(B, H, S, D)
 
 
 def attention_float64(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> np.ndarray:
@@ -178,7 +177,8 @@ def paged_gqa_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tens
     positions `visible` gives (decode.py:92-99: < lengths[b] for one new token; with T of them, token t sits
     at lengths[b] - T + t and sees the positions up to it), pages read through block_tables[b, p]
     (clamped) while p * P < lengths[b]; scores in f32, p rounded to bf16 before `p @ v`, one online-softmax
-    step per page; empty sequences give zeros."""
+    step per page; empty sequences give zeros. Each query row's softmax is its own: the heads of one kv
+    group, and the groups, run as batch rows of each page's products."""
     B, T, H, Dh = q.shape
     P, W = k_pages.shape[1], k_pages.shape[2]
     Hkv = W // Dh
@@ -194,23 +194,24 @@ def paged_gqa_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tens
         if not pages:
             continue
         for t in range(T):
-            for h in range(H):
-                g = h // group
-                row_max = torch.tensor(MASK_VALUE)
-                row_sum = torch.tensor(0.0)
-                acc = torch.zeros(Dh)
-                for n, page in enumerate(pages):
-                    s = (kf[page].reshape(P, Hkv, Dh)[:, g] @ qf[b, t, h])
-                    pos = n * P + torch.arange(P)
-                    ok = pos < L if T == 1 else pos <= L - T + t
-                    s = torch.where(ok, s, torch.tensor(MASK_VALUE))
-                    m_new = torch.maximum(row_max, s.max())
-                    p = torch.exp(s - m_new)
-                    alpha = torch.exp(row_max - m_new)
-                    row_sum = alpha * row_sum + p.sum()
-                    acc = alpha * acc + p.to(q.dtype).float() @ vf[page].reshape(P, Hkv, Dh)[:, g]
-                    row_max = m_new
-                out[b, t, h] = (acc / torch.clamp(row_sum, min=1e-30)).to(q.dtype)
+            qq = qf[b, t].reshape(Hkv, group, Dh)
+            row_max = torch.full((Hkv, group, 1), MASK_VALUE)
+            row_sum = torch.zeros((Hkv, group, 1))
+            acc = torch.zeros((Hkv, group, Dh))
+            for n, page in enumerate(pages):
+                kk = kf[page].reshape(P, Hkv, Dh).permute(1, 2, 0).contiguous()  # (Hkv, Dh, P)
+                vv = vf[page].reshape(P, Hkv, Dh).permute(1, 0, 2).contiguous()  # (Hkv, P, Dh)
+                s = qq @ kk
+                pos = n * P + torch.arange(P)
+                ok = pos < L if T == 1 else pos <= L - T + t
+                s = torch.where(ok, s, torch.tensor(MASK_VALUE))
+                m_new = torch.maximum(row_max, s.max(dim=2, keepdim=True).values)
+                p = torch.exp(s - m_new)
+                alpha = torch.exp(row_max - m_new)
+                row_sum = alpha * row_sum + p.sum(dim=2, keepdim=True)
+                acc = alpha * acc + p.to(q.dtype).float() @ vv
+                row_max = m_new
+            out[b, t] = (acc / torch.clamp(row_sum, min=1e-30)).reshape(H, Dh).to(q.dtype)
     return out
 
 

@@ -1,6 +1,6 @@
 """Parity of the generated gfx950 flash-attention kernels with the CPU oracle (oracle/kernels.py, the spec's
-loop nest with f32 accumulation) on the same seeded inputs, and at BASELINE.json config 3's shapes with a float32 torch
-reference on the GPU (the attention kernel is floating point).
+loop nest with f32 accumulation) on the same seeded inputs, at every size including BASELINE.json config 3's
+shapes, and there also with a float32 torch reference on the GPU.
 
 Tolerance (tests/tolerance.py): bf16 outputs within 2 bf16 ulp of the expected value plus a floor of
 (2^-8 + 2 S 2^-24 + 2 e_s) times softmax(s) @ |v|: the kernel and the oracle differ in f32 summation order
@@ -15,7 +15,7 @@ import torch
 
 from examples.causal_attention import AttentionBlocks, causal_attention
 from oracle import kernels
-from tests.tolerance import check_bf16, score_err, softmax_floor
+from tests.tolerance import SOFTMAX_BAR, check_bf16, score_err, softmax_floor
 
 pytestmark = pytest.mark.gpu
 
@@ -73,15 +73,20 @@ def _reference_f32(q, k, v):
                                          ((1, 16, 4096, 128), 256), ((1, 16, 4096, 128), 1024)])
 def test_causal_attention_baseline_shapes(shape, block):
     """both shapes at every block shape it lists (256^2, 512^2, 1024^2), every output
-    against a float32 softmax on the GPU."""
-    q, k, v = (t.cuda() for t in _inputs(*shape, seed=7))
+    against the CPU oracle at the same blocks (the spec's loop nest, which rounds p to bf16 as the spec does),
+    to the softmax bar (tests/tolerance.py: SOFTMAX_BAR), and against a float32 softmax on the GPU with p
+    unrounded, to the floor."""
+    q, k, v = _inputs(*shape, seed=7)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     blocks = AttentionBlocks(block, block)
     print(f"attention {shape} {blocks}", flush=True)
-    got = causal_attention(q, k, v, blocks)
-    want = _reference_f32(q, k, v)
-    floor = softmax_floor(_reference_f32(q, k, v.abs()), shape[2], score_err(q, k))
+    got = causal_attention(qd, kd, vd, blocks)
+    want = _reference_f32(qd, kd, vd)
+    floor = softmax_floor(_reference_f32(qd, kd, vd.abs()), shape[2], score_err(q, k))
     torch.cuda.synchronize()
     check_bf16(f"attention {shape} {blocks} vs f32", got, want, floor)
+    oracle = kernels.causal_attention(q, k, v, block, block)
+    check_bf16(f"attention {shape} {blocks} vs oracle", got.cpu(), oracle, floor.cpu(), **SOFTMAX_BAR)
 
 
 def test_verify_against_the_spec_reference():

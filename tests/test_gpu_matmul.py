@@ -13,7 +13,7 @@ import torch
 from examples.causal_matmul import causal_matmul
 from examples.matmul import MatmulTiles, matmul
 from oracle import kernels
-from tests.tolerance import check_bf16, matmul_floor
+from tests.tolerance import MATMUL_BAR, check_bf16, matmul_floor
 
 pytestmark = pytest.mark.gpu
 
@@ -26,9 +26,10 @@ def _inputs(m, k, n, seed=0):
     return x, y
 
 
-def _close(got, want, x, y, what="matmul"):
-    """2 bf16 ulp of the oracle plus the f32 summation floor of x @ y."""
-    check_bf16(what, got.cpu(), want.cpu(), matmul_floor(x.cpu(), y.cpu()))
+def _close(got, want, x, y, what="matmul", bar=None):
+    """2 bf16 ulp of the oracle plus the f32 summation floor of x @ y; with `bar` (the BASELINE sizes), also
+    the 2-ulp bar the floor leaves open (tests/tolerance.py: MATMUL_BAR)."""
+    check_bf16(what, got.cpu(), want.cpu(), matmul_floor(x.cpu(), y.cpu()), **(bar or {}))
 
 
 @pytest.mark.parametrize("m,k,n,tiles", [
@@ -75,7 +76,7 @@ def test_causal_matmul_full_size_balanced_split():
     got = lowered.run(x.cuda(), y.cuda())
     torch.cuda.synchronize()
     want = kernels.causal_matmul(x, y, tiles.tm, tiles.tn, tiles.tk)
-    _close(got, want, x, y, "causal")
+    _close(got, want, x, y, "causal", MATMUL_BAR)
     assert not got.cpu().float().triu(1).any()
 
 
@@ -95,7 +96,8 @@ def _f32_product_on_gpu(x, y):
 def test_dense_headline_full_output(tiles):
     """BASELINE.json config 2, the benchmark's headline: dense x @ y at 8192^3 (seeds 0 and 1, as bench.py
     draws them). Every output against a float32 product on the GPU rounded to bf16, within 2 bf16 ulp plus
-    the f32 summation floor; then a band of 512 rows against the CPU oracle's own loop nest."""
+    the f32 summation floor, and with every typical output within 2 ulp and 99.99 % of all within 2 ulp with no
+    floor; then a band of 512 rows against the CPU oracle's own loop nest, to the same bar."""
     n = 8192
     x, y = _inputs(n, n, n, seed=0)
     xd, yd = x.cuda(), y.cuda()
@@ -104,10 +106,10 @@ def test_dense_headline_full_output(tiles):
     got = lowered.run(xd, yd)
     want, floor = _f32_product_on_gpu(xd, yd)
     torch.cuda.synchronize()
-    check_bf16(f"dense {n}^3 {tiles} vs f32 product", got, want.to(torch.bfloat16), floor)
+    check_bf16(f"dense {n}^3 {tiles} vs f32 product", got, want.to(torch.bfloat16), floor, **MATMUL_BAR)
     del want, floor
     band = kernels.matmul(x[:512], y, 512, 512, 512)
-    _close(got[:512], band, x[:512], y, f"dense {n}^3 {tiles} rows 0..511 vs oracle")
+    _close(got[:512], band, x[:512], y, f"dense {n}^3 {tiles} rows 0..511 vs oracle", MATMUL_BAR)
 
 
 def test_causal_headline_1024x2048x1024():
@@ -121,7 +123,7 @@ def test_causal_headline_1024x2048x1024():
     got = lowered.run(x.cuda(), y.cuda())
     torch.cuda.synchronize()
     want = kernels.causal_matmul(x, y, tiles.tm, tiles.tn, tiles.tk)
-    _close(got, want, x, y, "causal 1024x2048x1024")
+    _close(got, want, x, y, "causal 1024x2048x1024", MATMUL_BAR)
     assert not got.cpu().float().triu(1).any()
 
 

@@ -16,7 +16,7 @@ import torch
 import tilejax_amd
 from tests.helpers import make_kernel, rand
 from tests.test_walk import (FFN_STACK, GATHER, LAYERED, MASKED_IN_PLACE, MOE, NESTED, OFFSETS, ONCE_PER_TILE,
-                             RAGGED, SCAN, SCATTER, SPANS, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, PICKED, EARLY, CHOSEN,
+                             RAGGED, SCAN, SCATTER, SPANS, WRAPPED, wrapped_float64, STATIC_RAGGED, SUMS, TWO_REPEATS, COUNTED, PICKED, EARLY, CHOSEN,
                              MIXED_MASKS, ONE_LAYER_STEPS, RUNTIME_IN_REPEAT, chosen_float64, chosen_inputs,
                              ONLY_IN_PLACE, RAGGED_BOTH, PAIRS_PER_ITERATION, only_in_place_float64,
                              ragged_both_float64, pairs_per_iteration_float64,
@@ -102,6 +102,15 @@ def test_scatter_into_an_input_updated_in_place():
     close(out, want_out, 0, 0)  # (x2: exact)
     close(new, want_new, 1e-6, 0)
     assert torch.equal(new[[1, 3, 4, 6]], pool[[1, 3, 4, 6]])  # the slots no tile stores, as they were
+
+
+def test_negative_indices_and_stores_outside_the_array():
+    """Slots (-1, 7, 2): the pool's last row, a dropped update (past the 7 rows), row 2; shift[b - 1] at b = 0
+    reads shift's last element; the row index -2 counts from the end. Exact (x2 plus one value)."""
+    x, pool, slots, shift = rand((3, 16, 128)), rand((7, 16, 128), 1), i32(-1, 7, 2), i32(4, -2, 5)
+    new = run(make_kernel(WRAPPED), x, pool, slots, shift, what="negative indices")
+    close(new, wrapped_float64(x, pool, slots, shift), 1e-6, 0)
+    assert torch.equal(new[[0, 1, 3, 4, 5]], pool[[0, 1, 3, 4, 5]])
 
 
 def test_masked_tiles_of_an_input_updated_in_place_keep_its_values():

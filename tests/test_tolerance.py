@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle import kernels
-from tests.tolerance import bf16_ulp, check_bf16, matmul_floor, score_err, softmax_floor
+from tests.tolerance import MATMUL_BAR, SOFTMAX_BAR, bf16_ulp, check_bf16, matmul_floor, score_err, softmax_floor
 
 
 def test_bf16_ulp_is_the_spacing_of_bf16_values():
@@ -54,6 +54,24 @@ def test_matmul_floor_is_not_loose_enough_to_hide_a_1_percent_error():
         check_bf16("scaled", (want.float() * 1.01).to(torch.bfloat16), want, matmul_floor(x, y))
 
 
+def test_strict_bar_catches_a_1_percent_error_at_k_8192():
+    """At K = 8192 (BASELINE config 2's depth) the worst-case floor alone admits a 1 % scale error on every
+    output; the 2-ulp bar on typical outputs and the 99.99 % share within 2 ulp do not. A correct evaluation
+    in another summation order passes all three."""
+    x, y = _mm(64, 8192, 128, 5)
+    want = kernels.matmul(x, y, 64, 128, 512)
+    floor = matmul_floor(x, y)
+    scaled = (want.float() * 1.01).to(torch.bfloat16)
+    check_bf16("1 % scaled, floor only", scaled, want, floor)  # the floor by itself is this loose
+    with pytest.raises(AssertionError, match="typical size"):
+        check_bf16("1 % scaled", scaled, want, floor, **MATMUL_BAR)
+    with pytest.raises(AssertionError, match="within 2 bf16 ulp"):
+        check_bf16("1 % scaled", scaled, want, floor, min_within=MATMUL_BAR["min_within"])
+    other = (x.double() @ y.double()).to(torch.bfloat16)
+    report = check_bf16("K 8192 vs float64", other, want, floor, **MATMUL_BAR)
+    assert report["ulp_max_typical"] <= 1.0
+
+
 def _attn(seed, S=256):
     gens = [torch.Generator().manual_seed(seed + i) for i in range(3)]
     q, k, v = (torch.randn(1, 2, S, 128, generator=g).to(torch.bfloat16) for g in gens)
@@ -69,6 +87,19 @@ def test_attention_other_blocking_passes():
     check_bf16("attention blockings", a, b, softmax_floor(weighted, 256, score_err(q, k)))
     check_bf16("attention vs float64", a, kernels.attention_float64(q, k, v),
                softmax_floor(weighted, 256, score_err(q, k)))
+    check_bf16("attention blockings, 2-ulp bar", a, b, softmax_floor(weighted, 256, score_err(q, k)),
+               **SOFTMAX_BAR)
+
+
+def test_softmax_bar_catches_a_1_percent_error():
+    """The softmax bar (typical outputs within 2 ulp) fails a 1 % scale error the floor alone admits."""
+    q, k, v = _attn(2, S=512)
+    want = kernels.causal_attention(q, k, v, 128, 128)
+    weighted = torch.as_tensor(kernels.attention_float64(q, k, v.float().abs()))
+    floor = softmax_floor(weighted, 512, score_err(q, k))
+    scaled = (want.float() * 1.01).to(torch.bfloat16)
+    with pytest.raises(AssertionError):
+        check_bf16("attention 1 % scaled", scaled, want, floor, **SOFTMAX_BAR)
 
 
 def test_attention_off_by_one_mask_fails():

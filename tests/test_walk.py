@@ -426,6 +426,47 @@ def scatter_float64(x, pool, slots):
     return out, new
 
 
+WRAPPED = """
+def wrapped(x, pool, slots, shift):
+    B, H, D = x.shape
+    new = pool
+    for b in range(B):
+        for h in range(0, H, 8):
+            new = new.at[slots[b], h : h + 8, :].set(x[b, h : h + 8, :] * 2 + pool[shift[b - 1], h : h + 8, :])
+    return new
+"""
+
+
+def wrapped_float64(x, pool, slots, shift):
+    """JAX's integer indices: a negative one counts from the end (a read at shift[-1] takes the last element,
+    a row index -2 the second to last), and an update at a row still outside the pool is dropped."""
+    pool, x = f64(pool), f64(x)
+    new = pool.copy()
+    slots, shift = np.asarray(slots), np.asarray(shift)
+    n = pool.shape[0]
+    for b in range(x.shape[0]):
+        row = int(shift[b - 1])  # numpy counts b - 1 = -1 from the end too
+        row = min(max(row + n if row < 0 else row, 0), n - 1)
+        s = int(slots[b])
+        s = s + n if s < 0 else s
+        if 0 <= s < n:
+            new[s] = 2 * x[b] + pool[row]
+    return new
+
+
+def test_negative_indices_count_from_the_end_and_stores_outside_are_dropped():
+    """The reference's `kernel.fn` semantics for integer indices the tile reads at run time: slots (-1, 7, 2)
+    store into the pool's last row, nowhere (7 is past the 7 rows), and row 2; shift[b - 1] at b = 0 reads
+    shift's last element, and the row index -2 read from it takes the pool's second to last row."""
+    kernel = make_kernel(WRAPPED)
+    x, pool, slots, shift = rand((3, 16, 128)), rand((7, 16, 128), 1), i32(-1, 7, 2), i32(4, -2, 5)
+    got = kernel.reference(x, pool, slots, shift)
+    want = wrapped_float64(x, pool, slots, shift)
+    close(got, want, 1e-6, 0)
+    assert np.array_equal(want[[0, 1, 3, 4, 5]], f64(pool)[[0, 1, 3, 4, 5]])
+    compiles(kernel.lower(x, pool, slots, shift))
+
+
 MASKED_IN_PLACE = """
 def masked_in_place(x):
     out = jnp.zeros((256, 256))
@@ -464,6 +505,24 @@ def scan_float64(x, w):
             out[i : i + 128, j : j + 128] = state
     last = np.concatenate([out[-128:-120, j : j + 128] for j in range(0, x.shape[1], 128)], 1)
     return out, last
+
+
+def test_random_index_arrays_that_place_stores_hold_distinct_values():
+    """The reference's tests/test_in_place.py:163-172: tuning draws an index array that places stores from 0
+    to the last slot of the dim it places (6 here, where the loops go to 16), without repeats, so no two
+    tiles store into one window; an array too long for that many distinct values still stays in bounds."""
+    from tilejax_amd.tune import _index_bounds, random_inputs
+
+    kernel = make_kernel(SCATTER)
+    signature = kernel.signature(rand((3, 16, 128)), rand((7, 16, 128), 1), i32(0, 1, 2))
+    bounds, distinct = _index_bounds(kernel, signature, kernel.default_config(signature))
+    assert bounds == {2: 6} and distinct == {2}
+    for seed in range(5):
+        slots = random_inputs(signature, bounds, seed, distinct, device="cpu")[2]
+        assert slots.dtype == torch.int32 and len(set(slots.tolist())) == 3
+        assert int(slots.min()) >= 0 and int(slots.max()) <= 6
+    many = random_inputs((((8,), jaxlite.int32),), {0: 3}, distinct=frozenset({0}), device="cpu")[0]
+    assert many.shape == (8,) and int(many.min()) >= 0 and int(many.max()) <= 3
 
 
 def test_scatter_into_an_input_updated_in_place():

@@ -15,6 +15,23 @@ from tilejax_amd.tune import Config
 pytestmark = pytest.mark.gpu
 
 
+def _allocator_counts():
+    """torch's caching allocator's counters for the current device: allocations made so far, and bytes
+    reserved from the device."""
+    stats = torch.cuda.memory_stats()
+    return stats.get("allocation.all.allocated", 0), stats.get("reserved_bytes.all.current", 0)
+
+
+def _run_without_allocating(program, ins, out):
+    """program.run_no_alloc, asserting that torch's allocator saw no allocation and reserved nothing more
+    during the call (the kernel's tables were uploaded by the ordinary call before)."""
+    torch.cuda.synchronize()
+    before = _allocator_counts()
+    program.run_no_alloc(*ins, outputs=[out])
+    torch.cuda.synchronize()
+    assert _allocator_counts() == before, (before, _allocator_counts())
+
+
 def _decode_inputs(B, pages, lengths, seed):
     g = torch.Generator().manual_seed(seed)
     q = (torch.randn(B, 1, 32, 128, generator=g) * 128 ** -0.5).to(torch.bfloat16)
@@ -37,8 +54,7 @@ def test_decode_without_allocating(cursor):
         print(f"no-alloc decode B={B} cursor={cursor} workspace {sum(program.workspace.values())} bytes", flush=True)
         want = lowered.run(*ins)
         out = torch.full_like(want, float("nan"))
-        program.run_no_alloc(*ins, outputs=[out])
-        torch.cuda.synchronize()
+        _run_without_allocating(program, ins, out)
         assert torch.equal(out, want)
 
 
@@ -53,8 +69,7 @@ def test_causal_split_without_allocating():
         print(f"no-alloc causal {n} {tiles} workspace {lowered.program.workspace}", flush=True)
         want = lowered.run(x, y)
         out = torch.full_like(want, float("nan"))
-        lowered.program.run_no_alloc(x, y, outputs=[out])
-        torch.cuda.synchronize()
+        _run_without_allocating(lowered.program, (x, y), out)
         assert torch.equal(out, want)
 
 

@@ -18,6 +18,28 @@ is a bound on d, derived per kind of computation:
 Every check also reports how close it came: the largest error in bf16 ulps over outputs of at least
 typical size (|want| >= rms(want)), the share of all outputs within 2 ulp with no floor at all, and the
 largest |got - want| / bound (<= 1 passes).
+
+The floor is a worst-case bound, and at large K it is loose: at K = 8192 with N(0, 1) operands it is about
+5 against 2 ulp of about 1 for a typical output of 90, so a scale error of a few percent would pass it.
+The checks of the BASELINE configurations therefore
+also assert the 2-ulp bar directly, on what the floor leaves open:
+- matmul family (`MATMUL_BAR`): every output of typical size within 2 ulp (`typical_ulps`), and at least
+  99.99 % of all outputs within 2 ulp with no floor at all (`min_within`);
+- softmax kernels (`SOFTMAX_BAR`), against the oracle that rounds p as the spec does: at least 99.95 % of the
+  outputs of typical size within 2 ulp (`typical_within`), none beyond 4, and at least 85 % of all outputs
+  within 2 ulp with no floor. The kernel rounds each p to bf16 against its own running maximum (attention
+  rescales per 64-key block and lazily; decode splits a sequence over workgroups, each starting its own
+  maximum), the spec against its block's, so the two round each p independently: an output's two
+  evaluations then differ by a sum of independent roundings, about 2^-9 * sqrt(2/3) of the output's own
+  spread in standard deviation, plus each side's final rounding. Over the 8.4 million outputs of an
+  attention config (0.99998 of the typical ones within 2 ulp, the largest 3) and the 262 thousand of the
+  decode config (0.99983, the largest 4) the tail of that sum passes 2 ulp for a few; outputs much smaller
+  than the weighted |v| average (cancellation) differ by more than 2 of their own ulps, which is what the
+  floor admits.
+
+Two bf16 ulp is about 1 % (2^-7 to 2^-8 relative), so a 1 % scale error still leaves most outputs within 2
+ulp once both sides are rounded to bf16: what tells it apart is the share within 2 ulp (about 98 % of the
+outputs of typical size for a 1 % error, against at least 99.98 % for the kernels), which the bars assert.
 """
 
 from __future__ import annotations
@@ -29,6 +51,8 @@ import torch
 U32 = 2.0 ** -24  # f32 unit roundoff
 P_ROUND = 2.0 ** -8  # two bf16 roundings of one value (each within 2^-9 relative) are within this of each other
 ULPS = 2.0
+MATMUL_BAR = {"typical_ulps": 2.0, "min_within": 0.9999}
+SOFTMAX_BAR = {"typical_ulps": 4.0, "typical_within": 0.9995, "min_within": 0.85}
 
 
 def bf16_ulp(w: torch.Tensor) -> torch.Tensor:
@@ -39,10 +63,14 @@ def bf16_ulp(w: torch.Tensor) -> torch.Tensor:
 
 
 def check_bf16(what: str, got: Any, want: Any, floor: Any = 0.0, ulps: float = ULPS,
-               chunk_rows: int = 1024) -> Dict[str, float]:
+               chunk_rows: int = 1024, typical_ulps: Optional[float] = None,
+               min_within: Optional[float] = None, typical_within: Optional[float] = None) -> Dict[str, float]:
     """Assert |got - want| <= ulps * ulp_bf16(want) + floor elementwise (floor: a tensor broadcastable to want,
-    or a number); return the report (see the module docstring). Works on the tensors' own device, a block of
-    rows at a time."""
+    or a number); return the report (see the module docstring). With `typical_ulps`, also assert that every
+    output of typical size (|want| >= rms(want)) is within that many ulps with no floor; with `typical_within`,
+    that at least that share of the outputs of typical size is within 2 ulp with no floor; with `min_within`,
+    that at least that share of all outputs is within 2 ulp with no floor. Works on the tensors' own device,
+    a block of rows at a time."""
     want = torch.as_tensor(want)
     got = torch.as_tensor(got).to(want.device)
     if got.shape != want.shape:
@@ -56,6 +84,7 @@ def check_bf16(what: str, got: Any, want: Any, floor: Any = 0.0, ulps: float = U
     sq = sum(float((w2[i:i + chunk_rows].double() ** 2).sum()) for i in range(0, w2.shape[0], chunk_rows))
     rms = (sq / max(w2.numel(), 1)) ** 0.5
     bad, within, ulp_max, ratio_max, err_max = 0, 0, 0.0, 0.0, 0.0
+    n_typical, n_typical_within = 0, 0
     first_bad: Optional[str] = None
     for i in range(0, w2.shape[0], chunk_rows):
         g = g2[i:i + chunk_rows].double()
@@ -77,14 +106,25 @@ def check_bf16(what: str, got: Any, want: Any, floor: Any = 0.0, ulps: float = U
         typical = w.abs() >= rms
         if typical.any():
             ulp_max = max(ulp_max, float((err / ulp)[typical].max()))
+            n_typical += int(typical.sum())
+            n_typical_within += int(((err <= ULPS * ulp) & typical).sum())
         ratio_max = max(ratio_max, float((err / bound).max()))
         err_max = max(err_max, float(err.max()))
     report = {"ulp_max_typical": round(ulp_max, 3), "within_2ulp": round(within / max(w2.numel(), 1), 6),
+              "typical_within_2ulp": round(n_typical_within / max(n_typical, 1), 7),
               "bound_use": round(ratio_max, 4), "max_abs_err": err_max}
     print(f"{what}: {report}", flush=True)
     if bad:
         raise AssertionError(f"{what}: {bad} of {w2.numel()} outputs beyond {ulps} bf16 ulp + floor; "
                              f"largest |diff| {err_max:.4g}; {first_bad}")
+    if typical_ulps is not None and ulp_max > typical_ulps:
+        raise AssertionError(f"{what}: an output of typical size is {ulp_max:.3g} bf16 ulp off (bar {typical_ulps})")
+    if typical_within is not None and report["typical_within_2ulp"] < typical_within:
+        raise AssertionError(f"{what}: {report['typical_within_2ulp']:.7f} of the outputs of typical size within "
+                             f"2 bf16 ulp (bar {typical_within})")
+    if min_within is not None and report["within_2ulp"] < min_within:
+        raise AssertionError(f"{what}: {report['within_2ulp']:.6f} of the outputs within 2 bf16 ulp "
+                             f"(bar {min_within})")
     return report
 
 

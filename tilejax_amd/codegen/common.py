@@ -61,12 +61,13 @@ class Index:
 
 def tile_base(tile: Tile, shape: Sequence[int], index: Index, loop_value: Callable[[str], str]) -> Tuple[str, List[int]]:
     """The flat offset (C) of a tile's first element given the loop values, and the strides of its sliced
-    dims. A runtime window index is clamped into its dim (as JAX clamps out-of-range indices)."""
+    dims. A runtime window index counts from the end when negative and is clamped into its dim, as JAX
+    reads."""
     terms = []
     sliced = []
     for w, dim, stride in zip(tile.windows, shape, strides(shape)):
         if w.index is not None:
-            terms.append(f"(long long)ak_clamp({index.read(w.index)}, 0, {dim - 1}) * {stride}")
+            terms.append(f"(long long)ak_index({index.read(w.index)}, {dim}) * {stride}")
         else:
             off = str(w.offset) if w.offset else ""
             if w.loop is not None:

@@ -33,6 +33,10 @@ AK_INLINE int ak_imin(int a, int b) { return a < b ? a : b; }
 template <typename T> AK_INLINE T ak_ldc(const T* p, long long i) { return ((const __attribute__((address_space(4))) T*)p)[i]; }
 AK_INLINE int ak_imax(int a, int b) { return a > b ? a : b; }
 AK_INLINE int ak_clamp(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+// An integer index into a dim of n as JAX takes it: a negative one counts from the end (ak_wrap); a read
+// then clamps it into the dim (ak_index), where an update out of the dim is dropped.
+AK_INLINE int ak_wrap(int v, int n) { return v < 0 ? v + n : v; }
+AK_INLINE int ak_index(int v, int n) { return ak_clamp(ak_wrap(v, n), 0, n - 1); }
 
 // bf16 <-> f32. Rounding is to nearest, ties to even (gfx950's v_cvt_pk_bf16_f32); NaN stays NaN.
 typedef __bf16 ak_bf16x2 __attribute__((ext_vector_type(2)));

@@ -404,6 +404,8 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
 # causal 8192^3 at 512^3 tiles: 484.8-487.7 us with the queue, 479.1-483.7 us without (the queue narrows the
 # workgroups' spread, but its pulls and the later stores cost more than that gains); with the last round in
 # 8 chunks per tile, 480.5-483.3 against 475.9-482.8 us.
+# With it on, the queue's heads are per program and device (Program.state): calls of one queued program
+# must not overlap on two streams.
 QUEUE_TAIL = [False]
 # The last round's K-split: at most MAX_SPLIT chunks per tile. Its chunks run at the kernel's end, when their
 # reads, f32 partials and the filled tiles' stores share HBM, and the fixup reads the partials again: causal

@@ -209,7 +209,7 @@ class _Elements(ElementEmitter):
             for k, d in enumerate(src.shape):
                 sel = key[k] if k < len(key) else slice(None)
                 if isinstance(sel, Node):
-                    inner.append(f"ak_clamp((int)({self._at(sel, ())}), 0, {d - 1})")
+                    inner.append(f"ak_index((int)({self._at(sel, ())}), {d})")
                 elif isinstance(sel, slice):
                     start, _, step = sel.indices(d)
                     inner.append(f"({start} + ({idx[k_out]}) * {step})")
@@ -274,7 +274,7 @@ class _Generic:
         terms, k = [], 0
         for w, dim, stride in zip(op.tile.windows, shape, strides(shape)):
             if w.index is not None:
-                base = f"ak_clamp({self.index.read(w.index)}, 0, {dim - 1})"
+                base = f"ak_index({self.index.read(w.index)}, {dim})"
             else:
                 base = f"(lv_{w.loop} + {w.offset})" if w.loop else str(w.offset)
             if w.size is not None:
@@ -311,7 +311,7 @@ class _Generic:
             if n.op == "index":  # an index-array element, clamped into the array as JAX clamps
                 ix = plan.index(n.kwargs["array"])
                 parts = [em.at(i, ()) if isinstance(i, Node) else literal(i) for i in n.args]
-                flat = " + ".join(f"ak_clamp((int)({p}), 0, {d - 1}) * {s}"
+                flat = " + ".join(f"ak_index((int)({p}), {d}) * {s}"
                                   for p, s, d in zip(parts, strides(ix.shape), ix.shape)) or "0"
                 return f"args.{ix.name}[{flat}]"
             if n.op in _WHOLE:
@@ -841,7 +841,7 @@ class _Walk(_Generic):
         dims = list(sub.slice.elts) if isinstance(sub.slice, ast.Tuple) else [sub.slice]
         if len(dims) != len(shape) or any(isinstance(d, ast.Slice) for d in dims):
             raise KernelError(f"`{ast.unparse(sub)}`: index every dim of `{name}` with an integer")
-        flat = " + ".join(f"ak_clamp({self._int(d)}, 0, {n - 1}) * {st}"
+        flat = " + ".join(f"ak_index({self._int(d)}, {n}) * {st}"
                           for d, n, st in zip(dims, shape, strides(shape))) or "0"
         return f"{ref}[{flat}]"
 
@@ -863,25 +863,32 @@ class _Walk(_Generic):
         terms = []
         for d, n, st in zip(dims, shape, strides(shape)):
             at = f"({self._int(d.lower)} + ({e}))" if isinstance(d, ast.Slice) else self._int(d)  # type: ignore[arg-type]
-            terms.append(f"ak_clamp({at}, 0, {n - 1}) * {st}")
+            terms.append(f"ak_index({at}, {n}) * {st}")
         return f"{ref}[{' + '.join(terms)}]"
 
     def _coords(self, acc: Any, shape: Sequence[int], idx: Tuple[str, ...], store: bool
                 ) -> Tuple[str, List[str]]:
         """The flat element address of `acc` at tile index `idx`, and the conditions a store writes under
-        (rows before `stop`; gathered elements inside the dim: JAX drops updates out of the array)."""
+        (rows before `stop`; gathered elements and element indices inside the dim once a negative one counts
+        from the end: JAX drops updates out of the array). Reads clamp into the dim instead."""
         terms, conds, k = [], [], 0
         for d, dim, stride in zip(acc.dims, shape, strides(shape)):
             if d.gather is not None:
                 g = self._gather(d.gather, idx[k], dim)
                 k += 1
                 if store:
-                    conds.append(f"(unsigned)({g}) < {dim}u")
-                    coord = g
+                    coord = f"ak_wrap({g}, {dim})"
+                    conds.append(f"(unsigned)({coord}) < {dim}u")
                 else:
-                    coord = f"ak_clamp({g}, 0, {dim - 1})"
+                    coord = f"ak_index({g}, {dim})"
             elif d.size is None:
-                coord = self._int(d.start) if isinstance(d.start, int) else f"ak_clamp({self._int(d.start)}, 0, {dim - 1})"
+                if isinstance(d.start, int):
+                    coord = self._int(d.start)
+                elif store:  # an update at an index out of the dim is dropped
+                    coord = f"ak_wrap({self._int(d.start)}, {dim})"
+                    conds.append(f"(unsigned)({coord}) < {dim}u")
+                else:
+                    coord = f"ak_index({self._int(d.start)}, {dim})"
             elif d.stop is not None:
                 at = f"({self._int(d.start)} + ({idx[k]}))"
                 k += 1

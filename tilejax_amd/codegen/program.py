@@ -57,7 +57,10 @@ class Program:
     tables: Dict[str, np.ndarray] = field(default_factory=dict)
     workspace: Dict[str, int] = field(default_factory=dict)  # name -> bytes (uninitialised: launches write before reading)
     # name -> int32 count: counters kept on the device from call to call, zero when made (once per device);
-    # a kernel that uses one leaves it zero again when it ends (the work queues' heads)
+    # a kernel that uses one leaves it zero again when it ends (the work queues' heads). One set per program
+    # and device, shared by every call: two calls of a program with state must not overlap (on two streams
+    # of one device), or each takes the other's items; nothing here checks that. No standard lowering has
+    # state: the matmul family's queued tail (gemm.QUEUE_TAIL) is off, since it measured slower.
     state: Dict[str, int] = field(default_factory=dict)
     lds_bytes: int = 0
     notes: Dict[str, Any] = field(default_factory=dict)  # what the lowering chose (hardware tiles, ...)

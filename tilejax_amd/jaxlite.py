@@ -559,12 +559,23 @@ def _clamped(index: Any, shape: Tuple[int, ...]) -> Any:
 
 
 def _set(target: torch.Tensor, index: Any, value: Any) -> None:
-    """`target[index] = value` as JAX updates: out-of-range integer indices are clamped, except the entries
-    of one integer index array (a gathered or ragged window), whose updates out of the array are dropped."""
+    """`target[index] = value` as JAX updates: a negative integer index counts from the end, and an update
+    at an index still out of its dim is dropped, for a single integer index (a whole update) as for the
+    entries of one integer index array (a gathered or ragged window)."""
     idx = index if isinstance(index, tuple) else (index,)
     v = value.to(target.dtype) if isinstance(value, torch.Tensor) else value
-    arrays = [k for k, i in enumerate(idx) if isinstance(i, torch.Tensor) and i.dtype != torch.bool]
     plain = all(i is not None and i is not Ellipsis for i in idx)
+    if plain and target.device.type != "meta":
+        for k, i in enumerate(idx):
+            scalar = isinstance(i, int) and not isinstance(i, bool)
+            scalar = scalar or (isinstance(i, torch.Tensor) and i.ndim == 0 and i.dtype != torch.bool
+                                and not i.dtype.is_floating_point and i.device.type != "meta")
+            if scalar and k < target.ndim:
+                n = target.shape[k]
+                at = int(i)
+                if not -n <= at < n:
+                    return  # the update falls outside the array: JAX drops it
+    arrays = [k for k, i in enumerate(idx) if isinstance(i, torch.Tensor) and i.dtype != torch.bool and i.ndim > 0]
     if len(arrays) == 1 and plain and idx[arrays[0]].ndim == 1 and target.device.type != "meta":
         k = arrays[0]
         n = target.shape[k]

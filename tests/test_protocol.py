@@ -17,7 +17,7 @@ from examples.matmul import MatmulTiles, matmul
 from examples.moe import GroupTiles, grouped_matmul
 from tests.helpers import spec
 from tilejax_amd import Pipeline, jaxlite
-from tilejax_amd.codegen.protocol import ProtocolError, check, loads_reads
+from tilejax_amd.codegen.protocol import ItemRecorder, ProtocolError, check, loads_reads
 from tilejax_amd.tune import Config
 
 BF, F32, I32 = jaxlite.bfloat16, jaxlite.float32, jaxlite.int32
@@ -41,15 +41,42 @@ def _matmul_cases():
 
 @pytest.mark.parametrize("name,lowered", list(_matmul_cases()), ids=lambda x: x if isinstance(x, str) else "")
 def test_matmul_ring(name, lowered):
+    """A workgroup's items back to back: the next loading item's first slices go into the stages during the
+    current item's last ones; items without slices (a tile without steps) load nothing in between."""
     prog = lowered.program
     rec, stages = prog.protocol, prog.notes["stages"]
+    assert isinstance(rec, ItemRecorder)
     covered = set()
     for rounds in (1, 2, 3, 5):
         T = rounds * stages  # slices per item: the kernel's loop takes whole rounds of its stages
-        events = rec.replay(T) + rec.replay(T) + rec.replay(2 * T)  # items back to back
-        check(events, name)
-        covered |= loads_reads(events)
+        for counts in ([T], [T, T, 2 * T], [T, 0, T], [0, T, 0, 0, 3 * T], [2 * T, T, 0]):
+            events = rec.replay(counts)
+            check(events, f"{name}, items of {counts} slices")
+            covered |= loads_reads(events)
+            assert events[-1] == ("wait_vm", 0)  # nothing in flight when the workgroup ends
     assert covered == {(k, s) for k in ("load", "read") for s in range(stages)}
+
+
+def test_matmul_items_prefetch_the_next():
+    """The second item's first slices are loaded during the first item (no load at its start), and a
+    dropped barrier at an item's start, or a dropped refill barrier, fails the check."""
+    sq = (spec(1024, 1024, dtype=BF), spec(1024, 1024, dtype=BF))
+    rec = _lowered(matmul, sq, MatmulTiles(512, 512, 512)).program.protocol
+    events = rec.replay([4, 4])
+    loads = [i for i, ev in enumerate(events) if ev[0] == "load"]
+    second_first = [i for i, ev in enumerate(events) if ev[0] == "load" and ev[2] == 4]
+    first_read_of_second = next(i for i, ev in enumerate(events) if ev[0] == "read" and ev[2] == 4)
+    assert second_first and second_first[0] < first_read_of_second
+    assert len(loads) == 2 + 4 + 4  # the first item's fill, then one refill per slice, no second fill
+    check(events, "two items")
+    barriers = [i for i, ev in enumerate(events) if ev[0] == "barrier"]
+    # the first item's fill barrier guards its first read; each refill barrier (followed by a load into the
+    # stage just read) guards that load, the next item's included
+    needed = [1] + [k + 1 for k, i in enumerate(barriers) if events[i + 1][0] == "load"]
+    assert len(needed) == 1 + 8
+    for k in needed:
+        with pytest.raises(ProtocolError):
+            check(_drop(events, "barrier", k), f"without barrier {k}")
 
 
 def _flash_cases():
@@ -101,7 +128,7 @@ def _loosen(events, which=2):
 
 def test_planted_mistakes_fail():
     sq = (spec(1024, 1024, dtype=BF), spec(1024, 1024, dtype=BF))
-    mm = _lowered(matmul, sq, MatmulTiles(512, 512, 512)).program.protocol.replay(8)
+    mm = _lowered(matmul, sq, MatmulTiles(512, 512, 512)).program.protocol.replay([8, 8])
     fa = _lowered(causal_attention, tuple(spec(2, 4, 1024, 128, dtype=BF) for _ in range(3)),
                   AttentionBlocks(256, 256)).program.protocol.replay(6)
     args = (spec(5, 1, 32, 128, dtype=BF), spec(500, 16, 1024, dtype=BF), spec(500, 16, 1024, dtype=BF),

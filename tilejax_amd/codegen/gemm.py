@@ -39,7 +39,7 @@ from .common import Index, decode_fill, decode_tile, static_tile_steps, strides,
 from .device import PRELUDE
 from .expr import ElementEmitter, Emitter, Interval, ctype, intervals, literal, nodes_between
 from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
-from .protocol import Recorder
+from .protocol import ItemRecorder, Recorder
 
 __all__ = ["GemmMatch", "match", "lower"]
 
@@ -1100,9 +1100,43 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             loop_head = "  for (int q = q_begin; q < q_end; ++q) {"
             tail = ""
         self._queue_tail = tail
+        # Without the shared queue a workgroup knows its whole list: the next item that loads gets its first S
+        # slices issued in place of this item's last S slices' refills, so its fill overlaps this item's last
+        # slices and epilogue (`cross`). With the queue, each item fills its stages itself.
+        cross = self.cross = not self.n_small
+        sb_cur = "sbeg" if sch.step_tables else "0"
+        a_off_expr = f"({a_base}) + (long long)(sm * {bm}) * {lda}"
+        b_off_expr = f"({b_base}) + (long long)(sn * {bn}) * {ldb}" if nt else f"({b_base}) + sn * {bn}"
+        probe = ""
+        if cross:
+            probe = f"""
+  // Slice g of an item whose K slices start at g0 (T of them; past the last, the last again), its K offset.
+  auto k_at = [&](int g0, int T, int sbeg, int g) -> int {{
+    const int gg = g0 + (g < T ? g : (T > 0 ? T - 1 : 0));
+    const int st_ = gg / {kslices};
+    return {kval} + (gg % {kslices}) * {bk};
+  }};
+  // Item q2's loads: its slices and operand offsets; false if it loads nothing (a filled or constant tile,
+  // or one without steps).
+  auto probe = [&](int q2, int& T_, int& g0_, int& sb_, long long& aoff_, long long& boff_) -> bool {{
+    const int t = args.items[3 * q2], code = args.items[3 * q2 + 1], slot = args.items[3 * q2 + 2];
+    const int sub = code & 0xffff, kind = code >> 16;
+    (void)slot;
+    if (kind == 1 || kind == 2) return false;
+    const int sm = sub / {self.sub_n}, sn = sub % {self.sub_n};
+    {tile_decode}
+    {setup}
+    int T = nsteps * {kslices}, g0 = 0;
+    if (kind == 3) {{ g0 = (slot % {split}) * {split_slices}; T = {split_slices}; }}
+    T_ = T; g0_ = g0; sb_ = {sb_cur};
+    aoff_ = {a_off_expr};
+    boff_ = {b_off_expr};
+    return T > 0;
+  }};
+  int pf_q = -1;  // the item whose first {S} slices are in flight"""
         w(f"""  const int q_begin = args.wg_items[blockIdx.x], q_end = args.wg_items[blockIdx.x + 1];
   {"__shared__ int ak_pulled;" if self.n_small else ""}
-  {trace_decl}
+  {trace_decl}{probe}
 {loop_head}
 {pull}
     const int sub = code & 0xffff, kind = code >> 16;
@@ -1119,15 +1153,24 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
     int g0 = 0;  // the first K slice (a chunk of a tile cut along the reduction starts later)
     if (kind == 3) {{ g0 = (slot % {split}) * {split_slices}; T = {split_slices}; }}
     asm volatile("" : "+s"(T));  // an opaque trip count: a known one makes the compiler spill in the loop
-    const long long a_off = ({a_base}) + (long long)(sm * {bm}) * {lda};""")
-        if nt:
-            w(f"    const long long b_off = ({b_base}) + (long long)(sn * {bn}) * {ldb};")
-        else:
-            w(f"    const long long b_off = ({b_base}) + sn * {bn};")
-        w(f"""    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)({A} + a_off), (short)0,
+    const long long a_off = {a_off_expr};
+    const long long b_off = {b_off_expr};
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)({A} + a_off), (short)0,
         (int)({a_numel}LL * 2 - a_off * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc((void*)({B} + b_off), (short)0,
-        (int)({b_numel}LL * 2 - b_off * 2), 0x00020000);
+        (int)({b_numel}LL * 2 - b_off * 2), 0x00020000);""")
+        if cross:
+            w(f"""    // the next item in this workgroup's list that loads (its first slices are issued during this item's last)
+    int nx_q = q_end, nx_T = 0, nx_g0 = 0, nx_sb = 0;
+    long long nx_aoff = 0, nx_boff = 0;
+    for (int q2 = q + 1; q2 < q_end; ++q2)
+      if (probe(q2, nx_T, nx_g0, nx_sb, nx_aoff, nx_boff)) {{ nx_q = q2; break; }}
+    const __amdgpu_buffer_rsrc_t nx_rsa = __builtin_amdgcn_make_buffer_rsrc((void*)({A} + nx_aoff), (short)0,
+        (int)({a_numel}LL * 2 - nx_aoff * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t nx_rsb = __builtin_amdgcn_make_buffer_rsrc((void*)({B} + nx_boff), (short)0,
+        (int)({b_numel}LL * 2 - nx_boff * 2), 0x00020000);
+    const int sb = {sb_cur};""")
+        w(f"""
     // A tile's chunks are summed by the fixup kernel: only the first starts from the initial value.
     const float acc_init = (kind == 3 && g0 != 0) ? 0.0f : {literal(m.init)};
     ak_f32x16 acc[{mi}][{ni}];
@@ -1137,26 +1180,35 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
       for (int j_ = 0; j_ < {ni}; ++j_)
 #pragma unroll
         for (int r_ = 0; r_ < 16; ++r_) acc[i_][j_][r_] = acc_init;
-    ak_bf16x8 fa[2][{mi}], fb[2][{ni}];
-    // Slice g's loads into stage s: the slice's step and K offset (slices past the tile's last reload it).
+    ak_bf16x8 fa[2][{mi}], fb[2][{ni}];""")
+        if not cross:
+            w(f"""    // Slice g's loads into stage s: the slice's step and K offset (slices past the tile's last reload it).
     auto k_of = [&](int g) -> int {{
       const int gg = g0 + (g < T ? g : (T > 0 ? T - 1 : 0));
       const int st_ = gg / {kslices};
       return {kval} + (gg % {kslices}) * {bk};
     }};""")
 
-        def issue(g: str, s: int, ind: str) -> List[str]:
-            out = [f"{ind}{{ const int k0 = k_of({g});"]
+        def issue(g: str, s: int, ind: str, refill: bool = False) -> List[str]:
+            if cross and refill:  # past this item's last slice, the next loading item's first ones
+                # the inputs are selected, then one k_at: no branch splits the MFMA stream here
+                out = [f"{ind}{{ const int gi = {g}; const bool nxt = gi >= T && nx_q < q_end;",
+                       f"{ind}  const int k0 = k_at(nxt ? nx_g0 : g0, nxt ? nx_T : T, nxt ? nx_sb : sb, nxt ? gi - T : gi);",
+                       f"{ind}  const __amdgpu_buffer_rsrc_t ra = nxt ? nx_rsa : rsa, rb = nxt ? nx_rsb : rsb;"]
+            elif cross:
+                out = [f"{ind}{{ const int k0 = k_at(g0, T, sb, {g}); const __amdgpu_buffer_rsrc_t ra = rsa, rb = rsb;"]
+            else:
+                out = [f"{ind}{{ const int k0 = k_of({g}); const __amdgpu_buffer_rsrc_t ra = rsa, rb = rsb;"]
             rows_a = T // kca
             for c in range(a_ld):
-                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, AK_LDS(&ak_sa{s}[({c * T} + wave * 64) * 8]), "
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, AK_LDS(&ak_sa{s}[({c * T} + wave * 64) * 8]), "
                            f"16, a_voff, {c * rows_a}u * pa + (unsigned)k0 * 2u, 0, 0);")
             for c in range(b_ld):
                 if nt:
                     soff = f"{c * rows_a}u * pb + (unsigned)k0 * 2u"
                 else:
                     soff = f"(unsigned)(k0 + {c * (T // nc)}) * pb"
-                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, AK_LDS(&ak_sb{s}[({c * T} + wave * 64) * 8]), "
+                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, AK_LDS(&ak_sb{s}[({c * T} + wave * 64) * 8]), "
                            f"16, b_voff, {soff}, 0, 0);")
             out.append(f"{ind}}}")
             return out
@@ -1194,22 +1246,41 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                     v -= 1
             return out
 
-        ind = "    "
-        # the LDS events of one item's slices, as emitted (`protocol.check` replays items back to back)
-        rec = self.protocol = Recorder()
-        if self.trace:
-            w(f"{ind}const unsigned long long tr_i0 = {now}; tr_slices += T;")
-        for s in range(S):
-            L.extend(issue(str(s), s, ind))
-            rec.add(("load", s, s, per_slice))
+        # The LDS events of an item's slices, as emitted: `protocol.check` replays items back to back. In the
+        # cross-item form (ItemRecorder) block ids are global: gid(k) is the item's k-th slice, then the next
+        # loading item's, or the item's last slice reloaded where none follows.
+        if cross:
+            rec = self.protocol = ItemRecorder()
+            ind = "      "
+            w(f"    if (T > 0) {{  // (an item without steps loads nothing: it stores the initial value)")
+            if self.trace:
+                w(f"{ind}const unsigned long long tr_i0 = {now}; tr_slices += T;")
+            w(f"{ind}if (pf_q != q) {{  // not loaded during the previous item: fill the stages now")
+            for s in range(S):
+                L.extend(issue(str(s), s, ind + "  "))
+                rec.add(lambda b, n, nxt, gid, s=s: ("load", s, gid(s), per_slice), lambda n, nxt, pre: n > 0 and not pre)
+            w(f"{ind}}}")
+            rec.add(lambda b, n, nxt, gid: ("wait_vm", per_slice * (S - 1)), lambda n, nxt, pre: n > 0)
+            rec.add(lambda b, n, nxt, gid: ("barrier",), lambda n, nxt, pre: n > 0)
+            rec.add(lambda b, n, nxt, gid: ("read", 0, gid(0)), lambda n, nxt, pre: n > 0)
+        else:
+            rec = self.protocol = Recorder()
+            ind = "    "
+            if self.trace:
+                w(f"{ind}const unsigned long long tr_i0 = {now}; tr_slices += T;")
+            for s in range(S):
+                L.extend(issue(str(s), s, ind))
+                rec.add(("load", s, s, per_slice))
+            rec.add(("wait_vm", per_slice * (S - 1)))
+            rec.add(("barrier",))
+            rec.add(("read", 0, 0))
+        # Slice 0 has landed here (at most S - 1 slices' loads are younger; the epilogue's stores, issued after
+        # them, are waited for too where they are still in flight) and, after the barrier, every wave's.
         w(f"{ind}AK_WAIT_VM({per_slice * (S - 1)});")
         w(f'{ind}asm volatile("s_barrier" ::: "memory");')
-        rec.add(("wait_vm", per_slice * (S - 1)))
-        rec.add(("barrier",))
         if self.trace:
             w(f"{ind}const unsigned long long tr_c0 = {now}; tr_fill += tr_c0 - tr_i0;")
         L.extend(reads(0, 0, 0, ind))
-        rec.add(("read", 0, 0))
         rec.loop(S)
         w(f"{ind}for (int g = 0; g < T; g += {S}) {{")
         ind2 = ind + "  "
@@ -1219,7 +1290,10 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                 w(f"{ind2}{{")
                 if k16 < k16s - 1:
                     L.extend(reads(s, k16 + 1, cur ^ 1, ind2 + "  "))
-                    rec.at(s, lambda b, n, st=s: ("read", st, b))
+                    if cross:
+                        rec.at(s, lambda b, n, nxt, gid, st=s: ("read", st, gid(b)))
+                    else:
+                        rec.at(s, lambda b, n, st=s: ("read", st, b))
                     L.extend(mfmas(cur, ind2 + "  "))
                     L.extend(hints(ind2 + "  ", False))
                 else:
@@ -1231,28 +1305,47 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                     w(f"{ind2}  AK_WAIT_LGKM0();")
                     w(f"{ind2}  AK_WAIT_VM({per_slice * (S - 2)});")
                     w(f'{ind2}  asm volatile("s_barrier" ::: "memory");')
-                    rec.at(s, lambda b, n: ("wait_lgkm",))
-                    rec.at(s, lambda b, n: ("wait_vm", per_slice * (S - 2)))
-                    rec.at(s, lambda b, n: ("barrier",))
                     if self.trace:
                         w(f"{ind2}  tr_wait += {now} - tr_w0;")
-                    L.extend(issue(f"g + {s + S}", s, ind2 + "  "))
-                    rec.at(s, lambda b, n, st=s: ("load", st, b + S, per_slice))
+                    L.extend(issue(f"g + {s + S}", s, ind2 + "  ", refill=True))
                     L.extend(reads((s + 1) % S, 0, cur ^ 1, ind2 + "  "))
-                    rec.at(s, lambda b, n, st=(s + 1) % S: ("read", st, b + 1))
+                    if cross:
+                        rec.at(s, lambda b, n, nxt, gid: ("wait_lgkm",))
+                        rec.at(s, lambda b, n, nxt, gid: ("wait_vm", per_slice * (S - 2)))
+                        rec.at(s, lambda b, n, nxt, gid: ("barrier",))
+                        rec.at(s, lambda b, n, nxt, gid, st=s: ("load", st, gid(b + S), per_slice))
+                        rec.at(s, lambda b, n, nxt, gid, st=(s + 1) % S: ("read", st, gid(b + 1)))
+                    else:
+                        rec.at(s, lambda b, n: ("wait_lgkm",))
+                        rec.at(s, lambda b, n: ("wait_vm", per_slice * (S - 2)))
+                        rec.at(s, lambda b, n: ("barrier",))
+                        rec.at(s, lambda b, n, st=s: ("load", st, b + S, per_slice))
+                        rec.at(s, lambda b, n, st=(s + 1) % S: ("read", st, b + 1))
                     L.extend(mfmas(cur, ind2 + "  "))
                     L.extend(hints(ind2 + "  ", True))
                 w(f"{ind2}}}")
         w(f"{ind}}}")
-        # every load and LDS read of the item done, in every wave, before the next item's loads reuse the stages
-        w(f"{ind}AK_WAIT_VM(0); AK_WAIT_LGKM0();")
-        w(f'{ind}asm volatile("s_barrier" ::: "memory");')
         rec.end_loop()
-        rec.add(("wait_vm", 0))
-        rec.add(("wait_lgkm",))
-        rec.add(("barrier",))
-        if self.trace:
-            w(f"{ind}const unsigned long long tr_o0 = {now}; tr_comp += tr_o0 - tr_c0;")
+        if cross:
+            # The next loading item's first slices are in flight in the stages: no drain here. The last loads
+            # are waited for once, before the workgroup ends.
+            w(f"{ind}pf_q = nx_q < q_end ? nx_q : -1;")
+            if self.trace:
+                w(f"{ind}tr_comp += {now} - tr_c0;")
+            w("    }")
+            rec.end.append(("wait_vm", 0))
+            self._queue_tail = "  AK_WAIT_VM(0);  // no load into LDS in flight when the workgroup ends\n"
+            if self.trace:
+                w(f"    const unsigned long long tr_o0 = {now};")
+        else:
+            # every load and LDS read of the item done, in every wave, before the next item's loads reuse the stages
+            w(f"{ind}AK_WAIT_VM(0); AK_WAIT_LGKM0();")
+            w(f'{ind}asm volatile("s_barrier" ::: "memory");')
+            rec.add(("wait_vm", 0))
+            rec.add(("wait_lgkm",))
+            rec.add(("barrier",))
+            if self.trace:
+                w(f"{ind}const unsigned long long tr_o0 = {now}; tr_comp += tr_o0 - tr_c0;")
         if self.split:
             w(f"""    if (kind == 3) {{  // a chunk: its f32 partial sums go to workspace slot `slot`, lane-contiguous
       // The lane index goes through an empty asm, as in the epilogue: the stores' addresses are then computed

@@ -26,7 +26,7 @@ from __future__ import annotations
 from dataclasses import dataclass, field
 from typing import Callable, Dict, List, Optional, Sequence, Set, Tuple
 
-__all__ = ["ProtocolError", "Recorder", "check"]
+__all__ = ["ProtocolError", "Recorder", "ItemRecorder", "check"]
 
 
 class ProtocolError(AssertionError):
@@ -137,6 +137,64 @@ class Recorder:
                     out.append(make(b, nblocks))
         out += [ev for ev, when in self.epilogue if when(nblocks)]
         return out
+
+
+@dataclass
+class ItemRecorder:
+    """Events of a persistent kernel whose work items each walk their own blocks through the same LDS stages,
+    the next item's first blocks loaded during the current item's last ones. An event maker takes the
+    item's block count `n`, whether a next item that loads follows (`nxt`), the block index `b` (the loop's
+    positions; for straight-line events 0) and the global id `gid(k)` of the item's k-th block: its own blocks
+    for k < n, then the next item's (k - n), or, with no next item, the item's last block again (a reload that
+    keeps the in-flight counts uniform). `replay([n0, n1, ...])` gives the events of those items back to back,
+    with block ids unique across items."""
+
+    head: List[Tuple[Callable, Callable]] = field(default_factory=list)  # at an item's start
+    body: Dict[int, List[Tuple[Callable, Callable]]] = field(default_factory=dict)
+    tail: List[Tuple[Callable, Callable]] = field(default_factory=list)  # at an item's end
+    end: List[Event] = field(default_factory=list)  # once, after the last item
+    unroll: int = 1
+    where: str = "head"
+
+    def add(self, make: Callable, when: Callable = lambda n, nxt, pre: True) -> None:
+        """A straight-line event at the item's start (before `loop`) or end (after `end_loop`); `when(n, nxt,
+        prefetched)`, where `prefetched` says the previous item already loaded this one's first blocks."""
+        (self.head if self.where == "head" else self.tail).append((make, when))
+
+    def loop(self, unroll: int) -> None:
+        self.unroll, self.where = unroll, "body"
+
+    def at(self, position: int, make: Callable, when: Callable = lambda b, n, nxt: True) -> None:
+        self.body.setdefault(position, []).append((make, when))
+
+    def end_loop(self) -> None:
+        self.where = "tail"
+
+    def replay(self, counts: Sequence[int]) -> List[Event]:
+        out: List[Event] = []
+        base, prefetched = 0, False
+        for i, n in enumerate(counts):
+            # items without blocks load nothing: the next item that loads is the first later one with blocks
+            nxt = n > 0 and any(c > 0 for c in counts[i + 1:])
+            nbase = base + n
+
+            def gid(k: int, base=base, n=n, nxt=nxt, nbase=nbase) -> int:
+                return base + k if k < n else (nbase + k - n if nxt else base + n - 1)
+
+            for make, when in self.head:
+                if when(n, nxt, prefetched):
+                    out.append(make(0, n, nxt, gid))
+            for b in range(n):
+                for make, when in self.body.get(b % self.unroll, []):
+                    if when(b, n, nxt):
+                        out.append(make(b, n, nxt, gid))
+            for make, when in self.tail:
+                if when(n, nxt, prefetched):
+                    out.append(make(0, n, nxt, gid))
+            if n > 0:
+                prefetched = nxt
+            base = nbase
+        return out + list(self.end)
 
 
 def loads_reads(events: Sequence[Event]) -> Set[Tuple[str, int]]:

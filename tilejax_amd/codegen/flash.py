@@ -464,7 +464,9 @@ class _Flash:
             for wv, (full, upto) in enumerate(waves):
                 table[row, 5 + 2 * wv] = full
                 table[row, 6 + 2 * wv] = upto
-        kvtab = np.array(blocks, np.int32).reshape(-1) if blocks else np.zeros(2, np.int32)
+        # one padding entry at the end: an item without blocks (its offset the table's length) still reads an
+        # entry in bounds where the kernel loads its first entries unconditionally
+        kvtab = np.array(list(blocks) + [(0, 0)], np.int32).reshape(-1)
         tables = {"fa_items": table.reshape(-1), "fa_blocks": kvtab}
         if merges:
             tables["fa_merge"] = np.array(merges, np.int32).reshape(-1)
@@ -514,7 +516,9 @@ class _Flash:
             args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
         return args
 
-    def _source(self, args: List[Arg], stride: int) -> str:
+    def _setup(self, args: List[Arg]) -> Dict[str, Any]:
+        """What every form of the kernel's source shares: the shapes of its fragments and loads, the operands'
+        bases and pitches, and the score and epilogue as C expressions per element."""
         plan, sch, m = self.plan, self.sch, self.m
         nw, bq, bkv = self.nw, self.bq, self.bkv
         D, DV = m.d, m.dv
@@ -591,6 +595,19 @@ class _Flash:
         tile_decode = "\n  ".join(decode_tile(plan, sch, "t"))
         Q, K, V, O = (f"args.{m.q.tile.array}", f"args.{m.k.tile.array}", f"args.{m.v.tile.array}",
                       f"args.{m.out.name}_out")
+        return locals()
+
+    def _source(self, args: List[Arg], stride: int) -> str:
+        c = self._setup(args)
+        plan, sch, m = self.plan, self.sch, self.m
+        nw, bq, bkv = self.nw, self.bq, self.bkv
+        (D, DV, T, kt, ds, ks, dt_n, chk, chv, ldk_n, ldv_n, vo_n, jvar, q_base, k_base, v_base, o_base, ldq, ldk,
+         ldv, ldo, kstride_j, vstride_j, k_numel, v_numel, score_lines, score_expr, epi_lines, out_expr, struct,
+         tile_decode, Q, K, V, O) = (c[n] for n in (
+            "D", "DV", "T", "kt", "ds", "ks", "dt_n", "chk", "chv", "ldk_n", "ldv_n", "vo_n", "jvar", "q_base",
+            "k_base", "v_base", "o_base", "ldq", "ldk", "ldv", "ldo", "kstride_j", "vstride_j", "k_numel",
+            "v_numel", "score_lines", "score_expr", "epi_lines", "out_expr", "struct", "tile_decode", "Q", "K", "V",
+            "O"))
         L: List[str] = []
         w = L.append
         w(f"""// Generated by tilejax_amd for `{plan.nest.name}`: a gfx950 flash-attention kernel.
@@ -670,7 +687,7 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
         # A block's table entry (key block start, column offset) is loaded into a ring of scalars one block
         # before it is first needed, so no scalar load's latency follows a barrier.
         def entry_load(x: str, r: int, ind: str) -> str:
-            return (f"{ind}{{ const int* bp = args.fa_blocks + 2 * (boff + ak_imin({x}, nblk - 1)); "
+            return (f"{ind}{{ const int* bp = args.fa_blocks + 2 * (boff + ak_imax(ak_imin({x}, nblk - 1), 0)); "
                     f"bj[{r}] = ak_ldc(bp, 0); bc[{r}] = ak_ldc(bp, 1); }}")
 
         def issue(r: int, s: int, ind: str) -> List[str]:
@@ -872,8 +889,18 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
   {trace_write}
 }}""")
         if self.slots:
-            per_item = bq * DV // 4 // 256
-            w(f"""
+            w(self._merge_kernel(c))
+        return "\n".join(L)
+
+    def _merge_kernel(self, c: Dict[str, Any]) -> str:
+        """The merge of tiles split along the keys: each thread combines four output elements of one row over
+        the tile's chunks with the online softmax's own rule (weights exp(m_c - M)), then applies the
+        epilogue."""
+        bq, DV = self.bq, self.m.dv
+        per_item = bq * DV // 4 // 256
+        tile_decode, O, o_base, ldo = c["tile_decode"], c["O"], c["o_base"], c["ldo"]
+        epi_lines, out_expr = c["epi_lines"], c["out_expr"]
+        return f"""
 // The merge of tiles split along the keys: each thread combines four output elements of one row over the
 // tile's chunks with the online softmax's own rule (weights exp(m_c - M)), then applies the epilogue.
 extern "C" __global__ void __launch_bounds__(256) {self.name}_merge(const {self.name}_args args) {{
@@ -905,8 +932,7 @@ extern "C" __global__ void __launch_bounds__(256) {self.name}_merge(const {self.
     res[e4] = (float)({out_expr});
   }}
   *(ak_u32x2*)op = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
-}}""")
-        return "\n".join(L)
+}}"""
 
 
 class _FlashF32(_Flash):

@@ -187,6 +187,21 @@ def _measured_traffic(tiles, source: str):
     return float(entry["bytes_per_launch"])
 
 
+def leg_regions(kernel, lowered, arrays) -> dict:
+    """The leg's kernel rebuilt with trace regions (the same kernel, stamping s_memrealtime around its waits,
+    compute and stores) and profiled: per call, its region totals and the shader clock its workgroups ran at,
+    measured in the kernel as s_memtime cycles over s_memrealtime ticks."""
+    from tilejax_amd import profiling
+
+    traced = kernel.lowered(kernel.signature(*arrays), lowered.config, trace=True)
+    p = profiling.measure(traced, list(arrays), runs=5)
+    _log("  " + str(p).replace("\n", "\n  "))
+    us = lambda s: round(s * 1e6, 1)  # noqa: E731
+    return {"device_us": us(p.device_s), "compute_us": us(p.compute_s), "input_wait_us": us(p.exposed_wait_s),
+            "fill_us": us(p.fill_s), "output_us": us(p.out_wait_s), "clock_ghz": round(p.clock_hz / 1e9, 3),
+            "bottleneck": p.bottleneck}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,6 +221,9 @@ def main() -> int:
                     help="first copy a 1 GiB tensor once: the known-size kernel rocprofv3 counters are scaled by")
     ap.add_argument("--warm-seconds", type=float, default=1.0,
                     help="seconds of untimed back-to-back calls before each leg's warm-up steps")
+    ap.add_argument("--regions", action="store_true",
+                    help="also profile each leg's kernel rebuilt with trace regions: where its time goes, and the "
+                         "shader clock it ran at, measured in the kernel")
     args = ap.parse_args()
     WARM_S[0] = args.warm_seconds
     if args.gpus != 1:
@@ -254,6 +272,8 @@ def main() -> int:
     _log(f"  {ms * 1e3:.1f} us/call, {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_TFLOPS:.1f}% of peak)")
     out["dense"] = {"tiles": [tiles.tm, tiles.tn, tiles.tk], "us": round(ms * 1e3, 2),
                     "tflops": round(tflops, 2), "hw": lowered.program.notes, "check": check}
+    if args.regions:
+        out["dense"]["regions"] = leg_regions(matmul, lowered, (x, y))
 
     if "library" in legs or not args.only:
         # the vendor library on the same inputs, for comparison: torch.matmul (hipBLASLt), bf16 out
@@ -280,6 +300,8 @@ def main() -> int:
         _log(f"  {cms * 1e3:.1f} us/call = {cms / ms:.3f} x dense")
         out["causal"] = {"tiles": [ct.tm, ct.tn, ct.tk], "us": round(cms * 1e3, 2), "vs_dense": round(cms / ms, 4),
                          "tflops_dense_equiv": round(flop / (cms * 1e-3) / 1e12, 2)}
+        if args.regions:
+            out["causal"]["regions"] = leg_regions(causal_matmul, cl, (x, y))
         cpu_jobs.append(("causal", f"kernel.reference of the whole 8192^3 causal matmul, {ct} (rate on the dense "
                          "FLOP count, as the GPU leg's tflops_dense_equiv)",
                          lambda: causal_matmul.reference(xh, yh, ct), flop, "TFLOP/s", 1))
@@ -325,6 +347,8 @@ def main() -> int:
                 _log(f"causal MHA {B}x{H}x{S}x{D}: {ams * 1e3:.1f} us, {atf:.1f} TFLOP/s")
                 out[key] = {"shape": [B, H, S, D], "blocks": [512, 512], "us": round(ams * 1e3, 2),
                             "tflops": round(atf, 2), "frac_peak": round(atf / PEAK_TFLOPS, 4)}
+                if args.regions:
+                    out[key]["regions"] = leg_regions(causal_attention, al, (q, k, v))
                 del q, k, v
         except Exception as e:  # not lowered yet: reported, not hidden
             _log(f"causal MHA: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
@@ -351,6 +375,8 @@ def main() -> int:
             _log(f"MoE grouped GEMM 16384x4096x14336 (8 experts): {mms * 1e3:.1f} us, {mtf:.1f} TFLOP/s")
             out["moe"] = {"shape": [16384, 4096, 14336, 8], "tiles": [512, 512], "us": round(mms * 1e3, 2),
                           "tflops": round(mtf, 2), "frac_peak": round(mtf / PEAK_TFLOPS, 4)}
+            if args.regions:
+                out["moe"]["regions"] = leg_regions(grouped_matmul, gl, (xs, w, ge))
             del xs, w
         except Exception as e:
             _log(f"MoE: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
@@ -393,6 +419,8 @@ def main() -> int:
                              "us": round(dms * 1e3, 2), "us_tables": round(tms * 1e3, 2),
                              "us_cursor": round(cms * 1e3, 2), "bytes": dbytes, "gbs": round(gbs, 1),
                              "frac_hbm_peak": round(gbs / 8000.0, 4)}
+            if args.regions:
+                out["decode"]["regions"] = leg_regions(paged_gqa_decode, dl, (q, kp, vp, table, ln))
             del kp, vp
             # the contiguous cache (the reference's gqa_decode): the same 64 sequences over 8192 positions
             from examples.decode import DecodeTiles, gqa_decode

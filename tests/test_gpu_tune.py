@@ -5,6 +5,7 @@ import torch
 
 import tilejax_amd as autokernel
 from examples.matmul import MatmulTiles, matmul
+from tilejax_amd.codegen.program import TRACE_FIELDS
 from tilejax_amd.jaxlite import jnp
 
 pytestmark = pytest.mark.gpu
@@ -27,6 +28,7 @@ def test_profile_has_trace_regions():
     assert p.steps == pytest.approx(matmul.lower(x, y, tiles).steps)
     assert 0 < p.compute_s < p.device_s and p.wait_s >= p.fill_s > 0
     assert p.bottleneck in ("dma", "overhead", "compute")
+    assert 0.5e9 < p.clock_hz <= 2.45e9, p.clock_hz  # measured in the kernel; the chip's peak is 2.4 GHz
 
 
 @autokernel.tunable
@@ -91,7 +93,9 @@ def test_attention_profile_has_trace_regions(shape, blocks):
     assert trace is not None and torch.equal(out, plain.run(q, k, v))
     # a workgroup's slices are the key blocks of its work item (the item table's block count column)
     items = traced.program.tables["fa_items"].reshape(-1, 5 + 2 * traced.program.notes["waves"])
-    assert trace.view(-1, 5)[:, 4].sum().item() == int(items[:, 3].sum())
+    assert trace.view(-1, TRACE_FIELDS)[:, 4].sum().item() == int(items[:, 3].sum())
+    # the shader clock the workgroups ran at, measured in the kernel: within the chip's range (2.4 GHz peak)
+    assert 0.5e9 < p.clock_hz <= 2.45e9, p.clock_hz
 
 
 def test_decode_profile_has_trace_regions():

@@ -40,3 +40,14 @@ def test_bottleneck_thresholds():
     assert prof(compute=10 - OVERHEAD_BOUND_SHARE * 10 - 0.5).bottleneck == "overhead"
     assert prof().bottleneck == "compute"
     assert "bottleneck: compute" in str(prof())
+
+
+def test_summarize_reads_the_shader_clock_weighted_by_run_time():
+    # [wait, fill, out_wait, compute, steps, shader cycles, 100 MHz ticks]: one workgroup at 2.0 GHz for
+    # 1000 ticks, one at 1.5 GHz for 3000 ticks; the clock is total cycles over total ticks (1.625 GHz)
+    stamps = np.array([[0, 0, 0, 1000, 4, 20000, 1000], [0, 0, 0, 3000, 4, 45000, 3000]])
+    p = summarize(stamps, "k", None, calls=1, device_s=40e-6, workgroups=2)
+    assert np.isclose(p.clock_hz, 65000 / 4000 * CLOCK_HZ)
+    assert "1.625 GHz" in str(p)
+    # rows without the clock fields (or no ticks) report none
+    assert summarize(stamps[:, :5], "k", None, 1, 40e-6, 2).clock_hz == 0.0

@@ -47,7 +47,7 @@ from .device import PRELUDE
 from .expr import ElementEmitter, literal
 from .flash import RESCALE_SLACK, Softmax, _is, _strip, softmax_structure
 from .protocol import Recorder
-from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
+from .program import CLOCK_END, CLOCK_START, NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 from .steps import attach_step_builder
 
 __all__ = ["DecodeMatch", "match", "lower"]
@@ -648,7 +648,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
     def _trace_start(self) -> str:
         if not self.trace:
             return ""
-        return (f"unsigned long long tr_fill = 0, tr_wait = 0, tr_out = 0; "
+        return (f"{CLOCK_START} unsigned long long tr_fill = 0, tr_wait = 0, tr_out = 0; "
                 f"const unsigned long long tr_i0 = {NOW};")
 
     def _trace_write(self, steps: str) -> str:
@@ -658,7 +658,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
         return (f"if (threadIdx.x == 0) {{ const unsigned long long tr_e = {NOW}; "
                 f"unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
                 f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_out; "
-                f"tr[3] = tr_e - tr_i0 - tr_fill - tr_wait - tr_out; tr[4] = (unsigned long long)({steps}); }}")
+                f"tr[3] = tr_e - tr_i0 - tr_fill - tr_wait - tr_out; tr[4] = (unsigned long long)({steps}); {CLOCK_END} }}")
 
     def _merge_source(self) -> str:
         plan, sch, m = self.plan, self.sch, self.m

@@ -46,7 +46,7 @@ from ..schedule import CODE_SHIFT, STEP_CODE, Schedule
 from .common import Index, decode_tile, static_tile_steps, strides, tile_base
 from .device import PRELUDE
 from .expr import Emitter, Interval, intervals, literal, nodes_between
-from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
+from .program import CLOCK_END, CLOCK_START, NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 from .protocol import Recorder
 
 __all__ = ["FlashMatch", "match", "lower"]
@@ -676,13 +676,13 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
             # trace regions: the wait for block 0 is the pipeline fill; later blocks' waits (their loads and the
             # barrier) are input waits; the rest of the loop is compute; the stores are output
             w(f"  unsigned long long tr_fill = 0, tr_wait = 0;")
-            w(f"  const unsigned long long tr_i0 = {NOW};")
+            w(f"  {CLOCK_START} const unsigned long long tr_i0 = {NOW};")
         # the last wave writes: its rows see every key block the tile visits, so its waits are for data
         # (and the barrier), never for want of work
         trace_write = (f"if (tid == {T - 64}) {{ const unsigned long long tr_e = {NOW}; "
                        f"unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
                        f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_e - tr_c1; "
-                       f"tr[3] = tr_c1 - tr_i0 - tr_fill - tr_wait; tr[4] = (unsigned long long)nblk; }}") if tr else ""
+                       f"tr[3] = tr_c1 - tr_i0 - tr_fill - tr_wait; tr[4] = (unsigned long long)nblk; {CLOCK_END} }}") if tr else ""
 
         # A block's table entry (key block start, column offset) is loaded into a ring of scalars one block
         # before it is first needed, so no scalar load's latency follows a barrier.
@@ -1065,9 +1065,9 @@ class _FlashF32(_Flash):
         tile_decode = "\n  ".join(decode_tile(plan, sch, "t"))
         Q, K, V, O = (f"args.{m.q.tile.array}", f"args.{m.k.tile.array}", f"args.{m.v.tile.array}",
                       f"args.{m.out.name}_out")
-        tr0 = f"const unsigned long long tr_0 = {NOW};" if self.trace else ""
+        tr0 = f"{CLOCK_START} const unsigned long long tr_0 = {NOW};" if self.trace else ""
         tr1 = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; tr[0] = 0; "
-               f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = nblk; }}" if self.trace else "")
+               f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = nblk; {CLOCK_END} }}" if self.trace else "")
         return f"""// Generated by tilejax_amd for `{plan.nest.name}`: f32 attention on the vector ALUs.
 // spec tile {m.rows} x {m.bk} (head dims {D}, {DV}); {T} query rows per workgroup, key blocks of {bkv}.
 {PRELUDE}

@@ -38,7 +38,7 @@ from ..schedule import CODE_SHIFT, FILL_TABLE, STEP_CODE, STEP_TILE, TILE_TABLE,
 from .common import Index, decode_fill, decode_tile, static_tile_steps, strides, tile_base, work_lists
 from .device import PRELUDE
 from .expr import ElementEmitter, Emitter, Interval, ctype, intervals, literal, nodes_between
-from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
+from .program import CLOCK_END, CLOCK_START, NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 from .protocol import ItemRecorder, Recorder
 
 __all__ = ["GemmMatch", "match", "lower"]
@@ -1071,9 +1071,9 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
             w("  }")
         trace_write = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
                        f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_out; tr[3] = tr_comp - tr_wait; "
-                       f"tr[4] = tr_slices; }}" if self.trace else "")
-        trace_decl = ("unsigned long long tr_wait = 0, tr_fill = 0, tr_out = 0, tr_comp = 0, tr_slices = 0;"
-                      if self.trace else "")
+                       f"tr[4] = tr_slices; {CLOCK_END} }}" if self.trace else "")
+        trace_decl = (f"{CLOCK_START} unsigned long long tr_wait = 0, tr_fill = 0, tr_out = 0, tr_comp = 0, "
+                      "tr_slices = 0;" if self.trace else "")
         now = NOW
         if self.n_small:
             pull = f"""    int t, code, slot;

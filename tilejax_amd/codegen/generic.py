@@ -43,7 +43,7 @@ from ..syntax import bound, used
 from .common import Index, decode_fill, decode_tile, static_tile_steps, strides, work_lists
 from .device import PRELUDE
 from .expr import ElementEmitter, _broadcast_index, _rounded, ctype, int_expr, literal
-from .program import NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
+from .program import CLOCK_END, CLOCK_START, NOW, TRACE, TRACE_FIELDS, Arg, Launch, Program, c_struct
 
 __all__ = ["lower", "lower_walk"]
 
@@ -744,9 +744,9 @@ class _Generic:
 {chr(10).join(fill_code)}
       continue;
     }}"""
-        t0 = f"const unsigned long long tr_0 = {NOW};" if self.trace else ""
+        t0 = f"{CLOCK_START} const unsigned long long tr_0 = {NOW};" if self.trace else ""
         t1 = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; tr[0] = 0; "
-              f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = q_end - q_begin; }}" if self.trace else "")
+              f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = q_end - q_begin; {CLOCK_END} }}" if self.trace else "")
         return f"""// Generated by tilejax_amd for `{plan.nest.name}`: the generic gfx950 lowering (tile code evaluated
 // pass by pass in each workgroup's tile memory of {self.buf.size} bytes).
 {PRELUDE}
@@ -1024,9 +1024,9 @@ class _Walk(_Generic):
 
     def _walk_source(self, args: List[Arg], decode: List[str], total: str, tile_code: List[str]) -> str:
         plan = self.plan
-        t0 = f"const unsigned long long tr_0 = {NOW};" if self.trace else ""
+        t0 = f"{CLOCK_START} const unsigned long long tr_0 = {NOW};" if self.trace else ""
         t1 = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; tr[0] = 0; "
-              f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = tiles_; }}" if self.trace else "")
+              f"tr[1] = 0; tr[2] = 0; tr[3] = {NOW} - tr_0; tr[4] = tiles_; {CLOCK_END} }}" if self.trace else "")
         body = "\n    ".join(decode[1:])
         return f"""// Generated by tilejax_amd for `{plan.nest.name}`: the generic gfx950 lowering of the tile as written
 // (blocks walked per tile in each workgroup's tile memory of {self.buf.size} bytes).

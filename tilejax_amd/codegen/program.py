@@ -18,14 +18,19 @@ import torch
 from .. import jaxlite, runtime
 from ..errors import KernelError
 
-__all__ = ["Arg", "Launch", "Program", "TRACE", "TRACE_FIELDS", "NOW"]
+__all__ = ["Arg", "Launch", "Program", "TRACE", "TRACE_FIELDS", "NOW", "CLOCK_START", "CLOCK_END"]
 
 # A kernel generated with trace regions writes, per workgroup, TRACE_FIELDS 64-bit totals into the
 # workspace buffer TRACE: input-wait ticks (pipeline fill included), fill ticks, output ticks, compute ticks
-# (of the 100 MHz constant clock NOW reads), then the slices (units of streamed work) it processed.
+# (of the 100 MHz constant clock NOW reads), the slices (units of streamed work) it processed, then the
+# shader clock's cycles (s_memtime) and the constant clock's ticks over the workgroup's whole run: their
+# ratio is the clock the kernel ran at, measured on the chip rather than derived from a counter.
 TRACE = "ak_trace"
-TRACE_FIELDS = 5
+TRACE_FIELDS = 7
 NOW = "__builtin_amdgcn_s_memrealtime()"
+CLOCK_START = ("const unsigned long long ak_cyc0 = __builtin_amdgcn_s_memtime(), "
+               "ak_rt0 = __builtin_amdgcn_s_memrealtime();")
+CLOCK_END = "tr[5] = __builtin_amdgcn_s_memtime() - ak_cyc0; tr[6] = __builtin_amdgcn_s_memrealtime() - ak_rt0;"
 
 
 @dataclass(frozen=True)

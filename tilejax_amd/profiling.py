@@ -19,7 +19,7 @@ import time
 from dataclasses import dataclass, field
 from typing import Any, Dict, Optional, Sequence
 
-from .codegen.program import TRACE_FIELDS  # per workgroup: wait, fill, out_wait, compute (ticks), steps
+from .codegen.program import TRACE_FIELDS  # per workgroup: wait, fill, out_wait, compute (ticks), steps, cycles, ticks
 from .errors import KernelError
 
 __all__ = ["DMA_BOUND_SHARE", "OVERHEAD_BOUND_SHARE", "KernelProfile", "enable_profiling", "measure", "profile",
@@ -46,6 +46,7 @@ class KernelProfile:
     compute_s: float = 0.0
     scopes: Dict[str, float] = field(default_factory=dict)
     samples: Sequence[float] = ()
+    clock_hz: float = 0.0  # the shader clock the traced workgroups ran at (s_memtime cycles over 100 MHz ticks)
 
     @property
     def exposed_wait_s(self) -> float:
@@ -76,6 +77,7 @@ class KernelProfile:
                 f"  input waits    {us(self.exposed_wait_s)}  (+{us(self.fill_s).strip()} filling the pipeline)",
                 f"  output waits   {us(self.out_wait_s)}",
                 f"  other          {us(self.other_s)}  (decoding steps, starting loads, draining)",
+                f"  shader clock   {self.clock_hz / 1e9:10.3f} GHz (cycles over constant-clock ticks, in the kernel)",
                 f"  bottleneck: {self.bottleneck}",
             ]
         return "\n".join(lines)
@@ -90,9 +92,10 @@ def enable_profiling() -> None:
 def summarize(stamps: Any, name: str, config: Any, calls: int, device_s: float, workgroups: int,
               slots: int = 0) -> KernelProfile:
     """A profile from a trace buffer of per-workgroup region totals (in clock ticks): rows of
-    [wait, fill, out_wait, compute, steps], summed over `calls` calls. Time per call is the total over
-    workgroups divided by the number that run side by side (`slots`, default all of them): with more
-    workgroups than that, a slot runs several in turn."""
+    [wait, fill, out_wait, compute, steps, shader cycles, ticks], summed over `calls` calls. Time per call is
+    the total over workgroups divided by the number that run side by side (`slots`, default all of them):
+    with more workgroups than that, a slot runs several in turn. The shader clock is the workgroups' cycles
+    over their ticks (each workgroup weighted by how long it ran)."""
     import numpy as np
 
     t = np.asarray(stamps, dtype=np.float64).reshape(workgroups, -1)
@@ -102,6 +105,7 @@ def summarize(stamps: Any, name: str, config: Any, calls: int, device_s: float, 
         name=name, config=config, calls=calls, device_s=device_s, regions=True,
         wait_s=per[0] * ticks, fill_s=per[1] * ticks, out_wait_s=per[2] * ticks, compute_s=per[3] * ticks,
         steps=float(t[:, 4].sum()) / max(calls, 1),
+        clock_hz=float(t[:, 5].sum() / t[:, 6].sum() * CLOCK_HZ) if t.shape[1] > 6 and t[:, 6].sum() > 0 else 0.0,
     )
 
 

@@ -407,6 +407,7 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
 # With it on, the queue's heads are per program and device (Program.state): calls of one queued program
 # must not overlap on two streams.
 QUEUE_TAIL = [False]
+PATCHES = [True]  # locality groups of a column band and a patch of rows (False: the column band alone)
 # The last round's K-split: at most MAX_SPLIT chunks per tile. Its chunks run at the kernel's end, when their
 # reads, f32 partials and the filled tiles' stores share HBM, and the fixup reads the partials again: causal
 # 8192^3 at 512^3 tiles measured 484 us at 16 chunks of 8 slices, 475-478 at 8 of 16, 477-480 at 4 of 32.
@@ -593,8 +594,19 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             steps_of = [int(offsets[t + 1] - offsets[t]) - int(np.sum((codes[offsets[t]:offsets[t + 1]] & 4) != 0))
                         for t in range(sch.pattern_tiles)]
         per_tile = (plan.phases[m.mphase].range.count if plan.phases else 1) if not sch.step_tables else None
-        out_cols = [w for w in m.out.tile.windows if w.size is not None][1]
-        col_loop = out_cols.loop
+        out_rows, out_cols = [w for w in m.out.tile.windows if w.size is not None][:2]
+        col_loop, row_loop = out_cols.loop, out_rows.loop
+        # Locality groups: a band of columns (four workgroup tiles wide, or 1024 columns), and within it a patch
+        # of rows, so that an XCD's round of equal items (32 of them, in group order) covers about as many row
+        # panels as column panels whatever order the spec's loops take
+        band = max(hw.bn * 4, 1024)
+        rows_per_patch = max(1, gfx950.CUS // gfx950.XCDS // max(1, band // hw.bn)) * hw.bm
+
+        def locality(values: Dict[str, int], sm: int, sn: int) -> Tuple[int, int]:
+            col = (values.get(col_loop, 0) if col_loop else 0) + sn * hw.bn
+            row = (values.get(row_loop, 0) if row_loop else 0) + sm * hw.bm
+            return (col // band, row // rows_per_patch) if PATCHES[0] else (col // band, 0)
+
         consts: set = set()
         for t in range(sch.tiles):
             blocks = sch.blocks_at(t)
@@ -613,19 +625,17 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
                     if const is not None:
                         consts.add(const)
                         kind, weight = 2, 0.25
-                col = (values.get(col_loop, 0) if col_loop else 0) + sn * hw.bn
                 items.append((t, s | (kind << 16)))
                 weights.append(weight)
-                groups.append(col // max(hw.bn * 4, 1024))
+                groups.append(locality(values, sm, sn))
         for f in range(sch.fills):
             blocks = sch.fill_blocks_at(f)
             values = {r.var: r.value(b) for r, b in zip(plan.parallel, blocks)}
             for s in range(self.subs):
-                sn = s % self.sub_n
-                col = (values.get(col_loop, 0) if col_loop else 0) + sn * hw.bn
+                sm, sn = divmod(s, self.sub_n)
                 items.append((f, s | (1 << 16)))
                 weights.append(0.25)
-                groups.append(col // max(hw.bn * 4, 1024))
+                groups.append(locality(values, sm, sn))
         if len(consts) > 1:  # one constant per kernel: compute the others
             keep = sorted(consts)[0]
             items = [(t, s & 0xFFFF) if (s >> 16) == 2 and self._constant_of(t, s) != keep else (t, s)
@@ -674,7 +684,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
                 # chunks are ordered by K range and equally loaded workgroups are taken an XCD at a time, so an
                 # XCD takes every remainder tile's chunks over the same K ranges (two of eight at 16 tiles): the
                 # tiles' A and B panels over those ranges are read into its L2 once
-                g_out.append(ch * gfx950.XCDS // split)
+                g_out.append((ch * gfx950.XCDS // split, 0))
         return out, w_out, g_out
 
     def _constant_of(self, t: int, s: int) -> Optional[float]:

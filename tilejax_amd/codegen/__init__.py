@@ -76,7 +76,20 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
              cursor: bool = False, hardware: Optional[Dict[str, int]] = None) -> Program:
     """The program for this plan, schedule and pipeline (and `hardware` knobs of the family's kernel shape,
     from `hardware_choices`); with `cursor`, a kernel with runtime masks finds its steps itself as it runs
-    rather than from device-built step tables (the decode family)."""
+    rather than from device-built step tables (the decode family). The knob `poison` builds the program's
+    poisoned form (codegen/poison.py: LDS, outputs and workspaces start as NaN), for tests."""
+    knobs = dict(hardware or {})
+    poison = knobs.pop("poison", 0)
+    program = _generate(plan, schedule, pipeline, trace=trace, cursor=cursor, hardware=knobs)
+    if poison:
+        from .poison import poison_program
+
+        poison_program(program)
+    return program
+
+
+def _generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool, cursor: bool,
+              hardware: Dict[str, int]) -> Program:
     from . import decode, flash, gemm, generic
 
     name = _symbol(plan)

@@ -166,16 +166,26 @@ class Program:
         runtime.require_gpu()
         self.check_inputs(arrays)
         device = arrays[0].device
+        poison = self.notes.get("poison", False)  # a poisoned build (codegen/poison.py): outputs and workspaces NaN
         if outputs is None:
-            outputs = [torch.empty(shape, dtype=dt.torch, device=device) for shape, dt in self.outputs]
+            outputs = [_poisoned(shape, dt.torch, device) if poison else torch.empty(shape, dtype=dt.torch, device=device)
+                       for shape, dt in self.outputs]
         tables = self.device_tables(device)
-        workspace = {name: torch.empty(max(n, 4), dtype=torch.uint8, device=device) for name, n in self.workspace.items()}
+        workspace = {name: (torch.full((max(n, 4),), 0xFF, dtype=torch.uint8, device=device) if poison
+                            else torch.empty(max(n, 4), dtype=torch.uint8, device=device))
+                     for name, n in self.workspace.items()}
         module = self.module(device.index or 0)
         stream = runtime.current_stream() if stream is None else stream
         for launch in launches:
             args = pack(launch.args, arrays, outputs, tables, workspace)
             module.kernel(launch.symbol).launch(launch.grid, launch.block, launch.lds, args, stream)
         return outputs, workspace
+
+
+def _poisoned(shape, dtype: torch.dtype, device) -> torch.Tensor:
+    """An output of a poisoned build: NaN, or -1 for an integer dtype."""
+    fill = float("nan") if dtype.is_floating_point else -1
+    return torch.full(shape, fill, dtype=dtype, device=device)
 
 
 class _Null:

@@ -40,6 +40,11 @@ sys.path.insert(0, ROOT)
 
 PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 N_DENSE = 8192
+# BASELINE.json config 2's sweep over {128..2048}^3: every cube, the two reported shapes, and shapes long along one
+# dimension each
+SWEEP_TILES = [(128, 128, 128), (256, 256, 256), (512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048),
+               (1024, 2048, 1024), (2048, 1024, 512), (512, 2048, 256), (2048, 512, 2048), (256, 1024, 2048),
+               (128, 2048, 512), (2048, 128, 1024)]
 
 
 def _log(msg: str) -> None:
@@ -214,13 +219,16 @@ def main() -> int:
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="",
-                    help="comma list of legs to run: dense,library,dense2,causal,rmsnorm,attention,moe,decode")
+                    help="comma list of legs to run: dense,library,dense2,config1,causal,rmsnorm,attention,moe,decode")
     ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3; "
                     "default: profiles/traffic.json")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first copy a 1 GiB tensor once: the known-size kernel rocprofv3 counters are scaled by")
     ap.add_argument("--warm-seconds", type=float, default=1.0,
                     help="seconds of untimed back-to-back calls before each leg's warm-up steps")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also time the dense 8192^3 matmul over spec tiles tm x tn x tk from {128..2048}^3 (BASELINE.json "
+                         "config 2's sweep) and print the table to stderr")
     ap.add_argument("--regions", action="store_true",
                     help="also profile each leg's kernel rebuilt with trace regions: where its time goes, and the "
                          "shader clock it ran at, measured in the kernel")
@@ -291,6 +299,44 @@ def main() -> int:
         _log(f"  {ms2 * 1e3:.1f} us/call, {flop / (ms2 * 1e-3) / 1e12:.1f} TFLOP/s")
         out["dense_1024x2048x1024"] = {"tiles": [t2.tm, t2.tn, t2.tk], "us": round(ms2 * 1e3, 2),
                                        "tflops": round(flop / (ms2 * 1e-3) / 1e12, 2)}
+
+    if "config1" in legs or not args.only:
+        # 1024^3 at MatmulTiles(512, 512, 512), the spec run as `matmul.fn` on the CPU (the
+        # function as written, the reference's plain-JAX path) and the kernel's output verified against it
+        t1 = MatmulTiles(512, 512, 512)
+        g = torch.Generator().manual_seed(0)
+        x1h = torch.randn(1024, 1024, generator=g).to(torch.bfloat16)
+        y1h = torch.randn(1024, 1024, generator=g).to(torch.bfloat16)
+        x1, y1 = x1h.to(dev), y1h.to(dev)
+        l1 = matmul.lower(x1, y1, t1)
+        got1 = l1.run(x1, y1).cpu()
+        from tilejax_amd.api import compare
+
+        fn_out = matmul.fn(x1h, y1h, t1)
+        diff1 = compare("config 1: the kernel against matmul.fn", got1, fn_out, inputs=(x1h.dtype, y1h.dtype))
+        ms1, _ = time_kernel(lambda: l1.run(x1, y1), args.steps, args.warmup)
+        flop1 = 2.0 * 1024**3
+        _log(f"config 1 (1024^3, {t1}): {ms1 * 1e3:.1f} us, {flop1 / (ms1 * 1e-3) / 1e12:.1f} TFLOP/s; the kernel "
+             f"against matmul.fn on the CPU: largest difference {diff1:.3g}")
+        out["config1"] = {"shape": [1024] * 3, "tiles": [512, 512, 512], "us": round(ms1 * 1e3, 2),
+                          "tflops": round(flop1 / (ms1 * 1e-3) / 1e12, 2), "vs_fn_max_abs_diff": diff1}
+        cpu_jobs.append(("config1", f"matmul.fn (the function as written, plain-JAX semantics) on the whole 1024^3 "
+                         f"workload, {t1}", lambda: matmul.fn(x1h, y1h, t1), flop1, "TFLOP/s", 3))
+
+    if args.sweep:
+        _log(f"dense matmul {N_DENSE}^3, spec tiles swept:")
+        sweep = []
+        for tm_, tn_, tk_ in SWEEP_TILES:
+            st = MatmulTiles(tm_, tn_, tk_)
+            sl = matmul.lower(x, y, st)
+            sms, _ = time_kernel(lambda: sl.run(x, y), args.steps, args.warmup)
+            hw_ = sl.program.notes
+            sweep.append({"tiles": [tm_, tn_, tk_], "us": round(sms * 1e3, 2),
+                          "tflops": round(flop / (sms * 1e-3) / 1e12, 2), "hw_tile": list(hw_["hw_tile"]),
+                          "waves": hw_["waves"], "stages": hw_["stages"]})
+            _log(f"  {tm_:5d} x {tn_:5d} x {tk_:5d}: {sms * 1e3:7.1f} us {flop / (sms * 1e-3) / 1e12:7.1f} TFLOP/s "
+                 f"(workgroup tile {hw_['hw_tile']}, {hw_['waves']} waves, {hw_['stages']} stages)")
+        out["dense_tile_sweep"] = sweep
 
     if "causal" in legs:
         ct = MatmulTiles(*(int(v) for v in args.causal_tiles.split(",")))

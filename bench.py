@@ -219,7 +219,8 @@ def main() -> int:
     ap.add_argument("--causal-tiles", default="512,512,512")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="",
-                    help="comma list of legs to run: dense,library,dense2,config1,causal,rmsnorm,attention,moe,decode")
+                    help="comma list of legs to run: dense,library,dense2,config1,causal,rmsnorm,attention,moe,ffn,"
+                         "decode")
     ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3; "
                     "default: profiles/traffic.json")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -255,7 +256,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    legs = set(args.only.split(",")) if args.only else {"dense", "causal", "rmsnorm", "attention", "moe", "decode"}
+    legs = set(args.only.split(",")) if args.only else {"dense", "causal", "rmsnorm", "attention", "moe", "ffn", "decode"}
     dev = torch.device("cuda:0")
     g = torch.Generator().manual_seed(0)
     xh = torch.randn(N_DENSE, N_DENSE, generator=g).to(torch.bfloat16)
@@ -427,6 +428,40 @@ def main() -> int:
         except Exception as e:
             _log(f"MoE: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
             out["moe"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
+
+    if "ffn" in legs:
+        # The MoE expert layer (examples/moe.py `expert_ffn`, the reference's examples/moe.py:167-187) at Mixtral
+        # 8x7B's width: config 4's 16384 routed rows in 64 tiles of 256 with the same seeded expert counts,
+        # D = 4096, F = 14336, 8 experts; gate, up and down products, 6 * 16384 * 4096 * 14336 FLOP per call.
+        try:
+            from examples.moe import ExpertTiles, expert_ffn
+
+            g = torch.Generator().manual_seed(0)
+            counts = torch.multinomial(torch.full((8,), 1 / 8), 64, replacement=True, generator=g).bincount(minlength=8)
+            teh = torch.repeat_interleave(torch.arange(8), counts).to(torch.int32)
+            xsh = torch.randn(16384, 4096, generator=g).to(torch.bfloat16)
+            wsh = [(torch.randn(8, *shape, generator=g) * 0.02).to(torch.bfloat16)
+                   for shape in ((4096, 14336), (4096, 14336), (14336, 4096))]
+            fargs = (xsh.to(dev), *(w_.to(dev) for w_ in wsh), teh.to(dev))
+            et = ExpertTiles(256)
+            fl = expert_ffn.lower(*fargs, et)
+            cpu_jobs.append(("ffn", f"kernel.reference on tiles 0 and 1 (512 rows), all 8 experts' weights, {et}",
+                             lambda: expert_ffn.reference(xsh[:512], *wsh, teh[:2], et), 6.0 * 512 * 4096 * 14336,
+                             "TFLOP/s", 1))
+            fms, _ = time_kernel(lambda: fl.run(*fargs), args.steps, args.warmup)
+            fflop = 6.0 * 16384 * 4096 * 14336
+            ftf = fflop / (fms * 1e-3) / 1e12
+            _log(f"MoE expert layer (expert_ffn) 16384 rows, 4096 -> 14336 -> 4096, 8 experts: {fms * 1e3:.1f} us, "
+                 f"{ftf:.1f} TFLOP/s ({100 * ftf / PEAK_TFLOPS:.1f}% of peak)")
+            out["ffn"] = {"shape": [16384, 4096, 14336, 8], "tiles": [256], "us": round(fms * 1e3, 2),
+                          "tflops": round(ftf, 2), "frac_peak": round(ftf / PEAK_TFLOPS, 4),
+                          "kernels": [launch.symbol for launch in fl.program.launches]}
+            if args.regions:
+                out["ffn"]["regions"] = leg_regions(expert_ffn, fl, fargs)
+            del fargs
+        except Exception as e:
+            _log(f"expert_ffn: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
+            out["ffn"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
 
     if "decode" in legs:
         try:

@@ -113,30 +113,17 @@ def test_baseline_config_against_torch():
     print(f"MoE config 4: largest bound use over all 64 groups {worst:.3f}", flush=True)
 
 
-@pytest.mark.parametrize("experts,block_f", [([0, 2, -1, 9], 128), ([1, 1, 0, -1], 512)])
-def test_expert_ffn_matches_oracle(experts, block_f):
-    """The reference's SwiGLU layer with runtime expert windows (examples/moe.py:167-187), lowered to the generic
-    kernel. Floor: the gate and up products' f32 summation floors carried through silu(g) * u (|silu'| <= 1.1),
-    the rounding of the hidden activations to bf16 moving each by up to 2^-8 of itself (the kernel and the
-    oracle can round to either side), both through |w_down|, plus the down product's own f32 floor."""
-    from examples.moe import ExpertTiles, expert_ffn
+def _ffn_floor(xs, wg, wu, wd, experts):
+    """The expert layer's bound beyond 2 bf16 ulp, per output: the gate and up products' f32 summation floors
+    carried through silu(g) * u (|silu'| <= 1.1), the rounding of the hidden activations to bf16 moving each by
+    up to 2^-8 of itself (the kernel and the reference can round to either side), both through |w_down|, plus
+    the down product's own f32 floor. Zero for unused tiles. All tensors on one device."""
     from tests.tolerance import P_ROUND
 
-    g = torch.Generator().manual_seed(11)
-    M, D, F, E = 512, 256, 512, 4
-    xs = torch.randn(M, D, generator=g).to(torch.bfloat16)
-    wg, wu = ((torch.randn(E, D, F, generator=g) / 16).to(torch.bfloat16) for _ in range(2))
-    wd = (torch.randn(E, F, D, generator=g) / 16).to(torch.bfloat16)
-    te = torch.tensor(experts, dtype=torch.int32)
-    tiles = ExpertTiles(block_f=block_f)
-    lowered = expert_ffn.lower(xs, wg, wu, wd, te, tiles)
-    assert lowered.program.notes["family"] == "generic"
-    print(f"expert_ffn experts={experts} {tiles}", flush=True)
-    got = lowered.run(xs.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), te.cuda())
-    torch.cuda.synchronize()
-    want = kernels.expert_ffn(xs, wg, wu, wd, te, block_f)
-    floor = torch.zeros(M, D)
+    M, D = xs.shape
+    E = wg.shape[0]
     G = M // len(experts)
+    floor = torch.zeros(M, D, device=xs.device)
     for t, e in enumerate(experts):
         if e < 0:
             continue
@@ -147,9 +134,99 @@ def test_expert_ffn_matches_oracle(experts, block_f):
         moved = 1.1 * matmul_floor(rows, wg[e]) * up.abs() + gate.abs() * matmul_floor(rows, wu[e])
         floor[t * G:(t + 1) * G] = ((moved + 2 * P_ROUND * hidden) @ wd[e].float().abs()
                                     + matmul_floor(hidden.to(torch.bfloat16), wd[e]))
-    check_bf16(f"expert_ffn experts={experts}", got.cpu(), want, floor)
+    return floor
+
+
+def _ffn_inputs(M, D, F, E, seed, scale=1 / 16):
+    g = torch.Generator().manual_seed(seed)
+    xs = torch.randn(M, D, generator=g).to(torch.bfloat16)
+    wg, wu = ((torch.randn(E, D, F, generator=g) * scale).to(torch.bfloat16) for _ in range(2))
+    wd = (torch.randn(E, F, D, generator=g) * scale).to(torch.bfloat16)
+    return xs, wg, wu, wd
+
+
+@pytest.mark.parametrize("experts,block_f", [([0, 2, -1, 9], 128), ([1, 1, 0, -1], 512)])
+def test_expert_ffn_matches_oracle(experts, block_f):
+    """The reference's SwiGLU layer with runtime expert windows (examples/moe.py:167-187), lowered as a chain
+    of two matmul-family kernels (codegen/chain.py): the gate kernel (gate and up products of one xs slice,
+    silu(g) * u in registers, stored as bf16 hidden activations) and the down kernel (the grouped product
+    with w_down under the original mask). Bar: 2 bf16 ulp of the oracle plus `_ffn_floor`, within 3e-2 of the
+    float64 layer's largest output, and zeros for unused tiles."""
+    from examples.moe import ExpertTiles, expert_ffn
+
+    M, D, F, E = 512, 256, 512, 4
+    xs, wg, wu, wd = _ffn_inputs(M, D, F, E, 11)
+    te = torch.tensor(experts, dtype=torch.int32)
+    tiles = ExpertTiles(block_f=block_f)
+    lowered = expert_ffn.lower(xs, wg, wu, wd, te, tiles)
+    notes = lowered.program.notes
+    assert notes["family"] == "gemm" and notes["chain"] and notes["products"] == 2
+    print(f"expert_ffn experts={experts} {tiles}", flush=True)
+    got = lowered.run(xs.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), te.cuda())
+    torch.cuda.synchronize()
+    want = kernels.expert_ffn(xs, wg, wu, wd, te, block_f)
+    check_bf16(f"expert_ffn experts={experts}", got.cpu(), want, _ffn_floor(xs, wg, wu, wd, experts))
     exact = torch.as_tensor(kernels.expert_ffn_float64(xs, wg, wu, wd, te))
     assert (got.cpu().double() - exact).abs().max().item() < 3e-2 * exact.abs().max().item()
+    G = M // len(experts)
     for t, e in enumerate(experts):
         if e < 0:
             assert not got[t * G:(t + 1) * G].float().any()
+
+
+def test_expert_ffn_step_tables_pin_the_steps():
+    """The program's step tables are the down kernel's, which are the original nest's (the reference's
+    tests/test_moe.py:277-283): one step per hidden block of each tile whose expert is used, and one empty
+    step per unused tile, bit-exact against the reference's table semantics (oracle/schedule.py)."""
+    from examples.moe import ExpertTiles, expert_ffn
+
+    experts = [2, -1, 0, -1, 1, 1, -1, 3]
+    M, D, F, E, bf = 1024, 256, 512, 4, 128
+    xs, wg, wu, wd = _ffn_inputs(M, D, F, E, 12)
+    te = torch.tensor(experts, dtype=torch.int32)
+    lowered = expert_ffn.lower(xs, wg, wu, wd, te, ExpertTiles(block_f=bf))
+    print("expert_ffn step tables, 8 tiles", flush=True)
+    got = lowered.program.step_tables(xs.cuda(), wg.cuda(), wu.cuda(), wd.cuda(), te.cuda())
+    G, nf = M // len(experts), F // bf
+    step_tile, step_code, count = oracle_schedule.runtime_tables(
+        [{"i": G * t} for t in range(len(experts))], [("f", 0, bf, nf, lambda v: experts[v["i"] // G] < 0)])
+    used = sum(1 for e in experts if e >= 0)
+    assert int(got["count"][0]) == count == nf * used + (len(experts) - used)
+    np.testing.assert_array_equal(got["step_tile"].cpu().numpy(), step_tile)
+    np.testing.assert_array_equal(got["step_code"].cpu().numpy(), step_code)
+    full = (got["step_code"].cpu().numpy()[:count] & 4) == 0  # the steps that compute
+    assert int(full.sum()) == nf * used
+    assert {experts[int(t)] for t in got["step_tile"].cpu().numpy()[:count][full]} == {e for e in experts if e >= 0}
+
+
+def test_expert_ffn_mixtral_width():
+    """The expert layer at Mixtral 8x7B's width (the bench's expert_ffn leg): 16384 routed rows in 64 tiles of
+    256, D = 4096, F = 14336, 8 experts, each tile's expert drawn at random and two tiles unused. Eight tiles
+    (the unused ones among them) are checked against a float32 GPU reference of the spec (h rounded to bf16
+    as the spec rounds it), with the same bar as the small cases."""
+    from examples.moe import ExpertTiles, expert_ffn
+
+    M, D, F, E, G = 16384, 4096, 14336, 8, 256
+    g = torch.Generator().manual_seed(13)
+    experts = torch.randint(0, E, (M // G,), generator=g)
+    experts[[5, 40]] = -1
+    xs = torch.randn(M, D, generator=g).to(torch.bfloat16).cuda()
+    wg, wu = ((torch.randn(E, D, F, generator=g) * 0.02).to(torch.bfloat16).cuda() for _ in range(2))
+    wd = (torch.randn(E, F, D, generator=g) * 0.02).to(torch.bfloat16).cuda()
+    te = experts.to(torch.int32).cuda()
+    print("expert_ffn 16384 x 4096 x 14336, 8 experts", flush=True)
+    got = expert_ffn(xs, wg, wu, wd, te, ExpertTiles(block_f=256))
+    torch.cuda.synchronize()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for t in (0, 5, 17, 31, 40, 41, 62, 63):
+        rows = slice(t * G, (t + 1) * G)
+        e = int(experts[t])
+        if e < 0:
+            assert not got[rows].float().any(), t
+            continue
+        x = xs[rows].float()
+        gate, up = x @ wg[e].float(), x @ wu[e].float()
+        h = (gate * torch.sigmoid(gate) * up).to(torch.bfloat16)
+        want = (h.float() @ wd[e].float()).to(torch.bfloat16)
+        floor = _ffn_floor(xs[rows], wg[e:e + 1], wu[e:e + 1], wd[e:e + 1], [0])
+        check_bf16(f"expert_ffn Mixtral width, tile {t} (expert {e})", got[rows].cpu(), want.cpu(), floor.cpu())

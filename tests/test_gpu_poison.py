@@ -115,8 +115,10 @@ def test_paged_decode(cursor):
     _same(f"paged decode cursor={cursor}", want, got)
 
 
-def test_expert_ffn_on_the_generic_kernel():
-    """The generic kernel: its tile memory is a workspace (global memory), and its step tables too."""
+def test_expert_ffn_chain():
+    """The chain of two matmul-family kernels: the hidden activations are a workspace the gate kernel writes
+    and the down kernel reads (poisoned, a row the gate kernel left unwritten would reach the output), and
+    both kernels' step tables are workspaces too."""
     from examples.moe import ExpertTiles, expert_ffn
 
     xs = _randn(512, 256, seed=22)
@@ -124,5 +126,27 @@ def test_expert_ffn_on_the_generic_kernel():
     wd = _randn(4, 512, 256, seed=25, scale=1 / 16)
     te = torch.tensor([0, 2, -1, 1], dtype=torch.int32).cuda()
     want, got, notes = _both(expert_ffn, (xs, wg, wu, wd, te), ExpertTiles(block_f=128))
-    assert notes["family"] == "generic"
+    assert notes["family"] == "gemm" and notes["chain"]
     _same("expert_ffn", want, got)
+
+
+def test_a_nest_on_the_generic_kernel():
+    """The generic kernel: its tile memory is a workspace (global memory). A nest of no family's form (an
+    elementwise map and a row sum in one tile)."""
+    from tests.helpers import make_kernel
+
+    kernel = make_kernel("""
+    def rowmix(x):
+        M, N = x.shape
+        dtype = x.dtype
+        out = jnp.zeros((M, N), dtype)
+        for i in range(0, M, 64):
+            t = x[i : i + 64, :].astype(jnp.float32)
+            s = jnp.sum(t * t, axis=1, keepdims=True)
+            out = out.at[i : i + 64, :].set((jnp.tanh(t) * s).astype(dtype))
+        return out
+    """)
+    x = _randn(256, 384, seed=26)
+    want, got, notes = _both(kernel, (x,))
+    assert notes["family"] == "generic"
+    _same("generic rowmix", want, got)

@@ -5,7 +5,9 @@ loop nest's traced tile code is matched against the kernel families the backend 
 HIP kernel generated from the plan and schedule:
 
 - `gemm`: `acc += a @ b` (or `@ b.T`) over a reduction loop, then a pointwise epilogue (dense, causal and
-  grouped matmuls);
+  grouped matmuls), also with two right operands whose products the epilogue combines; a feed-forward chain
+  (`acc += act(x @ w1, x @ w2) @ w3` over hidden blocks, the MoE expert layer) runs as two such kernels
+  (chain.py);
 - `flash`: the online-softmax reduction of attention over static masks (causal flash attention);
 - `decode`: the same reduction under runtime masks and runtime page windows (paged decode attention).
 
@@ -35,12 +37,12 @@ def _symbol(plan: Plan) -> str:
 def _family(plan: Plan) -> Tuple[str, Any]:
     """The kernel family that takes `plan` and its match, or ("generic", error or None): the first family
     whose matcher recognises the nest; a family that recognises it but can't take it leaves its KernelError."""
-    from . import decode, flash, gemm
+    from . import chain, decode, flash, gemm
 
     if plan.walk:
         return "generic", None
     try:
-        for name, module in (("gemm", gemm), ("flash", flash), ("decode", decode)):
+        for name, module in (("chain", chain), ("gemm", gemm), ("flash", flash), ("decode", decode)):
             found = module.match(plan)
             if found is not None:
                 return name, found
@@ -90,7 +92,7 @@ def generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool 
 
 def _generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool, cursor: bool,
               hardware: Dict[str, int]) -> Program:
-    from . import decode, flash, gemm, generic
+    from . import chain, decode, flash, gemm, generic
 
     name = _symbol(plan)
     if plan.walk:
@@ -100,6 +102,12 @@ def _generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool
         return generic.lower_walk(plan, schedule, pipeline, name, trace=trace)
     family_error = None
     try:
+        found = chain.match(plan)
+        if found is not None:
+            if cursor:
+                raise KernelError(f"{plan.nest.name}: the matmul family reads runtime masks from device step "
+                                  "tables (no cursor)")
+            return chain.lower(plan, schedule, pipeline, found, name, trace=trace)
         found = gemm.match(plan)
         if found is not None:
             if cursor:

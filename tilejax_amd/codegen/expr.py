@@ -115,6 +115,9 @@ class Emitter:
         self.leaves, self.shape, self.prefix = leaves, tuple(shape), prefix
         self.lines: List[str] = []
         self.done: Dict[int, str] = {}
+        # values are numbered in the order they are emitted (not by Node id, which depends on what was traced
+        # before), so one nest's source is the same text in every process
+        self.count = 0
 
     def value(self, arg: Any, want: Optional[DType] = None) -> str:
         if isinstance(arg, Node):
@@ -132,7 +135,8 @@ class Emitter:
             self.done[node.id] = leaf
             return leaf
         text = self._op(node)
-        name = f"{self.prefix}{node.id}"
+        name = f"{self.prefix}_{self.count}"
+        self.count += 1
         self.lines.append(f"const {ctype(node.dtype)} {name} = {text};")
         self.done[node.id] = name
         return name

@@ -24,6 +24,7 @@ BK-deep slices that stream through `stages` LDS stages:
 
 from __future__ import annotations
 
+import ast
 from dataclasses import dataclass
 from typing import Any, Dict, List, Optional, Tuple
 
@@ -74,6 +75,11 @@ class GemmMatch:
     pre: Tuple[Tuple[str, Node, str], ...] = ()
     stats: Tuple[Tuple[str, Node], ...] = ()
     mphase: int = 0  # the matmul's reduction loop
+    # A second product of the same left operand tile (`u += a[...] @ b2[...]` beside `acc += a[...] @ b[...]`,
+    # b2 an array of b's shape read at b's window): the epilogue reads both accumulators (`acc2`), as a gated
+    # feed-forward's gate and up projections do (the reference's examples/moe.py:180-182).
+    b2: Optional[Operand] = None
+    acc2: Optional[Node] = None
 
 
 def _is(node: Any, op: str) -> bool:
@@ -262,26 +268,36 @@ def match(plan: Plan) -> Optional[GemmMatch]:
     value = last.stores.get(out.name)
     root = value.node if isinstance(value, jaxlite.Sym) else None
     side: List[Tuple[str, Node, float]] = []
+    acc2, acc2_leaf, found2 = None, None, None  # a second product of the left operand (GemmMatch.b2)
     if plan.phases:
         body, seg0 = plan.scopes[f"body{mp}"], plan.scopes["seg0" if mp == 0 else f"end{mp - 1}"]
-        found = None
-        for acc in body.carried_in:  # the carried value a matmul accumulates into
-            new = body.values.get(acc)
+        products = []  # (carried value, its product's operands): the carried values matmuls accumulate into
+        for name in body.carried_in:
+            new = body.values.get(name)
             if not (isinstance(new, jaxlite.Sym) and _is(new.node, "add")):
                 continue
             x, y = new.node.args
-            leaf = body.carried_in.get(acc)
+            leaf = body.carried_in.get(name)
             dot = y if x is leaf else x if y is leaf else None
-            found = _dot_of_loads(plan, dot, frozenset(stats)) if isinstance(dot, Node) else None
-            if found is not None:
-                break
-        if found is None:
+            got = _dot_of_loads(plan, dot, frozenset(stats)) if isinstance(dot, Node) else None
+            if got is not None:
+                products.append((name, got))
+        if not products:
+            return None
+        products.sort(key=lambda p_: p_[0])  # (by name: the carried values' order varies from run to run)
+        acc, found = products[0]
+        if len(products) == 2 and mp == 0:
+            acc2, found2 = products[1]
+            if not _second_product(found, found2) or \
+                    tuple(plan.inputs[found[1].param].shape) != tuple(plan.inputs[found2[1].param].shape):
+                return None
+        elif len(products) > 1:
             return None
         if pre and plan.operand(found[4].kwargs["operand"]).tile.array != pre_array:
             return None
         init = seg0.values.get(acc)
         for name in plan.carried:  # every other carried value: a row sum of the left operand's prologue
-            if name != acc and name not in stats and not any(name == p_[0] for p_ in pre):
+            if name not in (acc, acc2) and name not in stats and not any(name == p_[0] for p_ in pre):
                 got = _side_sum(plan, name, found[4], mp)
                 if got is None:
                     return None
@@ -295,6 +311,13 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         acc_leaf = last.carried_in.get(acc)
         if acc_leaf is None or root is None:
             return None
+        if acc2 is not None:
+            acc2_leaf = last.carried_in.get(acc2)
+            init2 = seg0.values.get(acc2)
+            same = (isinstance(init2, jaxlite.Sym) and _is(init2.node, "full")
+                    and float(init2.node.kwargs["value"]) == init_value) or init2 == init_value
+            if acc2_leaf is None or side or not same:
+                return None
         kvar = plan.phases[mp].range.var
     else:
         if root is None:
@@ -341,8 +364,30 @@ def match(plan: Plan) -> Optional[GemmMatch]:
         return None
     if pre and a_expr is None:
         a_expr = found[4]  # (the row pass writes the operand: its first loop reads the same array)
+    b2 = found2[1] if found2 is not None else None
     return GemmMatch(opa, opb, nt, kvar, tm, tn, tk, acc_leaf, init_value, out, value, a_expr, tuple(side), k0,
-                     tuple(pre), tuple(stats.items()), mp)
+                     tuple(pre), tuple(stats.items()), mp, b2, acc2_leaf)
+
+
+def _windows(op: Operand) -> Tuple[Tuple[Any, ...], ...]:
+    """Where an operand's tile sits: each dim's loop, offset and size, and its runtime index's expression."""
+    return tuple((w.loop, w.offset, w.size, ast.dump(w.index) if w.index is not None else None, w.index_loops)
+                 for w in op.tile.windows)
+
+
+def _second_product(first: Tuple, second: Tuple) -> bool:
+    """Is `second` (a `_dot_of_loads` result) a second product of `first`'s left operand tile: the same window
+    of the same array, plain loads of bf16, and a right operand of another array of the same shape and dtype
+    read at the same window (runtime window indices included)?"""
+    opa, opb, nt, a_expr, _ = first
+    opa2, opb2, nt2, a_expr2, _ = second
+    if nt or nt2 or a_expr is not None or a_expr2 is not None:
+        return False
+    if opa.tile.array != opa2.tile.array or _windows(opa) != _windows(opa2):
+        return False
+    if opb.tile.array == opb2.tile.array or _windows(opb) != _windows(opb2):
+        return False
+    return opb.tile.shape == opb2.tile.shape and all(o.tile.dtype.name == "bfloat16" for o in (opa, opb, opb2))
 
 
 @dataclass(frozen=True)
@@ -355,14 +400,20 @@ class HwTile:
     bk: int
     stages: int
     waves: int = 4  # per workgroup: 4 (one per SIMD, 128 x 128 each of a 256 x 256 tile) or 8 (two per SIMD)
+    dual: bool = False  # two right operands (GemmMatch.b2): LDS holds BN columns of each, 2 BN in all
 
     @property
     def grid(self) -> Tuple[int, int]:
         return WAVE_GRIDS[self.waves]
 
     @property
+    def bn_lds(self) -> int:
+        """Right-operand columns a stage holds: BN, or BN of each of two operands."""
+        return 2 * self.bn if self.dual else self.bn
+
+    @property
     def lds(self) -> int:
-        return self.stages * (self.bm + self.bn) * self.bk * 2
+        return self.stages * (self.bm + self.bn_lds) * self.bk * 2
 
 
 def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str, int]] = None) -> HwTile:
@@ -372,8 +423,10 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
     is an odd multiple of 64, 16 for tk = 32) so every tile's slice count is even, and the LDS stages the
     pipeline asks for where they divide a step's slices and fit in LDS."""
     hardware = hardware or {}
-    bm, bn = min(m.tm, hardware.get("bm", 256)), min(m.tn, hardware.get("bn", 256))
-    waves = hardware.get("waves", default_waves(bm, bn))
+    dual = m.b2 is not None
+    # two right operands: 128 output columns of each fill the 256 LDS columns of a plain 256 x 256 tile
+    bm, bn = min(m.tm, hardware.get("bm", 256)), min(m.tn, hardware.get("bn", 128 if dual else 256))
+    waves = hardware.get("waves", default_waves(bm, 2 * bn if dual else bn))
     if waves not in WAVE_GRIDS:
         raise KernelError(f"the gfx950 matmul lowering runs workgroups of 4 or 8 waves, not {waves}")
     if m.tm % bm or m.tn % bn or bm % 64 or bn % 64:
@@ -385,7 +438,7 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
     def deepest(bk_: int) -> int:
         kslices = m.tk // bk_
         for s in range(max(2, pipeline.input_buffers), 1, -1):
-            if kslices % s == 0 and s * (bm + bn) * bk_ * 2 <= gfx950.LDS_BUDGET:
+            if kslices % s == 0 and s * (bm + (2 if dual else 1) * bn) * bk_ * 2 <= gfx950.LDS_BUDGET:
                 return s
         return 2
 
@@ -395,8 +448,9 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
         bk, stages = 32, deepest(32)
     wm, wn = WAVE_GRIDS[waves]
     if bm % (32 * wm) or bn % (32 * wn):
+        # (with two right operands each wave takes the same whole 32-column blocks of both)
         raise KernelError(f"a {bm} x {bn} workgroup tile does not split into {waves} waves of whole 32 x 32 blocks")
-    return HwTile(bm, bn, bk, stages, waves)
+    return HwTile(bm, bn, bk, stages, waves, dual)
 
 
 # Small items (K-split chunks, filled and constant tiles) pulled from a shared queue once a workgroup's own
@@ -435,7 +489,9 @@ def hardware_choices(m: GemmMatch) -> List[Dict[str, int]]:
     default; then 256 x 128, 128 x 256 and 128 x 128 where the spec tile divides into them), each also with
     the other number of waves per workgroup (four or eight) where the tile splits into them."""
     found, seen = [], set()
-    for bm, bn in ((256, 256), (256, 128), (128, 256), (128, 128)):
+    dual = m.b2 is not None
+    shapes = ((256, 128), (128, 128), (256, 64), (128, 64)) if dual else ((256, 256), (256, 128), (128, 256), (128, 128))
+    for bm, bn in shapes:
         got = (min(m.tm, bm), min(m.tn, bn))
         if got in seen or m.tm % got[0] or m.tn % got[1]:
             continue
@@ -444,7 +500,7 @@ def hardware_choices(m: GemmMatch) -> List[Dict[str, int]]:
     other = []
     for h in found:
         tile = (min(m.tm, h["bm"]), min(m.tn, h["bn"]))
-        waves = 12 - default_waves(*tile)  # the other of 4 and 8
+        waves = 12 - default_waves(tile[0], tile[1] * (2 if dual else 1))  # the other of 4 and 8
         wm, wn = WAVE_GRIDS[waves]
         if tile[0] % (32 * wm) == 0 and tile[1] % (32 * wn) == 0:
             other.append({**h, "waves": waves})
@@ -467,6 +523,9 @@ class _Gemm:
         # sixteenth of the bf16 rate. The parts array has six BK-deep slices for each of the operand's.
         self.x3 = _is_f32(m)
         self.kx = len(F32_PARTS["a"]) if self.x3 else 1
+        self.dual = hw.dual
+        if self.dual and (self.x3 or self.prologue):
+            raise KernelError("the gfx950 matmul lowering takes two right operands for bf16 loads without a prologue")
         if self.prologue:
             self._check_prologue()
         if self.x3:
@@ -658,7 +717,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             return items, weights, groups
         r = len(compute) % G
         T = int(round(weights[compute[0]])) - 1  # K slices per item
-        if r == 0 or 2 * r > G:
+        if r == 0 or 2 * r > G or self.dual:  # (two accumulators: no partial-sum fixup for them)
             return items, weights, groups
         split = 1
         while (2 * split * r <= G and 2 * split <= MAX_SPLIT and T % (2 * split) == 0 and (T // (2 * split)) % hw.stages == 0
@@ -788,7 +847,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
             notes={"family": "gemm", "hw_tile": (hw.bm, hw.bn, hw.bk), "stages": hw.stages, "waves": hw.waves, "grid": grid,
                    "items": len(items), "constant_items": sum(1 for _, s, _ in items if (s >> 16) == 2),
                    "queued_items": self.n_small,
-                   "split": self.split, "trace_workgroups": grid if self.trace else 0,
+                   "split": self.split, "dual": self.dual, "trace_workgroups": grid if self.trace else 0,
                    "slices_per_step": m.tk // hw.bk * self.kx * self.subs, "f32_operands": self.x3},
         )
         if sch.runtime:
@@ -926,8 +985,13 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         bm, bn, bk, S = hw.bm, hw.bn, hw.bk, hw.stages
         WM, WN = hw.grid
         T = 64 * WM * WN  # threads of the workgroup
-        wtm, wtn = bm // WM, bn // WN
+        dual, bnl = hw.dual, hw.bn_lds
+        wtm, wtn = bm // WM, bnl // WN
         mi, ni = wtm // MFMA, wtn // MFMA
+        # Output columns per wave and 32-column blocks of them: with two right operands a wave's fragments j and
+        # j + nio read the same columns of b and b2 (LDS holds b's BN columns, then b2's), and its outputs are
+        # the epilogue of each pair.
+        nio, wto = (ni // 2, wtn // 2) if dual else (ni, wtn)
         k16s = bk // 16
         kslices = m.tk // bk * self.kx  # K slices per step (with f32 operands, of the parts arrays)
         split, split_slices = (self.split[1], self.split[2]) if self.split else (1, 0)
@@ -937,6 +1001,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         no_k = lambda v: "0" if v == kvar else f"lv_{v}"  # the reduction loop's offset goes per slice
         a_base, a_str = tile_base(m.a.tile, a_shape, index, no_k)
         b_base, b_str = tile_base(m.b.tile, b_shape, index, no_k)
+        b2_base = tile_base(m.b2.tile, b_shape, index, no_k)[0] if dual else None
         o_base, o_str = tile_base(m.out.tile, m.out.shape, index, lambda v: f"lv_{v}")
         if a_str[1] != 1 or b_str[1] != 1 or o_str[1] != 1:
             raise KernelError("the gfx950 matmul lowering reads and writes tiles whose last dim is the array's last")
@@ -949,7 +1014,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         kca = bk // 8  # 16-byte chunks per K-contiguous row
         nc = bn // 8  # 16-byte chunks per N-contiguous row (B of `a @ b`)
         a_ld = bm * bk // 8 // T
-        b_ld = bn * bk // 8 // T
+        b_ld = bnl * bk // 8 // T  # (with two right operands, half for each)
         if a_ld < 1 or b_ld < 1 or (not nt and 64 % nc):
             raise KernelError(f"matmul hardware tile {bm} x {bn} x {bk} is too small for a {T}-thread workgroup")
 
@@ -984,6 +1049,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         def leaf(n: Node) -> Optional[str]:
             if n is m.acc:
                 return "acc_v"
+            if dual and n is m.acc2:
+                return "acc2_v"
             if n.op == "iota":
                 dim = n.kwargs["dimension"]
                 if dim == len(n.shape) - 2:
@@ -1023,6 +1090,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         # with a row prologue the left operand is its pass's output, laid out as the operand's array
         A = "args.rn_a" if self.prologue else "args.x3_a" if self.x3 else f"args.{m.a.tile.array}"
         B = "args.x3_b" if self.x3 else f"args.{m.b.tile.array}"
+        B2 = f"args.{m.b2.tile.array}" if dual else None
         O = f"args.{m.out.name}_out"
         a_numel, b_numel = int(np.prod(a_shape)), int(np.prod(b_shape))
         fill_value = literal(m.out.fill if m.out.fill is not None else 0, m.out.dtype)
@@ -1048,7 +1116,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
 {struct}""")
         for s in range(S):  # one array per stage and operand: the compiler then keeps prefetches in flight
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sa{s}[{bm * bk}];")
-            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sb{s}[{bn * bk}];")
+            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sb{s}[{bnl * bk}];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1076,8 +1144,10 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
         if not nt:
             w("  { const int G = lane >> 4, s = lane & 15, k = 8 * (G >> 1) + (s >> 2);")
             for j in range(ni):
-                w(f"    {{ const int n = wn * {wtn} + {j * 32} + 16 * (G & 1) + 4 * (s & 3);"
-                  f" b_roff[{j}] = k * {bn * 2} + (((n >> 3) ^ {swb('k')}) << 4) + (n & 7) * 2; }}")
+                half, jj = divmod(j, nio)  # (which right operand: 0 but with two)
+                at = f"{half * bk * bn * 2} + " if dual else ""
+                w(f"    {{ const int n = wn * {wto} + {jj * 32} + 16 * (G & 1) + 4 * (s & 3);"
+                  f" b_roff[{j}] = {at}k * {bn * 2} + (((n >> 3) ^ {swb('k')}) << 4) + (n & 7) * 2; }}")
             w("  }")
         trace_write = (f"if (tid == 0) {{ unsigned long long* tr = args.{TRACE} + blockIdx.x * {TRACE_FIELDS}; "
                        f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_out; tr[3] = tr_comp - tr_wait; "
@@ -1117,6 +1187,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
         sb_cur = "sbeg" if sch.step_tables else "0"
         a_off_expr = f"({a_base}) + (long long)(sm * {bm}) * {lda}"
         b_off_expr = f"({b_base}) + (long long)(sn * {bn}) * {ldb}" if nt else f"({b_base}) + sn * {bn}"
+        b2_off_expr = f"({b2_base}) + sn * {bn}" if dual else None
         probe = ""
         if cross:
             probe = f"""
@@ -1128,7 +1199,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
   }};
   // Item q2's loads: its slices and operand offsets; false if it loads nothing (a filled or constant tile,
   // or one without steps).
-  auto probe = [&](int q2, int& T_, int& g0_, int& sb_, long long& aoff_, long long& boff_) -> bool {{
+  auto probe = [&](int q2, int& T_, int& g0_, int& sb_, long long& aoff_, long long& boff_{", long long& boff2_" if dual else ""}) -> bool {{
     const int t = args.items[3 * q2], code = args.items[3 * q2 + 1], slot = args.items[3 * q2 + 2];
     const int sub = code & 0xffff, kind = code >> 16;
     (void)slot;
@@ -1140,7 +1211,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
     if (kind == 3) {{ g0 = (slot % {split}) * {split_slices}; T = {split_slices}; }}
     T_ = T; g0_ = g0; sb_ = {sb_cur};
     aoff_ = {a_off_expr};
-    boff_ = {b_off_expr};
+    boff_ = {b_off_expr};{f"{chr(10)}    boff2_ = {b2_off_expr};" if dual else ""}
     return T > 0;
   }};
   int pf_q = -1;  // the item whose first {S} slices are in flight"""
@@ -1169,17 +1240,24 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
         (int)({a_numel}LL * 2 - a_off * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc((void*)({B} + b_off), (short)0,
         (int)({b_numel}LL * 2 - b_off * 2), 0x00020000);""")
+        if dual:
+            w(f"""    const long long b2_off = {b2_off_expr};
+    const __amdgpu_buffer_rsrc_t rsb2 = __builtin_amdgcn_make_buffer_rsrc((void*)({B2} + b2_off), (short)0,
+        (int)({b_numel}LL * 2 - b2_off * 2), 0x00020000);""")
         if cross:
             w(f"""    // the next item in this workgroup's list that loads (its first slices are issued during this item's last)
     int nx_q = q_end, nx_T = 0, nx_g0 = 0, nx_sb = 0;
-    long long nx_aoff = 0, nx_boff = 0;
+    long long nx_aoff = 0, nx_boff = 0{", nx_boff2 = 0" if dual else ""};
     for (int q2 = q + 1; q2 < q_end; ++q2)
-      if (probe(q2, nx_T, nx_g0, nx_sb, nx_aoff, nx_boff)) {{ nx_q = q2; break; }}
+      if (probe(q2, nx_T, nx_g0, nx_sb, nx_aoff, nx_boff{", nx_boff2" if dual else ""})) {{ nx_q = q2; break; }}
     const __amdgpu_buffer_rsrc_t nx_rsa = __builtin_amdgcn_make_buffer_rsrc((void*)({A} + nx_aoff), (short)0,
         (int)({a_numel}LL * 2 - nx_aoff * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t nx_rsb = __builtin_amdgcn_make_buffer_rsrc((void*)({B} + nx_boff), (short)0,
         (int)({b_numel}LL * 2 - nx_boff * 2), 0x00020000);
     const int sb = {sb_cur};""")
+            if dual:
+                w(f"""    const __amdgpu_buffer_rsrc_t nx_rsb2 = __builtin_amdgcn_make_buffer_rsrc((void*)({B2} + nx_boff2), (short)0,
+        (int)({b_numel}LL * 2 - nx_boff2 * 2), 0x00020000);""")
         w(f"""
     // A tile's chunks are summed by the fixup kernel: only the first starts from the initial value.
     const float acc_init = (kind == 3 && g0 != 0) ? 0.0f : {literal(m.init)};
@@ -1205,21 +1283,30 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
                 out = [f"{ind}{{ const int gi = {g}; const bool nxt = gi >= T && nx_q < q_end;",
                        f"{ind}  const int k0 = k_at(nxt ? nx_g0 : g0, nxt ? nx_T : T, nxt ? nx_sb : sb, nxt ? gi - T : gi);",
                        f"{ind}  const __amdgpu_buffer_rsrc_t ra = nxt ? nx_rsa : rsa, rb = nxt ? nx_rsb : rsb;"]
+                if dual:
+                    out.append(f"{ind}  const __amdgpu_buffer_rsrc_t rb2 = nxt ? nx_rsb2 : rsb2;")
             elif cross:
                 out = [f"{ind}{{ const int k0 = k_at(g0, T, sb, {g}); const __amdgpu_buffer_rsrc_t ra = rsa, rb = rsb;"]
+                if dual:
+                    out.append(f"{ind}  const __amdgpu_buffer_rsrc_t rb2 = rsb2;")
             else:
                 out = [f"{ind}{{ const int k0 = k_of({g}); const __amdgpu_buffer_rsrc_t ra = rsa, rb = rsb;"]
+                if dual:
+                    out.append(f"{ind}  const __amdgpu_buffer_rsrc_t rb2 = rsb2;")
             rows_a = T // kca
             for c in range(a_ld):
                 out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, AK_LDS(&ak_sa{s}[({c * T} + wave * 64) * 8]), "
                            f"16, a_voff, {c * rows_a}u * pa + (unsigned)k0 * 2u, 0, 0);")
-            for c in range(b_ld):
-                if nt:
-                    soff = f"{c * rows_a}u * pb + (unsigned)k0 * 2u"
-                else:
-                    soff = f"(unsigned)(k0 + {c * (T // nc)}) * pb"
-                out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, AK_LDS(&ak_sb{s}[({c * T} + wave * 64) * 8]), "
-                           f"16, b_voff, {soff}, 0, 0);")
+            halves = (("rb", 0), ("rb2", bk * bn)) if dual else (("rb", 0),)
+            for rsrc, base in halves:  # with two right operands, b's BK x BN slice, then b2's after it
+                for c in range(b_ld // len(halves)):
+                    if nt:
+                        soff = f"{c * rows_a}u * pb + (unsigned)k0 * 2u"
+                    else:
+                        soff = f"(unsigned)(k0 + {c * (T // nc)}) * pb"
+                    at = f"{base} + " if base else ""
+                    out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds({rsrc}, AK_LDS(&ak_sb{s}[{at}({c * T} + wave * 64) * 8]), "
+                               f"16, b_voff, {soff}, 0, 0);")
             out.append(f"{ind}}}")
             return out
 
@@ -1377,16 +1464,18 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
       {"tr_out += " + now + " - tr_o0;" if self.trace else ""}
       continue;
     }}""")
+        # the second accumulator of each pair (two right operands), at the same output position
+        acc2_line = " const float acc2_v = acc[i_][j_ + " + str(nio) + "][g4 * 4 + e4];" if dual else ""
         old_loop = f"""#pragma unroll
-      for (int j_ = 0; j_ < {ni}; ++j_) {{
+      for (int j_ = 0; j_ < {nio}; ++j_) {{
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {{
-          const int ec0 = sn * {bn} + wn * {wtn} + j_ * 32 + g4 * 8 + (lane_e >> 5) * 4;
+          const int ec0 = sn * {bn} + wn * {wto} + j_ * 32 + g4 * 8 + (lane_e >> 5) * 4;
           float res[4];
 #pragma unroll
           for (int e4 = 0; e4 < 4; ++e4) {{
             const int ec = ec0 + e4;
-            const float acc_v = acc[i_][j_][g4 * 4 + e4];
+            const float acc_v = acc[i_][j_][g4 * 4 + e4];{acc2_line}
             (void)ec; (void)er;
             {epi}
             res[e4] = (float)({result});
@@ -1396,7 +1485,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
       }}
     }}"""
         paired_loop = f"""#pragma unroll
-      for (int j_ = 0; j_ < {ni}; ++j_) {{
+      for (int j_ = 0; j_ < {nio}; ++j_) {{
 #pragma unroll
         for (int p2 = 0; p2 < 2; ++p2) {{
           // groups 2 p2 and 2 p2 + 1, then one exchange with lane ^ 32: each lane stores 8 consecutive
@@ -1405,12 +1494,12 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) {{
             const int g4 = 2 * p2 + h2;
-            const int ec0 = sn * {bn} + wn * {wtn} + j_ * 32 + g4 * 8 + (lane_e >> 5) * 4;
+            const int ec0 = sn * {bn} + wn * {wto} + j_ * 32 + g4 * 8 + (lane_e >> 5) * 4;
             float res[4];
 #pragma unroll
             for (int e4 = 0; e4 < 4; ++e4) {{
               const int ec = ec0 + e4;
-              const float acc_v = acc[i_][j_][g4 * 4 + e4];
+              const float acc_v = acc[i_][j_][g4 * 4 + e4];{acc2_line}
               (void)ec; (void)er;
               {epi}
               res[e4] = (float)({result});
@@ -1424,7 +1513,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
           const auto s0 = __builtin_amdgcn_permlane32_swap(pk[0][0], pk[1][0], false, false);
           const auto s1 = __builtin_amdgcn_permlane32_swap(pk[0][1], pk[1][1], false, false);
           const ak_u32x4 v = ak_u32x4{{s0[0], s1[0], s0[1], s1[1]}};
-          const int ec8 = sn * {bn} + wn * {wtn} + j_ * 32 + 16 * p2 + (up ? 8 : 0);
+          const int ec8 = sn * {bn} + wn * {wto} + j_ * 32 + 16 * p2 + (up ? 8 : 0);
           *(ak_u32x4*)((ak_u16*){O} + obase + (long long)er * {ldo} + ec8) = v;
         }}
       }}

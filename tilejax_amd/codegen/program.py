@@ -70,6 +70,7 @@ class Program:
     lds_bytes: int = 0
     notes: Dict[str, Any] = field(default_factory=dict)  # what the lowering chose (hardware tiles, ...)
     protocol: Any = field(default=None, repr=False, compare=False)  # the LDS ring's events (protocol.Recorder)
+    parts: Tuple[Any, ...] = field(default=(), repr=False, compare=False)  # the programs a composite one joins
     _modules: Dict[int, runtime.Module] = field(default_factory=dict, repr=False)
     _tables: Dict[int, Dict[str, torch.Tensor]] = field(default_factory=dict, repr=False)
 
@@ -150,7 +151,7 @@ class Program:
             placeholders = {name: _Null() for name in self.workspace}
             args = pack(launch.args, arrays, outputs, tables, placeholders)
             pointer_args = [a for a in launch.args if a.kind != "int"]
-            placed = [(8 * i, *layout[a.key]) for i, a in enumerate(pointer_args) if a.kind == "workspace"]
+            placed = [(8 * i, *_placed(layout, a.key)) for i, a in enumerate(pointer_args) if a.kind == "workspace"]
             module.kernel(launch.symbol).launch_scratch(launch.grid, launch.block, launch.lds, args, stream, placed)
 
     def step_tables(self, *arrays: torch.Tensor) -> Dict[str, torch.Tensor]:
@@ -182,6 +183,14 @@ class Program:
         return outputs, workspace
 
 
+def _placed(layout: Dict[str, Tuple[int, int]], key: Any) -> Tuple[int, int]:
+    """Where a workspace argument sits in the scratch array: (offset, bytes) of its buffer, or past a byte
+    offset into it."""
+    name, offset = key if isinstance(key, tuple) else (key, 0)
+    at, n = layout[name]
+    return at + offset, n - offset
+
+
 def _poisoned(shape, dtype: torch.dtype, device) -> torch.Tensor:
     """An output of a poisoned build: NaN, or -1 for an integer dtype."""
     fill = float("nan") if dtype.is_floating_point else -1
@@ -210,8 +219,9 @@ def pack(args: Sequence[Arg], arrays: Sequence[torch.Tensor], outputs: Sequence[
             pointers.append(outputs[a.key].data_ptr())
         elif a.kind in ("table", "state"):
             pointers.append(tables[a.key].data_ptr())
-        elif a.kind == "workspace":
-            pointers.append(workspace[a.key].data_ptr())
+        elif a.kind == "workspace":  # a name, or (name, byte offset) for a pointer into the buffer
+            name, offset = a.key if isinstance(a.key, tuple) else (a.key, 0)
+            pointers.append(workspace[name].data_ptr() + offset if offset else workspace[name].data_ptr())
         else:
             raise KernelError(f"unknown argument kind {a.kind}")
     data = struct.pack(f"<{len(pointers)}Q", *pointers) + struct.pack(f"<{len(ints)}i", *ints)

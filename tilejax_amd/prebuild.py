@@ -57,6 +57,10 @@ def standard() -> Iterator[Tuple[object, tuple]]:
                                    ((16384, 4096, 14336, 8, 64), GT(512, 512))):
         yield moe.grouped_matmul, (_bf16(m, k), _bf16(e, k, n), _i32(g), tiles)
     yield moe.grouped_matmul, (_f32(1024, 512), _f32(4, 512, 1024), _i32(4), GT(512, 256))
+    ET = moe.ExpertTiles
+    for (m, d, f, e, t), tiles in (((512, 256, 512, 4, 4), ET(128)), ((512, 256, 512, 4, 4), ET(512)),
+                                   ((1024, 256, 512, 4, 8), ET(128)), ((16384, 4096, 14336, 8, 64), ET(256))):
+        yield moe.expert_ffn, (_bf16(m, d), _bf16(e, d, f), _bf16(e, d, f), _bf16(e, f, d), _i32(t), tiles)
     from examples import rmsnorm_matmul as rm
 
     R = rm.NormMatmulTiles

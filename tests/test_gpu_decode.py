@@ -221,3 +221,33 @@ def test_depths_the_tuner_tries(buffers, cursor):
     got = lowered.run(*(t.cuda() for t in ins))
     torch.cuda.synchronize()
     _close(f"paged decode depth {buffers} cursor={cursor}", got, kernels.paged_gqa_decode(*ins), ins)
+
+
+@pytest.mark.parametrize("cursor", [False, True])
+def test_merge_in_the_attention_kernel_is_bit_equal(cursor):
+    """The knob "fold" merges each sequence's partials in the attention kernel: the last workgroup to finish a
+    sequence (a device counter per sequence, left at zero for the next call) merges it after an agent-scope
+    acquire, each workgroup's partials released by one fence at its exit. The same partials summed in the
+    same order: bit-equal to the merge launch's output, on two calls in a row (the counters reset)."""
+    from tilejax_amd.tune import Config
+
+    g = torch.Generator().manual_seed(21)
+    B, pages, P, W = 8, 128, 16, 1024
+    q = (torch.randn(B, 1, 32, 128, generator=g) * 128 ** -0.5).to(torch.bfloat16).cuda()
+    kp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    vp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    table = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32).cuda()
+    lengths = torch.tensor([0, 1, 17, 300, 2048, 777, 1500, 2000], dtype=torch.int32).cuda()
+    ins = (q, kp, vp, table, lengths)
+    sig = paged_gqa_decode.signature(*ins)
+    base = paged_gqa_decode.default_config(sig)
+    plain = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor))
+    folded = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor, (("fold", 1),)))
+    assert folded.program.notes["merge_folded"] and not plain.program.notes["merge_folded"]
+    print(f"decode merge folded, cursor={cursor}", flush=True)
+    want = plain.run(*ins)
+    for call in range(2):
+        got = folded.run(*ins)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"call {call}"
+    assert not folded.program.device_tables(q.device)["dc_arrive"].any()  # every counter back at zero

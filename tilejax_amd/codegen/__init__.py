@@ -119,7 +119,7 @@ def _generate(plan: Plan, schedule: Schedule, pipeline: Pipeline, *, trace: bool
             return flash.lower(plan, schedule, pipeline, found, name, trace=trace, hardware=hardware)
         found = decode.match(plan)
         if found is not None:
-            return decode.lower(plan, schedule, pipeline, found, name, trace=trace, cursor=cursor)
+            return decode.lower(plan, schedule, pipeline, found, name, trace=trace, cursor=cursor, hardware=hardware)
     except KernelError as e:
         family_error = e
         if hardware:  # knobs of the family's kernel shape: that shape doesn't build, whatever else would

@@ -59,6 +59,12 @@ SUB = 16  # key positions per kernel step: a spec step of P positions (a page, a
 SP = SUB + 4  # floats per row of a wave's partial S in LDS (padded: rows 80 bytes apart)
 DEPTH = 3  # K register sets and V LDS stages (steps fetched ahead of the one computed): the default
 MAX_DEPTH = 4
+# The merge in the attention kernel (`_Decode._fold_merge`, the hardware knob "fold") rather than a launch of
+# its own: correct (tests/test_gpu_decode.py), but slower. At BASELINE config 5 the call took 312 us with a
+# release fence in every wave and 249 us with one per workgroup, against 214 us with the merge launch: each
+# agent-scope release writes the XCD's L2 back, each acquire invalidates it, and the merges then read the
+# partials from memory. So it is off unless asked for.
+FOLD_DEFAULT = False
 
 
 @dataclass
@@ -119,7 +125,7 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
 
 class _Decode:
     def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False,
-                 cursor: bool = False, depth: int = DEPTH) -> None:
+                 cursor: bool = False, depth: int = DEPTH, fold: bool = FOLD_DEFAULT) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
         self.trace, self.cursor, self.depth = trace, cursor, depth
         # eight waves where the width splits into them (an eighth each, a multiple of 32), else four
@@ -144,8 +150,19 @@ class _Decode:
             raise KernelError(f"decode over {sch.pattern_steps} pattern steps of {m.page} x {m.width} needs "
                               f"{self.lds} bytes of LDS per workgroup (gfx950 has {gfx950.LDS_BYTES})")
         self.phase = plan.phases[0].range
-        if (min(self.grid, self.phase.count * self.sub) + 1) * RP * 4 > 96 * 1024:
+        # partials per tile: at most its kernel steps or the grid (+1 for the division's edges)
+        self.maxs = min(self.grid, self.phase.count * self.sub) + 1
+        if self.maxs * RP * 4 > 96 * 1024:
             raise KernelError("too many pages per sequence for the merge kernel's LDS")
+        # With `fold` the merge runs in the attention kernel (the last workgroup to finish a tile merges it), its
+        # LDS (the partials' weights and row sums) beside the kernel's own; else it is a launch of its own.
+        merge_lds = self.maxs * m.rows * 4 + m.rows * 4 + 16
+        if fold and self.lds + merge_lds > gfx950.LDS_BYTES:
+            raise KernelError(f"the decode merge in the attention kernel needs {self.lds + merge_lds} bytes of LDS "
+                              f"per workgroup (gfx950 has {gfx950.LDS_BYTES})")
+        self.fold = fold
+        if self.fold:
+            self.lds += merge_lds
         self.index = Index(plan, lambda v: f"lv_{v}")
         self.seg0 = plan.scopes["seg0"]
         # The setup and merge kernels split each tile's elements over `chunks` workgroups (grid y), enough for
@@ -218,14 +235,20 @@ class _Decode:
         if self.trace:
             workspace[TRACE] = self.grid * TRACE_FIELDS * 8
             args.append(Arg("workspace", TRACE, "unsigned long long* __restrict__", TRACE))
+        # with the merge in the attention kernel: per tile, the workgroups done with it (zero between calls)
+        state = {"dc_arrive": sch.pattern_tiles} if self.fold else {}
+        if self.fold:
+            args.append(Arg("state", "dc_arrive", "int* __restrict__", "dc_arrive"))
         struct = c_struct(f"{self.name}_args", args)
         # With step tables the query rows are set up by extra workgroups of the table builder's launch (they
         # need no table); with a cursor, by a launch of their own.
         source = "\n".join([f"// Generated by tilejax_amd for `{plan.nest.name}`: gfx950 split-KV decode attention.",
                             PRELUDE, struct, self._setup_source() if self.cursor else "", self._attention_source(),
-                            self._merge_source()])
-        launches = [Launch(self.name, args, (self.grid, 1, 1), (self.threads, 1, 1), 0),
-                    Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1), (self.threads, 1, 1), 0)]
+                            "" if self.fold else self._merge_source()])
+        launches = [Launch(self.name, args, (self.grid, 1, 1), (self.threads, 1, 1), 0)]
+        if not self.fold:
+            launches.append(Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1),
+                                   (self.threads, 1, 1), 0))
         if self.cursor:
             launches.insert(0, Launch(f"{self.name}_setup", args, (sch.pattern_tiles, self.setup_chunks, 1),
                                       (self.threads, 1, 1), 0))
@@ -233,9 +256,9 @@ class _Decode:
             name=self.name, source=source,
             launches=launches,
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
-            tables=tables, workspace=workspace, lds_bytes=self.lds, protocol=self.protocol,
+            tables=tables, workspace=workspace, state=state, lds_bytes=self.lds, protocol=self.protocol,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
-                   "cursor": self.cursor,
+                   "cursor": self.cursor, "merge_folded": self.fold,
                    # trace regions cover the attention kernel; a slice is one kernel step, SUB positions
                    "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": self.sub},
         )
@@ -315,6 +338,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(c
         w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][5];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {self.name}_args args) {{
+  {f"__shared__ float dc_w[{self.maxs}][{m.rows}], dc_lsum[{m.rows}]; __shared__ int dc_last;" if self.fold else ""}
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   {self._trace_start()}
@@ -562,6 +586,12 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
             ind = ind[:-2]
             w(f"{ind}}}")
         w("  flush(cur_t);")
+        if self.fold:
+            if self.trace:
+                w(f"  const unsigned long long tr_m0 = {NOW};")
+            w(self._fold_merge("cs_start[{}]" if self.cursor else "args.rt_tile_steps[{}]"))
+            if self.trace:
+                w(f"  tr_out += {NOW} - tr_m0;  // the merges count as output time")
         if self.trace:
             w(f"  {self._trace_write('n')}")
         w("}")
@@ -660,15 +690,14 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
                 f"tr[0] = tr_fill + tr_wait; tr[1] = tr_fill; tr[2] = tr_out; "
                 f"tr[3] = tr_e - tr_i0 - tr_fill - tr_wait - tr_out; tr[4] = (unsigned long long)({steps}); {CLOCK_END} }}")
 
-    def _merge_source(self) -> str:
-        plan, sch, m = self.plan, self.sch, self.m
+    def _merge_body(self, e_begin: str, e_end: str) -> str:
+        """Merge tile `t`'s `n` partials (slots t + w0 onwards: row max m, row sum l, accumulator) and write
+        its output elements [e_begin, e_end), per element, by the workgroup's threads; `dc_w` and `dc_lsum`
+        are LDS arrays of the caller's."""
+        plan, m = self.plan, self.m
         R, W = m.rows, m.width
-        U = self.sub
-        # partials per tile: at most its kernel steps or the grid (+1 for the division's edges)
-        maxs = min(self.grid, self.phase.count * U) + 1
         out_shape = m.out.tile.shape
-        index = self.index
-        o_base, o_str = tile_base(m.out.tile, m.out.shape, index, lambda v: f"lv_{v}")
+        o_base, o_str = tile_base(m.out.tile, m.out.shape, self.index, lambda v: f"lv_{v}")
 
         def mleaf(n: Node, idx: Tuple[str, ...]) -> Optional[str]:
             if n is m.acc_leaf:
@@ -680,26 +709,13 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
             return None
 
         expr = self._emitter(mleaf).at(m.value.node, tuple(f"o{k}" for k in range(len(out_shape))))
-        total = math.prod(out_shape)
         unravel = []
         rest = "e"
         for k, st in enumerate(strides(out_shape)):
             unravel.append(f"const int o{k} = ({rest}) / {st};")
             rest = f"({rest}) % {st}"
         flat_out = " + ".join(f"(long long)o{k} * {s}" for k, s in enumerate(o_str))
-        chunk = -(-total // self.merge_chunks)
-        return f"""
-// Merge a tile's partials (row max m, row sum l, accumulator) and write its output, per element; workgroup\n// (t, y) writes chunk y of tile t's elements, each computing the tile's partial weights.
-extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_merge(const {self.name}_args args) {{
-  __shared__ float dc_w[{maxs}][{R}];
-  __shared__ float dc_lsum[{R}];
-  const int t = blockIdx.x;
-  {self._decode_tile("t")}
-  const int count = args.rt_count[0] * {U};  // kernel steps, as the attention kernel divides them
-  const int per = (count + {self.grid - 1}) / {self.grid};
-  const int ts = args.rt_tile_steps[t] * {U}, te = args.rt_tile_steps[t + 1] * {U};
-  const int w0 = ts / per, w1 = (te - 1) / per;
-  const int n = w1 - w0 + 1;
+        return f"""  {self._decode_tile("t")}
   // The partials' loads go out four at a time (they are independent); the sums run in partial order.
   for (int r = threadIdx.x; r < {R}; r += {self.threads}) {{
     const float* mp = args.dc_m + (t + w0) * {RP} + r;
@@ -737,20 +753,84 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_merge(c
     return v;
   }};
   ak_u16* op = args.{m.out.name}_out + ({o_base});
-  const int e1 = ak_imin((int)(blockIdx.y + 1) * {chunk}, {total});
-  for (int e = blockIdx.y * {chunk} + threadIdx.x; e < e1; e += {self.threads}) {{
+#pragma unroll 4
+  for (int e = {e_begin} + (int)threadIdx.x; e < {e_end}; e += {self.threads}) {{
     {" ".join(unravel)}
     op[{flat_out}] = (ak_u16)ak_bf16_bits((float)({expr}));
-  }}
+  }}"""
+
+    def _merge_source(self) -> str:
+        """The merge kernel, where the attention kernel doesn't merge (`fold` off): workgroup (t, y) merges
+        tile t's partials and writes chunk y of its elements, each computing the tile's partial weights."""
+        R = self.m.rows
+        total = math.prod(self.m.out.tile.shape)
+        chunk = -(-total // self.merge_chunks)
+        return f"""
+// Merge a tile's partials (row max m, row sum l, accumulator) and write its output, per element; workgroup
+// (t, y) writes chunk y of tile t's elements, each computing the tile's partial weights.
+extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_merge(const {self.name}_args args) {{
+  __shared__ float dc_w[{self.maxs}][{R}];
+  __shared__ float dc_lsum[{R}];
+  const int t = blockIdx.x;
+  const int count = args.rt_count[0] * {self.sub};  // kernel steps, as the attention kernel divides them
+  const int per = (count + {self.grid - 1}) / {self.grid};
+  const int ts = args.rt_tile_steps[t] * {self.sub}, te = args.rt_tile_steps[t + 1] * {self.sub};
+  const int w0 = ts / per, w1 = (te - 1) / per;
+  const int n = w1 - w0 + 1;
+{self._merge_body(f"(int)blockIdx.y * {chunk}", f"ak_imin((int)(blockIdx.y + 1) * {chunk}, {total})")}
 }}
+"""
+
+    def _fold_merge(self, tile_start: str) -> str:
+        """The attention kernel's exit: the merge, by the last workgroup to finish each tile. One release
+        fence makes this workgroup's partials visible device-wide; then, for each tile its steps covered
+        (`tile_start(t)`: the tile's first table step), a count of the workgroups done with it (device
+        state, left at zero for the next call by the one that merges). A tile wholly inside this workgroup
+        is merged at once; the workgroup that brings a shared tile's count to its number of workgroups
+        takes an acquire fence and merges it."""
+        U = self.sub
+        total = math.prod(self.m.out.tile.shape)
+        return f"""  // every thread's partial stores have reached the L2; then one wave's release fence writes the XCD's L2
+  // back for the whole workgroup (a fence in every wave would write it back once per wave)
+  AK_WAIT_VM(0);
+  __syncthreads();
+  if (wave == 0) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  {{
+    const int t_lo = dc_st[0][0], t_hi = dc_st[n - 1][0];
+    for (int t = t_lo; t <= t_hi; ++t) {{
+      const int ts = ({tile_start.format("t")}) * {U}, te = ({tile_start.format("t + 1")}) * {U};
+      const int w0 = ts / per, w1 = (te - 1) / per;
+      if (w1 > w0) {{
+        if (tid == 0) dc_last = atomicAdd(&args.dc_arrive[t], 1) == w1 - w0;
+        __syncthreads();
+        const bool last = dc_last;
+        __syncthreads();
+        if (!last) continue;
+        if (tid == 0) __hip_atomic_store(&args.dc_arrive[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the other workgroups' partials: one wave invalidates the CU's L1 and the XCD's L2 for all
+        if (wave == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __syncthreads();
+      }}
+      {{
+        const int n = w1 - w0 + 1;
+{self._merge_body("0", str(total))}
+      }}
+      __syncthreads();  // (dc_w and dc_lsum are the next tile's)
+    }}
+  }}
 """
 
 
 def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: str, trace: bool = False,
-          cursor: bool = False) -> Program:
+          cursor: bool = False, hardware: Optional[Dict[str, int]] = None) -> Program:
     """The decode program; its depth (K register sets and V LDS stages: steps fetched ahead) is the
-    pipeline's input buffers, 2 to MAX_DEPTH."""
+    pipeline's input buffers, 2 to MAX_DEPTH. The `hardware` knob "fold" (0 or 1) puts the merge in the
+    attention kernel."""
     if m.out.dtype.name != "bfloat16":
         raise KernelError("the gfx950 decode lowering stores bf16 outputs")
+    knobs = dict(hardware or {})
+    fold = bool(knobs.pop("fold", FOLD_DEFAULT))
+    if knobs:
+        raise KernelError(f"the decode lowering has no hardware knobs {sorted(knobs)}")
     depth = max(2, min(pipeline.input_buffers, MAX_DEPTH))
-    return _Decode(plan, sch, m, name, trace, cursor, depth).program()
+    return _Decode(plan, sch, m, name, trace, cursor, depth, fold).program()

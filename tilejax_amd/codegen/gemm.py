@@ -369,6 +369,12 @@ def match(plan: Plan) -> Optional[GemmMatch]:
                      tuple(pre), tuple(stats.items()), mp, b2, acc2_leaf)
 
 
+def _tile_level(phase: Any) -> bool:
+    """Does the reduction loop's mask (if any) leave its variable unread, so it keeps a tile's blocks all or
+    none?"""
+    return phase.mask is None or phase.var not in {n.id for n in ast.walk(phase.mask) if isinstance(n, ast.Name)}
+
+
 def _windows(op: Operand) -> Tuple[Tuple[Any, ...], ...]:
     """Where an operand's tile sits: each dim's loop, offset and size, and its runtime index's expression."""
     return tuple((w.loop, w.offset, w.size, ast.dump(w.index) if w.index is not None else None, w.index_loops)
@@ -1040,8 +1046,14 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
                 f"const int sbeg = __builtin_amdgcn_readfirstlane({offs}[tt_s]), send = {offs}[tt_s + 1];",
                 f"const int nsteps = (({codes}[sbeg] >> 2) & 1) ? 0 : send - sbeg;",
             ]
-            kval = (f"({phase.start} + (({codes}[sbeg + st_] >> {CODE_SHIFT}) / {sch.iterations} / "
-                    f"{sch.phase_radix}) * {phase.step})")
+            if _tile_level(phase) and len(plan.phases) == 1:
+                # A mask that doesn't read the reduction loop's variable keeps all of a tile's blocks or none:
+                # a kept tile's steps are the loop's blocks in order, so the K offset is arithmetic. (Read from
+                # the step code, it is a global load and a wait for it before every slice's loads are issued.)
+                kval = f"({phase.start} + st_ * {phase.step})"
+            else:
+                kval = (f"({phase.start} + (({codes}[sbeg + st_] >> {CODE_SHIFT}) / {sch.iterations} / "
+                        f"{sch.phase_radix}) * {phase.step})")
         if self.x3:  # the parts arrays hold kx slices for each of the operand's
             kval = f"({self.kx} * {kval})"
 

@@ -30,9 +30,13 @@ def strides(shape: Sequence[int]) -> List[int]:
 
 class Index:
     """C expressions for index-array elements, `lengths[b]` -> `args.lengths[b]`, clamped into the array's
-    dims where `clamp` (a runtime window index, which JAX clamps into the dim it indexes)."""
+    dims where `clamp` (a runtime window index, which JAX clamps into the dim it indexes). With `constant`,
+    elements are read through the constant address space (`ak_ldc`): inputs no kernel writes, so where the
+    index is uniform the read is a scalar load and leaves the vector memory queue's wait counts to the data
+    loads."""
 
-    def __init__(self, plan: Plan, names: Callable[[str], Optional[str]], args: str = "args") -> None:
+    def __init__(self, plan: Plan, names: Callable[[str], Optional[str]], args: str = "args",
+                 constant: bool = False) -> None:
         loops = {r.var for r in plan.loops}
 
         def resolve(v: str) -> Optional[str]:
@@ -45,7 +49,7 @@ class Index:
                 return str(value)
             return names(v)
 
-        self.plan, self.names, self.args = plan, resolve, args
+        self.plan, self.names, self.args, self.constant = plan, resolve, args, constant
 
     def read(self, node: ast.Subscript) -> str:
         ix = self.plan.index(node.value.id)  # type: ignore[attr-defined]
@@ -53,6 +57,8 @@ class Index:
         flat = "0"
         for d, (expr, stride) in enumerate(zip(dims, strides(ix.shape))):
             flat = f"({flat} + {self.expr(expr)} * {stride})"
+        if self.constant:
+            return f"ak_ldc({self.args}.{ix.name}, {flat})"
         return f"{self.args}.{ix.name}[{flat}]"
 
     def expr(self, node: ast.expr) -> str:
@@ -79,8 +85,9 @@ def tile_base(tile: Tile, shape: Sequence[int], index: Index, loop_value: Callab
     return (" + ".join(terms) if terms else "0"), sliced
 
 
-def decode_tile(plan: Plan, sch: Schedule, t: str, prefix: str = "lv_") -> List[str]:
-    """C statements setting `<prefix><var>` to each parallel loop's value at tile `t` (the t-th that runs)."""
+def decode_tile(plan: Plan, sch: Schedule, t: str, prefix: str = "lv_", constant: bool = False) -> List[str]:
+    """C statements setting `<prefix><var>` to each parallel loop's value at tile `t` (the t-th that runs);
+    with `constant`, the tile tables are read through the constant address space (`ak_ldc`)."""
     lines = []
     outer, inner = sch.outer, sch.inner
     if sch.tile_tables:
@@ -90,7 +97,8 @@ def decode_tile(plan: Plan, sch: Schedule, t: str, prefix: str = "lv_") -> List[
             lines.append(f"const int {prefix}{r.var} = {r.start} + ({rest} % {r.count}) * {r.step};")
             rest = f"({rest} / {r.count})"
         for r in inner:
-            lines.append(f"const int {prefix}{r.var} = {r.start} + args.{TILE_TABLE % r.var}[tt_] * {r.step};")
+            read = f"ak_ldc(args.{TILE_TABLE % r.var}, tt_)" if constant else f"args.{TILE_TABLE % r.var}[tt_]"
+            lines.append(f"const int {prefix}{r.var} = {r.start} + {read} * {r.step};")
     else:
         rest = t
         for r in reversed(plan.parallel):
@@ -99,15 +107,17 @@ def decode_tile(plan: Plan, sch: Schedule, t: str, prefix: str = "lv_") -> List[
     return lines
 
 
-def decode_fill(plan: Plan, sch: Schedule, f: str, prefix: str = "lv_") -> List[str]:
-    """C statements setting each parallel loop's value at the f-th tile a mask skips."""
+def decode_fill(plan: Plan, sch: Schedule, f: str, prefix: str = "lv_", constant: bool = False) -> List[str]:
+    """C statements setting each parallel loop's value at the f-th tile a mask skips (`constant`: as in
+    `decode_tile`)."""
     lines = [f"const int frep_ = {f} / {sch.pattern_fills}, ff_ = {f} % {sch.pattern_fills};"]
     rest = "frep_"
     for r in reversed(sch.outer):
         lines.append(f"const int {prefix}{r.var} = {r.start} + ({rest} % {r.count}) * {r.step};")
         rest = f"({rest} / {r.count})"
     for r in sch.inner:
-        lines.append(f"const int {prefix}{r.var} = {r.start} + args.{FILL_TABLE % r.var}[ff_] * {r.step};")
+        read = f"ak_ldc(args.{FILL_TABLE % r.var}, ff_)" if constant else f"args.{FILL_TABLE % r.var}[ff_]"
+        lines.append(f"const int {prefix}{r.var} = {r.start} + {read} * {r.step};")
     return lines
 
 

@@ -1002,7 +1002,10 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         kslices = m.tk // bk * self.kx  # K slices per step (with f32 operands, of the parts arrays)
         split, split_slices = (self.split[1], self.split[2]) if self.split else (1, 0)
         kvar = m.kvar
-        index = Index(plan, lambda v: f"lv_{v}")
+        # tables and index inputs are read through the constant address space: scalar loads, which leave the
+        # vector memory queue's in-order wait counts to the LDS loads in flight (a vector load of a table at an
+        # item's start would wait for the next item's prefetched slices too)
+        index = Index(plan, lambda v: f"lv_{v}", constant=True)
         a_shape, b_shape = self._shape("a"), self._shape("b")
         no_k = lambda v: "0" if v == kvar else f"lv_{v}"  # the reduction loop's offset goes per slice
         a_base, a_str = tile_base(m.a.tile, a_shape, index, no_k)
@@ -1043,8 +1046,8 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
                                                                                             "args.rt_tile_steps")
             steps_setup = [
                 f"const int tt_s = t % {sch.pattern_tiles};",
-                f"const int sbeg = __builtin_amdgcn_readfirstlane({offs}[tt_s]), send = {offs}[tt_s + 1];",
-                f"const int nsteps = (({codes}[sbeg] >> 2) & 1) ? 0 : send - sbeg;",
+                f"const int sbeg = __builtin_amdgcn_readfirstlane(ak_ldc({offs}, tt_s)), send = ak_ldc({offs}, tt_s + 1);",
+                f"const int nsteps = ((ak_ldc({codes}, sbeg) >> 2) & 1) ? 0 : send - sbeg;",
             ]
             if _tile_level(phase) and len(plan.phases) == 1:
                 # A mask that doesn't read the reduction loop's variable keeps all of a tile's blocks or none:
@@ -1052,7 +1055,7 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
                 # the step code, it is a global load and a wait for it before every slice's loads are issued.)
                 kval = f"({phase.start} + st_ * {phase.step})"
             else:
-                kval = (f"({phase.start} + (({codes}[sbeg + st_] >> {CODE_SHIFT}) / {sch.iterations} / "
+                kval = (f"({phase.start} + ((ak_ldc({codes}, sbeg + st_) >> {CODE_SHIFT}) / {sch.iterations} / "
                         f"{sch.phase_radix}) * {phase.step})")
         if self.x3:  # the parts arrays hold kx slices for each of the operand's
             kval = f"({self.kx} * {kval})"
@@ -1107,13 +1110,13 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_rows(const {
         a_numel, b_numel = int(np.prod(a_shape)), int(np.prod(b_shape))
         fill_value = literal(m.out.fill if m.out.fill is not None else 0, m.out.dtype)
         const_value = literal(self.const_value if self.const_value is not None else 0.0, m.out.dtype)
-        tile_decode = "\n    ".join(decode_tile(plan, sch, "t"))
+        tile_decode = "\n    ".join(decode_tile(plan, sch, "t", constant=True))
         fill_block = ""
         # a traced kernel counts the stores of filled and constant tiles as output time
         tr_s0 = f"const unsigned long long tr_s0 = {NOW}; " if self.trace else ""
         tr_s1 = f" tr_out += {NOW} - tr_s0;" if self.trace else ""
         if sch.fills:
-            fill_decode = "\n      ".join(decode_fill(plan, sch, "t"))
+            fill_decode = "\n      ".join(decode_fill(plan, sch, "t", constant=True))
             fill_block = (f"if (kind == 1) {{\n      {fill_decode}\n      const long long obase = {o_base};\n      "
                           f"{tr_s0}{_store_constant(bm, bn, out_bf16, O, 'obase', ldo, fill_value, T)}{tr_s1}\n"
                           f"      continue;\n    }}")
@@ -1170,7 +1173,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
         if self.n_small:
             pull = f"""    int t, code, slot;
     if (q < q_end) {{
-      t = args.items[3 * q]; code = args.items[3 * q + 1]; slot = args.items[3 * q + 2]; ++q;
+      t = ak_ldc(args.items, 3 * q); code = ak_ldc(args.items, 3 * q + 1); slot = ak_ldc(args.items, 3 * q + 2); ++q;
     }} else {{  // this workgroup's own list is done: the next item of the shared queue, if any is left
       if (tid == 0) ak_pulled = atomicAdd(&args.queue[0], 1);
       __syncthreads();
@@ -1188,7 +1191,8 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
   }
 """
         else:
-            pull = "    const int t = args.items[3 * q], code = args.items[3 * q + 1], slot = args.items[3 * q + 2];"
+            pull = ("    const int t = ak_ldc(args.items, 3 * q), code = ak_ldc(args.items, 3 * q + 1), "
+                    "slot = ak_ldc(args.items, 3 * q + 2);")
             loop_head = "  for (int q = q_begin; q < q_end; ++q) {"
             tail = ""
         self._queue_tail = tail
@@ -1212,7 +1216,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
   // Item q2's loads: its slices and operand offsets; false if it loads nothing (a filled or constant tile,
   // or one without steps).
   auto probe = [&](int q2, int& T_, int& g0_, int& sb_, long long& aoff_, long long& boff_{", long long& boff2_" if dual else ""}) -> bool {{
-    const int t = args.items[3 * q2], code = args.items[3 * q2 + 1], slot = args.items[3 * q2 + 2];
+    const int t = ak_ldc(args.items, 3 * q2), code = ak_ldc(args.items, 3 * q2 + 1), slot = ak_ldc(args.items, 3 * q2 + 2);
     const int sub = code & 0xffff, kind = code >> 16;
     (void)slot;
     if (kind == 1 || kind == 2) return false;
@@ -1227,7 +1231,7 @@ extern "C" __global__ void __launch_bounds__({T}) {self.name}(const {self.name}_
     return T > 0;
   }};
   int pf_q = -1;  // the item whose first {S} slices are in flight"""
-        w(f"""  const int q_begin = args.wg_items[blockIdx.x], q_end = args.wg_items[blockIdx.x + 1];
+        w(f"""  const int q_begin = ak_ldc(args.wg_items, blockIdx.x), q_end = ak_ldc(args.wg_items, blockIdx.x + 1);
   {"__shared__ int ak_pulled;" if self.n_small else ""}
   {trace_decl}{probe}
 {loop_head}

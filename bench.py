@@ -224,7 +224,8 @@ def main() -> int:
     ap.add_argument("--traffic", default="", help="HBM bytes per dense launch (FETCH+WRITE), from rocprofv3; "
                     "default: profiles/traffic.json")
     ap.add_argument("--calibrate-copy", action="store_true",
-                    help="first copy a 1 GiB tensor once: the known-size kernel rocprofv3 counters are scaled by")
+                    help="first fill a 1 GiB tensor and negate it once: the known-size kernels rocprofv3 counters are "
+                         "scaled by")
     ap.add_argument("--warm-seconds", type=float, default=1.0,
                     help="seconds of untimed back-to-back calls before each leg's warm-up steps")
     ap.add_argument("--sweep", action="store_true",
@@ -250,9 +251,10 @@ def main() -> int:
     from examples.matmul import MatmulTiles, matmul
 
     if args.calibrate_copy:
+        # kernels of known size for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE: a 1 GiB fill (writes 1 GiB)
+        # and a negation of it (reads 1 GiB and writes 1 GiB; no other leg runs torch.neg)
         src = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")  # 1 GiB
-        dst = torch.empty_like(src)
-        dst.copy_(src)
+        dst = torch.neg(src)
         torch.cuda.synchronize()
         del src, dst
 

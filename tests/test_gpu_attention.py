@@ -151,3 +151,24 @@ def test_kernel_shapes_the_tuner_tries(hardware, buffers):
     got = lowered.run(q.cuda(), k.cuda(), v.cuda())
     torch.cuda.synchronize()
     _close(f"attention {hardware} {buffers}", got, kernels.causal_attention(q, k, v, 256, 256), _floor(q, k, v))
+
+
+@pytest.mark.parametrize("shape,blocks", [((2, 4, 1024, 128), (256, 256)), ((1, 2, 1024, 128), (256, 256))])
+def test_k_fragments_in_registers_are_bit_equal(shape, blocks):
+    """The knob `kreg` loads each block's K fragments from memory straight into registers (LDS holds V only).
+    The S products read the same K values in the same order, so the output is the default kernel's, bit for
+    bit, split tiles included (both shapes split their longest items)."""
+    from tilejax_amd.tune import Config
+
+    q, k, v = _inputs(*shape, seed=4)
+    sig = causal_attention.signature(q, k, v)
+    base = causal_attention.default_config(sig)
+    tiles = AttentionBlocks(*blocks)
+    plain = causal_attention.lowered(sig, Config(tiles, base.pipeline, False, ()))
+    kreg = causal_attention.lowered(sig, Config(tiles, base.pipeline, False, (("kreg", 1),)))
+    assert kreg.program.lds_bytes * 2 == plain.program.lds_bytes
+    print(f"attention {shape} {blocks} with K in registers", flush=True)
+    dev = (q.cuda(), k.cuda(), v.cuda())
+    want, got = plain.run(*dev), kreg.run(*dev)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

@@ -65,6 +65,9 @@ MAX_AHEAD = 3
 WAVES = 4  # waves per workgroup (None: 8 for tiles of a multiple of 256 query rows, else 4)
 BKV = 64  # keys per block (a multiple of 32)
 K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
+# With K in registers (knob `kreg`): register sets of K fragments. With two, the next block's set is loaded
+# while this block's is read; with one, it is loaded over this block's once the S product has read it.
+KREG_SETS = 1
 V_AHEAD = 4  # V fragments in flight ahead of the O MFMAs
 # Split-KV: a work item's cost is its key blocks plus ITEM_COST (its Q load, pipeline fill and stores); a
 # workgroup's share is the total over the resident workgroups (two per CU). Items above SPLIT_ABOVE shares
@@ -299,13 +302,18 @@ class _Flash:
                               f"rows (got {m.rows})")
         self.bq = 32 * self.nw
         self.bkv = hardware.get("bkv", BKV)
+        # K fragments loaded from memory straight into registers (a register set per block, the next block's
+        # loaded after this block's S product) rather than through LDS, which then holds V only
+        self.kreg = bool(hardware.get("kreg", 0))
+        if self.kreg and self.ahead != 1:
+            raise KernelError("K fragments in registers are loaded one block ahead: two LDS stages for V")
         # split-KV above this many shares, in tenths (0: never split)
         self.split_tenths = hardware.get("split", round(10 * SPLIT_ABOVE))
         if self.split_tenths < 0:
             raise KernelError(f"the split share is a number of tenths of a share, 0 or more (got {self.split_tenths})")
         if m.bk % self.bkv:
             raise KernelError(f"the gfx950 attention lowering needs key blocks of a multiple of {self.bkv} (got {m.bk})")
-        lds = self.stages * self.bkv * (m.d + m.dv) * 2
+        lds = self.stages * self.bkv * ((0 if getattr(self, 'kreg', False) else m.d) + m.dv) * 2
         if lds > gfx950.LDS_BUDGET:
             raise KernelError(f"{self.stages} LDS stages of {self.bkv} keys (head dims {m.d}, {m.dv}) take {lds} bytes of "
                               f"LDS per workgroup; gfx950 has {gfx950.LDS_BUDGET}")
@@ -449,7 +457,7 @@ class _Flash:
     def program(self) -> Program:
         plan, sch, m = self.plan, self.sch, self.m
         items, weights, blocks = self._items()
-        lds = self.stages * self.bkv * (m.d + m.dv) * 2
+        lds = self.stages * self.bkv * ((0 if getattr(self, 'kreg', False) else m.d) + m.dv) * 2
         lanes = gfx950.CUS * max(1, min(2, gfx950.LDS_BYTES // lds))
         items, weights, merges = self._split(items, weights, lanes)
         self.slots = sum(c for _, _, _, c in merges)
@@ -614,8 +622,12 @@ class _Flash:
 // spec tile {m.rows} x {m.bk} (head dims {D}, {DV}); workgroup {bq} query rows in {nw} waves, key blocks of {bkv}.
 {PRELUDE}
 {struct}""")
+        kreg = self.kreg
+        if kreg and ldk != kstride_j:
+            raise KernelError("K fragments in registers need key rows one row pitch apart")
         for s in range(self.stages):
-            w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
+            if not kreg:
+                w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
         w(f"""
 extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.name}_args args) {{
@@ -671,6 +683,11 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
   float m_run = {literal(m.m_init)}, l_run = 0.f;""")
+        if kreg:
+            w(f"""  // K fragments straight from memory (srcA of S^T = K Q^T): key row 32 t + lane % 32 of the block, head dims
+  // 16 s + 8 (lane / 32) .. + 8; one register set per block, alternating
+  const unsigned kr_voff = (unsigned)((lane & 31) * {ldk * 2} + 16 * (lane >> 5));
+  {" ".join(f"ak_bf16x8 kr{k}[{kt * ds}];" for k in range(KREG_SETS))}""")
         tr = self.trace
         if tr:
             # trace regions: the wait for block 0 is the pipeline fill; later blocks' waits (their loads and the
@@ -692,8 +709,10 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
 
         def issue(r: int, s: int, ind: str) -> List[str]:
             out = [f"{ind}{{ const int kpos = bj[{r}] + {self.kwin.offset} + bc[{r}], vpos = bj[{r}] + {self.vwin.offset} + bc[{r}];"]
+            if kreg:
+                out[0] += " (void)kpos;"
             rows_k, rows_v = T // chk, T // chv
-            for c in range(ldk_n):
+            for c in range(0 if kreg else ldk_n):
                 out.append(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, AK_LDS(&ak_sk{s}[({c * T} + wave * 64) * 8]), 16, k_voff[{c % vo_n}], "
                            f"(unsigned)((kpos + {c * rows_k}) * {kstride_j * 2}), 0, 0);")
             for c in range(ldv_n):
@@ -704,6 +723,16 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
 
         v_order = [(kk, dt) for kk in range(ks) for dt in range(dt_n)]
         v_ahead = min(V_AHEAD, len(v_order))
+        k_order = [(t, sl) for sl in range(ds) for t in range(kt)]
+
+        def k_issue(r: int, kset: int, ind: str) -> List[str]:
+            """The K fragments of the block at ring slot r into register set `kset` (with `kreg`)."""
+            out = [f"{ind}{{ const unsigned ko_ = (unsigned)((bj[{r}] + {self.kwin.offset} + bc[{r}]) * {ldk * 2});"]
+            for i, (t, sl) in enumerate(k_order):
+                out.append(f"{ind}  kr{kset}[{i}] = __builtin_bit_cast(ak_bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, "
+                           f"kr_voff + {t * 32 * ldk * 2 + sl * 32}u, ko_, 0));")
+            out.append(f"{ind}}}")
+            return out
 
         def v_read(i: int, ind: str) -> str:
             kk, dt = v_order[i]
@@ -727,12 +756,16 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
                     a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);")
             return o
 
-        def compute(s: int, ind: str, r: Optional[int] = None) -> List[str]:
-            """Block b_ from stage s: S^T, the mask, the online softmax into `pf`, and O^T += V^T P^T."""
+        def compute(s: int, ind: str, r: Optional[int] = None, kset: int = 0) -> List[str]:
+            """Block b_ from stage s: S^T, the mask, the online softmax into `pf`, and O^T += V^T P^T (with
+            `kreg`, K from register set `kset`, and the next block's K loaded into the other after S)."""
             o: List[str] = []
             a = o.append
             a(f"{ind}if (b_ < n_w) {{")
-            a(f"{ind}  const char* ks = (const char*)ak_sk{s}; const char* vs = (const char*)ak_sv{s}; (void)vs;")
+            if kreg:
+                a(f"{ind}  const char* vs = (const char*)ak_sv{s};")
+            else:
+                a(f"{ind}  const char* ks = (const char*)ak_sk{s}; const char* vs = (const char*)ak_sv{s}; (void)vs;")
             r = s if r is None else r
             a(f"{ind}  const int lv_{jvar} = bj[{r}], ec0 = bc[{r}] + (lane >> 5) * 4;")
             a(f"{ind}  ak_f32x16 st[{kt}];")
@@ -741,25 +774,34 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
                 a(f"{ind}  for (int r = 0; r < 16; ++r) st[{t}][r] = 0.f;")
             # S^T = K Q^T: the key tiles' MFMA chains alternate (a chain's next MFMA waits for its last), and
             # the K fragments are read K_AHEAD MFMAs ahead of use, so LDS latency stays hidden.
-            order = [(t, sl) for sl in range(ds) for t in range(kt)]
-            ahead = min(K_AHEAD, len(order))
-            a(f"{ind}  ak_bf16x8 kf[{len(order)}];")
-            for i, (t, sl) in enumerate(order[:ahead]):
-                a(f"{ind}  kf[{i}] = *(const ak_bf16x8*)(ks + k_roff[{sl}] + {t * 32 * D * 2});")
-            for i, (t, sl) in enumerate(order):
-                a(f"{ind}  st[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[{i}], qf[{sl}], st[{t}], 0, 0, 0);")
-                if i + ahead < len(order):
-                    t2, sl2 = order[i + ahead]
-                    a(f"{ind}  kf[{i + ahead}] = *(const ak_bf16x8*)(ks + k_roff[{sl2}] + {t2 * 32 * D * 2});")
+            order = k_order
+            ahead = 0 if kreg else min(K_AHEAD, len(order))
+            if kreg:
+                for i, (t, sl) in enumerate(order):
+                    a(f"{ind}  st[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr{kset}[{i}], qf[{sl}], st[{t}], 0, 0, 0);")
+                # the next block's K into the other set, beside the softmax and O^T of this one
+                a(f"{ind}  if (b_ + 1 < n_w) {{")
+                o.extend(k_issue((r + 1) % self.ring, KREG_SETS - 1 - kset, ind + "    "))
+                a(f"{ind}  }}")
+            else:
+                a(f"{ind}  ak_bf16x8 kf[{len(order)}];")
+                for i, (t, sl) in enumerate(order[:ahead]):
+                    a(f"{ind}  kf[{i}] = *(const ak_bf16x8*)(ks + k_roff[{sl}] + {t * 32 * D * 2});")
+                for i, (t, sl) in enumerate(order):
+                    a(f"{ind}  st[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[{i}], qf[{sl}], st[{t}], 0, 0, 0);")
+                    if i + ahead < len(order):
+                        t2, sl2 = order[i + ahead]
+                        a(f"{ind}  kf[{i + ahead}] = *(const ak_bf16x8*)(ks + k_roff[{sl2}] + {t2 * 32 * D * 2});")
             # O^T += V^T P^T: its first V_AHEAD fragments (two transposed reads each) go out now, beside the
             # S MFMAs and the softmax.
             a(f"{ind}  ak_bf16x8 vf[{len(v_order)}];")
             for i in range(v_ahead):
                 a(v_read(i, ind))
-            a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, {ahead}, 0);")
+            if ahead:
+                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, {ahead}, 0);")
             for i in range(len(order)):
                 a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
-                if i + ahead < len(order):
+                if ahead and i + ahead < len(order):
                     a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);")
             a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, {2 * v_ahead}, 0);")
             # the mask's scores in place (blocks the mask keeps whole skip it); then one max for both
@@ -817,10 +859,16 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
         w(f"  int bj[{self.ring}], bc[{self.ring}];  // table entries of blocks b .. b + {self.ring - 1}, at b mod {self.ring}")
         for x in range(self.ahead + 1):
             w(entry_load(str(x), x, "  "))
+        if kreg:
+            per_block = ldv_n  # (the LDS ring holds V only)
         for s in range(self.ahead):
             w(f"  if ({s} < nblk) {{")
             L.extend(issue(s, s, "    "))
             rec.add(("load", s, s, per_block), lambda n, s=s: s < n)
+            w("  }")
+        if kreg:
+            w("  if (0 < n_w) {")
+            L.extend(k_issue(0, 0, "    "))
             w("  }")
         rec.loop(unroll)
         w("  ak_bf16x8 pf[" + str(ks) + "];  // P^T of the block (srcB of O^T = V^T P^T)")
@@ -849,7 +897,7 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
                    lambda b, n, A=self.ahead: b + A < n)
             w("        }")
             w(entry_load(f"b_ + {self.ahead + 1}", (r_ + self.ahead + 1) % self.ring, "        "))
-            L.extend(compute(s, "        ", r_))
+            L.extend(compute(s, "        ", r_, p_ % KREG_SETS))
             rec.at(p_, lambda b, n, st=s: ("read", st, b))
             w("      }")
             w("    }")

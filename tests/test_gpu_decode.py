@@ -224,6 +224,44 @@ def test_depths_the_tuner_tries(buffers, cursor):
 
 
 @pytest.mark.parametrize("cursor", [False, True])
+def test_waves_with_their_own_rows_are_bit_equal(cursor):
+    """Each wave scores its own query rows against its own kv head's columns and loads its own columns of V
+    (the default where the spec's rows are block-diagonal): every other column contributed exact zeros to
+    those scores, so the output is bit-equal to the kernel whose waves share the scores through LDS."""
+    from tilejax_amd.tune import Config
+
+    g = torch.Generator().manual_seed(23)
+    B, pages, P, W = 8, 128, 16, 1024
+    q = (torch.randn(B, 1, 32, 128, generator=g) * 128 ** -0.5).to(torch.bfloat16).cuda()
+    kp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    vp = torch.randn(B * pages, P, W, generator=g).to(torch.bfloat16).cuda()
+    table = torch.randperm(B * pages, generator=g).reshape(B, pages).to(torch.int32).cuda()
+    lengths = torch.tensor([0, 1, 17, 300, 2048, 777, 1500, 2000], dtype=torch.int32).cuda()
+    ins = (q, kp, vp, table, lengths)
+    sig = paged_gqa_decode.signature(*ins)
+    base = paged_gqa_decode.default_config(sig)
+    own = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor))
+    shared = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor, (("own", 0),)))
+    assert own.program.notes["own_rows"] and not shared.program.notes["own_rows"]
+    print(f"decode own rows vs shared scores, cursor={cursor}", flush=True)
+    want = shared.run(*ins)
+    got = own.run(*ins)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_multi_head_decode_gives_each_wave_one_head():
+    """MHA (8 query heads, 8 kv heads): 8 query rows, a row a wave, the kernel's other 24 rows owned by none."""
+    ins = _inputs(4, 8, 8, 128, 16, 64, (0, 33, 700, 1024), seed=5)
+    lowered = _with_tables(paged_gqa_decode, ins)
+    assert lowered.program.notes["own_rows"]
+    print("paged decode MHA 8 heads", flush=True)
+    got = lowered.run(*(t.cuda() for t in ins))
+    torch.cuda.synchronize()
+    _close("paged decode MHA", got, kernels.paged_gqa_decode(*ins), ins)
+
+
+@pytest.mark.parametrize("cursor", [False, True])
 def test_merge_in_the_attention_kernel_is_bit_equal(cursor):
     """The knob "fold" merges each sequence's partials in the attention kernel: the last workgroup to finish a
     sequence (a device counter per sequence, left at zero for the next call) merges it after an agent-scope

@@ -210,3 +210,67 @@ def test_decode_sets_up_query_rows_in_the_builders_launch():
         assert [ln.symbol for ln in folded.launches] == [first, "tj_paged_gqa_decode"]
         assert folded.notes["merge_folded"] and folded.state == {"dc_arrive": 4}
         assert "_merge(" not in folded.source and "__ATOMIC_RELEASE" in folded.source
+
+
+def _decode_signature(kernel, B, T, H, Hkv, pages=64, P=16, D=128):
+    I32 = jaxlite.int32
+    return kernel.signature(((B, T, H, D), BF16), ((B * pages, P, Hkv * D), BF16), ((B * pages, P, Hkv * D), BF16),
+                            ((B, pages), I32), ((B,), I32))
+
+
+@pytest.mark.parametrize("T,H,Hkv,owners", [
+    (1, 32, 8, [h // 4 for h in range(32)]),  # GQA: four query heads a kv head, a kv head a wave
+    (1, 8, 8, list(range(8))),  # MHA: a head a wave
+    (2, 16, 4, None),  # four kv heads: a head's 128 columns are two waves' spans of 64
+])
+def test_decode_waves_own_their_query_rows(T, H, Hkv, owners):
+    """Where each query row's values sit in one wave's span of columns (found by running the spec's setup and
+    epilogue eagerly), each wave scores its own rows and loads its own columns of V, and the kernel step has no
+    workgroup barrier; elsewhere the waves share the scores through LDS."""
+    from examples.decode import paged_gqa_decode
+    from tilejax_amd.codegen import decode
+    from tilejax_amd.tune import Config
+
+    sig = _decode_signature(paged_gqa_decode, 4, T, H, Hkv)
+    base = paged_gqa_decode.default_config(sig)
+    lowered = paged_gqa_decode.lowered(sig, base)
+    m = decode.match(lowered.plan)
+    assert decode.row_owners(lowered.plan, m, m.width // decode.WAVES) == owners
+    prog = lowered.program
+    assert prog.notes["own_rows"] == (owners is not None)
+    shared = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, False, (("own", 0),))).program
+    assert not shared.notes["own_rows"]
+    if owners is None:
+        assert prog.source == shared.source
+        return
+    assert "dc_owner" in prog.source and "dc_owner" not in shared.source
+    # the shared kernel synchronises the workgroup every step; the own-rows kernel only at its start
+    barriers = [sum(ev[0] == "barrier" for ev in p.protocol.replay(n)) for p in (prog, shared) for n in (2, 10)]
+    assert barriers[0] == barriers[1] and barriers[3] > barriers[2]
+
+
+@pytest.mark.parametrize("was,now", [
+    # every query row dense across the width: no row has one wave's span
+    ("block_diagonal(query_rows(q[b, :, :, :]), group, Hkv, dtype)",
+     "jnp.tile(query_rows(q[b, :, :, :]), (1, Hkv)).astype(dtype)"),
+    # the epilogue reads every row's first block, outside most rows' spans
+    ("own_blocks(acc, group, Hkv)", "acc[:, :Dh]"),
+    # the setup reads an index array, whose values the probe cannot know
+    ("block_diagonal(query_rows(q[b, :, :, :]), group, Hkv, dtype)",
+     "block_diagonal(query_rows(q[b, :, :, :]) * (lengths[b] > 0).astype(jnp.float32), group, Hkv, dtype)"),
+])
+def test_decode_rows_the_probe_does_not_give_to_one_wave(was, now):
+    import inspect
+
+    import examples.decode as ed
+    from tests.helpers import make_kernel, spec
+
+    source = inspect.getsource(ed.gqa_decode.fn.__wrapped__).split("\n", 1)[1]  # without the decorator
+    assert was in source
+    names = ("LANES", "MASK_VALUE", "row_index", "block_diagonal", "query_rows", "visible", "online_softmax",
+             "finish", "own_blocks", "widen", "DecodeTiles")
+    args = (spec(4, 1, 32, 128, dtype=BF16), spec(4, 2048, 1024, dtype=BF16), spec(4, 2048, 1024, dtype=BF16),
+            spec(4, dtype=jaxlite.int32))
+    assert make_kernel(source, **{n: getattr(ed, n) for n in names}).lower(*args).program.notes["own_rows"]
+    prog = make_kernel(source.replace(was, now), **{n: getattr(ed, n) for n in names}).lower(*args).program
+    assert prog.notes["family"] == "decode" and not prog.notes["own_rows"]

@@ -133,7 +133,7 @@ def test_planted_mistakes_fail():
                   AttentionBlocks(256, 256)).program.protocol.replay(6)
     args = (spec(5, 1, 32, 128, dtype=BF), spec(500, 16, 1024, dtype=BF), spec(500, 16, 1024, dtype=BF),
             spec(5, 100, dtype=I32), spec(5, dtype=I32))
-    dc = _lowered(paged_gqa_decode, args, None, 3).program.protocol.replay(8)
+    dc = _lowered(paged_gqa_decode, args, None, 3, (("own", 0),)).program.protocol.replay(8)
     for name, events in (("matmul", mm), ("attention", fa), ("decode", dc)):
         check(events, name)
         with pytest.raises(ProtocolError):  # (the first block's barriers can be redundant)
@@ -142,3 +142,24 @@ def test_planted_mistakes_fail():
             check(_loosen(events, 2), f"{name} with a loose wait")
     with pytest.raises(ProtocolError, match="still read"):  # the matmul's wait for its LDS reads dropped
         check(_drop(mm, "wait_lgkm", 1), "matmul without a read wait")
+
+
+@pytest.mark.parametrize("cursor", [False, True])
+def test_decode_waves_with_their_own_rows(cursor):
+    """Decode whose waves own their query rows: each wave loads its own columns of V into a region of the stage
+    only it reads ("read_mine"), so its own waits order its loads and reads and no step has a barrier. A
+    wait loosened, or the wait for the reads before the region's next load dropped, must fail."""
+    args = (spec(5, 1, 32, 128, dtype=BF), spec(500, 16, 1024, dtype=BF), spec(500, 16, 1024, dtype=BF),
+            spec(5, 100, dtype=I32), spec(5, dtype=I32))
+    prog = _lowered(paged_gqa_decode, args, None, 3, cursor=cursor).program
+    assert prog.notes["own_rows"]
+    for steps in range(1, 14):
+        events = prog.protocol.replay(steps)
+        check(events, f"decode with own rows, {steps} steps")
+        assert not any(ev[0] == "barrier" for ev in events)
+        assert {ev[0] for ev in events} >= {"read_mine", "read_own"} and not any(ev[0] == "read" for ev in events)
+    events = prog.protocol.replay(8)
+    with pytest.raises(ProtocolError, match="before its loads landed"):
+        check(_loosen(events, 2), "own rows with a loose wait")
+    with pytest.raises(ProtocolError, match="still read"):
+        check(_drop(events, "wait_lgkm", 1), "own rows without a read wait")

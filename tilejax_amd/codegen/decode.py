@@ -30,6 +30,7 @@ one, `k_pages[block_tables[b, p], :, :]`, or `k_cache[b, j : j + bk, :]`), runs 
 
 from __future__ import annotations
 
+import ast
 import math
 from dataclasses import dataclass
 from typing import Any, Dict, List, Optional, Tuple
@@ -65,6 +66,12 @@ MAX_DEPTH = 4
 # agent-scope release writes the XCD's L2 back, each acquire invalidates it, and the merges then read the
 # partials from memory. So it is off unless asked for.
 FOLD_DEFAULT = False
+# Waves that own their query rows (`row_owners`), where the spec's structure shows it (the hardware knob "own",
+# on unless set to 0): each wave scores its own rows against its own columns, loads its own columns of V into
+# a region of the stage only it reads, and the step has no workgroup barrier. Every other wave's columns
+# contributed exact zeros to those rows' scores, so the output is bit-equal to the shared-score kernel's; at
+# BASELINE config 5 the call went from 222 to 202 us with step tables and from 226 to 208 us with a cursor.
+OWN_DEFAULT = True
 
 
 @dataclass
@@ -80,6 +87,92 @@ class DecodeMatch:
     value: Any
     acc_leaf: Node
     sum_leaf: Node
+
+
+def row_owners(plan: Plan, m: DecodeMatch, span: int) -> Optional[List[int]]:
+    """For each query row, the one span of `span` columns its query values can be nonzero in, if every row
+    has one and the epilogue reads each row's accumulator only there; else None. The spec's own setup and
+    epilogue code is run eagerly on concrete inputs (four draws: normal, normal times 1e4, uniform in
+    [0.5, 1.5), and its negation): a value zero in all of them is taken to be zero by construction (the
+    block-diagonal query rows of GQA decode: a query head's values sit in its kv head's columns). Setup or
+    epilogue code that reads an integer input (an index array, whose values the probe cannot know) makes it
+    decline. For the epilogue, the accumulator is NaN outside each row's span, and the output must come out
+    finite. Rows with no nonzero value (none, for real queries) are given span 0."""
+    import torch
+
+    nest = plan.nest
+    seg0, last = plan.segments[0], plan.segments[-1]
+    qn = m.sm.qk.args[0]
+    if not (_is(qn, "carried") and qn.kwargs["name"] in m.sm.consts):
+        return None
+    q_name = qn.kwargs["name"]
+    rows, width = m.rows, m.width
+    if width % span:
+        return None
+    integers = {name for name, spec in zip(nest.params, plan.inputs) if spec.dtype.name in ("int32", "int64")}
+    read = {n.id for stmt in (*seg0, *last) for n in ast.walk(stmt) if isinstance(n, ast.Name)}
+    if integers & read:
+        return None
+
+    def run(stmts, env):
+        exec(compile(ast.Module(body=list(stmts), type_ignores=[]), f"<{nest.name}: row owners>", "exec"), env)
+
+    def draw(kind, shape, g):
+        if kind < 2:
+            return torch.randn(shape, generator=g) * (1e4 if kind else 1.0)
+        u = torch.rand(shape, generator=g) + 0.5
+        return u if kind == 2 else -u
+
+    nonzero = None
+    envs = []
+    for kind in range(4):
+        g = torch.Generator().manual_seed(kind + 1)
+        env = dict(plan.env)
+        for name, spec in zip(nest.params, plan.inputs):
+            if name in read:
+                t = draw(kind, spec.shape, g).to(spec.dtype.torch)
+            else:  # an input the setup and epilogue don't read (the cache): zeros of its shape, no memory
+                t = torch.zeros((), dtype=spec.dtype.torch).expand(spec.shape)
+            env[name] = jaxlite.asarray(t)
+        for r in plan.parallel:
+            env[r.var] = r.start + (r.count - 1) * r.step * (kind % 2)  # the first tile, then the last
+        try:
+            run(seg0, env)
+        except Exception:
+            return None
+        qt = env.get(q_name)
+        t = getattr(qt, "t", None) if qt is not None else None
+        if t is None or tuple(t.shape) != (rows, width):
+            return None
+        nz = t.float() != 0
+        nonzero = nz if nonzero is None else nonzero | nz
+        envs.append(env)
+    owners = []
+    for r in range(rows):
+        spans = sorted({int(c) // span for c in torch.nonzero(nonzero[r]).flatten().tolist()})
+        if len(spans) > 1:
+            return None
+        owners.append(spans[0] if spans else 0)
+    # the epilogue reads each row's accumulator only in its span
+    env = envs[0]
+    acc = torch.full((rows, width), float("nan"))
+    for r, o in enumerate(owners):
+        acc[r, o * span:(o + 1) * span] = torch.rand(span) + 0.5
+    env[m.sm.acc_name] = jaxlite.asarray(acc)
+    for name in (m.sm.l_name, m.sm.m_name):
+        cur = env.get(name)
+        shape = tuple(cur.t.shape) if getattr(cur, "t", None) is not None else (rows, 128)
+        env[name] = jaxlite.asarray(torch.rand(shape) + 0.5)
+    out = m.out
+    env[out.name] = jaxlite.zeros(out.shape, out.dtype)
+    try:
+        run(last, env)
+    except Exception:
+        return None
+    result = getattr(env.get(out.name), "t", None)
+    if result is None or not torch.isfinite(result.float()).all():
+        return None
+    return owners
 
 
 def match(plan: Plan) -> Optional[DecodeMatch]:
@@ -125,7 +218,7 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
 
 class _Decode:
     def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False,
-                 cursor: bool = False, depth: int = DEPTH, fold: bool = FOLD_DEFAULT) -> None:
+                 cursor: bool = False, depth: int = DEPTH, fold: bool = FOLD_DEFAULT, own: bool = OWN_DEFAULT) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
         self.trace, self.cursor, self.depth = trace, cursor, depth
         # eight waves where the width splits into them (an eighth each, a multiple of 32), else four
@@ -136,6 +229,9 @@ class _Decode:
                               f"of {SUB} positions and widths that are multiples of {32 * self.waves} "
                               f"(got {m.rows}, {m.page}, {m.width})")
         self.sub = m.page // SUB  # kernel steps per spec step
+        # Each query row's one wave (`row_owners`): with them, a wave computes its own rows' scores alone and
+        # loads its own columns of V, and the step needs no workgroup barrier
+        self.owners = row_owners(plan, m, m.width // self.waves) if own else None
         if sch.repeats != 1:
             raise KernelError("decode with parallel loops the runtime mask doesn't read is not lowered yet")
         self.grid = gfx950.CUS
@@ -258,7 +354,7 @@ class _Decode:
             outputs=[(m.out.shape, m.out.dtype)], inputs=[(s.shape, s.dtype) for s in plan.inputs],
             tables=tables, workspace=workspace, state=state, lds_bytes=self.lds, protocol=self.protocol,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
-                   "cursor": self.cursor, "merge_folded": self.fold,
+                   "cursor": self.cursor, "merge_folded": self.fold, "own_rows": self.owners is not None,
                    # trace regions cover the attention kernel; a slice is one kernel step, SUB positions
                    "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": self.sub},
         )
@@ -328,6 +424,53 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(c
 
         score = self._emitter(sleaf).at(m.sm.score, ("er", "ep"))
         chunks = W // 8
+        own = self.owners is not None
+        cw = WQ // 8  # 16-byte chunks of a wave's columns per row
+        vrow = WQ if own else W  # elements per V row in a stage (a wave's region, or the whole width)
+        acc_store = (f"""float* ap = args.dc_acc + (long long)slot * {RP * W} + row * {W} + cb + (lane >> 5) * 4;
+#pragma unroll
+    for (int dt = 0; dt < {dtiles}; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *(ak_f32x4*)(ap + 32 * dt + 8 * g4) = ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};""")
+        if own:
+            # each row's statistics and accumulator come from the wave that owns it (rows past R: none)
+            flush_body = (f"""if (dc_owner[row] == wave) {{  // this wave's rows: their statistics and columns
+      if (lane < 32) {{
+        args.dc_m[slot * {RP} + row] = m_run;
+        args.dc_l[slot * {RP} + row] = l_run;
+      }}
+      {acc_store}
+    }}""")
+        else:
+            flush_body = (f"""if (wave == 0 && lane < 32) {{
+      args.dc_m[slot * {RP} + row] = m_run;
+      args.dc_l[slot * {RP} + row] = l_run;
+    }}
+    {acc_store}""")
+        if own:
+            # each wave loads its own columns of V into its own region of the stage (rows of WQ elements)
+            v_load_setup = f"""// V loads: each wave its own {WQ} columns, into its own region of the stage: chunk position
+  // p = c * 64 + lane, row p / {cw}, chunk p % {cw}, rows swizzled for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2).
+  unsigned v_voff[{loads}];
+#pragma unroll
+  for (int c = 0; c < {loads}; ++c) {{
+    const int p = c * 64 + lane, row = p / {cw}, ch = p % {cw};
+    v_voff[c] = (unsigned)(row * {ldv * 2} + cb * 2 + ((ch ^ (((row & 3) << 2) & {cw - 1})) * 16));
+  }}"""
+            v_roff_line = (f"const int c = 32 * dt + 16 * (G & 1) + 4 * (s & 3); v_roff[dt] = wave * {P * WQ * 2} + "
+                           f"pos * {WQ * 2} + ((((c >> 3) ^ (((pos & 3) << 2) & {cw - 1}))) << 4) + (c & 7) * 2;")
+        else:
+            v_load_setup = f"""// V loads: LDS chunk position p = c * {self.threads} + tid: row p / {chunks}, chunk p % {chunks}, rows swizzled
+  // for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2).
+  unsigned v_voff[{loads}];
+#pragma unroll
+  for (int c = 0; c < {loads}; ++c) {{
+    const int p = c * {self.threads} + tid, row = p / {chunks}, ch = p % {chunks};
+    v_voff[c] = (unsigned)(row * {ldv * 2} + ((ch ^ ((row & 3) << 2)) * 16));
+  }}"""
+            v_roff_line = ("const int c = cb + 32 * dt + 16 * (G & 1) + 4 * (s & 3);\n"
+                           f"      v_roff[dt] = pos * {W * 2} + ((((c >> 3) ^ ((pos & 3) << 2))) << 4) + (c & 7) * 2;")
         L: List[str] = []
         w = L.append
         for s in range(D):  # one array per stage: the compiler then keeps the other stages' loads in flight
@@ -336,6 +479,10 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(c
         # and two 16-byte reads per lane), rows padded to SP floats so 16 lanes' rows fall in distinct banks
         w(f"__shared__ __attribute__((aligned(16))) float dc_sp[{self.waves}][{RP}][{SP}];")
         w(f"__shared__ __attribute__((aligned(16))) int dc_st[{self.max_per}][5];")
+        if own:
+            owner = list(self.owners) + [-1] * (RP - len(self.owners))
+            w(f"// each query row's wave (its values lie in that wave's columns only); rows past R: none")
+            w(f"__constant__ int dc_owner[{RP}] = {{{', '.join(map(str, owner))}}};")
         w(f"""
 extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {self.name}_args args) {{
   {f"__shared__ float dc_w[{self.maxs}][{m.rows}], dc_lsum[{m.rows}]; __shared__ int dc_last;" if self.fold else ""}
@@ -366,14 +513,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
       (int)({math.prod(k_shape)}LL * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)args.{m.v.tile.array}, (short)0,
       (int)({math.prod(v_shape)}LL * 2), 0x00020000);
-  // V loads: LDS chunk position p = c * {self.threads} + tid: row p / {chunks}, chunk p % {chunks}, rows swizzled
-  // for ds_read_b64_tr_b16 (chunk ^ (row & 3) << 2).
-  unsigned v_voff[{loads}];
-#pragma unroll
-  for (int c = 0; c < {loads}; ++c) {{
-    const int p = c * {self.threads} + tid, row = p / {chunks}, ch = p % {chunks};
-    v_voff[c] = (unsigned)(row * {ldv * 2} + ((ch ^ ((row & 3) << 2)) * 16));
-  }}
+  {v_load_setup}
   // K fragments (srcA of S^T, 16x16x32) straight from HBM into registers: position lane % 16, columns
   // cb + 32 s + 8 (lane / 16)
   const unsigned k_voff = (unsigned)((lane & 15) * {ldk * 2} + (cb + 8 * (lane >> 4)) * 2);
@@ -383,8 +523,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
     const int G = lane >> 4, s = lane & 15, pos = 8 * (G >> 1) + (s >> 2);
 #pragma unroll
     for (int dt = 0; dt < {dtiles}; ++dt) {{
-      const int c = cb + 32 * dt + 16 * (G & 1) + 4 * (s & 3);
-      v_roff[dt] = pos * {W * 2} + ((((c >> 3) ^ ((pos & 3) << 2))) << 4) + (c & 7) * 2;
+      {v_roff_line}
     }}
   }}
   ak_bf16x8 qf[2][{slabs}];
@@ -396,16 +535,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
     {f"const unsigned long long tr_f0 = {NOW};" if self.trace else ""}
     const int slot = t + blockIdx.x;
     const int row = lane & 31;
-    if (wave == 0 && lane < 32) {{
-      args.dc_m[slot * {RP} + row] = m_run;
-      args.dc_l[slot * {RP} + row] = l_run;
-    }}
-    float* ap = args.dc_acc + (long long)slot * {RP * W} + row * {W} + cb + (lane >> 5) * 4;
-#pragma unroll
-    for (int dt = 0; dt < {dtiles}; ++dt)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4)
-        *(ak_f32x4*)(ap + 32 * dt + 8 * g4) = ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};
+    {flush_body}
     {f"tr_out += {NOW} - tr_f0;" if self.trace else ""}
   }};
   auto start_tile = [&](int t) {{
@@ -438,11 +568,15 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
                 f"{ind}}}",
             ]
 
+        def v_dest(c: int) -> str:
+            """The stage element instruction c of this thread's V loads starts at (1 KiB per wave)."""
+            return f"wave * {P * WQ} + {c * 64 * 8}" if own else f"({c * self.threads} + wave * 64) * 8"
+
         def issue_v(x: str, vs: int, ind: str) -> List[str]:
             return [
                 f"{ind}{{ const int x_ = {x}; const unsigned ob_ = x_ < n ? 0u : 0x80000000u;",
                 f"{ind}  const int vo_ = __builtin_amdgcn_readfirstlane(dc_st[ak_imin(x_, n - 1)][3]);",
-                *(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, AK_LDS(&dc_sv{vs}[({c * self.threads} + wave * 64) * 8]), 16, "
+                *(f"{ind}  __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, AK_LDS(&dc_sv{vs}[{v_dest(c)}]), 16, "
                   f"v_voff[{c}] + ob_, vo_, 0, 0);" for c in range(loads)),
                 f"{ind}}}",
             ]
@@ -460,11 +594,15 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
                 a(f"{ind}  const unsigned long long tr_w0 = {NOW}, tr_o0 = tr_out;")
             a(f"{ind}  if (t != cur_t) {{ if (cur_t >= 0) flush(cur_t); start_tile(t); cur_t = t; AK_WAIT_VM(0); }}")
             a(f"{ind}  AK_WAIT_VM({wait_n});")
-            # every wave is past step j - 1, so its V stage is free; every thread's part of V(j) has landed
-            a(f'{ind}  asm volatile("s_barrier" ::: "memory");')
-            if record:
-                rec.at(u, lambda b, n: ("wait_vm", wait_n))
-                rec.at(u, lambda b, n: ("barrier",))
+            if own:  # V(j) is in this wave's own region: its own wait suffices
+                if record:
+                    rec.at(u, lambda b, n: ("wait_vm", wait_n))
+            else:
+                # every wave is past step j - 1, so its V stage is free; every thread's part of V(j) has landed
+                a(f'{ind}  asm volatile("s_barrier" ::: "memory");')
+                if record:
+                    rec.at(u, lambda b, n: ("wait_vm", wait_n))
+                    rec.at(u, lambda b, n: ("barrier",))
             if self.trace:
                 # the first step's wait is the pipeline fill; a flush inside the wait is output time
                 a(f"{ind}  {{ const unsigned long long d_ = {NOW} - tr_w0 - (tr_out - tr_o0);"
@@ -474,7 +612,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
                 rec.at(u, lambda b, n, st=(u + D - 1) % D: ("load", st, b + D - 1, loads))
                 # V(j) is visible (its wait, then the barrier): its V^T fragments are read now, so the P V
                 # MFMAs after the softmax don't wait for LDS
-                rec.at(u, lambda b, n, st=u: ("read", st, b))
+                rec.at(u, lambda b, n, st=u: ("read_mine" if own else "read", st, b))
                 rec.at(u, lambda b, n, ku=u: ("read_own", ("k", ku), b))  # the S product reads kb{u}
             a(f"{ind}  const bool run = !(code & 4);")
             a(f"{ind}  ak_bf16x8 vf[{dtiles}];")
@@ -484,7 +622,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int dt = 0; dt < {dtiles}; ++dt) {{")
             a(f"{ind}      const ak_i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt]));")
-            a(f"{ind}      const ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt] + {4 * W * 2}));")
+            a(f"{ind}      const ak_i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(AK_LDS4(vs + v_roff[dt] + {4 * vrow * 2}));")
             a(f"{ind}      vf[dt] = __builtin_bit_cast(ak_bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));")
             a(f"{ind}    }}")
             a(f"{ind}    ak_f32x4 st[4] = {{ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}, ak_f32x4{{0.f, 0.f, 0.f, 0.f}}}};")
@@ -507,22 +645,30 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
             a(f"{ind}    {self._decode_tile('t')}")
             a(f"{ind}    const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step}; (void)lv_{jvar};")
             a(f"{ind}    const int su = __builtin_amdgcn_readfirstlane(dc_st[j_][4]); (void)su;")
-            # an LDS-only barrier: the pages in flight stay in flight
+            # an LDS-only barrier: the pages in flight stay in flight (with rows of its own, a wave reads back
+            # only its own partial S: its own wait suffices)
             a(f"{ind}    AK_WAIT_LGKM0();")
-            a(f'{ind}    asm volatile("s_barrier" ::: "memory");')
+            if not own:
+                a(f'{ind}    asm volatile("s_barrier" ::: "memory");')
             if record:
                 rec.at(u, lambda b, n: ("wait_lgkm",))
-                rec.at(u, lambda b, n: ("barrier",))
+                if not own:
+                    rec.at(u, lambda b, n: ("barrier",))
             # softmax: lane = query row er, positions 8 (lane / 32) + e
             # the lane's row; the mask sees rows past R (zero queries, never stored) as row R - 1
             a(f"{ind}    const int lr = lane & 31, er = {'lr' if m.rows == RP else f'ak_imin(lr, {m.rows - 1})'};")
             a(f"{ind}    float sc[8];")
-            a(f"{ind}    ak_f32x4 s_lo = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5)], s_hi = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5) + 4];")
-            a(f"{ind}    #pragma unroll")
-            a(f"{ind}    for (int w_ = 1; w_ < {self.waves}; ++w_) {{")
-            a(f"{ind}      s_lo += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5)];")
-            a(f"{ind}      s_hi += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5) + 4];")
-            a(f"{ind}    }}")
+            if own:
+                # the rows this wave owns have their whole S here (the other waves' are zeros for them); its
+                # other rows are computed but never stored
+                a(f"{ind}    const ak_f32x4 s_lo = *(const ak_f32x4*)&dc_sp[wave][lr][8 * (lane >> 5)], s_hi = *(const ak_f32x4*)&dc_sp[wave][lr][8 * (lane >> 5) + 4];")
+            else:
+                a(f"{ind}    ak_f32x4 s_lo = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5)], s_hi = *(const ak_f32x4*)&dc_sp[0][lr][8 * (lane >> 5) + 4];")
+                a(f"{ind}    #pragma unroll")
+                a(f"{ind}    for (int w_ = 1; w_ < {self.waves}; ++w_) {{")
+                a(f"{ind}      s_lo += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5)];")
+                a(f"{ind}      s_hi += *(const ak_f32x4*)&dc_sp[w_][lr][8 * (lane >> 5) + 4];")
+                a(f"{ind}    }}")
             a(f"{ind}    float mx = -__builtin_inff();")
             a(f"{ind}    #pragma unroll")
             a(f"{ind}    for (int e = 0; e < 8; ++e) {{")
@@ -830,7 +976,8 @@ def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: s
         raise KernelError("the gfx950 decode lowering stores bf16 outputs")
     knobs = dict(hardware or {})
     fold = bool(knobs.pop("fold", FOLD_DEFAULT))
+    own = bool(knobs.pop("own", OWN_DEFAULT))
     if knobs:
         raise KernelError(f"the decode lowering has no hardware knobs {sorted(knobs)}")
     depth = max(2, min(pipeline.input_buffers, MAX_DEPTH))
-    return _Decode(plan, sch, m, name, trace, cursor, depth, fold).program()
+    return _Decode(plan, sch, m, name, trace, cursor, depth, fold, own).program()

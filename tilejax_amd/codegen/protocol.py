@@ -17,7 +17,9 @@ of blocks, as every wave runs them, and enforces:
 
 Events are tuples: ("load", stage, block, instructions), ("read", stage, block), ("wait_vm", n),
 ("wait_lgkm",), ("barrier",); a "stage" may also be a set of registers a wave loads for itself, used with
-("read_own", stage, block), which needs only that wave's wait. A loop is recorded once per position of its unrolled body, with the block as an
+("read_own", stage, block), which needs only that wave's wait, or an LDS region only its own wave loads and
+reads, used with ("read_mine", stage, block): a read needs that wave's wait for the loads, and a later load
+into the region needs its wait for the reads (wait_lgkm), no barrier. A loop is recorded once per position of its unrolled body, with the block as an
 offset from the loop's block variable and a condition on it; `Recorder.replay` instantiates it.
 """
 
@@ -53,7 +55,7 @@ def check(events: Sequence[Event], what: str = "kernel") -> None:
         if kind == "load":
             _, s, b, n = ev
             st = stages.setdefault(s, _Stage())
-            if st.block is not None and any(r != "all" for r in st.reads):
+            if st.block is not None and any(r not in ("all", "mine_done") for r in st.reads):
                 raise ProtocolError(f"{what}: event {at}: block {b} is loaded into stage {s} while a wave may still "
                                     f"read block {st.block} there (no wait and barrier after its reads)")
             if any(o[0] == s for o in outstanding):
@@ -76,13 +78,13 @@ def check(events: Sequence[Event], what: str = "kernel") -> None:
             outstanding = remaining[::-1]
         elif kind == "wait_lgkm":
             for st in stages.values():
-                st.reads = ["done" if r == "issued" else r for r in st.reads]
+                st.reads = ["done" if r == "issued" else "mine_done" if r == "mine_issued" else r for r in st.reads]
         elif kind == "barrier":
             for st in stages.values():
                 if st.loaded:
                     st.visible = True
                 st.reads = ["all" if r == "done" else r for r in st.reads]
-        elif kind in ("read", "read_own"):
+        elif kind in ("read", "read_own", "read_mine"):
             _, s, b = ev
             st = stages.get(s)
             if st is None or st.block != b:
@@ -92,6 +94,11 @@ def check(events: Sequence[Event], what: str = "kernel") -> None:
                 if not st.loaded:
                     raise ProtocolError(f"{what}: event {at}: block {b} is used from {s} before its loads landed")
                 st.reads.append("all")
+                continue
+            if kind == "read_mine":  # an LDS region only this wave loads: its own waits order loads and reads
+                if not st.loaded:
+                    raise ProtocolError(f"{what}: event {at}: block {b} is read from {s} before its loads landed")
+                st.reads.append("mine_issued")
                 continue
             if not st.visible:
                 raise ProtocolError(f"{what}: event {at}: block {b} is read from stage {s} before every wave's loads "

@@ -78,6 +78,8 @@ def standard() -> Iterator[Tuple[object, tuple]]:
                                         _i32(b, pages), _i32(b))
     yield decode.paged_gqa_decode, (_bf16(4, 1, 32, 128), _bf16(16, 128, 1024), _bf16(16, 128, 1024), _i32(4, 4),
                                     _i32(4))
+    yield decode.paged_gqa_decode, (_bf16(4, 1, 8, 128), _bf16(256, 16, 1024), _bf16(256, 16, 1024), _i32(4, 64),
+                                    _i32(4))
     for b, s, block in ((4, 512, 128), (4, 512, 256), (4, 512, 512), (64, 8192, 512)):
         yield decode.gqa_decode, (_bf16(b, 1, 32, 128), _bf16(b, s, 1024), _bf16(b, s, 1024), _i32(b),
                                   decode.DecodeTiles(block))
@@ -145,6 +147,12 @@ def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
     for n in (2, 4):
         for cursor in (False, True):
             yield decode.paged_gqa_decode, ins, Config(None, Pipeline(n, 2), cursor), False
+    ins = (_bf16(8, 1, 32, 128), _bf16(1024, 16, 1024), _bf16(1024, 16, 1024), _i32(8, 128), _i32(8))
+    sig = decode.paged_gqa_decode.signature(*ins)
+    base = decode.paged_gqa_decode.default_config(sig)
+    for hw in ((("own", 0),), (("fold", 1),)):
+        for cursor in (False, True):
+            yield decode.paged_gqa_decode, ins, Config(base.tunable, base.pipeline, cursor, hw), False
 
 
 def compile_all(verbose: bool = True) -> List[str]:

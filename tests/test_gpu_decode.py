@@ -242,12 +242,15 @@ def test_waves_with_their_own_rows_are_bit_equal(cursor):
     base = paged_gqa_decode.default_config(sig)
     own = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor))
     shared = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor, (("own", 0),)))
+    # without the barrier every few steps that keeps the waves together
+    drifting = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor, (("sync", 0),)))
     assert own.program.notes["own_rows"] and not shared.program.notes["own_rows"]
     print(f"decode own rows vs shared scores, cursor={cursor}", flush=True)
     want = shared.run(*ins)
     got = own.run(*ins)
+    unsynced = drifting.run(*ins)
     torch.cuda.synchronize()
-    assert torch.equal(got, want)
+    assert torch.equal(got, want) and torch.equal(unsynced, want)
 
 
 def test_multi_head_decode_gives_each_wave_one_head():

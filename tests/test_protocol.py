@@ -144,19 +144,24 @@ def test_planted_mistakes_fail():
         check(_drop(mm, "wait_lgkm", 1), "matmul without a read wait")
 
 
-@pytest.mark.parametrize("cursor", [False, True])
-def test_decode_waves_with_their_own_rows(cursor):
+@pytest.mark.parametrize("cursor,sync", [(False, None), (True, None), (False, 0), (False, 3)])
+def test_decode_waves_with_their_own_rows(cursor, sync):
     """Decode whose waves own their query rows: each wave loads its own columns of V into a region of the stage
-    only it reads ("read_mine"), so its own waits order its loads and reads and no step has a barrier. A
-    wait loosened, or the wait for the reads before the region's next load dropped, must fail."""
+    only it reads ("read_mine"), so its own waits order its loads and reads, and the only barrier is the one
+    every `sync` steps that keeps the waves together. A wait loosened, or the wait for the reads before the
+    region's next load dropped, must fail."""
+    from tilejax_amd.codegen.decode import SYNC_DEFAULT
+
     args = (spec(5, 1, 32, 128, dtype=BF), spec(500, 16, 1024, dtype=BF), spec(500, 16, 1024, dtype=BF),
             spec(5, 100, dtype=I32), spec(5, dtype=I32))
-    prog = _lowered(paged_gqa_decode, args, None, 3, cursor=cursor).program
+    hw = () if sync is None else (("sync", sync),)
+    every = SYNC_DEFAULT if sync is None else sync
+    prog = _lowered(paged_gqa_decode, args, None, 3, hw, cursor=cursor).program
     assert prog.notes["own_rows"]
-    for steps in range(1, 14):
+    for steps in range(1, 20):
         events = prog.protocol.replay(steps)
         check(events, f"decode with own rows, {steps} steps")
-        assert not any(ev[0] == "barrier" for ev in events)
+        assert sum(ev[0] == "barrier" for ev in events) == (-(-steps // every) if every else 0)
         assert {ev[0] for ev in events} >= {"read_mine", "read_own"} and not any(ev[0] == "read" for ev in events)
     events = prog.protocol.replay(8)
     with pytest.raises(ProtocolError, match="before its loads landed"):

@@ -64,7 +64,8 @@ MAX_DEPTH = 4
 # its own: correct (tests/test_gpu_decode.py), but slower. At BASELINE config 5 the call took 312 us with a
 # release fence in every wave and 249 us with one per workgroup, against 214 us with the merge launch: each
 # agent-scope release writes the XCD's L2 back, each acquire invalidates it, and the merges then read the
-# partials from memory. So it is off unless asked for.
+# partials from memory. With own rows (partials of 16 KB, not 128) it still took 231 against 201 us: the
+# whole-L2 writeback is the cost, not the bytes. So it is off unless asked for.
 FOLD_DEFAULT = False
 # Waves that own their query rows (`row_owners`), where the spec's structure shows it (the hardware knob "own",
 # on unless set to 0): each wave scores its own rows against its own columns, loads its own columns of V into
@@ -72,6 +73,12 @@ FOLD_DEFAULT = False
 # contributed exact zeros to those rows' scores, so the output is bit-equal to the shared-score kernel's; at
 # BASELINE config 5 the call went from 222 to 202 us with step tables and from 226 to 208 us with a cursor.
 OWN_DEFAULT = True
+# With own rows nothing else synchronises a workgroup's waves, and they drift apart: at config 5 the first
+# wave ended 38-43 us before the workgroup's last (3.6 us with shared scores), the early waves winning the
+# memory queues. A bare s_barrier (the loads stay in flight) every SYNC_DEFAULT steps, the hardware knob
+# "sync" (0: none), keeps them together: 199.9-201.9 us per call without, 195.9-197.5 with one every 6 or
+# 8 steps (tables; 206 against 202-203 us with a cursor), every count bit-equal.
+SYNC_DEFAULT = 8
 
 
 @dataclass
@@ -218,9 +225,10 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
 
 class _Decode:
     def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False,
-                 cursor: bool = False, depth: int = DEPTH, fold: bool = FOLD_DEFAULT, own: bool = OWN_DEFAULT) -> None:
+                 cursor: bool = False, depth: int = DEPTH, fold: bool = FOLD_DEFAULT, own: bool = OWN_DEFAULT,
+                 sync: int = SYNC_DEFAULT) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
-        self.trace, self.cursor, self.depth = trace, cursor, depth
+        self.trace, self.cursor, self.depth, self.sync = trace, cursor, depth, sync
         # eight waves where the width splits into them (an eighth each, a multiple of 32), else four
         self.waves = WAVES if m.width % (32 * WAVES) == 0 else 4
         self.threads = 64 * self.waves
@@ -597,6 +605,12 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
             if own:  # V(j) is in this wave's own region: its own wait suffices
                 if record:
                     rec.at(u, lambda b, n: ("wait_vm", wait_n))
+                if self.sync:
+                    # nothing else holds a workgroup's waves together: without a barrier now and then they
+                    # drift apart (the first waves win the memory queues), and the last ones finish alone
+                    a(f'{ind}  if (j_ % {self.sync} == 0) asm volatile("s_barrier" ::: "memory");')
+                    if record:
+                        rec.at(u, lambda b, n: ("barrier",), lambda b, n, k=self.sync: b % k == 0)
             else:
                 # every wave is past step j - 1, so its V stage is free; every thread's part of V(j) has landed
                 a(f'{ind}  asm volatile("s_barrier" ::: "memory");')
@@ -977,7 +991,10 @@ def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: s
     knobs = dict(hardware or {})
     fold = bool(knobs.pop("fold", FOLD_DEFAULT))
     own = bool(knobs.pop("own", OWN_DEFAULT))
+    sync = int(knobs.pop("sync", SYNC_DEFAULT))
     if knobs:
         raise KernelError(f"the decode lowering has no hardware knobs {sorted(knobs)}")
+    if sync < 0:
+        raise KernelError(f"the decode knob sync is a count of steps (0: no barrier), not {sync}")
     depth = max(2, min(pipeline.input_buffers, MAX_DEPTH))
-    return _Decode(plan, sch, m, name, trace, cursor, depth, fold, own).program()
+    return _Decode(plan, sch, m, name, trace, cursor, depth, fold, own, sync).program()

@@ -150,7 +150,7 @@ def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
     ins = (_bf16(8, 1, 32, 128), _bf16(1024, 16, 1024), _bf16(1024, 16, 1024), _i32(8, 128), _i32(8))
     sig = decode.paged_gqa_decode.signature(*ins)
     base = decode.paged_gqa_decode.default_config(sig)
-    for hw in ((("own", 0),), (("fold", 1),)):
+    for hw in ((("own", 0),), (("fold", 1),), (("sync", 0),)):
         for cursor in (False, True):
             yield decode.paged_gqa_decode, ins, Config(base.tunable, base.pipeline, cursor, hw), False
 

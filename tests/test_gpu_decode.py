@@ -154,10 +154,12 @@ def _cursor_run(kernel, ins):
 
     plain = _with_tables(kernel, ins)
     cursor = kernel.lowered(kernel.signature(*ins), Config(plain.config.tunable, plain.config.pipeline, True))
-    # with tables, the builder's launch also sets up the query rows; with a cursor, a setup launch does
+    # with tables, the builder's launch also sets up the query rows; with a cursor, the attention kernel
+    # computes its waves' own rows (or, where the waves own none, a setup launch does)
     builders = [[ln.symbol.endswith("_steps") for ln in lt.program.launches] for lt in (plain, cursor)]
     assert cursor.program.notes["cursor"] and any(builders[0]) and not any(builders[1])
-    assert len(cursor.program.launches) == len(plain.program.launches) == 3
+    in_kernel = cursor.program.notes["query_rows_in_kernel"]
+    assert len(plain.program.launches) == 3 and len(cursor.program.launches) == (2 if in_kernel else 3)
     dev = [t.cuda() for t in ins]
     return plain.run(*dev), cursor.run(*dev)
 
@@ -244,13 +246,17 @@ def test_waves_with_their_own_rows_are_bit_equal(cursor):
     shared = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor, (("own", 0),)))
     # without the barrier every few steps that keeps the waves together
     drifting = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor, (("sync", 0),)))
+    # the query rows the other way: computed by the attention kernel (tables), or by a setup launch (cursor)
+    other_q = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, cursor, (("qrows", int(not cursor)),)))
     assert own.program.notes["own_rows"] and not shared.program.notes["own_rows"]
+    assert own.program.notes["query_rows_in_kernel"] == cursor != other_q.program.notes["query_rows_in_kernel"]
     print(f"decode own rows vs shared scores, cursor={cursor}", flush=True)
     want = shared.run(*ins)
     got = own.run(*ins)
     unsynced = drifting.run(*ins)
+    rows_other_way = other_q.run(*ins)
     torch.cuda.synchronize()
-    assert torch.equal(got, want) and torch.equal(unsynced, want)
+    assert torch.equal(got, want) and torch.equal(unsynced, want) and torch.equal(rows_other_way, want)
 
 
 def test_multi_head_decode_gives_each_wave_one_head():

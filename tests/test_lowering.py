@@ -184,9 +184,11 @@ def test_attention_stages_past_lds_are_refused_before_compiling():
 
 def test_decode_sets_up_query_rows_in_the_builders_launch():
     """Decode with step tables takes three launches: the step-table builder, whose launch carries the
-    workgroups that set up each sequence's query rows, the attention kernel and the merge; with a cursor,
-    a setup launch takes the builder's place. With the knob "fold", the attention kernel merges each
-    sequence's partials itself (the last workgroup to finish it; a device counter per sequence)."""
+    workgroups that set up each sequence's query rows, the attention kernel and the merge. With a cursor the
+    attention kernel computes its waves' own query rows itself (knob "qrows", on with a cursor), so the call
+    is two launches; without it a setup launch takes the builder's place. With the knob "fold", the
+    attention kernel merges each sequence's partials itself (the last workgroup to finish it; a device
+    counter per sequence)."""
     from examples.decode import paged_gqa_decode
     from tilejax_amd.codegen.steps import builder_groups
     from tilejax_amd.tune import Config
@@ -201,13 +203,20 @@ def test_decode_sets_up_query_rows_in_the_builders_launch():
     words = 4 * 1  # 4 sequences x one 64-block word of their 64 pages
     assert tables.launches[0].grid[0] > builder_groups(words)  # the setup workgroups come after the builder's
     assert "xb_" in tables.source and "_setup(" not in tables.source
+    assert not tables.notes["query_rows_in_kernel"] and "dc_q" in tables.workspace
     base = paged_gqa_decode.default_config(sig)
     cursor = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, True)).program
-    assert [ln.symbol for ln in cursor.launches] == ["tj_paged_gqa_decode_setup", "tj_paged_gqa_decode",
+    assert [ln.symbol for ln in cursor.launches] == ["tj_paged_gqa_decode", "tj_paged_gqa_decode_merge"]
+    assert cursor.notes["query_rows_in_kernel"] and "dc_q" not in cursor.workspace and "dc_rows" in cursor.source
+    staged = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, True, (("qrows", 0),))).program
+    assert [ln.symbol for ln in staged.launches] == ["tj_paged_gqa_decode_setup", "tj_paged_gqa_decode",
                                                       "tj_paged_gqa_decode_merge"]
-    for use_cursor, first in ((False, "tj_paged_gqa_decode_steps"), (True, "tj_paged_gqa_decode_setup")):
+    own_q = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, False, (("qrows", 1),))).program
+    assert own_q.launches[0].grid[0] == builder_groups(words) and "xb_" not in own_q.source
+    assert "dc_q" not in own_q.workspace
+    for use_cursor, first in ((False, ["tj_paged_gqa_decode_steps"]), (True, [])):
         folded = paged_gqa_decode.lowered(sig, Config(base.tunable, base.pipeline, use_cursor, (("fold", 1),))).program
-        assert [ln.symbol for ln in folded.launches] == [first, "tj_paged_gqa_decode"]
+        assert [ln.symbol for ln in folded.launches] == first + ["tj_paged_gqa_decode"]
         assert folded.notes["merge_folded"] and folded.state == {"dc_arrive": 4}
         assert "_merge(" not in folded.source and "__ATOMIC_RELEASE" in folded.source
 

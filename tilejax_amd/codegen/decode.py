@@ -79,6 +79,15 @@ OWN_DEFAULT = True
 # "sync" (0: none), keeps them together: 199.9-201.9 us per call without, 195.9-197.5 with one every 6 or
 # 8 steps (tables; 206 against 202-203 us with a cursor), every count bit-equal.
 SYNC_DEFAULT = 8
+# The query rows computed by the attention kernel itself (the hardware knob "qrows"): each wave evaluates the
+# spec's setup code for its own fragments' elements when it starts a tile, so no workgroup materialises them
+# in a workspace first (with a cursor that is a launch of its own, with step tables more workgroups of the
+# builder's launch). The same per-element code and rounding: the same bits. Only a wave's own rows are nonzero
+# in its columns, so it needs owned rows. A tile start then costs about 3 us more (the tile's loop values,
+# then the query loads, where the workspace took one load); with a cursor it saves a launch of 6 us, with
+# tables only the builder launch's extra workgroups. At config 5: tables 190.9 us without, 194.0 with; a
+# cursor 196.4 without, 193.0 with. None: with a cursor only.
+QROWS_DEFAULT = None
 
 
 @dataclass
@@ -226,9 +235,9 @@ def match(plan: Plan) -> Optional[DecodeMatch]:
 class _Decode:
     def __init__(self, plan: Plan, sch: Schedule, m: DecodeMatch, name: str, trace: bool = False,
                  cursor: bool = False, depth: int = DEPTH, fold: bool = FOLD_DEFAULT, own: bool = OWN_DEFAULT,
-                 sync: int = SYNC_DEFAULT) -> None:
+                 sync: int = SYNC_DEFAULT, qrows: bool = False) -> None:
         self.plan, self.sch, self.m, self.name = plan, sch, m, name
-        self.trace, self.cursor, self.depth, self.sync = trace, cursor, depth, sync
+        self.trace, self.cursor, self.depth, self.sync, self.qrows = trace, cursor, depth, sync, qrows
         # eight waves where the width splits into them (an eighth each, a multiple of 32), else four
         self.waves = WAVES if m.width % (32 * WAVES) == 0 else 4
         self.threads = 64 * self.waves
@@ -240,6 +249,14 @@ class _Decode:
         # Each query row's one wave (`row_owners`): with them, a wave computes its own rows' scores alone and
         # loads its own columns of V, and the step needs no workgroup barrier
         self.owners = row_owners(plan, m, m.width // self.waves) if own else None
+        # Query rows in the kernel need owned rows: a wave's fragments are zero outside its own rows, whose
+        # block (rows x its columns, bf16) it stages in its partial-S area of LDS
+        if self.owners is None:
+            self.qrows = False
+        else:
+            most = max(self.owners.count(w_) for w_ in range(self.waves))
+            if most * (m.width // self.waves) * 2 > RP * SP * 4:
+                self.qrows = False
         if sch.repeats != 1:
             raise KernelError("decode with parallel loops the runtime mask doesn't read is not lowered yet")
         self.grid = gfx950.CUS
@@ -324,8 +341,9 @@ class _Decode:
         for r in sch.inner:
             tables[f"tv_{r.var}"] = np.asarray(sch.tile_values[r.var], np.int32)
             args.append(Arg("table", f"tv_{r.var}", "const int* __restrict__", f"tv_{r.var}"))
-        workspace = {"dc_q": 2 * sch.pattern_tiles * RP * W, "dc_m": 4 * self.slots * RP, "dc_l": 4 * self.slots * RP,
-                     "dc_acc": 4 * self.slots * RP * W}
+        workspace = {"dc_m": 4 * self.slots * RP, "dc_l": 4 * self.slots * RP, "dc_acc": 4 * self.slots * RP * W}
+        if not self.qrows:
+            workspace["dc_q"] = 2 * sch.pattern_tiles * RP * W
         # the step tables (device-built) or, with a cursor, only what the merge reads: the count and each
         # tile's first step, which the attention kernel's workgroup 0 writes
         for ws in (("count", "tile_steps") if self.cursor else ("step_tile", "step_code", "count", "tile_steps")):
@@ -333,7 +351,8 @@ class _Decode:
         if self.cursor:
             workspace["count"] = 4
             workspace["tile_steps"] = 4 * (sch.pattern_tiles + 1)
-        args.append(Arg("workspace", "dc_q", "ak_u16* __restrict__", "dc_q"))
+        if not self.qrows:
+            args.append(Arg("workspace", "dc_q", "ak_u16* __restrict__", "dc_q"))
         for ws in ("dc_m", "dc_l", "dc_acc"):
             args.append(Arg("workspace", ws, "float* __restrict__", ws))
         if self.trace:
@@ -344,16 +363,17 @@ class _Decode:
         if self.fold:
             args.append(Arg("state", "dc_arrive", "int* __restrict__", "dc_arrive"))
         struct = c_struct(f"{self.name}_args", args)
-        # With step tables the query rows are set up by extra workgroups of the table builder's launch (they
-        # need no table); with a cursor, by a launch of their own.
+        # Unless the attention kernel computes them itself (`qrows`), the query rows are set up by extra workgroups
+        # of the table builder's launch (they need no table), or with a cursor by a launch of their own.
+        setup = self.cursor and not self.qrows
         source = "\n".join([f"// Generated by tilejax_amd for `{plan.nest.name}`: gfx950 split-KV decode attention.",
-                            PRELUDE, struct, self._setup_source() if self.cursor else "", self._attention_source(),
+                            PRELUDE, struct, self._setup_source() if setup else "", self._attention_source(),
                             "" if self.fold else self._merge_source()])
         launches = [Launch(self.name, args, (self.grid, 1, 1), (self.threads, 1, 1), 0)]
         if not self.fold:
             launches.append(Launch(f"{self.name}_merge", args, (sch.pattern_tiles, self.merge_chunks, 1),
                                    (self.threads, 1, 1), 0))
-        if self.cursor:
+        if setup:
             launches.insert(0, Launch(f"{self.name}_setup", args, (sch.pattern_tiles, self.setup_chunks, 1),
                                       (self.threads, 1, 1), 0))
         prog = Program(
@@ -363,10 +383,13 @@ class _Decode:
             tables=tables, workspace=workspace, state=state, lds_bytes=self.lds, protocol=self.protocol,
             notes={"family": "decode", "grid": self.grid, "slots": self.slots, "rows": R, "width": W, "page": m.page,
                    "cursor": self.cursor, "merge_folded": self.fold, "own_rows": self.owners is not None,
+                   "query_rows_in_kernel": self.qrows,
                    # trace regions cover the attention kernel; a slice is one kernel step, SUB positions
                    "trace_workgroups": self.grid if self.trace else 0, "slices_per_step": self.sub},
         )
-        if not self.cursor:
+        if not self.cursor and self.qrows:
+            attach_step_builder(prog, plan, sch, self.name)
+        elif not self.cursor:
             setup_args = [a for a in args if a.kind in ("input", "table") or a.key == "dc_q"]
             attach_step_builder(prog, plan, sch, self.name,
                                 extra=self._setup_body(f"xb_ / {self.setup_chunks}", f"xb_ % {self.setup_chunks}"),
@@ -479,6 +502,48 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(c
   }}"""
             v_roff_line = ("const int c = cb + 32 * dt + 16 * (G & 1) + 4 * (s & 3);\n"
                            f"      v_roff[dt] = pos * {W * 2} + ((((c >> 3) ^ ((pos & 3) << 2))) << 4) + (c & 7) * 2;")
+        # the Q^T fragments of tile t (srcB of S^T, 16x16x32): query rows lane % 16 and 16 + lane % 16, columns
+        # cb + 32 s + 8 (lane / 16) .. + 8
+        table_lines: List[str] = []  # file-scope constant tables they read
+        if self.qrows:
+            # Evaluated here from the setup code, per element, as the setup kernel would write them. Only this
+            # wave's own rows are nonzero in its columns: the lanes evaluate that block (its elements spread over
+            # the wave, their loads all in flight at once) into the wave's partial-S area of LDS, and each
+            # fragment is read back from there, or is zero for a row of another wave's. (LDS operations of one
+            # wave run in order: no barrier.)
+            owned = [[r for r, o in enumerate(self.owners) if o == w_] for w_ in range(self.waves)]
+            most = max(len(rows) for rows in owned)
+            per_lane = -(-most * WQ // 64)
+            slot_of = [[rows.index(r) if r in rows else -1 for r in range(RP)] for rows in owned]
+            table_lines.append(f"// per wave: its own query rows, in order (-1 past them), and each row's place among them")
+            table_lines.append(f"__constant__ int dc_rows[{self.waves}][{max(most, 1)}] = {{"
+                               + ", ".join("{" + ", ".join(map(str, rows + [-1] * (max(most, 1) - len(rows)))) + "}"
+                                           for rows in owned) + "};")
+            table_lines.append(f"__constant__ int dc_slot[{self.waves}][{RP}] = {{"
+                               + ", ".join("{" + ", ".join(map(str, sl)) + "}" for sl in slot_of) + "};")
+            q_expr = self._emitter(lambda n, idx: None).at(m.q_node, ("qr", "qc"))
+            q_load = f"""{self._decode_tile("t")}
+    ak_u16* stg = (ak_u16*)&dc_sp[wave][0][0];  // this wave's own rows x its {WQ} columns
+#pragma unroll
+    for (int i = 0; i < {per_lane}; ++i) {{
+      const int e = lane + 64 * i, k = e / {WQ}, col = e % {WQ};
+      const int qr = k < {most} ? dc_rows[wave][k] : -1, qc = cb + col;
+      if (qr >= 0) stg[e] = (ak_u16)ak_bf16_bits((float)({q_expr}));
+    }}
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {{
+      const int k = dc_slot[wave][(lane & 15) + 16 * tt];
+#pragma unroll
+      for (int s = 0; s < {slabs}; ++s)
+        qf[tt][s] = k >= 0 ? *(const ak_bf16x8*)&stg[k * {WQ} + 32 * s + 8 * (lane >> 4)] : ak_bf16x8{{}};
+    }}"""
+        else:
+            q_load = f"""const ak_u16* qp = args.dc_q + (long long)t * {RP * W} + cb + 8 * (lane >> 4);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int s = 0; s < {slabs}; ++s)
+        qf[tt][s] = *(const ak_bf16x8*)(qp + (long long)((lane & 15) + 16 * tt) * {W} + 32 * s);"""
         L: List[str] = []
         w = L.append
         for s in range(D):  # one array per stage: the compiler then keeps the other stages' loads in flight
@@ -491,6 +556,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(c
             owner = list(self.owners) + [-1] * (RP - len(self.owners))
             w(f"// each query row's wave (its values lie in that wave's columns only); rows past R: none")
             w(f"__constant__ int dc_owner[{RP}] = {{{', '.join(map(str, owner))}}};")
+        L.extend(table_lines)
         w(f"""
 extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {self.name}_args args) {{
   {f"__shared__ float dc_w[{self.maxs}][{m.rows}], dc_lsum[{m.rows}]; __shared__ int dc_last;" if self.fold else ""}
@@ -547,12 +613,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
     {f"tr_out += {NOW} - tr_f0;" if self.trace else ""}
   }};
   auto start_tile = [&](int t) {{
-    const ak_u16* qp = args.dc_q + (long long)t * {RP * W} + cb + 8 * (lane >> 4);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int s = 0; s < {slabs}; ++s)
-        qf[tt][s] = *(const ak_bf16x8*)(qp + (long long)((lane & 15) + 16 * tt) * {W} + 32 * s);
+    {q_load}
 #pragma unroll
     for (int i = 0; i < {dtiles}; ++i)
 #pragma unroll
@@ -767,25 +828,52 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
         pt, count, nb = sch.pattern_tiles, phase.count, -(-phase.count // 64)
         mask = Index(plan, lambda v: f"lv_{v}").expr(phase.mask)
         per_t = -(-pt // self.threads)
-        return f"""__shared__ unsigned long long cs_run[{self.words}];
-  __shared__ int cs_start[{pt + 1}], cs_part[{self.threads}];
-  // (unrolled so that several tiles' loop values and index reads are in flight at once)
+        rounds = -(-pt // self.waves)  # tiles per wave
+        kb_run = (f"const int kb = wi * 64 + lane;\n        bool run = false;\n"
+                  f"        if (kb < {count}) {{ const int lv_{phase.var} = {phase.start} + kb * {phase.step}; run = !({mask}); }}")
+        inner = self.sch.inner
+        if rounds * nb <= 64:
+            # Straight-line code: all the wave's tiles' loop values are loaded at once, then their masks' index
+            # reads, so the latencies overlap; each ballot word is kept by one lane (a select, no branch) and
+            # the lanes store them together.
+            ballots = f"""{{
+    {" ".join(f"int lvA_{r.var}[{rounds}];" for r in inner)}
+#pragma unroll
+    for (int i = 0; i < {rounds}; ++i) {{
+      const int t_ = ak_imin(wave + {self.waves} * i, {pt - 1});
+      {" ".join(f"lvA_{r.var}[i] = ak_ldc(args.tv_{r.var}, t_);" for r in inner)}
+    }}
+    unsigned long long word_ = 0;
+#pragma unroll
+    for (int i = 0; i < {rounds}; ++i) {{
+      {" ".join(f"const int lv_{r.var} = lvA_{r.var}[i];" for r in inner)}
+#pragma unroll
+      for (int wi = 0; wi < {nb}; ++wi) {{
+        {kb_run}
+        const unsigned long long m_ = __ballot(run);
+        word_ = lane == i * {nb} + wi ? m_ : word_;
+      }}
+    }}
+    const int t_ = wave + {self.waves} * (lane / {nb});
+    if (lane < {rounds * nb} && t_ < {pt}) cs_run[t_ * {nb} + lane % {nb}] = word_;
+  }}"""
+        else:
+            ballots = f"""// (unrolled so that several tiles' loop values and index reads are in flight at once)
 #pragma unroll 8
   for (int t = wave; t < {pt}; t += {self.waves}) {{
     {self._decode_tile("t")}
     for (int wi = 0; wi < {nb}; ++wi) {{
-      const int kb = wi * 64 + lane;
-      bool run = false;
-      if (kb < {count}) {{
-        const int lv_{phase.var} = {phase.start} + kb * {phase.step};
-        run = !({mask});
-      }}
+      {kb_run}
       const unsigned long long m_ = __ballot(run);
       if (lane == 0) cs_run[t * {nb} + wi] = m_;
     }}
-  }}
+  }}"""
+        return f"""__shared__ unsigned long long cs_run[{self.words}];
+  __shared__ int cs_start[{pt + 1}], cs_part[{self.threads}];
+  {ballots}
   __syncthreads();
-  {{  // kept steps per tile, summed over runs of {per_t} tiles per thread, then a block-wide scan
+  {{  // kept steps per tile, summed over runs of {per_t} tiles per thread; a scan within each wave (shuffles),
+    // then over the waves' totals
     const int t0 = tid * {per_t}, t1 = ak_imin(t0 + {per_t}, {pt});
     int mine = 0;
     for (int t = t0; t < t1; ++t) {{
@@ -794,17 +882,19 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
       cs_start[t] = k ? k : 1;
       mine += k ? k : 1;
     }}
-    cs_part[tid] = mine;
-    __syncthreads();
-    for (int d = 1; d < {self.threads}; d <<= 1) {{
-      const int add = tid >= d ? cs_part[tid - d] : 0;
-      __syncthreads();
-      cs_part[tid] += add;
-      __syncthreads();
+    int inc = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {{
+      const int y_ = __shfl_up(inc, d);
+      if (lane >= d) inc += y_;
     }}
-    int at = cs_part[tid] - mine;
+    if (lane == 63) cs_part[wave] = inc;
+    __syncthreads();
+    int before = 0;
+    for (int w_ = 0; w_ < wave; ++w_) before += cs_part[w_];
+    int at = before + inc - mine;
     for (int t = t0; t < t1; ++t) {{ const int k = cs_start[t]; cs_start[t] = at; at += k; }}
-    if (tid == {self.threads - 1}) cs_start[{pt}] = cs_part[{self.threads - 1}];
+    if (tid == {self.threads - 1}) cs_start[{pt}] = before + inc;
     __syncthreads();
     if (blockIdx.x == 0) {{
       for (int t = tid; t <= {pt}; t += {self.threads}) args.rt_tile_steps[t] = cs_start[t];
@@ -827,9 +917,14 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
       for (int wi = 0; wi < {nb}; ++wi) {{
         unsigned long long w_ = cs_run[t * {nb} + wi];
         const int c = __popcll(w_);
-        if (r < c) {{
-          for (; r > 0; --r) w_ &= w_ - 1;
-          code = ((wi * 64 + __ffsll((long long)w_) - 1) * {radix}) << {CODE_SHIFT};
+        if (r < c) {{  // the word's r-th set bit, by halving: is it among the low `h` bits of what is left?
+          int pos = 0;
+#pragma unroll
+          for (int h = 32; h >= 1; h >>= 1) {{
+            const int lo = __popcll(w_ & ((1ull << h) - 1));
+            if (r >= lo) {{ r -= lo; w_ >>= h; pos += h; }}
+          }}
+          code = ((wi * 64 + pos) * {radix}) << {CODE_SHIFT};
           break;
         }}
         r -= c;
@@ -992,9 +1087,10 @@ def lower(plan: Plan, sch: Schedule, pipeline: Pipeline, m: DecodeMatch, name: s
     fold = bool(knobs.pop("fold", FOLD_DEFAULT))
     own = bool(knobs.pop("own", OWN_DEFAULT))
     sync = int(knobs.pop("sync", SYNC_DEFAULT))
+    qrows = bool(knobs.pop("qrows", QROWS_DEFAULT if QROWS_DEFAULT is not None else cursor))
     if knobs:
         raise KernelError(f"the decode lowering has no hardware knobs {sorted(knobs)}")
     if sync < 0:
         raise KernelError(f"the decode knob sync is a count of steps (0: no barrier), not {sync}")
     depth = max(2, min(pipeline.input_buffers, MAX_DEPTH))
-    return _Decode(plan, sch, m, name, trace, cursor, depth, fold, own, sync).program()
+    return _Decode(plan, sch, m, name, trace, cursor, depth, fold, own, sync, qrows).program()

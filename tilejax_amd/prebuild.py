@@ -153,6 +153,8 @@ def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
     for hw in ((("own", 0),), (("fold", 1),), (("sync", 0),)):
         for cursor in (False, True):
             yield decode.paged_gqa_decode, ins, Config(base.tunable, base.pipeline, cursor, hw), False
+    for cursor in (False, True):
+        yield decode.paged_gqa_decode, ins, Config(base.tunable, base.pipeline, cursor, (("qrows", int(not cursor)),)), False
 
 
 def compile_all(verbose: bool = True) -> List[str]:

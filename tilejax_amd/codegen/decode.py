@@ -64,8 +64,10 @@ MAX_DEPTH = 4
 # its own: correct (tests/test_gpu_decode.py), but slower. At BASELINE config 5 the call took 312 us with a
 # release fence in every wave and 249 us with one per workgroup, against 214 us with the merge launch: each
 # agent-scope release writes the XCD's L2 back, each acquire invalidates it, and the merges then read the
-# partials from memory. With own rows (partials of 16 KB, not 128) it still took 231 against 201 us: the
-# whole-L2 writeback is the cost, not the bytes. So it is off unless asked for.
+# partials from memory. With own rows (partials of 16 KB, not 128) it still took 231 against 201 us, and
+# with the partials stored and loaded at agent scope (sc1) and no fence at all, 245 us: the cost is the last
+# workgroup of each sequence merging it alone at the kernel's end, where the merge launch spreads it over
+# 512 workgroups. So it is off unless asked for.
 FOLD_DEFAULT = False
 # Waves that own their query rows (`row_owners`), where the spec's structure shows it (the hardware knob "own",
 # on unless set to 0): each wave scores its own rows against its own columns, loads its own columns of V into

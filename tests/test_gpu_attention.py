@@ -153,6 +153,29 @@ def test_kernel_shapes_the_tuner_tries(hardware, buffers):
     _close(f"attention {hardware} {buffers}", got, kernels.causal_attention(q, k, v, 256, 256), _floor(q, k, v))
 
 
+def test_sixty_four_query_rows_a_wave():
+    """The knob `rows` 64: a wave's rows as two 32-row halves that share every K and V fragment it reads from
+    LDS. Each row's products and softmax are the same, so without split tiles the output is the default
+    kernel's bit for bit; with them (their chunks cut elsewhere) it is within the attention tolerance of the
+    oracle."""
+    from tilejax_amd import Pipeline
+    from tilejax_amd.tune import Config
+
+    shape, blocks = (2, 4, 1024, 128), AttentionBlocks(256, 256)
+    q, k, v = _inputs(*shape, seed=5)
+    sig = causal_attention.signature(q, k, v)
+    whole = [causal_attention.lowered(sig, Config(blocks, Pipeline(2, 2), False, (("split", 0),) + hw))
+             for hw in ((), (("rows", 64),))]
+    split64 = causal_attention.lowered(sig, Config(blocks, Pipeline(2, 2), False, (("rows", 64),)))
+    assert whole[1].program.notes["block_q"] == 256 and split64.program.notes["split_items"] > 0
+    print(f"attention {shape} with 64 query rows a wave", flush=True)
+    dev = (q.cuda(), k.cuda(), v.cuda())
+    want, got, chunked = whole[0].run(*dev), whole[1].run(*dev), split64.run(*dev)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    _close("attention 64 rows a wave, split", chunked, kernels.causal_attention(q, k, v, 256, 256), _floor(q, k, v))
+
+
 @pytest.mark.parametrize("shape,blocks", [((2, 4, 1024, 128), (256, 256)), ((1, 2, 1024, 128), (256, 256))])
 def test_k_fragments_in_registers_are_bit_equal(shape, blocks):
     """The knob `kreg` loads each block's K fragments from memory straight into registers (LDS holds V only).

@@ -63,6 +63,7 @@ MASKED_BELOW = -1e20  # a constant score this low contributes exp(c - m) == 0 on
 # + 1 are kept in a ring of ahead + 2 scalars, at b modulo the ring.
 MAX_AHEAD = 3
 WAVES = 4  # waves per workgroup (None: 8 for tiles of a multiple of 256 query rows, else 4)
+ROWS = 32  # query rows per wave (the knob `rows`: 32, or 64 as two halves sharing the K and V fragments)
 BKV = 64  # keys per block (a multiple of 32)
 K_AHEAD = 8  # K fragments in flight ahead of the S MFMAs
 # With K in registers (knob `kreg`): register sets of K fragments. With two, the next block's set is loaded
@@ -297,10 +298,14 @@ class _Flash:
             raise KernelError(f"the gfx950 attention lowering takes head dims that are multiples of 32 up to 128 "
                               f"(got {m.d} and {m.dv})")
         self.nw = hardware.get("waves", WAVES) or (8 if m.rows % 256 == 0 else 4 if m.rows % 128 == 0 else 0)
-        if not self.nw or m.rows % (32 * self.nw):
-            raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of {32 * (self.nw or 4)} "
-                              f"rows (got {m.rows})")
-        self.bq = 32 * self.nw
+        # query rows per wave: 32, or 64 as two 32-row halves that share every K and V fragment it reads
+        self.wr = hardware.get("rows", ROWS)
+        if self.wr not in (32, 64):
+            raise KernelError(f"the attention knob rows is 32 or 64 query rows a wave (got {self.wr})")
+        if not self.nw or m.rows % (self.wr * self.nw):
+            raise KernelError(f"the gfx950 attention lowering needs query tiles of a multiple of "
+                              f"{self.wr * (self.nw or 4)} rows (got {m.rows})")
+        self.bq = self.wr * self.nw
         self.bkv = hardware.get("bkv", BKV)
         # K fragments loaded from memory straight into registers (a register set per block, the next block's
         # loaded after this block's S product) rather than through LDS, which then holds V only
@@ -398,8 +403,8 @@ class _Flash:
             vals = {**values, m.jvar: jv}
             row = []
             for wv in range(self.nw):
-                r0 = sub * bq + wv * 32
-                row.append(self._classify(vals, r0, r0 + 31, off, off + bkv - 1))
+                r0 = sub * bq + wv * self.wr
+                row.append(self._classify(vals, r0, r0 + self.wr - 1, off, off + bkv - 1))
             classes.append(row)
         # Blocks after which each wave's rows all have a real score: a block whose first column keeps every
         # one of the wave's scores.
@@ -411,8 +416,8 @@ class _Flash:
                 if classes[b][wv] != "none" or not established:
                     last = b + 1
                 if not established:
-                    r0 = sub * bq + wv * 32
-                    first = self._classify({**values, m.jvar: jv}, r0, r0 + 31, off, off)
+                    r0 = sub * bq + wv * self.wr
+                    first = self._classify({**values, m.jvar: jv}, r0, r0 + self.wr - 1, off, off)
                     established = first == "full"
             keep_until[wv] = last
         n_blocks = max(keep_until) if keep_until else 0
@@ -458,7 +463,8 @@ class _Flash:
         plan, sch, m = self.plan, self.sch, self.m
         items, weights, blocks = self._items()
         lds = self.stages * self.bkv * ((0 if getattr(self, 'kreg', False) else m.d) + m.dv) * 2
-        lanes = gfx950.CUS * max(1, min(2, gfx950.LDS_BYTES // lds))
+        # workgroups at a time: two a CU where their LDS fits, one with 64-row waves (their registers)
+        lanes = gfx950.CUS * (1 if self.wr == 64 else max(1, min(2, gfx950.LDS_BYTES // lds)))
         items, weights, merges = self._split(items, weights, lanes)
         self.slots = sum(c for _, _, _, c in merges)
         order = sorted(range(len(items)), key=lambda i: (-weights[i], i))
@@ -492,7 +498,7 @@ class _Flash:
             workspace["fa_part"] = self.slots * self.bq * (m.dv + 2) * 4
             per_item = self.bq * m.dv // 4 // 256
             launches.append(Launch(f"{self.name}_merge", args, (len(merges) * per_item, 1, 1), (256, 1, 1), 0))
-        flop = 2.0 * sum(w for w in weights) * 32 * self.bkv * (m.d + m.dv)
+        flop = 2.0 * sum(w for w in weights) * self.wr * self.bkv * (m.d + m.dv)
         return Program(
             name=self.name, source=source, launches=launches, outputs=[(m.out.shape, m.out.dtype)],
             inputs=[(s.shape, s.dtype) for s in plan.inputs], tables=tables, workspace=workspace,
@@ -623,6 +629,9 @@ class _Flash:
 {PRELUDE}
 {struct}""")
         kreg = self.kreg
+        two = self.wr == 64  # a wave's rows in two halves: rows er (state as named) and er_b (the same, `_b`)
+        if two and kreg:
+            raise KernelError("64 query rows a wave read K from LDS (the knob kreg is for 32)")
         if kreg and ldk != kstride_j:
             raise KernelError("K fragments in registers need key rows one row pitch apart")
         for s in range(self.stages):
@@ -630,7 +639,7 @@ class _Flash:
                 w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sk{s}[{bkv * D}];")
             w(f"__shared__ __attribute__((aligned(1024))) ak_u16 ak_sv{s}[{bkv * DV}];")
         w(f"""
-extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.name}_args args) {{
+extern "C" __global__ void __launch_bounds__({T}, {1 if two else 2}) {self.name}(const {self.name}_args args) {{
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int* item = args.fa_items + blockIdx.x * {stride};
@@ -639,13 +648,16 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
   const int f_w = ak_ldc(item, 5 + 2 * wave), n_w = ak_ldc(item, 6 + 2 * wave);
   (void)slot;
   {tile_decode}
-  const int er = sub * {bq} + wave * 32 + (lane & 31);   // this lane's query row in the spec tile
+  {f"const int er = sub * {bq} + wave * 64 + (lane & 31), er_b = er + 32;  // this lane's query rows in the spec tile (two halves)" if two else
+   f"const int er = sub * {bq} + wave * 32 + (lane & 31);   // this lane's query row in the spec tile"}
   // Q^T fragments (srcB of S^T = K Q^T): row er, head dims 16 s + 8 (lane / 32) .. + 8
-  ak_bf16x8 qf[{ds}];
+  ak_bf16x8 qf[{ds}];{f" ak_bf16x8 qf_b[{ds}];" if two else ""}
   {{
     const ak_u16* qp = {Q} + ({q_base}) + (long long)er * {ldq} + 8 * (lane >> 5);
 #pragma unroll
-    for (int s = 0; s < {ds}; ++s) qf[s] = *(const ak_bf16x8*)(qp + 16 * s);
+    for (int s = 0; s < {ds}; ++s) qf[s] = *(const ak_bf16x8*)(qp + 16 * s);{f'''
+#pragma unroll
+    for (int s = 0; s < {ds}; ++s) qf_b[s] = *(const ak_bf16x8*)(qp + 32LL * {ldq} + 16 * s);''' if two else ""}
   }}
   const long long k_off = {k_base};
   const long long v_off = {v_base};
@@ -677,12 +689,16 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
       v_roff[dt] = kv * {DV * 2} + ((((d >> 3) ^ (((kv & 3) << 2) & {chv - 1}))) << 4) + (d & 7) * 2;
     }}
   }}
-  ak_f32x16 acc[{dt_n}];
+  ak_f32x16 acc[{dt_n}];{f" ak_f32x16 acc_b[{dt_n}];" if two else ""}
 #pragma unroll
   for (int i = 0; i < {dt_n}; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
-  float m_run = {literal(m.m_init)}, l_run = 0.f;""")
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;{f'''
+#pragma unroll
+  for (int i = 0; i < {dt_n}; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_b[i][r] = 0.f;''' if two else ""}
+  float m_run = {literal(m.m_init)}, l_run = 0.f;{f" float m_run_b = {literal(m.m_init)}, l_run_b = 0.f;" if two else ""}""")
         if kreg:
             w(f"""  // K fragments straight from memory (srcA of S^T = K Q^T): key row 32 t + lane % 32 of the block, head dims
   // 16 s + 8 (lane / 32) .. + 8; one register set per block, alternating
@@ -748,12 +764,67 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
             a = o.append
             for i, (kk, dt) in enumerate(v_order):
                 a(f"{ind}  acc[{dt}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[{i}], pf[{kk}], acc[{dt}], 0, 0, 0);")
+                if two:  # the same V fragment for the second half's rows
+                    a(f"{ind}  acc_b[{dt}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[{i}], pf_b[{kk}], acc_b[{dt}], 0, 0, 0);")
                 if i + v_ahead < len(v_order):
                     a(v_read(i + v_ahead, ind))
             for i in range(len(v_order)):
-                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
+                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, {2 if two else 1}, 0);")
                 if i + v_ahead < len(v_order):
                     a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);")
+            return o
+
+        def softmax(ind: str, x: str) -> List[str]:
+            """The mask's scores in place and the online softmax of the half with state suffix `x` ('' or
+            '_b'), into pf{x}."""
+            o: List[str] = []
+            a = o.append
+            st, er_x = f"st{x}", f"er{x}"
+            # the mask's scores in place (blocks the mask keeps whole skip it); then one max for both
+            a(f"{ind}  if (b_ >= f_w) {{")
+            if x:
+                a(f"{ind}    const int er = {er_x}; (void)er;")
+            for t in range(kt):
+                a(f"{ind}    #pragma unroll")
+                a(f"{ind}    for (int r = 0; r < 16; ++r) {{")
+                a(f"{ind}      const int ec = ec0 + {32 * t} + (r >> 2) * 8 + (r & 3); (void)ec;")
+                a(f"{ind}      const float sv = {st}[{t}][r];")
+                a(f"{ind}      {score_lines}")
+                a(f"{ind}      {st}[{t}][r] = (float)({score_expr});")
+                a(f"{ind}    }}")
+            a(f"{ind}  }}")
+            a(f"{ind}  {{")
+            a(f"{ind}  float mx = -__builtin_inff();")
+            for t in range(kt):
+                a(f"{ind}  #pragma unroll")
+                a(f"{ind}  for (int r = 0; r < 16; ++r) mx = fmaxf(mx, {st}[{t}][r]);")
+            a(f"{ind}  mx = ak_xor32_max(mx);")
+            a(f"{ind}  const float m_new = ak_maximum(m_run{x}, mx);")
+            # Lazy rescaling: the running max moves (and acc, l are rescaled) only when some row's new max
+            # exceeds it by more than RESCALE_SLACK; otherwise p = exp(s - m_run) stays below e^slack and
+            # acc, l keep one common scale, so acc / l is unchanged.
+            a(f"{ind}  if (__ballot(!(m_new <= m_run{x} + {RESCALE_SLACK}f))) {{")
+            a(f"{ind}    const float alpha = ak_exp(m_run{x} - m_new);")
+            a(f"{ind}    l_run{x} *= alpha;")
+            a(f"{ind}    m_run{x} = m_new;")
+            a(f"{ind}    #pragma unroll")
+            a(f"{ind}    for (int i = 0; i < {dt_n}; ++i) acc{x}[i] *= alpha;")
+            a(f"{ind}  }}")
+            # p = exp(s - m) as one fma and v_exp_f32 (2^x)
+            a(f"{ind}  const float mb = -m_run{x} * {LOG2E!r}f;")
+            a(f"{ind}  float ps = 0.f;")
+            for t in range(kt):
+                for half in range(2):
+                    a(f"{ind}  {{ unsigned pk[4];")
+                    a(f"{ind}    #pragma unroll")
+                    a(f"{ind}    for (int r = 0; r < 8; r += 2) {{")
+                    a(f"{ind}      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf({st}[{t}][{8 * half} + r], {LOG2E!r}f, mb));")
+                    a(f"{ind}      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf({st}[{t}][{8 * half} + r + 1], {LOG2E!r}f, mb));")
+                    a(f"{ind}      ps += p0 + p1; pk[r >> 1] = ak_pack_bf16x2(p0, p1); }}")
+                    a(f"{ind}    pf{x}[{2 * t + half}] = __builtin_bit_cast(ak_bf16x8, (ak_u32x4){{pk[0], pk[1], pk[2], pk[3]}}); }}")
+            a(f"{ind}  ps = ak_xor32_sum(ps);")
+            a(f"{ind}  l_run{x} += ps;")
+            a(f"{ind}  }}")
             return o
 
         def compute(s: int, ind: str, r: Optional[int] = None, kset: int = 0) -> List[str]:
@@ -772,6 +843,11 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
             for t in range(kt):
                 a(f"{ind}  #pragma unroll")
                 a(f"{ind}  for (int r = 0; r < 16; ++r) st[{t}][r] = 0.f;")
+            if two:
+                a(f"{ind}  ak_f32x16 st_b[{kt}];")
+                for t in range(kt):
+                    a(f"{ind}  #pragma unroll")
+                    a(f"{ind}  for (int r = 0; r < 16; ++r) st_b[{t}][r] = 0.f;")
             # S^T = K Q^T: the key tiles' MFMA chains alternate (a chain's next MFMA waits for its last), and
             # the K fragments are read K_AHEAD MFMAs ahead of use, so LDS latency stays hidden.
             order = k_order
@@ -789,6 +865,8 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
                     a(f"{ind}  kf[{i}] = *(const ak_bf16x8*)(ks + k_roff[{sl}] + {t * 32 * D * 2});")
                 for i, (t, sl) in enumerate(order):
                     a(f"{ind}  st[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[{i}], qf[{sl}], st[{t}], 0, 0, 0);")
+                    if two:  # the same K fragment for the second half's rows
+                        a(f"{ind}  st_b[{t}] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[{i}], qf_b[{sl}], st_b[{t}], 0, 0, 0);")
                     if i + ahead < len(order):
                         t2, sl2 = order[i + ahead]
                         a(f"{ind}  kf[{i + ahead}] = *(const ak_bf16x8*)(ks + k_roff[{sl2}] + {t2 * 32 * D * 2});")
@@ -800,10 +878,16 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
             if ahead:
                 a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, {ahead}, 0);")
             for i in range(len(order)):
-                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);")
+                a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x008, {2 if two else 1}, 0);")
                 if ahead and i + ahead < len(order):
                     a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);")
             a(f"{ind}  __builtin_amdgcn_sched_group_barrier(0x100, {2 * v_ahead}, 0);")
+            if two:
+                o.extend(softmax(ind, ""))
+                o.extend(softmax(ind, "_b"))
+                o.extend(pv(ind))
+                a(f"{ind}}}")
+                return o
             # the mask's scores in place (blocks the mask keeps whole skip it); then one max for both
             a(f"{ind}  if (b_ >= f_w) {{")
             for t in range(kt):
@@ -872,6 +956,8 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
             w("  }")
         rec.loop(unroll)
         w("  ak_bf16x8 pf[" + str(ks) + "];  // P^T of the block (srcB of O^T = V^T P^T)")
+        if two:
+            w(f"  ak_bf16x8 pf_b[{ks}];  // (the second half's)")
         w(f"  for (int b = 0; b < nblk; b += {unroll}) {{")
         for p_ in range(unroll):
             s, r_ = p_ % self.stages, p_ % self.ring
@@ -905,16 +991,31 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
         if tr:
             w(f"  const unsigned long long tr_c1 = {NOW};")
         if self.slots:
-            w(f"""  if (slot >= 0) {{  // a chunk: (m, l, acc) of its rows to the workspace, for the merge kernel
-    float* part = args.fa_part + (long long)slot * {bq * (DV + 2)};
-    const int lr = wave * 32 + (lane & 31);
+            def part_store(x: str, lr: str) -> str:
+                return f"""  {{
+    const int lr = {lr};
+#pragma unroll
+    for (int dt = 0; dt < {dt_n}; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *(ak_f32x4*)(part + lr * {DV} + 32 * dt + g4 * 8 + (lane >> 5) * 4) =
+            ak_f32x4{{acc{x}[dt][4 * g4], acc{x}[dt][4 * g4 + 1], acc{x}[dt][4 * g4 + 2], acc{x}[dt][4 * g4 + 3]}};
+    if (lane < 32) {{ part[{bq * DV} + lr] = m_run{x}; part[{bq * DV + bq} + lr] = l_run{x}; }}
+    }}"""
+            if two:
+                stores = part_store("", "wave * 64 + (lane & 31)") + "\n" + part_store("_b", "wave * 64 + 32 + (lane & 31)")
+            else:
+                stores = f"""    const int lr = wave * 32 + (lane & 31);
 #pragma unroll
     for (int dt = 0; dt < {dt_n}; ++dt)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4)
         *(ak_f32x4*)(part + lr * {DV} + 32 * dt + g4 * 8 + (lane >> 5) * 4) =
             ak_f32x4{{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]}};
-    if (lane < 32) {{ part[{bq * DV} + lr] = m_run; part[{bq * DV + bq} + lr] = l_run; }}
+    if (lane < 32) {{ part[{bq * DV} + lr] = m_run; part[{bq * DV + bq} + lr] = l_run; }}"""
+            w(f"""  if (slot >= 0) {{  // a chunk: (m, l, acc) of its rows to the workspace, for the merge kernel
+    float* part = args.fa_part + (long long)slot * {bq * (DV + 2)};
+{stores}
     {trace_write}
     return;
   }}""")
@@ -933,7 +1034,25 @@ extern "C" __global__ void __launch_bounds__({T}, 2) {self.name}(const {self.nam
         res[e4] = (float)({out_expr});
       }}
       *(ak_u32x2*)(op + 32 * dt + g4 * 8 + (lane >> 5) * 4) = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
-    }}
+    }}{f'''
+  {{  // the second half's rows: the epilogue sees its row and row sum under the same names
+    const int er = er_b; const float l_run = l_run_b; (void)l_run;
+    ak_u16* op_b = (ak_u16*){O} + ({o_base}) + (long long)er * {ldo};
+#pragma unroll
+    for (int dt = 0; dt < {dt_n}; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {{
+        float res[4];
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {{
+          const int ed = 32 * dt + g4 * 8 + (lane >> 5) * 4 + e4; (void)ed;
+          const float acc_v = acc_b[dt][4 * g4 + e4];
+          {epi_lines}
+          res[e4] = (float)({out_expr});
+        }}
+        *(ak_u32x2*)(op_b + 32 * dt + g4 * 8 + (lane >> 5) * 4) = ak_u32x2{{ak_pack_bf16x2(res[0], res[1]), ak_pack_bf16x2(res[2], res[3])}};
+      }}
+  }}''' if two else ""}
   {trace_write}
 }}""")
         if self.slots:
@@ -999,6 +1118,7 @@ class _FlashF32(_Flash):
             raise KernelError(f"the gfx950 f32 attention lowering takes head dims that are multiples of 4 up to 128 "
                               f"(got {m.d} and {m.dv})")
         self.nw = 4  # rows in groups of 32 for the block lists' mask classes: 128 rows per work item
+        self.wr = 32
         self.bq = 128
         self.bkv = BKV
         if m.rows % self.bq or m.bk % self.bkv:

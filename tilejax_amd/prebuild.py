@@ -143,6 +143,8 @@ def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
                   ((("bkv", 32), ("waves", 8)), 2), ((), 3), ((), 4),
                   ((("bkv", 64), ("split", 0), ("waves", 4)), 2)):
         yield ca.causal_attention, tuple(_bf16(2, 4, 1024, 128) for _ in range(3)), Config(blocks, Pipeline(n, 2), False, hw), False
+    for hw in ((("split", 0),), (("split", 0), ("rows", 64)), (("rows", 64),)):
+        yield ca.causal_attention, tuple(_bf16(2, 4, 1024, 128) for _ in range(3)), Config(blocks, Pipeline(2, 2), False, hw), False
     ins = (_bf16(5, 1, 32, 128), _bf16(500, 16, 1024), _bf16(500, 16, 1024), _i32(5, 100), _i32(5))
     for n in (2, 4):
         for cursor in (False, True):

@@ -6,24 +6,26 @@ contiguous cache (:175-196): per output tile (one sequence) some setup code comp
 runtime mask (`p * P >= lengths[b]`, `j >= lengths[b]`) and reading each through a window (a runtime
 one, `k_pages[block_tables[b, p], :, :]`, or `k_cache[b, j : j + bk, :]`), runs the online softmax that
 `flash.softmax_structure` recognises, and the output is some epilogue of the accumulator and the row sum
-(`finish(own_blocks(acc))`). It computes exactly that, as three launches on one stream:
+(`finish(own_blocks(acc))`). It computes exactly that, as two or three launches on one stream:
 
-1. the device step-table builder (codegen/steps.py) evaluates the runtime mask: every sequence's pages in
-   order, compacted; more workgroups of the same launch materialise each tile's query rows (the setup
-   code's value, per element) in a workspace, so the attention kernel reads them as plain loads (with a
-   cursor instead of tables, a setup launch of its own does);
+1. with step tables, the device step-table builder (codegen/steps.py) evaluates the runtime mask: every
+   sequence's pages in order, compacted; more workgroups of the same launch materialise each tile's query
+   rows (the setup code's value, per element) in a workspace. With a cursor there is no builder: the
+   attention kernel evaluates the mask itself, and computes its query rows itself (`qrows`) or, where the
+   waves own no rows, a setup launch materialises them;
 2. the attention kernel works in kernel steps of SUB = 16 positions (a table step of P positions is P / 16
    of them, in order) and splits the compacted list of them evenly over one workgroup per CU (a sequence's
    pages may span several workgroups, a workgroup several short sequences). It decodes its range's steps
    (tile, code, page offsets) into LDS first, then streams pages with three in flight under each step's
    compute: K fragments HBM -> registers (`buffer_load_dwordx4`, three register sets), V rows HBM -> LDS
    (`buffer_load_dwordx4 ... lds`, three stages); only a tile change drains the queue. Its eight waves each
-   take an eighth of the query rows' width, so S = Q K^T is eight partial products
-   (`v_mfma_f32_16x16x32_bf16`, in four chains) summed through LDS behind an LDS-only barrier; every wave
-   then runs the softmax on the full scores (rescaling only when a row's max grows by more than e^8) and
-   accumulates its eighth of `p @ V` (`v_mfma_f32_32x32x16_bf16`, V read transposed with
-   `ds_read_b64_tr_b16` as soon as the page has landed). When a workgroup leaves a sequence it writes its
-   partial (row max, row sum, accumulator) to a workspace slot;
+   take an eighth of the query rows' width. Where the spec's block-diagonal query rows put every row's
+   values in one wave's columns (`row_owners`), each wave scores its own rows against its own columns and
+   loads its own columns of V, with a workgroup barrier only every few steps; otherwise S = Q K^T is eight
+   partial products (`v_mfma_f32_16x16x32_bf16`, in four chains) summed through LDS behind an LDS-only
+   barrier. The softmax rescales only when a row's max grows by more than e^8, and `p @ V` runs on
+   `v_mfma_f32_32x32x16_bf16` with V read transposed (`ds_read_b64_tr_b16`). When a workgroup leaves a
+   sequence it writes its partial (row max, row sum, accumulator) to a workspace slot;
 3. a merge kernel per sequence rescales and sums its partials (the online softmax's own merge rule:
    exact reassociation of the same sums) and evaluates the epilogue per output element.
 """

@@ -14,11 +14,12 @@ and whose output is a pointwise function of acc and l. `match` recognises that s
 tile code (whatever the spelling: widened statistics, `jnp.tile`, operand order) and extracts the two
 pointwise pieces, `score` and the epilogue, which are emitted per element.
 
-The kernel (one workgroup per block of BQ query rows, BQ = 32 x waves; blocks largest-first so the GPU
-balances them):
+The kernel (one workgroup per block of BQ query rows, BQ = 32 x waves, or 64 x waves with the knob `rows`;
+blocks largest-first so the GPU balances them):
 
-- each wave owns 32 query rows and computes S^T = K Q^T with `v_mfma_f32_32x32x16_bf16`, so a lane holds
-  one query row's scores: the row max and sum are an in-lane reduction plus one exchange with lane ^ 32;
+- each wave owns 32 query rows (or two halves of 32 that share every K and V fragment it reads) and
+  computes S^T = K Q^T with `v_mfma_f32_32x32x16_bf16`, so a lane holds one query row's scores: the row
+  max and sum are an in-lane reduction plus one exchange with lane ^ 32;
 - P^T (bf16) feeds O^T = V^T P^T straight from the S^T accumulators, V read transposed from LDS with
   `ds_read_b64_tr_b16` in the order the accumulator layout gives the key positions;
 - K and V blocks of BKV rows stream HBM -> LDS (`buffer_load_dwordx4 ... lds`) through two stages, the next

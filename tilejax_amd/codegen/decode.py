@@ -45,6 +45,7 @@ from ..jaxlite import Node
 from ..pipeline import Pipeline
 from ..plan import Kind, Operand, Output, Plan
 from ..schedule import CODE_SHIFT, Schedule
+from ..syntax import element_reads
 from .common import Index, strides, tile_base
 from .device import PRELUDE
 from .expr import ElementEmitter, literal
@@ -403,6 +404,13 @@ class _Decode:
     def _decode_tile(self, t: str) -> str:
         return " ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, {t});" for r in self.sch.inner)
 
+    def _tile_values(self, t: str) -> str:
+        """The attention kernel's loop values of tile `t` after the cursor's scan: from its copy in LDS (with
+        step tables, from the table)."""
+        if not self.cursor:
+            return self._decode_tile(t)
+        return " ".join(f"const int lv_{r.var} = cs_lv_{r.var}[{t}];" for r in self.sch.inner)
+
     def _setup_body(self, t: str, y: str) -> str:
         """Chunk `y` of tile `t`'s query rows (the setup code's value, per element), by the workgroup's
         threads."""
@@ -526,7 +534,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(c
             table_lines.append(f"__constant__ int dc_slot[{self.waves}][{RP}] = {{"
                                + ", ".join("{" + ", ".join(map(str, sl)) + "}" for sl in slot_of) + "};")
             q_expr = self._emitter(lambda n, idx: None).at(m.q_node, ("qr", "qc"))
-            q_load = f"""{self._decode_tile("t")}
+            q_load = f"""{self._tile_values("t")}
     ak_u16* stg = (ak_u16*)&dc_sp[wave][0][0];  // this wave's own rows x its {WQ} columns
 #pragma unroll
     for (int i = 0; i < {per_lane}; ++i) {{
@@ -577,7 +585,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
   for (int j = tid; j < n; j += {self.threads}) {{
     const int x = g0 + j, js = x / {U}, su = x - js * {U};  // the table's step, and the part of its block
     {self._cursor_step() if self.cursor else "const int t = args.rt_step_tile[js], code = args.rt_step_code[js];"}
-    {self._decode_tile("t")}
+    {self._tile_values("t")}
     const int lv_{jvar} = {phase.start} + ((code >> {CODE_SHIFT}) / {radix}) * {phase.step};
     dc_st[j][0] = t;
     dc_st[j][1] = code;
@@ -836,7 +844,27 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
         kb_run = (f"const int kb = wi * 64 + lane;\n        bool run = false;\n"
                   f"        if (kb < {count}) {{ const int lv_{phase.var} = {phase.start} + kb * {phase.step}; run = !({mask}); }}")
         inner = self.sch.inner
-        if rounds * nb <= 64:
+        # whether the mask's index-array reads are the tile's alone (`lengths[b]`), not the block's
+        reads = element_reads(phase.mask, {ix.name for ix in plan.indices})
+        tile_reads = all(phase.var not in {n.id for n in ast.walk(r.slice) if isinstance(n, ast.Name)} for r in reads)
+        if rounds * nb <= 64 and tile_reads:
+            # A lane per (tile, word): its tile's loop values (one vector load), then the mask's index reads
+            # (the same for the word's 64 blocks, so loaded once), then the word's bits in a loop.
+            ballots = f"""{{
+    const int i_ = lane / {nb}, wi = lane % {nb}, t = wave + {self.waves} * i_;
+    if (lane < {rounds * nb} && t < {pt}) {{
+      {" ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, t);" for r in inner)}
+      unsigned long long word_ = 0;
+      for (int b_ = 0; b_ < 64; ++b_) {{
+        const int kb = wi * 64 + b_;
+        bool run = false;
+        if (kb < {count}) {{ const int lv_{phase.var} = {phase.start} + kb * {phase.step}; run = !({mask}); }}
+        word_ |= (unsigned long long)run << b_;
+      }}
+      cs_run[t * {nb} + wi] = word_;
+    }}
+  }}"""
+        elif rounds * nb <= 64:
             # Straight-line code: all the wave's tiles' loop values are loaded at once, then their masks' index
             # reads, so the latencies overlap; each ballot word is kept by one lane (a select, no branch) and
             # the lanes store them together.
@@ -872,8 +900,13 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
       if (lane == 0) cs_run[t * {nb} + wi] = m_;
     }}
   }}"""
+        # every tile's loop values, for the steps' decode and the tiles' starts (one load a thread, beside
+        # the ballots)
+        lv_copy = "\n  ".join(f"__shared__ int cs_lv_{r.var}[{pt}];\n  for (int t_ = tid; t_ < {pt}; t_ += {self.threads}) "
+                              f"cs_lv_{r.var}[t_] = ak_ldc(args.tv_{r.var}, t_);" for r in inner)
         return f"""__shared__ unsigned long long cs_run[{self.words}];
   __shared__ int cs_start[{pt + 1}], cs_part[{self.threads}];
+  {lv_copy}
   {ballots}
   __syncthreads();
   {{  // kept steps per tile, summed over runs of {per_t} tiles per thread; a scan within each wave (shuffles),

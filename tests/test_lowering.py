@@ -285,3 +285,21 @@ def test_decode_rows_the_probe_does_not_give_to_one_wave(was, now):
     assert make_kernel(source, **{n: getattr(ed, n) for n in names}).lower(*args).program.notes["own_rows"]
     prog = make_kernel(source.replace(was, now), **{n: getattr(ed, n) for n in names}).lower(*args).program
     assert prog.notes["family"] == "decode" and not prog.notes["own_rows"]
+
+
+def test_tile_values_in_arithmetic_sequence_are_computed():
+    """A runtime schedule's per-tile loop values are computed where they form an arithmetic sequence (no load
+    then waits for them) and read from their table otherwise; the expression gives the table's values."""
+    from types import SimpleNamespace
+
+    import numpy as np
+
+    from tilejax_amd.codegen.common import tile_value
+
+    sch = SimpleNamespace(tile_values={"b": np.arange(64, dtype=np.int32), "g": np.array([256, 768, 1280], np.int32),
+                                       "p": np.array([0, 1, 3], np.int32), "one": np.array([7], np.int32)})
+    assert tile_value(sch, "b", "t") == "(0 + (t) * 1)"
+    assert tile_value(sch, "one", "t") == "(7 + (t) * 0)"
+    assert tile_value(sch, "p", "t") == "ak_ldc(args.tv_p, t)"
+    expr = tile_value(sch, "g", "t")
+    assert [eval(expr, {"t": t}) for t in range(3)] == [256, 768, 1280]

@@ -85,6 +85,17 @@ def tile_base(tile: Tile, shape: Sequence[int], index: Index, loop_value: Callab
     return (" + ".join(terms) if terms else "0"), sliced
 
 
+def tile_value(sch: Schedule, var: str, t: str) -> str:
+    """Inner loop `var`'s value at pattern tile `t` (a runtime schedule's `tile_values`): `start + t * step`
+    where that table is an arithmetic sequence (so no load waits for it), else a read of the table, which
+    the kernel takes as `args.tv_<var>`."""
+    vals = np.asarray(sch.tile_values[var], np.int64)
+    step = int(vals[1] - vals[0]) if len(vals) > 1 else 0
+    if len(vals) and np.array_equal(vals, vals[0] + step * np.arange(len(vals))):
+        return f"({int(vals[0])} + ({t}) * {step})"
+    return f"ak_ldc(args.tv_{var}, {t})"
+
+
 def decode_tile(plan: Plan, sch: Schedule, t: str, prefix: str = "lv_", constant: bool = False) -> List[str]:
     """C statements setting `<prefix><var>` to each parallel loop's value at tile `t` (the t-th that runs);
     with `constant`, the tile tables are read through the constant address space (`ak_ldc`)."""

@@ -46,7 +46,7 @@ from ..pipeline import Pipeline
 from ..plan import Kind, Operand, Output, Plan
 from ..schedule import CODE_SHIFT, Schedule
 from ..syntax import element_reads
-from .common import Index, strides, tile_base
+from .common import Index, strides, tile_base, tile_value
 from .device import PRELUDE
 from .expr import ElementEmitter, literal
 from .flash import RESCALE_SLACK, Softmax, _is, _strip, softmax_structure
@@ -402,7 +402,7 @@ class _Decode:
         return prog
 
     def _decode_tile(self, t: str) -> str:
-        return " ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, {t});" for r in self.sch.inner)
+        return " ".join(f"const int lv_{r.var} = {tile_value(self.sch, r.var, t)};" for r in self.sch.inner)
 
     def _tile_values(self, t: str) -> str:
         """The attention kernel's loop values of tile `t` after the cursor's scan: from its copy in LDS (with
@@ -853,7 +853,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
             ballots = f"""{{
     const int i_ = lane / {nb}, wi = lane % {nb}, t = wave + {self.waves} * i_;
     if (lane < {rounds * nb} && t < {pt}) {{
-      {" ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, t);" for r in inner)}
+      {" ".join(f"const int lv_{r.var} = {tile_value(sch, r.var, 't')};" for r in inner)}
       unsigned long long word_ = 0;
       for (int b_ = 0; b_ < 64; ++b_) {{
         const int kb = wi * 64 + b_;
@@ -873,7 +873,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
 #pragma unroll
     for (int i = 0; i < {rounds}; ++i) {{
       const int t_ = ak_imin(wave + {self.waves} * i, {pt - 1});
-      {" ".join(f"lvA_{r.var}[i] = ak_ldc(args.tv_{r.var}, t_);" for r in inner)}
+      {" ".join(f"lvA_{r.var}[i] = {tile_value(sch, r.var, 't_')};" for r in inner)}
     }}
     unsigned long long word_ = 0;
 #pragma unroll
@@ -903,7 +903,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
         # every tile's loop values, for the steps' decode and the tiles' starts (one load a thread, beside
         # the ballots)
         lv_copy = "\n  ".join(f"__shared__ int cs_lv_{r.var}[{pt}];\n  for (int t_ = tid; t_ < {pt}; t_ += {self.threads}) "
-                              f"cs_lv_{r.var}[t_] = ak_ldc(args.tv_{r.var}, t_);" for r in inner)
+                              f"cs_lv_{r.var}[t_] = {tile_value(sch, r.var, 't_')};" for r in inner)
         return f"""__shared__ unsigned long long cs_run[{self.words}];
   __shared__ int cs_start[{pt + 1}], cs_part[{self.threads}];
   {lv_copy}

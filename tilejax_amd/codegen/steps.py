@@ -24,7 +24,7 @@ import numpy as np
 from ..errors import KernelError
 from ..plan import Plan
 from ..schedule import CODE_SHIFT, Schedule
-from .common import Index
+from .common import Index, tile_value
 from .expr import int_expr
 from .program import Arg, Launch, Program, c_struct
 
@@ -47,7 +47,7 @@ def builder_source(plan: Plan, sch: Schedule, name: str, args: List[Arg], extra:
     index = Index(plan, lambda v: f"lv_{v}")
     mask = index.expr(phase.mask)
     radix = sch.phase_radix * sch.iterations
-    decode = " ".join(f"const int lv_{r.var} = ak_ldc(args.tv_{r.var}, t);" for r in sch.inner)
+    decode = " ".join(f"const int lv_{r.var} = {tile_value(sch, r.var, 't')};" for r in sch.inner)
     struct = c_struct(f"{name}_args", args)
     per = (pt + THREADS - 1) // THREADS
     nb = -(-count // 64)  # 64-block words per tile

@@ -278,7 +278,7 @@ class _Decode:
         self.phase = plan.phases[0].range
         # partials per tile: at most its kernel steps or the grid (+1 for the division's edges)
         self.maxs = min(self.grid, self.phase.count * self.sub) + 1
-        if self.maxs * RP * 4 > 96 * 1024:
+        if 2 * self.maxs * RP * 4 > 96 * 1024:  # the merge kernel's weights and row sums per partial and row
             raise KernelError("too many pages per sequence for the merge kernel's LDS")
         # With `fold` the merge runs in the attention kernel (the last workgroup to finish a tile merges it), its
         # LDS (the partials' weights and row sums) beside the kernel's own; else it is a launch of its own.
@@ -984,8 +984,8 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
 
     def _merge_body(self, e_begin: str, e_end: str) -> str:
         """Merge tile `t`'s `n` partials (slots t + w0 onwards: row max m, row sum l, accumulator) and write
-        its output elements [e_begin, e_end), per element, by the workgroup's threads; `dc_w` and `dc_lsum`
-        are LDS arrays of the caller's."""
+        its output elements [e_begin, e_end), per element, by the workgroup's threads; `dc_w`, `dc_lsum` and
+        (without `fold`) `dc_lw` are LDS arrays of the caller's."""
         plan, m = self.plan, self.m
         R, W = m.rows, m.width
         out_shape = m.out.tile.shape
@@ -1007,28 +1007,35 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
             unravel.append(f"const int o{k} = ({rest}) / {st};")
             rest = f"({rest}) % {st}"
         flat_out = " + ".join(f"(long long)o{k} * {s}" for k, s in enumerate(o_str))
+        # the row sums: loaded with the maxima into LDS `dc_lw` (one round of loads; the merge launch), or read
+        # in the second pass (the fold, whose LDS holds the attention kernel's too)
+        together = not self.fold
+        lw = (lambda k: f"dc_lw[{k}][r]") if together else (lambda k: f"lp[({k}) * {RP}]")
+        keep_l = (f"\n      dc_lw[k][r] = lp[k * {RP}]; dc_lw[k + 1][r] = lp[(k + 1) * {RP}]; "
+                  f"dc_lw[k + 2][r] = lp[(k + 2) * {RP}]; dc_lw[k + 3][r] = lp[(k + 3) * {RP}];") if together else ""
         return f"""  {self._decode_tile("t")}
-  // The partials' loads go out four at a time (they are independent); the sums run in partial order.
+  // The partials' loads go out four at a time (they are independent){", the row maxima and row sums together" if together else ""};
+  // the sums run in partial order.
   for (int r = threadIdx.x; r < {R}; r += {self.threads}) {{
     const float* mp = args.dc_m + (t + w0) * {RP} + r;
     const float* lp = args.dc_l + (t + w0) * {RP} + r;
     float mm = -__builtin_inff();
     int k = 0;
     for (; k + 4 <= n; k += 4) {{
-      const float a0 = mp[k * {RP}], a1 = mp[(k + 1) * {RP}], a2 = mp[(k + 2) * {RP}], a3 = mp[(k + 3) * {RP}];
+      const float a0 = mp[k * {RP}], a1 = mp[(k + 1) * {RP}], a2 = mp[(k + 2) * {RP}], a3 = mp[(k + 3) * {RP}];{keep_l}
       dc_w[k][r] = a0; dc_w[k + 1][r] = a1; dc_w[k + 2][r] = a2; dc_w[k + 3][r] = a3;
       mm = fmaxf(fmaxf(fmaxf(fmaxf(mm, a0), a1), a2), a3);
     }}
-    for (; k < n; ++k) {{ const float a = mp[k * {RP}]; dc_w[k][r] = a; mm = fmaxf(mm, a); }}
+    for (; k < n; ++k) {{ const float a = mp[k * {RP}]; {f"dc_lw[k][r] = lp[k * {RP}]; " if together else ""}dc_w[k][r] = a; mm = fmaxf(mm, a); }}
     float ls = 0.f;
     for (k = 0; k + 4 <= n; k += 4) {{
-      const float l0 = lp[k * {RP}], l1 = lp[(k + 1) * {RP}], l2 = lp[(k + 2) * {RP}], l3 = lp[(k + 3) * {RP}];
+      const float l0 = {lw("k")}, l1 = {lw("k + 1")}, l2 = {lw("k + 2")}, l3 = {lw("k + 3")};
       const float e0 = ak_exp(dc_w[k][r] - mm), e1 = ak_exp(dc_w[k + 1][r] - mm);
       const float e2 = ak_exp(dc_w[k + 2][r] - mm), e3 = ak_exp(dc_w[k + 3][r] - mm);
       dc_w[k][r] = e0; dc_w[k + 1][r] = e1; dc_w[k + 2][r] = e2; dc_w[k + 3][r] = e3;
       ls += e0 * l0; ls += e1 * l1; ls += e2 * l2; ls += e3 * l3;
     }}
-    for (; k < n; ++k) {{ const float e = ak_exp(dc_w[k][r] - mm); dc_w[k][r] = e; ls += e * lp[k * {RP}]; }}
+    for (; k < n; ++k) {{ const float e = ak_exp(dc_w[k][r] - mm); dc_w[k][r] = e; ls += e * {lw("k")}; }}
     dc_lsum[r] = ls;
   }}
   __syncthreads();
@@ -1061,7 +1068,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
 // Merge a tile's partials (row max m, row sum l, accumulator) and write its output, per element; workgroup
 // (t, y) writes chunk y of tile t's elements, each computing the tile's partial weights.
 extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_merge(const {self.name}_args args) {{
-  __shared__ float dc_w[{self.maxs}][{R}];
+  __shared__ float dc_w[{self.maxs}][{R}], dc_lw[{self.maxs}][{R}];
   __shared__ float dc_lsum[{R}];
   const int t = blockIdx.x;
   const int count = args.rt_count[0] * {self.sub};  // kernel steps, as the attention kernel divides them

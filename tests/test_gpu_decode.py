@@ -259,15 +259,21 @@ def test_waves_with_their_own_rows_are_bit_equal(cursor):
     assert torch.equal(got, want) and torch.equal(unsynced, want) and torch.equal(rows_other_way, want)
 
 
-def test_multi_head_decode_gives_each_wave_one_head():
-    """MHA (8 query heads, 8 kv heads): 8 query rows, a row a wave, the kernel's other 24 rows owned by none."""
+@pytest.mark.parametrize("cursor", [False, True])
+def test_multi_head_decode_gives_each_wave_one_head(cursor):
+    """MHA (8 query heads, 8 kv heads): 8 query rows, a row a wave, the kernel's other 24 rows owned by none;
+    with a cursor the attention kernel computes each wave's one row itself."""
+    from tilejax_amd.tune import Config
+
     ins = _inputs(4, 8, 8, 128, 16, 64, (0, 33, 700, 1024), seed=5)
-    lowered = _with_tables(paged_gqa_decode, ins)
-    assert lowered.program.notes["own_rows"]
-    print("paged decode MHA 8 heads", flush=True)
+    plain = _with_tables(paged_gqa_decode, ins)
+    lowered = paged_gqa_decode.lowered(paged_gqa_decode.signature(*ins),
+                                       Config(plain.config.tunable, plain.config.pipeline, cursor))
+    assert lowered.program.notes["own_rows"] and lowered.program.notes["query_rows_in_kernel"] == cursor
+    print(f"paged decode MHA 8 heads, cursor={cursor}", flush=True)
     got = lowered.run(*(t.cuda() for t in ins))
     torch.cuda.synchronize()
-    _close("paged decode MHA", got, kernels.paged_gqa_decode(*ins), ins)
+    _close(f"paged decode MHA cursor={cursor}", got, kernels.paged_gqa_decode(*ins), ins)
 
 
 @pytest.mark.parametrize("cursor", [False, True])

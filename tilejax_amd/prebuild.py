@@ -157,6 +157,9 @@ def shapes() -> Iterator[Tuple[object, tuple, object, bool]]:
             yield decode.paged_gqa_decode, ins, Config(base.tunable, base.pipeline, cursor, hw), False
     for cursor in (False, True):
         yield decode.paged_gqa_decode, ins, Config(base.tunable, base.pipeline, cursor, (("qrows", int(not cursor)),)), False
+    ins = (_bf16(4, 1, 8, 128), _bf16(256, 16, 1024), _bf16(256, 16, 1024), _i32(4, 64), _i32(4))  # MHA
+    base = decode.paged_gqa_decode.default_config(decode.paged_gqa_decode.signature(*ins))
+    yield decode.paged_gqa_decode, ins, Config(base.tunable, base.pipeline, True), False
 
 
 def compile_all(verbose: bool = True) -> List[str]:

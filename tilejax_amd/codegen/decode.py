@@ -439,7 +439,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}_setup(c
 
     def _attention_source(self) -> str:
         plan, sch, m = self.plan, self.sch, self.m
-        R, P, W = m.rows, SUB, m.width
+        P, W = SUB, m.width
         U = self.sub
         WQ = W // self.waves  # a wave's share of the width
         slabs = WQ // 32  # K = 32 slabs of S^T = K Q^T per wave
@@ -986,7 +986,7 @@ extern "C" __global__ void __launch_bounds__({self.threads}) {self.name}(const {
         """Merge tile `t`'s `n` partials (slots t + w0 onwards: row max m, row sum l, accumulator) and write
         its output elements [e_begin, e_end), per element, by the workgroup's threads; `dc_w`, `dc_lsum` and
         (without `fold`) `dc_lw` are LDS arrays of the caller's."""
-        plan, m = self.plan, self.m
+        m = self.m
         R, W = m.rows, m.width
         out_shape = m.out.tile.shape
         o_base, o_str = tile_base(m.out.tile, m.out.shape, self.index, lambda v: f"lv_{v}")

@@ -364,9 +364,8 @@ class _Flash:
 
     def _items(self):
         plan, sch, m = self.plan, self.sch, self.m
-        jr, bkv, bq, nw = self.jr, self.bkv, self.bq, self.nw
+        jr, bq = self.jr, self.bq
         subs = m.rows // bq
-        per_spec = m.bk // bkv
         offsets = static_tile_steps(sch) if sch.step_tables else None
         codes = sch.tables.get(STEP_CODE)
         patterns: Dict[Tuple, Tuple[List[Tuple[int, int]], List[Tuple[int, int]]]] = {}
@@ -517,7 +516,6 @@ class _Flash:
         plan, m = self.plan, self.m
         args = []
         for k, name in enumerate(plan.nest.params):
-            spec = plan.inputs[k]
             if any(ix.name == name for ix in plan.indices):
                 args.append(Arg("input", k, "const int* __restrict__", name))
             else:
@@ -614,7 +612,7 @@ class _Flash:
 
     def _source(self, args: List[Arg], stride: int) -> str:
         c = self._setup(args)
-        plan, sch, m = self.plan, self.sch, self.m
+        plan, m = self.plan, self.m
         nw, bq, bkv = self.nw, self.bq, self.bkv
         (D, DV, T, kt, ds, ks, dt_n, chk, chv, ldk_n, ldv_n, vo_n, jvar, q_base, k_base, v_base, o_base, ldq, ldk,
          ldv, ldo, kstride_j, vstride_j, k_numel, v_numel, score_lines, score_expr, epi_lines, out_expr, struct,

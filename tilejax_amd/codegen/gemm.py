@@ -472,7 +472,11 @@ PATCHES = [True]  # locality groups of a column band and a patch of rows (False:
 # reads, f32 partials and the filled tiles' stores share HBM, and the fixup reads the partials again: causal
 # 8192^3 at 512^3 tiles measured 484 us at 16 chunks of 8 slices, 475-478 at 8 of 16, 477-480 at 4 of 32.
 # Running a workgroup's small items (fills, constants, its chunk) before its whole tiles, all of them or the
-# fills alone, or after its first or second whole tile by workgroup, measured 5-25 us slower.
+# fills alone, or after its first or second whole tile by workgroup, measured 5-25 us slower. The fixup inside
+# this kernel (chunks first in their lists, each counted in after an agent-scope release, the fixup in parts
+# last in the lists of the workgroups without a chunk, each after an agent-scope acquire) was bit-equal and
+# slower: 514-523 against 461-471 us with a release per wave (each an L2 write-back), 470-474 with one per
+# chunk, 465-470 with no fence at all; at 1024^3, 75, 43 and 27 against 23 us.
 MAX_SPLIT = 8
 
 

@@ -8,7 +8,8 @@ carries the other BASELINE.json configurations in `legs`, each timed the same wa
 - dense at MatmulTiles(1024, 2048, 1024);
 - causal `tril(x @ y)` at the same size, with its time over the dense time;
 - RMSNorm fused with the same matmul (`rmsnorm_matmul`, the reference's examples/rmsnorm_matmul.py);
-- causal MHA at (4, 16, 2048, 128) and (1, 16, 4096, 128);
+- causal MHA at (4, 16, 2048, 128) and (1, 16, 4096, 128), each beside torch's scaled_dot_product_attention
+  (its flash backend) on the same inputs;
 - the MoE grouped GEMM (16384 x 4096 x 14336, 8 experts);
 - paged GQA decode (64 sequences, HBM GB/s), with step tables and with a cursor, and the same sequences
   over a contiguous cache (the reference's gqa_decode).
@@ -167,6 +168,29 @@ def cpu_baseline(budget_s: float = 12.0):
             "kind": "port",
             "sample": f"oracle.kernels.matmul (torch CPU, f32 accumulate) on x[:512] @ y of the 8192^3 workload, "
                       f"512^3 tiles, median of {len(times)} calls ({t * 1e3:.1f} ms each)"}
+
+
+def library_attention(q, k, v, ours, args):
+    """torch's scaled_dot_product_attention on the same inputs (causal, scale 1: q is pre-scaled), for
+    comparison: its flash backend, else its memory-efficient one. Never its math path, whose bf16 batched
+    products of transposed views this build avoids. None if neither backend runs here."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    for backend in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        def run():
+            with sdpa_kernel([backend]):
+                return torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, scale=1.0)
+        try:
+            got = run()
+        except RuntimeError:
+            continue
+        diff = (got.float() - ours.float()).abs().max().item()
+        ms, _ = time_kernel(run, args.steps, args.warmup)
+        return {"what": f"torch scaled_dot_product_attention, {backend.name} backend", "us": round(ms * 1e3, 2),
+                "tflops": round(2.0 * q.shape[0] * q.shape[1] * q.shape[2] ** 2 * q.shape[3] / (ms * 1e-3) / 1e12, 2),
+                "max_abs_diff_to_kernel": diff}
+    return None
 
 
 def source_hash(source: str) -> str:
@@ -396,6 +420,10 @@ def main() -> int:
                 _log(f"causal MHA {B}x{H}x{S}x{D}: {ams * 1e3:.1f} us, {atf:.1f} TFLOP/s")
                 out[key] = {"shape": [B, H, S, D], "blocks": [512, 512], "us": round(ams * 1e3, 2),
                             "tflops": round(atf, 2), "frac_peak": round(atf / PEAK_TFLOPS, 4)}
+                lib = library_attention(q, k, v, al.run(q, k, v), args)
+                if lib:
+                    out[key]["library"] = lib
+                    _log(f"  {lib['what']}: {lib['us']:.1f} us, {aflop / (lib['us'] * 1e-6) / 1e12:.1f} TFLOP/s")
                 if args.regions:
                     out[key]["regions"] = leg_regions(causal_attention, al, (q, k, v))
                 del q, k, v

@@ -468,6 +468,11 @@ def hardware_tile(m: GemmMatch, pipeline: Pipeline, hardware: Optional[Dict[str,
 # must not overlap on two streams.
 QUEUE_TAIL = [False]
 PATCHES = [True]  # locality groups of a column band and a patch of rows (False: the column band alone)
+# A locality group's column band, in workgroup tiles: an XCD's round of 32 tiles is then a patch 8 tiles wide
+# and 4 high. Measured at 8192^3 (256 x 256 tiles, four rounds alternating): 8 wide 812-839 us against 817-846
+# at 4 wide (dense), 456-459 against 460-465 (causal), the MoE grouped matmul level; 1, 2, 16 and 32 wide
+# 1006-1026, 911-925, 856-863 and 860-866 us (dense).
+BAND_TILES = [8]
 # The last round's K-split: at most MAX_SPLIT chunks per tile. Its chunks run at the kernel's end, when their
 # reads, f32 partials and the filled tiles' stores share HBM, and the fixup reads the partials again: causal
 # 8192^3 at 512^3 tiles measured 484 us at 16 chunks of 8 slices, 475-478 at 8 of 16, 477-480 at 4 of 32.
@@ -665,10 +670,10 @@ extern "C" __global__ void __launch_bounds__({THREADS}) {self.name}_parts_{role}
         per_tile = (plan.phases[m.mphase].range.count if plan.phases else 1) if not sch.step_tables else None
         out_rows, out_cols = [w for w in m.out.tile.windows if w.size is not None][:2]
         col_loop, row_loop = out_cols.loop, out_rows.loop
-        # Locality groups: a band of columns (four workgroup tiles wide, or 1024 columns), and within it a patch
-        # of rows, so that an XCD's round of equal items (32 of them, in group order) covers about as many row
-        # panels as column panels whatever order the spec's loops take
-        band = max(hw.bn * 4, 1024)
+        # Locality groups: a band of columns (BAND_TILES workgroup tiles wide), and within it a patch of rows,
+        # so that an XCD's round of equal items (32 of them, in group order) covers a patch of the output
+        # whatever order the spec's loops take
+        band = hw.bn * BAND_TILES[0]
         rows_per_patch = max(1, gfx950.CUS // gfx950.XCDS // max(1, band // hw.bn)) * hw.bm
 
         def locality(values: Dict[str, int], sm: int, sn: int) -> Tuple[int, int]:

@@ -170,6 +170,29 @@ def test_causal_remainder_chunks_go_to_xcds_by_k_range():
     assert sum(1 for _, code, _ in items if code >> 16 == 3) == 128
 
 
+def test_dense_rounds_give_each_xcd_a_patch_8_tiles_wide_and_4_high():
+    """Dense 8192^3 at 512^3 tiles: 1024 256^2 tiles, four rounds of 256 workgroups. In every round, the 32
+    tiles an XCD runs together (workgroup w runs on XCD w % 8) form one patch of 8 tile columns by 4 tile
+    rows, so the XCD's L2 serves 12 operand panels for them, and the 8 XCDs' patches tile the output."""
+    prog = matmul.lower(((8192, 8192), BF16), ((8192, 8192), BF16), MatmulTiles(512, 512, 512)).program
+    offsets, items = prog.tables["wg_items"], prog.tables["items"].reshape(-1, 3)
+    assert all(offsets[w + 1] - offsets[w] == 4 for w in range(256))
+    sub_n = 2  # 256^2 sub-tiles of a 512^2 spec tile, 2 x 2
+    for rnd in range(4):
+        covered = set()
+        for x in range(8):
+            cells = set()
+            for w in range(x, 256, 8):
+                t, code, _ = (int(v) for v in items[offsets[w] + rnd])
+                sm, sn = divmod(code & 0xFFFF, sub_n)
+                cells.add(((t // 16) * 2 + sm, (t % 16) * 2 + sn))  # (tile row, tile column) of the output
+            rows, cols = {r for r, _ in cells}, {c for _, c in cells}
+            assert (len(cells), len(rows), len(cols)) == (32, 4, 8), (rnd, x)
+            assert max(rows) - min(rows) == 3 and max(cols) - min(cols) == 7, (rnd, x)
+            covered |= cells
+        assert len(covered) == 256, rnd
+
+
 def test_attention_stages_past_lds_are_refused_before_compiling():
     """Three LDS stages of 128-key blocks at head dim 128 would take 192 KiB (gfx950 has 160 KiB per CU):
     a KernelError on the host, so the tuner skips the shape, rather than a compiler error."""

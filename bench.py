@@ -325,7 +325,8 @@ def main() -> int:
         ms2, _ = time_kernel(lambda: l2.run(x, y), args.steps, args.warmup)
         _log(f"  {ms2 * 1e3:.1f} us/call, {flop / (ms2 * 1e-3) / 1e12:.1f} TFLOP/s")
         out["dense_1024x2048x1024"] = {"tiles": [t2.tm, t2.tn, t2.tk], "us": round(ms2 * 1e3, 2),
-                                       "tflops": round(flop / (ms2 * 1e-3) / 1e12, 2)}
+                                       "tflops": round(flop / (ms2 * 1e-3) / 1e12, 2),
+                                       "frac_peak": round(flop / (ms2 * 1e-3) / 1e12 / PEAK_TFLOPS, 4)}
 
     if "config1" in legs or not args.only:
         # 1024^3 at MatmulTiles(512, 512, 512), the spec run as `matmul.fn` on the CPU (the
@@ -346,7 +347,8 @@ def main() -> int:
         _log(f"config 1 (1024^3, {t1}): {ms1 * 1e3:.1f} us, {flop1 / (ms1 * 1e-3) / 1e12:.1f} TFLOP/s; the kernel "
              f"against matmul.fn on the CPU: largest difference {diff1:.3g}")
         out["config1"] = {"shape": [1024] * 3, "tiles": [512, 512, 512], "us": round(ms1 * 1e3, 2),
-                          "tflops": round(flop1 / (ms1 * 1e-3) / 1e12, 2), "vs_fn_max_abs_diff": diff1}
+                          "tflops": round(flop1 / (ms1 * 1e-3) / 1e12, 2),
+                          "frac_peak": round(flop1 / (ms1 * 1e-3) / 1e12 / PEAK_TFLOPS, 4), "vs_fn_max_abs_diff": diff1}
         cpu_jobs.append(("config1", f"matmul.fn (the function as written, plain-JAX semantics) on the whole 1024^3 "
                          f"workload, {t1}", lambda: matmul.fn(x1h, y1h, t1), flop1, "TFLOP/s", 3))
 
@@ -371,8 +373,15 @@ def main() -> int:
         cl = causal_matmul.lower(x, y, ct)
         cms, _ = time_kernel(lambda: cl.run(x, y), args.steps, args.warmup)
         _log(f"  {cms * 1e3:.1f} us/call = {cms / ms:.3f} x dense")
+        # the work the kernel executes: its computed workgroup tiles (whole ones, and those cut into K-chunks)
+        notes, items = cl.program.notes, cl.program.tables["items"].reshape(-1, 3)
+        bm, bn, _ = notes["hw_tile"]
+        computed = int(((items[:, 1] >> 16) == 0).sum()) + (notes["split"][0] if notes["split"] else 0)
+        exec_tf = 2.0 * computed * bm * bn * N_DENSE / (cms * 1e-3) / 1e12
         out["causal"] = {"tiles": [ct.tm, ct.tn, ct.tk], "us": round(cms * 1e3, 2), "vs_dense": round(cms / ms, 4),
-                         "tflops_dense_equiv": round(flop / (cms * 1e-3) / 1e12, 2)}
+                         "tflops_dense_equiv": round(flop / (cms * 1e-3) / 1e12, 2),
+                         "computed_tiles": computed, "tflops_executed": round(exec_tf, 2),
+                         "frac_peak": round(exec_tf / PEAK_TFLOPS, 4)}
         if args.regions:
             out["causal"]["regions"] = leg_regions(causal_matmul, cl, (x, y))
         cpu_jobs.append(("causal", f"kernel.reference of the whole 8192^3 causal matmul, {ct} (rate on the dense "
@@ -394,7 +403,8 @@ def main() -> int:
             rms_, _ = time_kernel(lambda: rl.run(x, gamma, y), args.steps, args.warmup)
             _log(f"RMSNorm + matmul {N_DENSE}^3: {rms_ * 1e3:.1f} us = {rms_ / ms:.3f} x dense")
             out["rmsnorm_matmul"] = {"shape": [N_DENSE] * 3, "us": round(rms_ * 1e3, 2), "vs_dense": round(rms_ / ms, 4),
-                                     "tflops": round(flop / (rms_ * 1e-3) / 1e12, 2)}
+                                     "tflops": round(flop / (rms_ * 1e-3) / 1e12, 2),
+                                     "frac_peak": round(flop / (rms_ * 1e-3) / 1e12 / PEAK_TFLOPS, 4)}
         except Exception as e:  # reported, not hidden
             _log(f"RMSNorm + matmul: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
             out["rmsnorm_matmul"] = {"error": f"{type(e).__name__}: {str(e).splitlines()[0][:200]}"}
@@ -554,7 +564,8 @@ def main() -> int:
             gbytes = blocks * Hkv * D * 2 * 2 + 2 * q.numel() * 2 + B * 4
             _log(f"contiguous GQA decode 64 x 8192, block_kv 512: {gms * 1e3:.1f} us, {gbytes / (gms * 1e-3) / 1e9:.0f} GB/s")
             out["decode_contiguous"] = {"sequences": B, "cache": S, "block_kv": 512, "us": round(gms * 1e3, 2),
-                                        "bytes": gbytes, "gbs": round(gbytes / (gms * 1e-3) / 1e9, 1)}
+                                        "bytes": gbytes, "gbs": round(gbytes / (gms * 1e-3) / 1e9, 1),
+                                        "frac_hbm_peak": round(gbytes / (gms * 1e-3) / 1e9 / 8000.0, 4)}
             del kc, vc
         except Exception as e:
             _log(f"decode: not measured ({type(e).__name__}: {str(e).splitlines()[0]})")
